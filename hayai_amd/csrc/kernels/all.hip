@@ -1,0 +1,4 @@
+// Single translation unit for the gfx950 code object (hayai_kernels.hsaco).
+#include "gemv.hip"
+#include "dequant.hip"
+#include "synth.hip"

@@ -1,0 +1,490 @@
+// extern "C" surface declared in include/hayai_hip.h.
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+
+#include "engine.h"
+
+namespace hh {
+const std::string& last_error();
+}
+hh_status engine_create(int device, hh_engine** out);
+void engine_destroy(hh_engine* e);
+
+using namespace hh;
+
+#define HH_NOT_NULL(p, what) \
+    if (!(p)) return fail(HH_ERR_INVALID, "%s is NULL", what)
+
+// [off, off + bytes) must lie inside the buffer.
+static hh_status check_range(const hh_buf* b, size_t off, size_t bytes, const char* what) {
+    if (!b) return fail(HH_ERR_INVALID, "%s: buffer is NULL", what);
+    if (off > b->size || bytes > b->size - off)
+        return fail(HH_ERR_INVALID, "%s: range [%zu, +%zu) outside a %zu-byte buffer", what, off, bytes, b->size);
+    return HH_OK;
+}
+
+static hh_status check_engine(hh_engine* e, const hh_buf* b, const char* what) {
+    if (b && b->engine != e) return fail(HH_ERR_INVALID, "%s: buffer belongs to another engine", what);
+    return HH_OK;
+}
+
+struct hh_pending {
+    hh_engine* engine;
+    void* dx;
+    void* dy;
+    size_t m;
+    hipEvent_t done;
+    bool waited;
+};
+
+extern "C" {
+
+int hh_abi_version(void) { return HH_ABI_VERSION; }
+
+const char* hh_last_error(void) { return last_error().c_str(); }
+
+const char* hh_status_name(hh_status st) {
+    switch (st) {
+    case HH_OK: return "HH_OK";
+    case HH_ERR_NO_DEVICE: return "HH_ERR_NO_DEVICE";
+    case HH_ERR_INVALID: return "HH_ERR_INVALID";
+    case HH_ERR_KERNEL_MISSING: return "HH_ERR_KERNEL_MISSING";
+    case HH_ERR_RUNTIME: return "HH_ERR_RUNTIME";
+    case HH_ERR_OUT_OF_MEMORY: return "HH_ERR_OUT_OF_MEMORY";
+    case HH_ERR_UNSUPPORTED_DEVICE: return "HH_ERR_UNSUPPORTED_DEVICE";
+    }
+    return "HH_ERR_UNKNOWN";
+}
+
+hh_status hh_row_bytes(int t, size_t n, size_t* out) {
+    HH_NOT_NULL(out, "out");
+    return row_bytes(t, n, out);
+}
+
+hh_status hh_validate_gemv_shape(int t, size_t m, size_t n) { return validate_shape(t, m, n); }
+
+hh_status hh_validate_gemv_weights(int t, size_t m, size_t n, size_t len) { return validate_weights(t, m, n, len); }
+
+hh_status hh_device_count(int* count) {
+    HH_NOT_NULL(count, "count");
+    *count = 0;
+    hipError_t err = hipGetDeviceCount(count);
+    if (err == hipErrorNoDevice) {
+        *count = 0;
+        return HH_OK;
+    }
+    if (err != hipSuccess) return hip_fail(err, "hipGetDeviceCount");
+    return HH_OK;
+}
+
+hh_status hh_engine_create(int device, hh_engine** out) {
+    HH_NOT_NULL(out, "out");
+    try {
+        return engine_create(device, out);
+    } catch (const std::bad_alloc&) {
+        return fail(HH_ERR_OUT_OF_MEMORY, "host allocation failed");
+    }
+}
+
+void hh_engine_destroy(hh_engine* e) { engine_destroy(e); }
+
+hh_status hh_engine_info(const hh_engine* e, hh_device_info* out) {
+    HH_NOT_NULL(e, "engine");
+    HH_NOT_NULL(out, "out");
+    memset(out, 0, sizeof *out);
+    snprintf(out->name, sizeof out->name, "%s", e->props.name);
+    snprintf(out->arch, sizeof out->arch, "%s", e->props.gcnArchName);
+    out->device_index = e->device;
+    out->compute_units = e->props.multiProcessorCount;
+    out->wavefront_size = e->props.warpSize;
+    out->clock_khz = e->props.clockRate;
+    out->memory_clock_khz = e->props.memoryClockRate;
+    out->memory_bus_width = e->props.memoryBusWidth;
+    out->total_mem = e->props.totalGlobalMem;
+    out->lds_per_block = e->props.sharedMemPerBlock;
+    out->l2_bytes = (size_t)e->props.l2CacheSize;
+    return HH_OK;
+}
+
+hh_status hh_engine_sync(hh_engine* e) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(e->select());
+    HH_TRY_HIP(hipStreamSynchronize(e->stream), "hipStreamSynchronize(compute)");
+    HH_TRY_HIP(hipStreamSynchronize(e->copy_stream), "hipStreamSynchronize(copy)");
+    return HH_OK;
+}
+
+uint64_t hh_engine_ffn_calls(const hh_engine* e) { return e ? e->ffn_calls.load() : 0; }
+
+// ---------------------------------------------------------------- buffers ------------
+
+hh_status hh_buf_alloc(hh_engine* e, size_t bytes, int kind, hh_buf** out) {
+    HH_NOT_NULL(e, "engine");
+    HH_NOT_NULL(out, "out");
+    *out = nullptr;
+    if (kind != HH_BUF_DEVICE && kind != HH_BUF_PINNED_HOST) return fail(HH_ERR_INVALID, "unknown buffer kind %d", kind);
+    HH_TRY(e->select());
+    void* p = nullptr;
+    const size_t sz = std::max<size_t>(bytes, 1);
+    if (kind == HH_BUF_DEVICE) {
+        HH_TRY_HIP(hipMalloc(&p, sz), "hipMalloc");
+    } else {
+        HH_TRY_HIP(hipHostMalloc(&p, sz, hipHostMallocDefault), "hipHostMalloc");
+    }
+    hh_buf* b = new (std::nothrow) hh_buf{e, p, bytes, kind};
+    if (!b) {
+        if (kind == HH_BUF_DEVICE)
+            hipFree(p);
+        else
+            hipHostFree(p);
+        return fail(HH_ERR_OUT_OF_MEMORY, "host allocation failed");
+    }
+    *out = b;
+    return HH_OK;
+}
+
+void hh_buf_free(hh_buf* b) {
+    if (!b) return;
+    hipSetDevice(b->engine->device);
+    // Work queued on the engine may still read the buffer.
+    hipStreamSynchronize(b->engine->stream);
+    hipStreamSynchronize(b->engine->copy_stream);
+    if (b->kind == HH_BUF_DEVICE)
+        hipFree(b->ptr);
+    else
+        hipHostFree(b->ptr);
+    delete b;
+}
+
+size_t hh_buf_size(const hh_buf* b) { return b ? b->size : 0; }
+
+int hh_buf_kind(const hh_buf* b) { return b ? b->kind : -1; }
+
+void* hh_buf_host_ptr(hh_buf* b) { return (b && b->kind == HH_BUF_PINNED_HOST) ? b->ptr : nullptr; }
+
+hh_status hh_buf_write(hh_engine* e, hh_buf* dst, size_t off, const void* src, size_t bytes) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(check_engine(e, dst, "hh_buf_write"));
+    HH_TRY(check_range(dst, off, bytes, "hh_buf_write"));
+    if (bytes == 0) return HH_OK;
+    HH_NOT_NULL(src, "src");
+    HH_TRY(e->select());
+    HH_TRY_HIP(hipMemcpyAsync((char*)dst->ptr + off, src, bytes, hipMemcpyDefault, e->stream), "hipMemcpyAsync(H2D)");
+    HH_TRY_HIP(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
+    return HH_OK;
+}
+
+hh_status hh_buf_read(hh_engine* e, const hh_buf* src, size_t off, void* dst, size_t bytes) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(check_engine(e, src, "hh_buf_read"));
+    HH_TRY(check_range(src, off, bytes, "hh_buf_read"));
+    if (bytes == 0) return HH_OK;
+    HH_NOT_NULL(dst, "dst");
+    HH_TRY(e->select());
+    HH_TRY_HIP(hipMemcpyAsync(dst, (const char*)src->ptr + off, bytes, hipMemcpyDefault, e->stream),
+               "hipMemcpyAsync(D2H)");
+    HH_TRY_HIP(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
+    return HH_OK;
+}
+
+hh_status hh_buf_fill(hh_engine* e, hh_buf* dst, size_t off, uint8_t value, size_t bytes) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(check_engine(e, dst, "hh_buf_fill"));
+    HH_TRY(check_range(dst, off, bytes, "hh_buf_fill"));
+    if (bytes == 0) return HH_OK;
+    HH_TRY(e->select());
+    HH_TRY_HIP(hipMemsetAsync((char*)dst->ptr + off, value, bytes, e->stream), "hipMemsetAsync");
+    return HH_OK;
+}
+
+// ---------------------------------------------------------------- GEMV ---------------
+
+hh_status hh_gemv_dev(hh_engine* e, int t, size_t m, size_t n, const hh_buf* w, size_t w_off, const hh_buf* x,
+                      size_t x_off, hh_buf* y, size_t y_off) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_shape(t, m, n));
+    size_t rb;
+    HH_TRY(row_bytes(t, n, &rb));
+    HH_TRY(check_engine(e, w, "weights"));
+    HH_TRY(check_engine(e, x, "x"));
+    HH_TRY(check_engine(e, y, "y"));
+    HH_TRY(check_range(w, w_off, m * rb, "weights"));
+    HH_TRY(check_range(x, x_off, n * sizeof(float), "x"));
+    HH_TRY(check_range(y, y_off, m * sizeof(float), "y"));
+    HH_TRY(e->select());
+    e->ffn_calls++;
+    return e->enqueue_gemv(t, m, n, (const uint8_t*)w->ptr + w_off, (const float*)((const char*)x->ptr + x_off),
+                           (float*)((char*)y->ptr + y_off));
+}
+
+static hh_status gemv_host_io(hh_engine* e, int t, size_t m, size_t n, const uint8_t* wdev, const float* x, float* y) {
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    HH_TRY(e->grow(&e->ws_x, &e->ws_x_cap, n * sizeof(float)));
+    HH_TRY(e->grow(&e->ws_y, &e->ws_y_cap, m * sizeof(float)));
+    HH_TRY_HIP(hipMemcpyAsync(e->ws_x, x, n * sizeof(float), hipMemcpyHostToDevice, e->stream), "hipMemcpyAsync(x)");
+    e->ffn_calls++;
+    HH_TRY(e->enqueue_gemv(t, m, n, wdev, (const float*)e->ws_x, (float*)e->ws_y));
+    HH_TRY_HIP(hipMemcpyAsync(y, e->ws_y, m * sizeof(float), hipMemcpyDeviceToHost, e->stream), "hipMemcpyAsync(y)");
+    HH_TRY_HIP(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
+    return HH_OK;
+}
+
+hh_status hh_gemv_bound(hh_engine* e, int t, size_t m, size_t n, const hh_buf* w, size_t w_off, const float* x,
+                        float* y) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_shape(t, m, n));
+    size_t rb;
+    HH_TRY(row_bytes(t, n, &rb));
+    HH_TRY(check_engine(e, w, "weights"));
+    HH_TRY(check_range(w, w_off, m * rb, "weights"));
+    HH_NOT_NULL(x, "x");
+    HH_NOT_NULL(y, "y");
+    HH_TRY(e->select());
+    return gemv_host_io(e, t, m, n, (const uint8_t*)w->ptr + w_off, x, y);
+}
+
+hh_status hh_gemv(hh_engine* e, int t, size_t m, size_t n, const uint8_t* weights, size_t weights_len,
+                  const float* x, float* y) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_shape(t, m, n));
+    HH_TRY(validate_weights(t, m, n, weights_len));
+    HH_NOT_NULL(weights, "weights");
+    HH_NOT_NULL(x, "x");
+    HH_NOT_NULL(y, "y");
+    size_t rb;
+    HH_TRY(row_bytes(t, n, &rb));
+    HH_TRY(e->select());
+    {
+        std::lock_guard<std::mutex> lk(e->ws_mutex);
+        HH_TRY(e->grow(&e->ws_w, &e->ws_w_cap, m * rb));
+        HH_TRY_HIP(hipMemcpyAsync(e->ws_w, weights, m * rb, hipMemcpyHostToDevice, e->stream), "hipMemcpyAsync(w)");
+    }
+    return gemv_host_io(e, t, m, n, (const uint8_t*)e->ws_w, x, y);
+}
+
+hh_status hh_gemv_begin(hh_engine* e, int t, size_t m, size_t n, const hh_buf* w, size_t w_off, const float* x,
+                        hh_pending** out) {
+    HH_NOT_NULL(e, "engine");
+    HH_NOT_NULL(out, "out");
+    *out = nullptr;
+    HH_TRY(validate_shape(t, m, n));
+    size_t rb;
+    HH_TRY(row_bytes(t, n, &rb));
+    HH_TRY(check_engine(e, w, "weights"));
+    HH_TRY(check_range(w, w_off, m * rb, "weights"));
+    HH_NOT_NULL(x, "x");
+    HH_TRY(e->select());
+    hh_pending* p = new (std::nothrow) hh_pending{e, nullptr, nullptr, m, nullptr, false};
+    if (!p) return fail(HH_ERR_OUT_OF_MEMORY, "host allocation failed");
+    auto bail = [&](hh_status st) {
+        if (p->dx) hipFree(p->dx);
+        if (p->dy) hipFree(p->dy);
+        if (p->done) hipEventDestroy(p->done);
+        delete p;
+        return st;
+    };
+    hipError_t err = hipMalloc(&p->dx, n * sizeof(float));
+    if (err == hipSuccess) err = hipMalloc(&p->dy, m * sizeof(float));
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&p->done, hipEventDisableTiming);
+    if (err == hipSuccess) err = hipMemcpyAsync(p->dx, x, n * sizeof(float), hipMemcpyHostToDevice, e->stream);
+    if (err != hipSuccess) return bail(hip_fail(err, "hh_gemv_begin"));
+    e->ffn_calls++;
+    hh_status st = e->enqueue_gemv(t, m, n, (const uint8_t*)w->ptr + w_off, (const float*)p->dx, (float*)p->dy);
+    if (st != HH_OK) {
+        hipStreamSynchronize(e->stream);
+        return bail(st);
+    }
+    err = hipEventRecord(p->done, e->stream);
+    if (err != hipSuccess) {
+        hipStreamSynchronize(e->stream);
+        return bail(hip_fail(err, "hipEventRecord"));
+    }
+    *out = p;
+    return HH_OK;
+}
+
+hh_status hh_pending_wait(hh_pending* p, float* y, size_t m) {
+    HH_NOT_NULL(p, "pending");
+    HH_NOT_NULL(y, "y");
+    if (m < p->m) return fail(HH_ERR_INVALID, "hh_pending_wait: output holds %zu < %zu floats", m, p->m);
+    HH_TRY(p->engine->select());
+    HH_TRY_HIP(hipEventSynchronize(p->done), "hipEventSynchronize");
+    p->waited = true;
+    HH_TRY_HIP(hipMemcpy(y, p->dy, p->m * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy(y)");
+    return HH_OK;
+}
+
+void hh_pending_destroy(hh_pending* p) {
+    if (!p) return;
+    hipSetDevice(p->engine->device);
+    hipEventSynchronize(p->done);  // never free buffers a queued kernel still uses
+    hipFree(p->dx);
+    hipFree(p->dy);
+    hipEventDestroy(p->done);
+    delete p;
+}
+
+hh_status hh_dequant_dev(hh_engine* e, int t, const hh_buf* w, size_t w_off, size_t n, hh_buf* out, size_t out_off) {
+    HH_NOT_NULL(e, "engine");
+    const Format* f = format_of(t);
+    if (!f || t == HH_TYPE_F32) return fail(HH_ERR_KERNEL_MISSING, "no dequant kernel for GGML type %d", t);
+    if (t != HH_TYPE_Q4_0 && n % f->block != 0)
+        return fail(HH_ERR_INVALID, "dequant_%s: n=%zu not a multiple of %u", f->name, n, f->block);
+    const size_t nblk = (n + f->block - 1) / f->block;
+    HH_TRY(check_engine(e, w, "weights"));
+    HH_TRY(check_engine(e, out, "out"));
+    HH_TRY(check_range(w, w_off, nblk * f->bytes, "weights"));
+    HH_TRY(check_range(out, out_off, n * sizeof(float), "out"));
+    if ((w_off & 1u) || (out_off & 3u)) return fail(HH_ERR_INVALID, "dequant_%s: misaligned offsets", f->name);
+    if (n == 0) return HH_OK;
+    HH_TRY(e->select());
+    hipFunction_t fn;
+    HH_TRY(e->kernel(std::string("hh_dequant_") + f->name, &fn));
+    hh_dequant_args a{(const uint8_t*)w->ptr + w_off, (float*)((char*)out->ptr + out_off), (uint64_t)n};
+    const size_t threads = t == HH_TYPE_F16 ? n : nblk;
+    return e->launch(fn, (uint32_t)((threads + 255) / 256), 256, a);
+}
+
+// ---------------------------------------------------------------- FFN ----------------
+
+static hh_status validate_ffn(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off) {
+    HH_NOT_NULL(d, "desc");
+    if (d->act != HH_ACT_SILU && d->act != HH_ACT_GELU_TANH) return fail(HH_ERR_INVALID, "ffn: unknown act %d", d->act);
+    HH_TRY(validate_shape(d->type_gate, d->d_ff, d->d_model));
+    HH_TRY(validate_shape(d->type_up, d->d_ff, d->d_model));
+    HH_TRY(validate_shape(d->type_down, d->d_model, d->d_ff));
+    size_t rg, ru, rd;
+    HH_TRY(row_bytes(d->type_gate, d->d_model, &rg));
+    HH_TRY(row_bytes(d->type_up, d->d_model, &ru));
+    HH_TRY(row_bytes(d->type_down, d->d_ff, &rd));
+    HH_TRY(check_engine(e, pack, "pack"));
+    if (pack_off > pack->size) return fail(HH_ERR_INVALID, "ffn: pack offset outside the buffer");
+    HH_TRY(check_range(pack, pack_off + d->gate_off, d->d_ff * rg, "ffn gate"));
+    HH_TRY(check_range(pack, pack_off + d->up_off, d->d_ff * ru, "ffn up"));
+    HH_TRY(check_range(pack, pack_off + d->down_off, d->d_model * rd, "ffn down"));
+    return HH_OK;
+}
+
+hh_status hh_ffn_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off, const hh_buf* x,
+                     size_t x_off, hh_buf* y, size_t y_off) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_ffn(e, d, pack, pack_off));
+    HH_TRY(check_engine(e, x, "x"));
+    HH_TRY(check_engine(e, y, "y"));
+    HH_TRY(check_range(x, x_off, d->d_model * sizeof(float), "x"));
+    HH_TRY(check_range(y, y_off, d->d_model * sizeof(float), "y"));
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    return e->enqueue_ffn(d, (const uint8_t*)pack->ptr + pack_off, (const float*)((const char*)x->ptr + x_off),
+                          (float*)((char*)y->ptr + y_off));
+}
+
+hh_status hh_ffn(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off, const float* x, float* y) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_ffn(e, d, pack, pack_off));
+    HH_NOT_NULL(x, "x");
+    HH_NOT_NULL(y, "y");
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    HH_TRY(e->grow(&e->ws_x, &e->ws_x_cap, d->d_model * sizeof(float)));
+    HH_TRY(e->grow(&e->ws_y, &e->ws_y_cap, d->d_model * sizeof(float)));
+    HH_TRY_HIP(hipMemcpyAsync(e->ws_x, x, d->d_model * sizeof(float), hipMemcpyHostToDevice, e->stream),
+               "hipMemcpyAsync(x)");
+    HH_TRY(e->enqueue_ffn(d, (const uint8_t*)pack->ptr + pack_off, (const float*)e->ws_x, (float*)e->ws_y));
+    HH_TRY_HIP(hipMemcpyAsync(y, e->ws_y, d->d_model * sizeof(float), hipMemcpyDeviceToHost, e->stream),
+               "hipMemcpyAsync(y)");
+    HH_TRY_HIP(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
+    return HH_OK;
+}
+
+hh_status hh_gateup_dev(hh_engine* e, int tg, int tu, size_t d_ff, size_t d_model, const hh_buf* wg, size_t wg_off,
+                        const hh_buf* wu, size_t wu_off, const hh_buf* x, size_t x_off, hh_buf* h, size_t h_off,
+                        int act) {
+    HH_NOT_NULL(e, "engine");
+    if (act != HH_ACT_SILU && act != HH_ACT_GELU_TANH) return fail(HH_ERR_INVALID, "gateup: unknown act %d", act);
+    HH_TRY(validate_shape(tg, d_ff, d_model));
+    HH_TRY(validate_shape(tu, d_ff, d_model));
+    size_t rg, ru;
+    HH_TRY(row_bytes(tg, d_model, &rg));
+    HH_TRY(row_bytes(tu, d_model, &ru));
+    for (const hh_buf* b : {wg, wu, (const hh_buf*)x, (const hh_buf*)h}) HH_TRY(check_engine(e, b, "gateup"));
+    HH_TRY(check_range(wg, wg_off, d_ff * rg, "gate"));
+    HH_TRY(check_range(wu, wu_off, d_ff * ru, "up"));
+    HH_TRY(check_range(x, x_off, d_model * sizeof(float), "x"));
+    HH_TRY(check_range(h, h_off, d_ff * sizeof(float), "h"));
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    e->ffn_calls += 2;
+    return e->enqueue_gateup(tg, tu, d_ff, d_model, (const uint8_t*)wg->ptr + wg_off, (const uint8_t*)wu->ptr + wu_off,
+                             (const float*)((const char*)x->ptr + x_off), (float*)((char*)h->ptr + h_off), act);
+}
+
+// ---------------------------------------------------------------- events -------------
+
+hh_status hh_event_create(hh_engine* e, hh_event** out) {
+    HH_NOT_NULL(e, "engine");
+    HH_NOT_NULL(out, "out");
+    HH_TRY(e->select());
+    hh_event* ev = new (std::nothrow) hh_event{nullptr, e->device};
+    if (!ev) return fail(HH_ERR_OUT_OF_MEMORY, "host allocation failed");
+    hipError_t err = hipEventCreate(&ev->ev);
+    if (err != hipSuccess) {
+        delete ev;
+        return hip_fail(err, "hipEventCreate");
+    }
+    *out = ev;
+    return HH_OK;
+}
+
+void hh_event_destroy(hh_event* ev) {
+    if (!ev) return;
+    hipSetDevice(ev->device);
+    hipEventDestroy(ev->ev);
+    delete ev;
+}
+
+hh_status hh_event_record(hh_engine* e, hh_event* ev) {
+    HH_NOT_NULL(e, "engine");
+    HH_NOT_NULL(ev, "event");
+    HH_TRY(e->select());
+    HH_TRY_HIP(hipEventRecord(ev->ev, e->stream), "hipEventRecord");
+    return HH_OK;
+}
+
+hh_status hh_event_elapsed_ms(hh_event* a, hh_event* b, float* ms) {
+    HH_NOT_NULL(a, "start");
+    HH_NOT_NULL(b, "stop");
+    HH_NOT_NULL(ms, "ms");
+    HH_TRY_HIP(hipEventSynchronize(b->ev), "hipEventSynchronize");
+    HH_TRY_HIP(hipEventElapsedTime(ms, a->ev, b->ev), "hipEventElapsedTime");
+    return HH_OK;
+}
+
+// ---------------------------------------------------------------- synthetic data -----
+
+hh_status hh_synth_weights_dev(hh_engine* e, int t, hh_buf* dst, size_t off, size_t n_blocks, uint64_t seed, float lo,
+                               float hi) {
+    HH_NOT_NULL(e, "engine");
+    const Format* f = format_of(t);
+    if (!f) return fail(HH_ERR_KERNEL_MISSING, "no synthetic generator for GGML type %d", t);
+    const size_t bytes = n_blocks * f->bytes;
+    HH_TRY(check_engine(e, dst, "dst"));
+    HH_TRY(check_range(dst, off, bytes, "synth"));
+    if (off & 7u) return fail(HH_ERR_INVALID, "synth: offset must be 8-byte aligned");
+    if (bytes == 0) return HH_OK;
+    HH_TRY(e->select());
+    hipFunction_t fb, fs;
+    HH_TRY(e->kernel("hh_synth_bytes", &fb));
+    HH_TRY(e->kernel("hh_synth_scales", &fs));
+    hh_synth_args a{(uint8_t*)dst->ptr + off, (uint64_t)bytes, seed, (uint64_t)n_blocks, t, lo, hi, 0};
+    const size_t words = (bytes + 7) / 8;
+    const uint32_t grid = (uint32_t)std::min<size_t>((words + 255) / 256, 65536);
+    HH_TRY(e->launch(fb, grid, 256, a));
+    if (t == HH_TYPE_F32 || t == HH_TYPE_F16) return HH_OK;
+    return e->launch(fs, (uint32_t)((n_blocks + 255) / 256), 256, a);
+}
+
+}  // extern "C"

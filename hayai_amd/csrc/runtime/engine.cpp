@@ -1,0 +1,308 @@
+// HIP runtime of the FFN engine: device bring-up, code-object loading, validation,
+// workspaces and kernel dispatch.  The extern "C" surface is in capi.cpp.
+#include "engine.h"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+// gfx950 code object embedded by blob.S (.incbin of the --genco output).
+extern "C" const unsigned char hh_kernels_blob[];
+extern "C" const unsigned char hh_kernels_blob_end[];
+
+namespace hh {
+
+static thread_local std::string g_last_error;
+
+const std::string& last_error() { return g_last_error; }
+
+hh_status fail(hh_status st, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return st;
+}
+
+hh_status hip_fail(hipError_t err, const char* what) {
+    return fail(err == hipErrorOutOfMemory ? HH_ERR_OUT_OF_MEMORY : HH_ERR_RUNTIME, "%s: %s (%d)", what,
+                hipGetErrorString(err), (int)err);
+}
+
+// Formats with kernels here; block geometry from compute.rs:877-907.
+static const Format kFormats[] = {
+    {HH_TYPE_F32, "f32", 1, 4, 32, false},
+    {HH_TYPE_F16, "f16", 1, 2, 32, false},
+    {HH_TYPE_Q4_0, "q4_0", 32, 18, 32, true},
+    {HH_TYPE_Q4_K, "q4_k", 256, 144, 64, true},
+    {HH_TYPE_IQ2_XXS, "iq2_xxs", 256, 66, 32, true},
+    {HH_TYPE_IQ3_XXS, "iq3_xxs", 256, 98, 32, true},
+};
+
+const Format* format_of(int t) {
+    for (const Format& f : kFormats)
+        if (f.type == t) return &f;
+    return nullptr;
+}
+
+const TeamCfg kTeamCfgs[] = {{16, 1}, {32, 1}, {64, 1}, {128, 1}, {256, 1}, {512, 1}, {512, 2}};
+const int kNumTeamCfgs = (int)(sizeof kTeamCfgs / sizeof kTeamCfgs[0]);
+
+hh_status row_bytes(int t, size_t n, size_t* out) {
+    const Format* f = format_of(t);
+    if (!f) return fail(HH_ERR_KERNEL_MISSING, "no GEMV kernel for GGML type %d", t);
+    if (n % f->block != 0)
+        return fail(HH_ERR_INVALID, "ggml_gemv_%s: n=%zu is not a valid column count for this layout", f->name,
+                    n);
+    *out = (n / f->block) * f->bytes;
+    return HH_OK;
+}
+
+// validate_gemv_shape, compute.rs:935-949.
+hh_status validate_shape(int t, size_t m, size_t n) {
+    const Format* f = format_of(t);
+    if (!f) return fail(HH_ERR_KERNEL_MISSING, "no GEMV kernel for GGML type %d", t);
+    if (m == 0 || n == 0) return fail(HH_ERR_INVALID, "ggml_gemv_%s: empty shape m=%zu n=%zu", f->name, m, n);
+    size_t rb;
+    return row_bytes(t, n, &rb);
+}
+
+// validate_gemv_weights, compute.rs:912-931.
+hh_status validate_weights(int t, size_t m, size_t n, size_t len) {
+    size_t rb;
+    HH_TRY(row_bytes(t, n, &rb));
+    const Format* f = format_of(t);
+    if (m != 0 && rb > SIZE_MAX / m)
+        return fail(HH_ERR_INVALID, "ggml_gemv_%s: weight size overflow for %zux%zu", f->name, m, n);
+    if (len < m * rb)
+        return fail(HH_ERR_INVALID, "ggml_gemv_%s: weight buffer %zu B < %zu B required for %zux%zu", f->name,
+                    len, m * rb, m, n);
+    return HH_OK;
+}
+
+// Pick the smallest instantiated team covering `units` lane units of a row.
+static const TeamCfg* pick_team(size_t units) {
+    for (int i = 0; i < kNumTeamCfgs; i++)
+        if ((size_t)kTeamCfgs[i].team * kTeamCfgs[i].upl >= units) return &kTeamCfgs[i];
+    return nullptr;
+}
+
+// Workgroup size of a team kernel; must equal hh_geom<TEAM>::BLOCK in gemv.hip.
+static int block_of(int team) { return team > 64 ? team : 256; }
+
+}  // namespace hh
+
+using namespace hh;
+
+hh_status hh_engine::select() {
+    hipError_t err = hipSetDevice(device);
+    if (err != hipSuccess) return hip_fail(err, "hipSetDevice");
+    return HH_OK;
+}
+
+hh_status hh_engine::kernel(const std::string& name, hipFunction_t* out) {
+    auto it = fns.find(name);
+    if (it != fns.end()) {
+        *out = it->second;
+        return HH_OK;
+    }
+    hipFunction_t f = nullptr;
+    hipError_t err = hipModuleGetFunction(&f, module, name.c_str());
+    if (err != hipSuccess || !f)
+        return fail(HH_ERR_KERNEL_MISSING, "kernel %s missing from the gfx950 code object", name.c_str());
+    fns[name] = f;
+    *out = f;
+    return HH_OK;
+}
+
+int hh_engine::resident_blocks(const std::string& name, int block) {
+    if (blocks_per_cu_override > 0) return blocks_per_cu_override;
+    auto it = blocks_per_cu.find(name);
+    if (it != blocks_per_cu.end()) return it->second;
+    hipFunction_t f;
+    int nb = 1;
+    if (kernel(name, &f) == HH_OK) {
+        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, block, 0) != hipSuccess || nb < 1) nb = 1;
+    }
+    blocks_per_cu[name] = nb;
+    return nb;
+}
+
+hh_status hh_engine::grow(void** p, size_t* cap, size_t need) {
+    if (need <= *cap && *p) return HH_OK;
+    if (*p) {
+        hipError_t e1 = hipStreamSynchronize(stream);
+        if (e1 != hipSuccess) return hip_fail(e1, "hipStreamSynchronize");
+        hipFree(*p);
+        *p = nullptr;
+        *cap = 0;
+    }
+    size_t sz = std::max<size_t>(need, 256);
+    hipError_t err = hipMalloc(p, sz);
+    if (err != hipSuccess) return hip_fail(err, "hipMalloc(workspace)");
+    *cap = sz;
+    return HH_OK;
+}
+
+hh_status hh_engine::enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w, const float* x, float* y) {
+    const Format* f = format_of(type);
+    if (!f) return fail(HH_ERR_KERNEL_MISSING, "no GEMV kernel for GGML type %d", type);
+    size_t rb;
+    HH_TRY(row_bytes(type, n, &rb));
+    if (((uintptr_t)x & 3u) || ((uintptr_t)y & 3u))
+        return fail(HH_ERR_INVALID, "ggml_gemv_%s: activations must be 4-byte aligned", f->name);
+    hh_gemv_args a{w, x, y, (uint32_t)m, (uint32_t)n, (uint64_t)rb};
+    if (m > UINT32_MAX / 2 || n > UINT32_MAX / 2)
+        return fail(HH_ERR_INVALID, "ggml_gemv_%s: shape %zux%zu too large", f->name, m, n);
+
+    if (type != HH_TYPE_Q4_K && type != HH_TYPE_F32 && ((uintptr_t)w & 1u))
+        return fail(HH_ERR_INVALID, "ggml_gemv_%s: weight address must be 2-byte aligned", f->name);
+    const bool aligned16 = (((uintptr_t)w & 15u) == 0) && (rb % 16 == 0);
+    std::string name;
+    int team = 0, upl = 1;
+    if ((type == HH_TYPE_F32 || type == HH_TYPE_F16) && (n % 32 != 0 || !aligned16)) {
+        name = type == HH_TYPE_F32 ? "hh_gemv_f32_plain" : "hh_gemv_f16_plain";
+        hipFunction_t fn;
+        HH_TRY(kernel(name, &fn));
+        uint32_t grid = (uint32_t)std::min<size_t>((m + 3) / 4, (size_t)props.multiProcessorCount * 8);
+        return launch(fn, std::max<uint32_t>(grid, 1), 256, a);
+    }
+    const TeamCfg* tc = pick_team(n / f->unit);
+    if (!tc)
+        return fail(HH_ERR_INVALID, "ggml_gemv_%s: row of %zu columns is wider than the widest team", f->name, n);
+    team = tc->team;
+    upl = tc->upl;
+    std::string stem = f->name;
+    if (type == HH_TYPE_Q4_K && !aligned16) stem += "_unaligned";
+    name = "hh_gemv_" + stem + "_t" + std::to_string(team) + "_u" + std::to_string(upl);
+    hipFunction_t fn;
+    HH_TRY(kernel(name, &fn));
+    const int block = block_of(team);
+    const int tpb = block / team;
+    const int rows_per_step = upl == 1 ? 4 : 2;
+    const size_t teams = (m + rows_per_step - 1) / rows_per_step;
+    const size_t need = (teams + tpb - 1) / tpb;
+    const size_t cap = (size_t)props.multiProcessorCount * resident_blocks(name, block);
+    const uint32_t grid = (uint32_t)std::max<size_t>(1, std::min(need, cap));
+    return launch(fn, grid, (uint32_t)block, a);
+}
+
+hh_status hh_engine::enqueue_gateup(int tg, int tu, size_t d_ff, size_t d_model, const uint8_t* wg,
+                                    const uint8_t* wu, const float* x, float* h, int act) {
+    const Format* f = format_of(tg);
+    if (!f || !format_of(tu)) return fail(HH_ERR_KERNEL_MISSING, "no GEMV kernel for GGML type %d/%d", tg, tu);
+    size_t rb;
+    HH_TRY(row_bytes(tg, d_model, &rb));
+    if (tg == tu && f->fused_gateup) {
+        if (tg != HH_TYPE_Q4_K && (((uintptr_t)wg | (uintptr_t)wu) & 1u))
+            return fail(HH_ERR_INVALID, "ffn gate/up %s: weight address must be 2-byte aligned", f->name);
+        const TeamCfg* tc = pick_team(d_model / f->unit);
+        if (!tc) return fail(HH_ERR_INVALID, "ffn: d_model=%zu wider than the widest team", d_model);
+        const bool aligned16 = (((uintptr_t)wg & 15u) == 0) && (((uintptr_t)wu & 15u) == 0) && (rb % 16 == 0);
+        std::string stem = f->name;
+        if (tg == HH_TYPE_Q4_K && !aligned16) stem += "_unaligned";
+        std::string name = "hh_gateup_" + stem + "_t" + std::to_string(tc->team) + "_u" + std::to_string(tc->upl);
+        hipFunction_t fn;
+        HH_TRY(kernel(name, &fn));
+        const int block = block_of(tc->team);
+        const int tpb = block / tc->team;
+        const int rows_per_step = tc->upl == 1 ? 2 : 1;
+        const size_t teams = (d_ff + rows_per_step - 1) / rows_per_step;
+        const size_t need = (teams + tpb - 1) / tpb;
+        const size_t cap = (size_t)props.multiProcessorCount * resident_blocks(name, block);
+        hh_gateup_args a{wg, wu, x, h, (uint32_t)d_ff, (uint32_t)d_model, (uint64_t)rb, act, 0};
+        return launch(fn, (uint32_t)std::max<size_t>(1, std::min(need, cap)), (uint32_t)block, a);
+    }
+    // Unfused: gate and up in their own formats, then act(g) * u.
+    HH_TRY(grow(&ws_g, &ws_g_cap, d_ff * sizeof(float)));
+    HH_TRY(grow(&ws_u, &ws_u_cap, d_ff * sizeof(float)));
+    HH_TRY(enqueue_gemv(tg, d_ff, d_model, wg, x, (float*)ws_g));
+    HH_TRY(enqueue_gemv(tu, d_ff, d_model, wu, x, (float*)ws_u));
+    hipFunction_t fn;
+    HH_TRY(kernel("hh_act_mul_kernel", &fn));
+    hh_act_args a{(const float*)ws_g, (const float*)ws_u, h, (uint32_t)d_ff, act};
+    return launch(fn, (uint32_t)((d_ff + 255) / 256), 256, a);
+}
+
+hh_status hh_engine::enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y) {
+    HH_TRY(grow(&ws_h, &ws_h_cap, d->d_ff * sizeof(float)));
+    HH_TRY(enqueue_gateup(d->type_gate, d->type_up, d->d_ff, d->d_model, pack + d->gate_off, pack + d->up_off, x,
+                          (float*)ws_h, d->act));
+    HH_TRY(enqueue_gemv(d->type_down, d->d_model, d->d_ff, pack + d->down_off, (const float*)ws_h, y));
+    ffn_calls += 3;
+    return HH_OK;
+}
+
+// ---------------------------------------------------------------- bring-up -----------
+
+static std::vector<std::string> required_kernels() {
+    std::vector<std::string> k;
+    const char* gemv_fmts[] = {"q4_k", "q4_k_unaligned", "q4_0", "iq2_xxs", "iq3_xxs", "f32", "f16"};
+    const char* gateup_fmts[] = {"q4_k", "q4_k_unaligned", "q4_0", "iq2_xxs", "iq3_xxs"};
+    for (int i = 0; i < kNumTeamCfgs; i++) {
+        std::string suf = "_t" + std::to_string(kTeamCfgs[i].team) + "_u" + std::to_string(kTeamCfgs[i].upl);
+        for (const char* f : gemv_fmts) k.push_back(std::string("hh_gemv_") + f + suf);
+        for (const char* f : gateup_fmts) k.push_back(std::string("hh_gateup_") + f + suf);
+    }
+    for (const char* s : {"hh_gemv_f32_plain", "hh_gemv_f16_plain", "hh_act_mul_kernel", "hh_dequant_q4_0",
+                          "hh_dequant_q4_k", "hh_dequant_iq2_xxs", "hh_dequant_iq3_xxs", "hh_dequant_f16",
+                          "hh_synth_bytes", "hh_synth_scales"})
+        k.push_back(s);
+    return k;
+}
+
+hh_status engine_create(int device, hh_engine** out) {
+    *out = nullptr;
+    int count = 0;
+    hipError_t err = hipGetDeviceCount(&count);
+    if (err != hipSuccess || count == 0) return fail(HH_ERR_NO_DEVICE, "no HIP device found");
+    if (device < 0 || device >= count) return fail(HH_ERR_NO_DEVICE, "device %d out of range (%d devices)", device, count);
+    hh_engine* e = new hh_engine();
+    e->device = device;
+    auto bail = [&](hh_status st) {
+        if (e->stream) hipStreamDestroy(e->stream);
+        if (e->copy_stream) hipStreamDestroy(e->copy_stream);
+        if (e->module) hipModuleUnload(e->module);
+        delete e;
+        return st;
+    };
+    if (hh_status st = e->select(); st != HH_OK) return bail(st);
+    err = hipGetDeviceProperties(&e->props, device);
+    if (err != hipSuccess) return bail(hip_fail(err, "hipGetDeviceProperties"));
+    if (strncmp(e->props.gcnArchName, "gfx950", 6) != 0)
+        return bail(fail(HH_ERR_UNSUPPORTED_DEVICE, "device %d is %s; this build targets gfx950 (MI355X) only",
+                         device, e->props.gcnArchName));
+    const char* path = getenv("HAYAI_HIP_CODE_OBJECT");
+    if (path && *path)
+        err = hipModuleLoad(&e->module, path);
+    else
+        err = hipModuleLoadData(&e->module, hh_kernels_blob);
+    if (err != hipSuccess) return bail(hip_fail(err, "hipModuleLoad(gfx950 code object)"));
+    err = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
+    if (err != hipSuccess) return bail(hip_fail(err, "hipStreamCreate(compute)"));
+    err = hipStreamCreateWithFlags(&e->copy_stream, hipStreamNonBlocking);
+    if (err != hipSuccess) return bail(hip_fail(err, "hipStreamCreate(copy)"));
+    for (const std::string& k : required_kernels()) {
+        hipFunction_t f;
+        if (hh_status st = e->kernel(k, &f); st != HH_OK) return bail(st);
+    }
+    if (const char* b = getenv("HAYAI_HIP_BLOCKS_PER_CU")) e->blocks_per_cu_override = atoi(b);
+    *out = e;
+    return HH_OK;
+}
+
+void engine_destroy(hh_engine* e) {
+    if (!e) return;
+    hipSetDevice(e->device);
+    if (e->stream) hipStreamSynchronize(e->stream);
+    if (e->copy_stream) hipStreamSynchronize(e->copy_stream);
+    for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w})
+        if (p) hipFree(p);
+    if (e->stream) hipStreamDestroy(e->stream);
+    if (e->copy_stream) hipStreamDestroy(e->copy_stream);
+    if (e->module) hipModuleUnload(e->module);
+    delete e;
+}

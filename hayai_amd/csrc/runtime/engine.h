@@ -1,0 +1,124 @@
+// Internal C++ runtime of the HIP FFN engine (not part of the ABI).
+//
+// Engine is the MI355X counterpart of the reference's OpenClEngine
+// (crates/hayai-opencl/src/context.rs:23-69): one device, its loaded gfx950 code object,
+// a compute stream and a copy stream, and persistent activation workspaces that grow on
+// demand (GemvSyncWorkspace, compute.rs:8-17).
+#ifndef HH_RUNTIME_ENGINE_H
+#define HH_RUNTIME_ENGINE_H
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../../include/hayai_hip.h"
+#include "../kargs.h"
+
+namespace hh {
+
+// Thread-local last error.
+hh_status fail(hh_status st, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+hh_status hip_fail(hipError_t err, const char* what);
+
+#define HH_TRY_HIP(call, what)                        \
+    do {                                              \
+        hipError_t _e = (call);                       \
+        if (_e != hipSuccess) return hh::hip_fail(_e, what); \
+    } while (0)
+
+#define HH_TRY(call)                  \
+    do {                              \
+        hh_status _s = (call);        \
+        if (_s != HH_OK) return _s;   \
+    } while (0)
+
+// Block geometry of a GGML format with a kernel here (compute.rs:877-907).
+struct Format {
+    int type;
+    const char* name;   // kernel-name stem
+    uint32_t block;     // elements per block
+    uint32_t bytes;     // bytes per block
+    uint32_t unit;      // columns per lane unit of the team kernels
+    bool fused_gateup;  // has a fused gate/up kernel
+};
+const Format* format_of(int ggml_type);
+hh_status row_bytes(int ggml_type, size_t n, size_t* out);
+hh_status validate_shape(int ggml_type, size_t m, size_t n);
+hh_status validate_weights(int ggml_type, size_t m, size_t n, size_t len);
+
+// Team configurations instantiated in gemv.hip, in selection order.
+struct TeamCfg {
+    int team;
+    int upl;
+};
+extern const TeamCfg kTeamCfgs[];
+extern const int kNumTeamCfgs;
+
+}  // namespace hh
+
+struct hh_buf {
+    hh_engine* engine;
+    void* ptr;  // device pointer, or pinned host pointer (also device-accessible)
+    size_t size;
+    int kind;
+};
+
+struct hh_event {
+    hipEvent_t ev;
+    int device;
+};
+
+struct hh_engine {
+    int device = 0;
+    hipDeviceProp_t props{};
+    hipModule_t module = nullptr;
+    hipStream_t stream = nullptr;       // compute stream (default priority)
+    hipStream_t copy_stream = nullptr;  // side stream for host<->device DMA
+    std::unordered_map<std::string, hipFunction_t> fns;
+    std::unordered_map<std::string, int> blocks_per_cu;  // occupancy per kernel
+    std::atomic<uint64_t> ffn_calls{0};
+    std::mutex ws_mutex;  // guards the workspaces below (the reference's sync_ws Mutex)
+    // Growable device workspaces: x / y for host-activation calls, the FFN intermediate,
+    // separate gate/up outputs for the unfused path, staged host weights for hh_gemv.
+    void* ws_x = nullptr;
+    size_t ws_x_cap = 0;
+    void* ws_y = nullptr;
+    size_t ws_y_cap = 0;
+    void* ws_h = nullptr;
+    size_t ws_h_cap = 0;
+    void* ws_g = nullptr;
+    size_t ws_g_cap = 0;
+    void* ws_u = nullptr;
+    size_t ws_u_cap = 0;
+    void* ws_w = nullptr;
+    size_t ws_w_cap = 0;
+    int blocks_per_cu_override = 0;  // HAYAI_HIP_BLOCKS_PER_CU
+
+    hh_status select();  // hipSetDevice(device)
+    hh_status kernel(const std::string& name, hipFunction_t* out);
+    int resident_blocks(const std::string& name, int block);
+    template <class A>
+    hh_status launch(hipFunction_t f, uint32_t grid, uint32_t block, const A& args) {
+        void* params[] = {const_cast<A*>(&args)};
+        hipError_t err = hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, stream, params, nullptr);
+        if (err != hipSuccess) return hh::hip_fail(err, "hipModuleLaunchKernel");
+        return HH_OK;
+    }
+    hh_status grow(void** p, size_t* cap, size_t need);
+
+    // Enqueue one GEMV y = W . x on the compute stream (all pointers device-visible).
+    hh_status enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w, const float* x, float* y);
+    // Enqueue the fused or unfused gate/up + activation into h.
+    hh_status enqueue_gateup(int type_g, int type_u, size_t d_ff, size_t d_model, const uint8_t* wg,
+                             const uint8_t* wu, const float* x, float* h, int act);
+    hh_status enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y);
+};
+
+#endif

@@ -1,0 +1,363 @@
+"""Host-side mirror of the reference's FFN device interface, over the C ABI.
+
+Names and argument meaning follow the reference so parity tests read like its own tests:
+
+* :class:`HipEngine` <- ``OpenClEngine`` (crates/hayai-opencl/src/context.rs:23-69) and its
+  GEMV methods (compute.rs:39-461, async_gemv.rs:15-305);
+* :class:`PendingGemv` <- ``PendingGemv`` (async_gemv.rs:15-57): ``wait()`` returns the
+  outputs, dropping it waits;
+* :class:`QuantMatrix` <- ``QuantMatrix`` (crates/hayai-model/src/quant.rs:31-54);
+* :class:`LayerPackLayout` <- ``LayerPackLayout`` (crates/hayai-model/src/gguf_stream.rs:1416-1444).
+
+Errors raise :class:`HipError` carrying the ABI status (``HH_ERR_INVALID`` for the
+shape/size rejections of compute.rs:912-949, ``HH_ERR_KERNEL_MISSING`` for a GGML type with
+no kernel -- never a CPU fallback, orchestrator.rs:403-409).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import weakref
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _abi
+
+F32, F16, Q4_0, Q4_K, IQ2_XXS, IQ3_XXS = 0, 1, 2, 12, 16, 18
+ACT_SILU, ACT_GELU_TANH = 0, 1
+BUF_DEVICE, BUF_PINNED_HOST = 0, 1
+TYPE_NAMES = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q4_K: "q4_k", IQ2_XXS: "iq2_xxs", IQ3_XXS: "iq3_xxs"}
+
+
+class HipError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        self.status = status
+        self.status_name = _abi.STATUS_NAMES.get(status, f"status {status}")
+        super().__init__(f"{self.status_name}: {message}")
+
+
+def _check(st: int) -> None:
+    if st != _abi.HH_OK:
+        lib = _abi.load()
+        raise HipError(st, (lib.hh_last_error() or b"").decode(errors="replace"))
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def row_bytes(ggml_type: int, n: int) -> int:
+    out = C.c_size_t(0)
+    _check(_abi.load().hh_row_bytes(ggml_type, n, C.byref(out)))
+    return out.value
+
+
+def validate_gemv_shape(ggml_type: int, m: int, n: int) -> None:
+    _check(_abi.load().hh_validate_gemv_shape(ggml_type, m, n))
+
+
+def validate_gemv_weights(ggml_type: int, m: int, n: int, weights_len: int) -> None:
+    _check(_abi.load().hh_validate_gemv_weights(ggml_type, m, n, weights_len))
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    _check(_abi.load().hh_device_count(C.byref(n)))
+    return n.value
+
+
+class DeviceBuffer:
+    """A device (HBM) or pinned-host buffer owned by an engine."""
+
+    def __init__(self, engine: "HipEngine", nbytes: int, kind: int = BUF_DEVICE):
+        self.engine = engine
+        self.nbytes = int(nbytes)
+        self.kind = kind
+        h = C.c_void_p()
+        _check(engine.lib.hh_buf_alloc(engine.handle, self.nbytes, kind, C.byref(h)))
+        self.handle = h
+        engine._children.add(self)
+
+    def write(self, data: np.ndarray, offset: int = 0) -> None:
+        data = np.ascontiguousarray(data)
+        _check(self.engine.lib.hh_buf_write(self.engine.handle, self.handle, offset, _ptr(data), data.nbytes))
+
+    def read(self, dtype, count: int, offset: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        _check(self.engine.lib.hh_buf_read(self.engine.handle, self.handle, offset, _ptr(out), out.nbytes))
+        return out
+
+    def fill(self, value: int, nbytes: int | None = None, offset: int = 0) -> None:
+        n = self.nbytes - offset if nbytes is None else nbytes
+        _check(self.engine.lib.hh_buf_fill(self.engine.handle, self.handle, offset, value, n))
+
+    def host_view(self) -> np.ndarray:
+        """numpy view of a pinned buffer (HH_BUF_PINNED_HOST only)."""
+        p = self.engine.lib.hh_buf_host_ptr(self.handle)
+        if not p:
+            raise HipError(2, "host_view on a device buffer")
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint8)), shape=(self.nbytes,))
+
+    def free(self) -> None:
+        if self.handle:
+            self.engine.lib.hh_buf_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class PendingGemv:
+    """In-flight GEMV; ``wait()`` returns y.  Dropping it waits first (async_gemv.rs:48-57)."""
+
+    def __init__(self, engine: "HipEngine", handle, m: int):
+        self.engine, self.handle, self.m = engine, handle, m
+        engine._children.add(self)
+
+    def wait(self) -> np.ndarray:
+        y = np.empty(self.m, np.float32)
+        _check(self.engine.lib.hh_pending_wait(self.handle, _ptr(y), self.m))
+        self.close()
+        return y
+
+    def close(self) -> None:
+        if self.handle:
+            self.engine.lib.hh_pending_destroy(self.handle)
+            self.handle = None
+
+    free = close
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self, engine: "HipEngine"):
+        self.engine = engine
+        h = C.c_void_p()
+        _check(engine.lib.hh_event_create(engine.handle, C.byref(h)))
+        self.handle = h
+        engine._children.add(self)
+
+    def record(self) -> None:
+        _check(self.engine.lib.hh_event_record(self.engine.handle, self.handle))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float(0)
+        _check(self.engine.lib.hh_event_elapsed_ms(self.handle, end.handle, C.byref(ms)))
+        return ms.value
+
+    def free(self) -> None:
+        if self.handle:
+            self.engine.lib.hh_event_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+@dataclass
+class QuantMatrix:
+    """Weight descriptor (quant.rs:31-54): y[nrows] = W . x[ncols] in GGML layout."""
+
+    name: str
+    ncols: int
+    nrows: int
+    ggml_type: int
+
+    @property
+    def row_bytes(self) -> int:
+        return row_bytes(self.ggml_type, self.ncols)
+
+    @property
+    def nbytes(self) -> int:
+        return self.nrows * self.row_bytes
+
+
+@dataclass
+class LayerPackLayout:
+    """FFN byte offsets inside a contiguous layer pack (gguf_stream.rs:1416-1444)."""
+
+    gate_off: int
+    up_off: int
+    down_off: int
+    gate_len: int
+    up_len: int
+    down_len: int
+    total: int
+
+    @staticmethod
+    def ffn_only(gate: QuantMatrix, up: QuantMatrix, down: QuantMatrix, align: int = 256) -> "LayerPackLayout":
+        """Pack [gate, up, down] back to back (pack order, gguf_stream.rs:456-464), each
+        region starting on an `align`-byte boundary."""
+        def up_to(v):
+            return (v + align - 1) // align * align
+        g = 0
+        u = up_to(g + gate.nbytes)
+        d = up_to(u + up.nbytes)
+        return LayerPackLayout(g, u, d, gate.nbytes, up.nbytes, down.nbytes, up_to(d + down.nbytes))
+
+    def ffn_region(self, role: int) -> tuple[int, int]:
+        r = role % 3
+        return [(self.gate_off, self.gate_len), (self.up_off, self.up_len), (self.down_off, self.down_len)][r]
+
+
+class HipEngine:
+    """One MI355X device (OpenClEngine analogue)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = _abi.load()
+        # buffers, events and pending GEMVs of this engine; freed before the engine
+        self._children = weakref.WeakSet()
+        h = C.c_void_p()
+        _check(self.lib.hh_engine_create(device, C.byref(h)))
+        self.handle = h
+        info = _abi.DeviceInfo()
+        _check(self.lib.hh_engine_info(self.handle, C.byref(info)))
+        self.device_info = info
+
+    # ---------------------------------------------------------------- lifetime
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            for child in list(self._children):
+                child.free()
+            self.lib.hh_engine_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def device_name(self) -> str:
+        return self.device_info.name.decode()
+
+    @property
+    def arch(self) -> str:
+        return self.device_info.arch.decode()
+
+    @property
+    def ffn_calls(self) -> int:
+        return int(self.lib.hh_engine_ffn_calls(self.handle))
+
+    def sync(self) -> None:
+        _check(self.lib.hh_engine_sync(self.handle))
+
+    # ---------------------------------------------------------------- buffers
+    def alloc(self, nbytes: int, kind: int = BUF_DEVICE) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes, kind)
+
+    def upload(self, data: np.ndarray) -> DeviceBuffer:
+        data = np.ascontiguousarray(data)
+        b = DeviceBuffer(self, data.nbytes)
+        b.write(data)
+        return b
+
+    def event(self) -> Event:
+        return Event(self)
+
+    # ---------------------------------------------------------------- GEMV (compute.rs)
+    def ggml_gemv_dispatch(self, ggml_type: int, m: int, n: int, weights: np.ndarray, inp: np.ndarray) -> np.ndarray:
+        """compute.rs:281-383: host weights uploaded per call."""
+        w = np.ascontiguousarray(weights, dtype=np.uint8)
+        x = np.ascontiguousarray(inp, dtype=np.float32)
+        if x.size != n:
+            raise HipError(2, f"input has {x.size} floats, expected n={n}")
+        y = np.empty(m, np.float32)
+        _check(self.lib.hh_gemv(self.handle, ggml_type, m, n, _ptr(w), w.nbytes, _ptr(x), _ptr(y)))
+        return y
+
+    def ggml_gemv_q4_0(self, m, n, weights, inp):
+        return self.ggml_gemv_dispatch(Q4_0, m, n, weights, inp)
+
+    def ggml_gemv_q4_k(self, m, n, weights, inp):
+        return self.ggml_gemv_dispatch(Q4_K, m, n, weights, inp)
+
+    def ggml_gemv_iq2_xxs(self, m, n, weights, inp):
+        return self.ggml_gemv_dispatch(IQ2_XXS, m, n, weights, inp)
+
+    def ggml_gemv_iq3_xxs(self, m, n, weights, inp):
+        return self.ggml_gemv_dispatch(IQ3_XXS, m, n, weights, inp)
+
+    def ggml_gemv_dispatch_bound(self, ggml_type: int, m: int, n: int, weights: DeviceBuffer, weight_off: int,
+                                 inp: np.ndarray) -> np.ndarray:
+        """compute.rs:388-461: resident weights at a byte offset."""
+        x = np.ascontiguousarray(inp, dtype=np.float32)
+        if x.size != n:
+            raise HipError(2, f"input has {x.size} floats, expected n={n}")
+        y = np.empty(m, np.float32)
+        _check(self.lib.hh_gemv_bound(self.handle, ggml_type, m, n, weights.handle, weight_off, _ptr(x), _ptr(y)))
+        return y
+
+    def ggml_gemv_async_from_device(self, ggml_type: int, m: int, n: int, weights: DeviceBuffer, weight_off: int,
+                                    inp: np.ndarray) -> PendingGemv:
+        """async_gemv.rs:103-121."""
+        x = np.ascontiguousarray(inp, dtype=np.float32)
+        if x.size != n:
+            raise HipError(2, f"input has {x.size} floats, expected n={n}")
+        h = C.c_void_p()
+        _check(self.lib.hh_gemv_begin(self.handle, ggml_type, m, n, weights.handle, weight_off, _ptr(x), C.byref(h)))
+        return PendingGemv(self, h, m)
+
+    def gemv_dev(self, ggml_type, m, n, w: DeviceBuffer, w_off, x: DeviceBuffer, x_off, y: DeviceBuffer, y_off):
+        _check(self.lib.hh_gemv_dev(self.handle, ggml_type, m, n, w.handle, w_off, x.handle, x_off, y.handle, y_off))
+
+    def dequant_dev(self, ggml_type, w: DeviceBuffer, w_off, n, out: DeviceBuffer, out_off=0):
+        _check(self.lib.hh_dequant_dev(self.handle, ggml_type, w.handle, w_off, n, out.handle, out_off))
+
+    def dequant(self, ggml_type: int, data: np.ndarray, n: int) -> np.ndarray:
+        """Dequantize host bytes through the device probe (bit-exact with hayai-model)."""
+        w = self.upload(np.ascontiguousarray(data, dtype=np.uint8))
+        out = self.alloc(max(4 * n, 4))
+        self.dequant_dev(ggml_type, w, 0, n, out)
+        return out.read(np.float32, n)
+
+    # ---------------------------------------------------------------- FFN
+    @staticmethod
+    def ffn_desc(types, d_model, d_ff, layout: LayerPackLayout, act=ACT_SILU) -> _abi.FfnDesc:
+        tg, tu, td = types
+        return _abi.FfnDesc(tg, tu, td, act, d_model, d_ff, layout.gate_off, layout.up_off, layout.down_off)
+
+    def ffn(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, x: np.ndarray) -> np.ndarray:
+        """ffn_begin_gate_up_scratch + ffn_finish_scratch (stream_infer.rs:3752-3864), one call."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.size != desc.d_model:
+            raise HipError(2, f"x has {x.size} floats, expected d_model={desc.d_model}")
+        y = np.empty(desc.d_model, np.float32)
+        _check(self.lib.hh_ffn(self.handle, C.byref(desc), pack.handle, pack_off, _ptr(x), _ptr(y)))
+        return y
+
+    def ffn_dev(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, x: DeviceBuffer, x_off: int,
+                y: DeviceBuffer, y_off: int) -> None:
+        _check(self.lib.hh_ffn_dev(self.handle, C.byref(desc), pack.handle, pack_off, x.handle, x_off, y.handle,
+                                   y_off))
+
+    def gateup_dev(self, types, d_ff: int, d_model: int, wg: DeviceBuffer, wg_off: int, wu: DeviceBuffer,
+                   wu_off: int, x: DeviceBuffer, x_off: int, h: DeviceBuffer, h_off: int, act: int = ACT_SILU) -> None:
+        """h = act(W_gate . x) * (W_up . x) (gate/up half of the FFN op), enqueue only."""
+        tg, tu = types
+        _check(self.lib.hh_gateup_dev(self.handle, tg, tu, d_ff, d_model, wg.handle, wg_off, wu.handle, wu_off,
+                                      x.handle, x_off, h.handle, h_off, act))
+
+    # ---------------------------------------------------------------- synthetic data
+    def synth_weights_dev(self, ggml_type: int, dst: DeviceBuffer, off: int, n_blocks: int, seed: int,
+                          lo: float, hi: float) -> None:
+        _check(self.lib.hh_synth_weights_dev(self.handle, ggml_type, dst.handle, off, n_blocks, seed & ((1 << 64) - 1),
+                                             lo, hi))

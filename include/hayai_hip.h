@@ -1,0 +1,233 @@
+/*
+ * hayai_hip.h -- C ABI of the MI355X (gfx950) FFN GEMV engine.
+ *
+ * This is the drop-in boundary for Hayai's FFN hot path.  Every entry point replaces a
+ * method of the reference's OpenCL device runtime (crates/hayai-opencl) or the FFN seam
+ * in crates/hayai-core that calls it; the comment on each declaration names the reference
+ * interface (file:line, paths relative to the reference repository root).  Plain C types
+ * only: pointers, sizes, integers.  A Rust `hayai-hip` crate binds this header with an
+ * `extern "C"` block; INTEGRATION.md shows that binding.
+ *
+ * Conventions
+ *   - Every function returns hh_status (0 = HH_OK).  On failure a message is stored in a
+ *     thread-local buffer that hh_last_error() returns (valid until the next failing call
+ *     on the same thread).
+ *   - Weights are unmodified GGUF bytes in a device buffer, addressed by byte offset
+ *     (the reference's GgmlWeightBind::Device + weight_off, compute.rs:21-27,388-461).
+ *     GEMV shape: y[m] = W[m x n] . x[n], W row-major with GGUF blocks along n
+ *     (crates/hayai-model/src/quant.rs:28-29).
+ *   - Shapes are validated before any launch exactly as compute.rs:877-949 does
+ *     (m, n > 0; n a multiple of the format's block; weight bytes >= m * row_bytes).
+ *   - A format with no kernel is a hard HH_ERR_KERNEL_MISSING, never a CPU fallback
+ *     (orchestrator.rs:72-98,403-409).  There is no CPU compute path in this library.
+ *   - An engine is externally synchronised (one compute stream + one copy stream), like
+ *     the reference's orchestrator behind a Mutex (orchestrator.rs:65-68).
+ *   - Functions with host x/y pointers block until y is written (the reference's
+ *     blocking enqueue_read_buffer).  Functions suffixed _dev take device buffers for
+ *     activations too and only enqueue on the engine's compute stream.
+ */
+#ifndef HAYAI_HIP_H
+#define HAYAI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HH_ABI_VERSION 1
+
+/* Status codes.  OpenClError::{NoDeviceFound, ClError, UnsupportedPlatformVersion}
+ * (crates/hayai-opencl/src/context.rs:13-21) map to NO_DEVICE, RUNTIME and
+ * UNSUPPORTED_DEVICE; shape/size rejections (compute.rs:912-949) to INVALID. */
+typedef enum hh_status {
+    HH_OK = 0,
+    HH_ERR_NO_DEVICE = 1,
+    HH_ERR_INVALID = 2,
+    HH_ERR_KERNEL_MISSING = 3,
+    HH_ERR_RUNTIME = 4,
+    HH_ERR_OUT_OF_MEMORY = 5,
+    HH_ERR_UNSUPPORTED_DEVICE = 6
+} hh_status;
+
+/* GGML type ids (crates/hayai-model/src/gguf_types.rs:6-78) with a kernel here. */
+enum {
+    HH_TYPE_F32 = 0,
+    HH_TYPE_F16 = 1,
+    HH_TYPE_Q4_0 = 2,
+    HH_TYPE_Q4_K = 12,
+    HH_TYPE_IQ2_XXS = 16,
+    HH_TYPE_IQ3_XXS = 18
+};
+
+/* FFN activation: SiLU(gate)*up (stream_infer.rs:3836-3840) or tanh-GELU(gate)*up
+ * (ffn_finish_gelu_scratch, stream_infer.rs:3889-3895). */
+enum { HH_ACT_SILU = 0, HH_ACT_GELU_TANH = 1 };
+
+/* Buffer kinds: device HBM, or pinned host memory from hipHostMalloc (replaces the
+ * CL_MEM_ALLOC_HOST_PTR / SVM host slots of crates/hayai-opencl/src/memory.rs:72-147). */
+enum { HH_BUF_DEVICE = 0, HH_BUF_PINNED_HOST = 1 };
+
+typedef struct hh_engine hh_engine;   /* OpenClEngine, context.rs:23-69 */
+typedef struct hh_buf hh_buf;         /* cl_mem Buffer<u8> / PinnedHostBuffer */
+typedef struct hh_pending hh_pending; /* PendingGemv, async_gemv.rs:15-57 */
+typedef struct hh_event hh_event;     /* timing event on the compute stream */
+
+typedef struct hh_device_info {
+    char name[256];       /* marketing name */
+    char arch[64];        /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int device_index;
+    int compute_units;
+    int wavefront_size;
+    int clock_khz;
+    int memory_clock_khz;
+    int memory_bus_width;
+    size_t total_mem;
+    size_t lds_per_block;
+    size_t l2_bytes;
+} hh_device_info;
+
+/* ------------------------------------------------------------------ errors / info --- */
+
+int hh_abi_version(void);
+const char* hh_last_error(void);
+/* Name of a status code ("HH_ERR_INVALID", ...). */
+const char* hh_status_name(hh_status st);
+
+/* Packed bytes per row of n columns (compute.rs:877-907, gemv_row_bytes).
+ * HH_ERR_INVALID when n is not a block multiple; HH_ERR_KERNEL_MISSING for a type
+ * with no kernel here. */
+hh_status hh_row_bytes(int ggml_type, size_t n, size_t* out);
+
+/* Pre-launch validation, callable without a device (compute.rs:912-949):
+ * validate_gemv_shape and validate_gemv_weights. */
+hh_status hh_validate_gemv_shape(int ggml_type, size_t m, size_t n);
+hh_status hh_validate_gemv_weights(int ggml_type, size_t m, size_t n, size_t weights_len);
+
+/* ------------------------------------------------------------------ engine ---------- */
+
+/* Number of HIP devices (discover_opencl_devices, crates/hayai-opencl/src/device.rs:86-184). */
+hh_status hh_device_count(int* count);
+
+/* Bring up one device: select it, load the gfx950 code object (embedded in this library,
+ * or the file named by HAYAI_HIP_CODE_OBJECT) with hipModuleLoadData/hipModuleLoad,
+ * resolve every kernel, create the compute and copy streams.  Fails with
+ * HH_ERR_UNSUPPORTED_DEVICE on a non-gfx950 device and HH_ERR_KERNEL_MISSING if a kernel
+ * is absent from the code object.  Replaces OpenClEngine::init_device
+ * (crates/hayai-opencl/src/context.rs:106-232). */
+hh_status hh_engine_create(int device, hh_engine** out);
+void hh_engine_destroy(hh_engine* e);
+hh_status hh_engine_info(const hh_engine* e, hh_device_info* out);
+/* Wait for all work on both engine streams. */
+hh_status hh_engine_sync(hh_engine* e);
+/* Count of FFN GEMVs dispatched (the ffn_calls counter, context.rs:64-65). */
+uint64_t hh_engine_ffn_calls(const hh_engine* e);
+
+/* ------------------------------------------------------------------ buffers --------- */
+
+/* Allocate a device (HH_BUF_DEVICE) or pinned host (HH_BUF_PINNED_HOST) buffer.
+ * Buffer::create (compute.rs) / PinnedHostBuffer::new (memory.rs:72-147). */
+hh_status hh_buf_alloc(hh_engine* e, size_t bytes, int kind, hh_buf** out);
+void hh_buf_free(hh_buf* b);
+size_t hh_buf_size(const hh_buf* b);
+int hh_buf_kind(const hh_buf* b);
+/* Host address of a pinned buffer (NULL for device buffers). */
+void* hh_buf_host_ptr(hh_buf* b);
+/* Blocking host <-> buffer copies (enqueue_write_buffer / enqueue_read_buffer with
+ * CL_BLOCKING).  Ordered after all work already queued on the compute stream. */
+hh_status hh_buf_write(hh_engine* e, hh_buf* dst, size_t dst_off, const void* src, size_t bytes);
+hh_status hh_buf_read(hh_engine* e, const hh_buf* src, size_t src_off, void* dst, size_t bytes);
+/* Device fill with a byte value (enqueued on the compute stream). */
+hh_status hh_buf_fill(hh_engine* e, hh_buf* dst, size_t off, uint8_t value, size_t bytes);
+
+/* ------------------------------------------------------------------ GEMV ------------ */
+
+/* ggml_gemv_dispatch (crates/hayai-opencl/src/compute.rs:281-383): host weights are
+ * uploaded into a persistent engine workspace, then GEMV, then blocking readback. */
+hh_status hh_gemv(hh_engine* e, int ggml_type, size_t m, size_t n, const uint8_t* weights,
+                  size_t weights_len, const float* x, float* y);
+
+/* ggml_gemv_dispatch_bound (compute.rs:388-461): weights resident in a device buffer at
+ * byte offset w_off; x uploaded, y read back (blocking). */
+hh_status hh_gemv_bound(hh_engine* e, int ggml_type, size_t m, size_t n, const hh_buf* w,
+                        size_t w_off, const float* x, float* y);
+
+/* ggml_gemv_async_from_device (crates/hayai-opencl/src/async_gemv.rs:90-196): enqueue
+ * and return a pending handle that owns its activation buffers. */
+hh_status hh_gemv_begin(hh_engine* e, int ggml_type, size_t m, size_t n, const hh_buf* w,
+                        size_t w_off, const float* x, hh_pending** out);
+/* PendingGemv::wait (async_gemv.rs:27-46): block, copy the m outputs into y. */
+hh_status hh_pending_wait(hh_pending* p, float* y, size_t m);
+/* Drop for PendingGemv (async_gemv.rs:48-57): waits for the kernel, then frees. */
+void hh_pending_destroy(hh_pending* p);
+
+/* Device-resident GEMV: x and y are device buffers (byte offsets), enqueue only. */
+hh_status hh_gemv_dev(hh_engine* e, int ggml_type, size_t m, size_t n, const hh_buf* w,
+                      size_t w_off, const hh_buf* x, size_t x_off, hh_buf* y, size_t y_off);
+
+/* Dequant probe: n weights of a packed tensor at (w, w_off) -> f32 at (out, out_off),
+ * bit-identical to hayai-model's dequant (gguf.rs:348-372, q4k.rs:162-203,
+ * iq2.rs:504-523, iq3.rs:147-173; F16: gguf.rs:521-545).  Enqueue only. */
+hh_status hh_dequant_dev(hh_engine* e, int ggml_type, const hh_buf* w, size_t w_off, size_t n,
+                         hh_buf* out, size_t out_off);
+
+/* ------------------------------------------------------------------ FFN ------------- */
+
+/* One FFN op of a layer pack: gate/up/down descriptors with byte offsets into the pack
+ * (LayerPackLayout gate_off/up_off/down_off, crates/hayai-model/src/gguf_stream.rs:1416-1444;
+ * QuantMatrix nrows/ncols/ggml_type, quant.rs:31-54). */
+typedef struct hh_ffn_desc {
+    int type_gate;
+    int type_up;
+    int type_down;
+    int act; /* HH_ACT_* */
+    size_t d_model;
+    size_t d_ff;
+    size_t gate_off;
+    size_t up_off;
+    size_t down_off;
+} hh_ffn_desc;
+
+/* ffn_begin_gate_up_scratch + ffn_finish_scratch (crates/hayai-core/src/stream_infer.rs:
+ * 3752-3864) as one call: y = W_down . (act(W_gate . x) * (W_up . x)).  Gate/up and the
+ * activation run as one fused kernel when gate and up share a format, then down.
+ * Host x / y, blocking. */
+hh_status hh_ffn(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                 const float* x, float* y);
+/* Same with device activations (x: d_model floats, y: d_model floats); enqueue only.
+ * The d_ff intermediate lives in an engine workspace. */
+hh_status hh_ffn_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                     const hh_buf* x, size_t x_off, hh_buf* y, size_t y_off);
+
+/* The first half of the FFN op: ffn_begin_gate_up_scratch (stream_infer.rs:3752-3806)
+ * fused with the activation of ffn_finish_scratch (:3836-3840):
+ * h[d_ff] = act(W_gate . x) * (W_up . x), one kernel when gate and up share a format.
+ * Enqueue only; x holds d_model floats, h receives d_ff floats. */
+hh_status hh_gateup_dev(hh_engine* e, int type_gate, int type_up, size_t d_ff, size_t d_model, const hh_buf* wg,
+                        size_t wg_off, const hh_buf* wu, size_t wu_off, const hh_buf* x, size_t x_off, hh_buf* h,
+                        size_t h_off, int act);
+
+/* ------------------------------------------------------------------ timing ---------- */
+
+hh_status hh_event_create(hh_engine* e, hh_event** out);
+void hh_event_destroy(hh_event* ev);
+/* Record on the engine's compute stream (the stream every kernel here runs on). */
+hh_status hh_event_record(hh_engine* e, hh_event* ev);
+hh_status hh_event_elapsed_ms(hh_event* start, hh_event* stop, float* ms);
+
+/* ------------------------------------------------------------------ synthetic data -- */
+
+/* Fill n_blocks GGUF blocks of ggml_type at (dst, off) with the seeded synthetic stream
+ * (splitmix64 bytes, then every f16 scale field drawn U(lo, hi) and rounded to nearest
+ * even).  Enqueue only.  The byte recipe is specified in hayai_amd/synth.py, which
+ * generates the same bytes on the host.  Benchmark harness input, the analogue of the
+ * reference's bench_* helpers (async_gemv.rs:309-428). */
+hh_status hh_synth_weights_dev(hh_engine* e, int ggml_type, hh_buf* dst, size_t off, size_t n_blocks,
+                               uint64_t seed, float lo, float hi);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HAYAI_HIP_H */

@@ -1,0 +1,103 @@
+"""GPU FFN op parity: hh_ffn / hh_ffn_dev (the fused replacement of
+ffn_begin_gate_up_scratch + ffn_finish_scratch, stream_infer.rs:3752-3864) against the
+oracle's gate GEMV, up GEMV, SiLU*up, down GEMV in fp32."""
+import numpy as np
+import pytest
+
+import hayai_amd
+import oracle
+from hayai_amd import synth
+
+pytestmark = pytest.mark.gpu
+REL_TOL = 1e-3
+
+
+def rel_err(y, ref):
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(y - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def make_pack(engine, types, d_model, d_ff, config_id, layer=0):
+    tg, tu, td = types
+    gate = hayai_amd.QuantMatrix("ffn_gate", d_model, d_ff, tg)
+    up = hayai_amd.QuantMatrix("ffn_up", d_model, d_ff, tu)
+    down = hayai_amd.QuantMatrix("ffn_down", d_ff, d_model, td)
+    lay = hayai_amd.LayerPackLayout.ffn_only(gate, up, down)
+    wg = synth.matrix(tg, d_ff, d_model, synth.seed_for(config_id, layer, synth.GATE))
+    wu = synth.matrix(tu, d_ff, d_model, synth.seed_for(config_id, layer, synth.UP))
+    wd = synth.matrix(td, d_model, d_ff, synth.seed_for(config_id, layer, synth.DOWN))
+    pack = engine.alloc(lay.total)
+    pack.write(wg, lay.gate_off)
+    pack.write(wu, lay.up_off)
+    pack.write(wd, lay.down_off)
+    return lay, (wg, wu, wd), pack
+
+
+FFN_CASES = [
+    # (types, d_model, d_ff, act, config id): config 1 SmolLM Q4_0, config 2 8B Q4_K,
+    # config 4 expert shape, config 5-like IQ2_XXS (reduced d_ff), IQ3_XXS, mixed formats
+    ((2, 2, 2), 576, 1536, 0, 1),
+    ((12, 12, 12), 4096, 14336, 0, 2),
+    ((12, 12, 12), 2048, 768, 0, 4),
+    ((16, 16, 16), 8192, 3584, 0, 5),
+    ((18, 18, 18), 4096, 14336, 0, 6),
+    ((12, 12, 12), 4096, 14336, 1, 7),   # GELU(tanh) activation
+    ((12, 2, 18), 1024, 2048, 0, 8),     # gate/up formats differ -> unfused gate/up path
+]
+
+
+@pytest.mark.parametrize("types,d_model,d_ff,act,cfg", FFN_CASES)
+def test_ffn_matches_oracle(engine, types, d_model, d_ff, act, cfg):
+    oracle.set_threads(min(16, oracle.max_threads()))
+    print(f"[case] ffn types={types} d_model={d_model} d_ff={d_ff} act={act}", flush=True)
+    lay, (wg, wu, wd), pack = make_pack(engine, types, d_model, d_ff, cfg)
+    x = synth.normal(synth.seed_for(cfg, 0, synth.ACT), d_model)
+    desc = engine.ffn_desc(types, d_model, d_ff, lay, act)
+    y = engine.ffn(desc, pack, 0, x)
+    ref, h_ref = oracle.ffn(types, d_model, d_ff, wg, wu, wd, x, act=act, return_h=True)
+    assert np.isfinite(y).all()
+    assert rel_err(y, ref) <= REL_TOL, rel_err(y, ref)
+    # per-element check where the output is not near zero
+    big = np.abs(ref) > 1e-3 * np.abs(ref).max()
+    per = np.abs(y[big] - ref[big]) / np.abs(ref[big])
+    print(f"  rel_inf={rel_err(y, ref):.3e} per_elem_max={per.max():.3e}", flush=True)
+
+
+def test_ffn_dev_chain_and_pack_offset(engine):
+    # two layers resident in one buffer at layer * stride (resident scratch addressing,
+    # hetero_scratch.rs:915-925); chain y0 -> x1 on the device
+    types, d_model, d_ff = (2, 2, 2), 576, 1536
+    lay0, w0, pack0 = make_pack(engine, types, d_model, d_ff, 11, layer=0)
+    lay1, w1, pack1 = make_pack(engine, types, d_model, d_ff, 11, layer=1)
+    stride = lay0.total
+    big = engine.alloc(2 * stride)
+    for i, (wg, wu, wd) in enumerate((w0, w1)):
+        big.write(wg, i * stride + lay0.gate_off)
+        big.write(wu, i * stride + lay0.up_off)
+        big.write(wd, i * stride + lay0.down_off)
+    desc = engine.ffn_desc(types, d_model, d_ff, lay0)
+    x = synth.normal(5, d_model)
+    xb = engine.upload(x)
+    ya = engine.alloc(4 * d_model)
+    yb = engine.alloc(4 * d_model)
+    engine.ffn_dev(desc, big, 0, xb, 0, ya, 0)
+    engine.ffn_dev(desc, big, stride, ya, 0, yb, 0)
+    y = yb.read(np.float32, d_model)
+    r0 = oracle.ffn(types, d_model, d_ff, *w0, x)
+    r1 = oracle.ffn(types, d_model, d_ff, *w1, r0)
+    assert rel_err(y, r1) <= REL_TOL
+
+
+def test_ffn_rejects_bad_pack(engine):
+    types, d_model, d_ff = (12, 12, 12), 256, 512
+    lay, _, pack = make_pack(engine, types, d_model, d_ff, 12)
+    desc = engine.ffn_desc(types, d_model, d_ff, lay)
+    with pytest.raises(hayai_amd.HipError):
+        engine.ffn(desc, pack, 512, synth.normal(1, d_model))  # pushes down past the end
+    bad = engine.ffn_desc(types, d_model, 500, lay)
+    with pytest.raises(hayai_amd.HipError):
+        engine.ffn(bad, pack, 0, synth.normal(1, d_model))
+    before = engine.ffn_calls
+    engine.ffn(desc, pack, 0, synth.normal(1, d_model))
+    assert engine.ffn_calls == before + 3
