@@ -1,4 +1,5 @@
 // Single translation unit for the gfx950 code object (hayai_kernels.hsaco).
 #include "gemv.hip"
+#include "q4k.hip"
 #include "dequant.hip"
 #include "synth.hip"

@@ -147,6 +147,56 @@ hh_status hh_engine::grow(void** p, size_t* cap, size_t need) {
     return HH_OK;
 }
 
+// Kernel argument block of q4k.hip (same layout).
+struct hh_q4k_args {
+    const uint8_t* w0;
+    const uint8_t* w1;
+    const float* x;
+    float* y;
+    uint32_t m;
+    uint32_t n;
+    uint64_t row_bytes;
+    int32_t act;
+    int32_t pad;
+};
+
+hh_status hh_engine::enqueue_q4k(size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const float* x, float* y,
+                                 int act, bool gateup) {
+    const size_t units = n / 64;
+    const size_t rb = (n / 256) * 144;
+    if (q4k_generic || units == 0 || units > 512 || ((uintptr_t)x & 15u) || ((uintptr_t)w0 & 15u) ||
+        (gateup && ((uintptr_t)w1 & 15u)))
+        return HH_ERR_UNSUPPORTED_DEVICE;
+    int wpt = 1;
+    while ((size_t)wpt * 64 < units) wpt *= 2;
+    const int waves = 8, tpw = waves / wpt;
+    const int rows_per_team_step = gateup ? 1 : 2;
+    const std::string name = std::string(gateup ? "hh_q4k_gateup_w" : "hh_q4k_gemv_w") + std::to_string(wpt);
+    hipFunction_t fn;
+    HH_TRY(kernel(name, &fn));
+    const size_t smem = 2 * n + (n / 32) * 8 + (size_t)waves * 4 * sizeof(float);
+    int occ = blocks_per_cu_override;
+    if (occ <= 0) {
+        auto it = blocks_per_cu.find(name);
+        if (it != blocks_per_cu.end()) {
+            occ = it->second;
+        } else {
+            if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, waves * 64, smem) != hipSuccess || occ < 1)
+                occ = 1;
+            blocks_per_cu[name] = occ;
+        }
+    }
+    const size_t rows_per_wg_step = (size_t)tpw * rows_per_team_step;
+    const size_t need = (m + rows_per_wg_step - 1) / rows_per_wg_step;
+    const size_t grid = std::max<size_t>(1, std::min(need, (size_t)props.multiProcessorCount * occ));
+    hh_q4k_args a{w0, w1, x, y, (uint32_t)m, (uint32_t)n, (uint64_t)rb, act, 0};
+    void* params[] = {&a};
+    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, waves * 64, 1, 1, (unsigned)smem, stream, params,
+                                           nullptr);
+    if (err != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel(q4k)");
+    return HH_OK;
+}
+
 hh_status hh_engine::enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w, const float* x, float* y) {
     const Format* f = format_of(type);
     if (!f) return fail(HH_ERR_KERNEL_MISSING, "no GEMV kernel for GGML type %d", type);
@@ -161,6 +211,10 @@ hh_status hh_engine::enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w
     if (type != HH_TYPE_Q4_K && type != HH_TYPE_F32 && ((uintptr_t)w & 1u))
         return fail(HH_ERR_INVALID, "ggml_gemv_%s: weight address must be 2-byte aligned", f->name);
     const bool aligned16 = (((uintptr_t)w & 15u) == 0) && (rb % 16 == 0);
+    if (type == HH_TYPE_Q4_K && aligned16) {
+        hh_status st = enqueue_q4k(m, n, w, nullptr, x, y, 0, false);
+        if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
+    }
     std::string name;
     int team = 0, upl = 1;
     if ((type == HH_TYPE_F32 || type == HH_TYPE_F16) && (n % 32 != 0 || !aligned16)) {
@@ -196,6 +250,10 @@ hh_status hh_engine::enqueue_gateup(int tg, int tu, size_t d_ff, size_t d_model,
     if (!f || !format_of(tu)) return fail(HH_ERR_KERNEL_MISSING, "no GEMV kernel for GGML type %d/%d", tg, tu);
     size_t rb;
     HH_TRY(row_bytes(tg, d_model, &rb));
+    if (tg == HH_TYPE_Q4_K && tu == HH_TYPE_Q4_K) {
+        hh_status st = enqueue_q4k(d_ff, d_model, wg, wu, x, h, act, true);
+        if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
+    }
     if (tg == tu && f->fused_gateup) {
         if (tg != HH_TYPE_Q4_K && (((uintptr_t)wg | (uintptr_t)wu) & 1u))
             return fail(HH_ERR_INVALID, "ffn gate/up %s: weight address must be 2-byte aligned", f->name);
@@ -249,7 +307,9 @@ static std::vector<std::string> required_kernels() {
     }
     for (const char* s : {"hh_gemv_f32_plain", "hh_gemv_f16_plain", "hh_act_mul_kernel", "hh_dequant_q4_0",
                           "hh_dequant_q4_k", "hh_dequant_iq2_xxs", "hh_dequant_iq3_xxs", "hh_dequant_f16",
-                          "hh_synth_bytes", "hh_synth_scales"})
+                          "hh_synth_bytes", "hh_synth_scales", "hh_q4k_gemv_w1", "hh_q4k_gemv_w2", "hh_q4k_gemv_w4",
+                          "hh_q4k_gemv_w8", "hh_q4k_gateup_w1", "hh_q4k_gateup_w2", "hh_q4k_gateup_w4",
+                          "hh_q4k_gateup_w8"})
         k.push_back(s);
     return k;
 }
@@ -290,6 +350,7 @@ hh_status engine_create(int device, hh_engine** out) {
         if (hh_status st = e->kernel(k, &f); st != HH_OK) return bail(st);
     }
     if (const char* b = getenv("HAYAI_HIP_BLOCKS_PER_CU")) e->blocks_per_cu_override = atoi(b);
+    if (const char* g = getenv("HAYAI_HIP_Q4K_GENERIC")) e->q4k_generic = atoi(g) != 0;
     *out = e;
     return HH_OK;
 }

@@ -100,6 +100,7 @@ struct hh_engine {
     void* ws_w = nullptr;
     size_t ws_w_cap = 0;
     int blocks_per_cu_override = 0;  // HAYAI_HIP_BLOCKS_PER_CU
+    bool q4k_generic = false;        // HAYAI_HIP_Q4K_GENERIC=1: skip the int8-digit Q4_K kernels
 
     hh_status select();  // hipSetDevice(device)
     hh_status kernel(const std::string& name, hipFunction_t* out);
@@ -119,6 +120,10 @@ struct hh_engine {
     hh_status enqueue_gateup(int type_g, int type_u, size_t d_ff, size_t d_model, const uint8_t* wg,
                              const uint8_t* wu, const float* x, float* h, int act);
     hh_status enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y);
+    // Q4_K batch-1 kernels (q4k.hip); returns HH_ERR_UNSUPPORTED_DEVICE when the shape or
+    // alignment needs the generic kernels instead (the caller then falls back).
+    hh_status enqueue_q4k(size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const float* x, float* y,
+                          int act, bool gateup);
 };
 
 #endif

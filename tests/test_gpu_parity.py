@@ -248,7 +248,9 @@ def test_gemv_config_shapes(engine, t, m, n):
 
 
 def test_gemv_full_size_properties(engine):
-    # 8B down projection at full size, resident: determinism and linearity in x
+    # 8B down projection at full size, resident: determinism and linearity in x.  The
+    # batch-1 Q4_K kernels carry x as two int8 digits per element (error <= amax/65024 per
+    # 32-element sub-block), so GPU-vs-GPU linearity holds to ~1e-4, not to fp32 rounding.
     t, m, n = hayai_amd.Q4_K, 4096, 14336
     rb = hayai_amd.row_bytes(t, n)
     wb = engine.alloc(m * rb)
@@ -261,4 +263,4 @@ def test_gemv_full_size_properties(engine):
     assert np.array_equal(y1, y1b)
     y2 = engine.ggml_gemv_dispatch_bound(t, m, n, wb, 0, x2)
     y12 = engine.ggml_gemv_dispatch_bound(t, m, n, wb, 0, (a * x1 + b * x2).astype(np.float32))
-    assert rel_err(y12, a * y1.astype(np.float64) + b * y2.astype(np.float64)) <= 1e-5
+    assert rel_err(y12, a * y1.astype(np.float64) + b * y2.astype(np.float64)) <= 2e-4
