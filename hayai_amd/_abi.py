@@ -81,6 +81,7 @@ SIGNATURES = {
     "hh_buf_host_ptr": (P, [P]),
     "hh_buf_write": (ST, [P, P, SZ, P, SZ]),
     "hh_buf_read": (ST, [P, P, SZ, P, SZ]),
+    "hh_buf_copy": (ST, [P, P, SZ, P, SZ, SZ]),
     "hh_buf_fill": (ST, [P, P, SZ, C.c_uint8, SZ]),
     "hh_gemv": (ST, [P, I, SZ, SZ, P, SZ, P, P]),
     "hh_gemv_bound": (ST, [P, I, SZ, SZ, P, SZ, P, P]),

@@ -5,36 +5,50 @@
 //     time; lane l owns "unit" l of the row: Q4_K group g = l & 3 of superblock l >> 2, i.e.
 //     qs[32g, 32g+32) (low nibbles = sub-block 2g, high nibbles = sub-block 2g+1) plus the
 //     16-byte block header (d, dmin, scales[12]); crates/hayai-model/src/q4k.rs:178-203.
-//   - x never leaves the chip after the prologue: the workgroup turns x into two int8 digits
-//     per element, x ~= s * (q1 + q2/256) with s = amax/127 per 32-element sub-block (error
-//     <= s/512), stored in LDS with the per-sub-block scale and exact f32 sum.  Each lane then
-//     holds its unit's 64 x 2 digits in 32 VGPRs.
+//   - x enters as two int8 digits per element, x ~= s * (q1 + q2/256) with s = amax/127 per
+//     32-element sub-block (error <= s/512), plus the per-sub-block scale and exact f32 sum.
+//     Either the workgroup builds them from f32 x in LDS (4 lanes per sub-block), or they
+//     come pre-built from global memory: the fused gate/up kernel writes the digits of h for
+//     the down projection.  Each lane holds its unit's 64 x 2 digits in 32 VGPRs.
 //   - Per weight dword (8 nibbles): one AND (low nibbles), shift+AND (high nibbles) and four
 //     v_dot4_i32_i8 (nibbles x digit 1, nibbles x digit 2, for both sub-blocks) -- integer
 //     sums, exact.  Per (row, group): the sub-block sums are scaled once in f32:
 //       d*sc*s*(sum1 + sum2/256) - dmin*m*sum(x)     (factored form of (d*sc)*q - dmin*m)
 //   - Loads are double-buffered in registers: row step k+1's 16-byte loads are in flight
-//     while step k is computed.  Consecutive lanes read consecutive 32-byte qs chunks, so
-//     each wave reads whole rows front to back.
+//     while step k is computed, and step 0 is issued before the x prologue.  Consecutive
+//     lanes read consecutive 32-byte qs chunks, so a wave reads its rows front to back.
+//     Row base addresses are wave-uniform (scalar registers).
 //   - Team sums: DPP butterfly/broadcast within the wave (v_add_f32_dpp, row_bcast15/31),
 //     then an LDS step across the team's waves when WPT > 1.
-//   - Each workgroup owns a contiguous row range; row steps are uniform across the
-//     workgroup (barriers in the multi-wave reduction stay convergent).
+//   - Each workgroup owns a contiguous row range (32-row aligned for gate/up, so it can
+//     quantize its own slice of h); row steps are uniform across the workgroup, so the
+//     barriers of the multi-wave reduction stay convergent.
 #include "quant.h"
 
 #define HH_Q4K_WAVES 8
 #define HH_Q4K_BLOCK (HH_Q4K_WAVES * HH_WAVE)
 
+// Pre-quantized activation digits in global memory (layout of the h workspace):
+// q1[n] int8 | q2[n] int8 | scale[n/32] f32 | sum[n/32] f32
+struct hh_digits_ptr {
+    int8_t* q1;
+    int8_t* q2;
+    float* sc;
+    float* sum;
+};
+
 struct hh_q4k_args {
     const uint8_t* w0;  // the matrix (GEMV) or W_gate (gate/up)
     const uint8_t* w1;  // W_up (gate/up only)
-    const float* x;     // n floats, 16-byte aligned
+    const float* x;     // n floats, 16-byte aligned (f32 input mode)
     float* y;           // m floats (y, or h for gate/up)
+    hh_digits_ptr xq;   // digits of x (digit input mode)
+    hh_digits_ptr hq;   // gate/up: where to write the digits of h (q1 == NULL: skip)
     uint32_t m;
     uint32_t n;
     uint64_t row_bytes;
     int32_t act;
-    int32_t pad;
+    uint32_t hrows;  // gate/up: LDS rows reserved for h (max rows of one workgroup)
 };
 
 template <int CTRL, int ROW_MASK = 0xF>
@@ -54,67 +68,60 @@ HH_DEV float hh_wave_sum(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
-// LDS layout (dynamic): q1[n] int8 | q2[n] int8 | scale[n/32] f32 | sum[n/32] f32 | red[]
-struct hh_xdig {
-    const int8_t* q1;
-    const int8_t* q2;
-    const float* sc;
-    const float* sum;
-    float* red;
-};
+// Quad (4 consecutive lanes) reductions.
+HH_DEV float hh_quad_sum(float v) {
+    v += hh_dpp<0xB1>(v);
+    v += hh_dpp<0x4E>(v);
+    return v;
+}
+HH_DEV float hh_quad_max(float v) {
+    v = fmaxf(v, hh_dpp<0xB1>(v));
+    v = fmaxf(v, hh_dpp<0x4E>(v));
+    return v;
+}
 
-// Prologue: x -> digits in LDS, one 32-element sub-block per thread.
-HH_DEV hh_xdig hh_q4k_stage_x(const float* __restrict__ x, uint32_t n, char* smem) {
-    int8_t* q1 = reinterpret_cast<int8_t*>(smem);
-    int8_t* q2 = q1 + n;
-    float* sc = reinterpret_cast<float*>(q2 + n);
-    float* sm = sc + n / 32;
-    for (uint32_t sb = threadIdx.x; sb < n / 32; sb += HH_Q4K_BLOCK) {
-        const float4* p = reinterpret_cast<const float4*>(x + (size_t)sb * 32);
-        float v[32];
+// Digits of 8 consecutive elements of one sub-block (scale s = amax/127, inv = 127/amax).
+HH_DEV void hh_digits8(const float (&v)[8], float scale, float inv, uint2& o1, uint2& o2) {
+    uint32_t p1[2] = {0, 0}, p2[2] = {0, 0};
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 t = p[i];
-            v[4 * i] = t.x;
-            v[4 * i + 1] = t.y;
-            v[4 * i + 2] = t.z;
-            v[4 * i + 3] = t.w;
-        }
+    for (int i = 0; i < 8; i++) {
+        const float a = fminf(fmaxf(rintf(v[i] * inv), -127.f), 127.f);
+        const float r = v[i] - a * scale;
+        const float b = fminf(fmaxf(rintf(r * inv * 256.0f), -127.f), 127.f);
+        p1[i / 4] |= ((uint32_t)(int)a & 0xFFu) << (8 * (i % 4));
+        p2[i / 4] |= ((uint32_t)(int)b & 0xFFu) << (8 * (i % 4));
+    }
+    o1 = make_uint2(p1[0], p1[1]);
+    o2 = make_uint2(p2[0], p2[1]);
+}
+
+// Quantize n f32 values (n % 32 == 0) into digits: 4 lanes per 32-element sub-block,
+// chunk c = 8 elements.  All threads of the workgroup must call it (quads stay whole
+// because the stride is a multiple of 4 and n/8 is a multiple of 4).
+HH_DEV void hh_quantize_digits(const float* src, uint32_t n, const hh_digits_ptr& dst) {
+    for (uint32_t c = threadIdx.x; c < n / 8; c += blockDim.x) {
+        const float4 t0 = reinterpret_cast<const float4*>(src)[2 * c];
+        const float4 t1 = reinterpret_cast<const float4*>(src)[2 * c + 1];
+        const float v[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
         float amax = 0.f, s = 0.f;
 #pragma unroll
-        for (int i = 0; i < 32; i++) {
+        for (int i = 0; i < 8; i++) {
             amax = fmaxf(amax, fabsf(v[i]));
             s += v[i];
         }
+        amax = hh_quad_max(amax);
+        s = hh_quad_sum(s);
         const float scale = amax * (1.0f / 127.0f);
         const float inv = amax > 0.f ? 127.0f / amax : 0.f;
-        uint32_t d1[8], d2[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            uint32_t p1 = 0, p2 = 0;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const float xv = v[4 * i + k];
-                const float a = fminf(fmaxf(rintf(xv * inv), -127.f), 127.f);
-                const float r = xv - a * scale;
-                const float b = fminf(fmaxf(rintf(r * inv * 256.0f), -127.f), 127.f);
-                p1 |= ((uint32_t)(int)a & 0xFFu) << (8 * k);
-                p2 |= ((uint32_t)(int)b & 0xFFu) << (8 * k);
-            }
-            d1[i] = p1;
-            d2[i] = p2;
+        uint2 o1, o2;
+        hh_digits8(v, scale, inv, o1, o2);
+        reinterpret_cast<uint2*>(dst.q1)[c] = o1;
+        reinterpret_cast<uint2*>(dst.q2)[c] = o2;
+        if ((c & 3u) == 0) {
+            dst.sc[c / 4] = scale;
+            dst.sum[c / 4] = s;
         }
-        uint4* o1 = reinterpret_cast<uint4*>(q1 + (size_t)sb * 32);
-        uint4* o2 = reinterpret_cast<uint4*>(q2 + (size_t)sb * 32);
-        o1[0] = make_uint4(d1[0], d1[1], d1[2], d1[3]);
-        o1[1] = make_uint4(d1[4], d1[5], d1[6], d1[7]);
-        o2[0] = make_uint4(d2[0], d2[1], d2[2], d2[3]);
-        o2[1] = make_uint4(d2[4], d2[5], d2[6], d2[7]);
-        sc[sb] = scale;
-        sm[sb] = s;
     }
-    hh_xdig xd{q1, q2, sc, sm, sm + n / 32};
-    return xd;
 }
 
 // A lane's x digits for its unit u (64 columns): lo = sub-block 2u, hi = 2u+1.
@@ -126,22 +133,31 @@ struct hh_q4k_x {
     bool hi_form;            // groups 2,3 use the 6-bit split encoding
 };
 
-HH_DEV void hh_q4k_load_lane_x(const hh_xdig& xd, uint32_t u, hh_q4k_x& xr) {
+HH_DEV void hh_unpack4(const uint4& t, uint32_t* d) {
+    d[0] = t.x;
+    d[1] = t.y;
+    d[2] = t.z;
+    d[3] = t.w;
+}
+
+// Works for digits in LDS or in global memory (generic address space).
+HH_DEV void hh_q4k_load_lane_x(const hh_digits_ptr& xd, uint32_t u, hh_q4k_x& xr) {
     const uint4* a = reinterpret_cast<const uint4*>(xd.q1 + (size_t)u * 64);
     const uint4* b = reinterpret_cast<const uint4*>(xd.q2 + (size_t)u * 64);
-    uint4 t;
-    t = a[0]; xr.q1lo[0] = t.x; xr.q1lo[1] = t.y; xr.q1lo[2] = t.z; xr.q1lo[3] = t.w;
-    t = a[1]; xr.q1lo[4] = t.x; xr.q1lo[5] = t.y; xr.q1lo[6] = t.z; xr.q1lo[7] = t.w;
-    t = a[2]; xr.q1hi[0] = t.x; xr.q1hi[1] = t.y; xr.q1hi[2] = t.z; xr.q1hi[3] = t.w;
-    t = a[3]; xr.q1hi[4] = t.x; xr.q1hi[5] = t.y; xr.q1hi[6] = t.z; xr.q1hi[7] = t.w;
-    t = b[0]; xr.q2lo[0] = t.x; xr.q2lo[1] = t.y; xr.q2lo[2] = t.z; xr.q2lo[3] = t.w;
-    t = b[1]; xr.q2lo[4] = t.x; xr.q2lo[5] = t.y; xr.q2lo[6] = t.z; xr.q2lo[7] = t.w;
-    t = b[2]; xr.q2hi[0] = t.x; xr.q2hi[1] = t.y; xr.q2hi[2] = t.z; xr.q2hi[3] = t.w;
-    t = b[3]; xr.q2hi[4] = t.x; xr.q2hi[5] = t.y; xr.q2hi[6] = t.z; xr.q2hi[7] = t.w;
-    xr.slo = xd.sc[2 * u] * (1.0f / 256.0f);
-    xr.shi = xd.sc[2 * u + 1] * (1.0f / 256.0f);
-    xr.xlo = xd.sum[2 * u];
-    xr.xhi = xd.sum[2 * u + 1];
+    hh_unpack4(a[0], xr.q1lo);
+    hh_unpack4(a[1], xr.q1lo + 4);
+    hh_unpack4(a[2], xr.q1hi);
+    hh_unpack4(a[3], xr.q1hi + 4);
+    hh_unpack4(b[0], xr.q2lo);
+    hh_unpack4(b[1], xr.q2lo + 4);
+    hh_unpack4(b[2], xr.q2hi);
+    hh_unpack4(b[3], xr.q2hi + 4);
+    const float2 sc = reinterpret_cast<const float2*>(xd.sc)[u];
+    const float2 sm = reinterpret_cast<const float2*>(xd.sum)[u];
+    xr.slo = sc.x * (1.0f / 256.0f);
+    xr.shi = sc.y * (1.0f / 256.0f);
+    xr.xlo = sm.x;
+    xr.xhi = sm.y;
     const uint32_t g = u & 3u;
     const uint32_t kk = 2u * (g & 1u);  // byte pair of each scale word this group uses
     // perm(src0 = z-word, src1 = y-word): bytes [y_kk, y_kk+1, z_kk, z_kk+1]
@@ -166,7 +182,6 @@ struct hh_q4k_data {
     uint4 h, q0, q1;
 };
 
-template <bool ACTIVE>
 HH_DEV void hh_q4k_load(const uint8_t* row, uint32_t u, hh_q4k_data& d) {
     const uint8_t* blk = row + (size_t)(u >> 2) * 144;
     const uint8_t* q = blk + 16 + (u & 3u) * 32;
@@ -199,39 +214,63 @@ HH_DEV float hh_q4k_unit(const hh_q4k_data& d, const hh_q4k_x& xr) {
     return dd * q - dm * mn;
 }
 
-// Row loop of one team.  NV = values per row (1 = GEMV, 2 = gate/up), R rows per step.
-template <int WPT, int R, bool GATEUP>
+// One kernel body for all variants.
+//   WPT     waves per team (row width up to 64*WPT units)
+//   R       rows per team step
+//   GATEUP  two matrices, output act(gate)*up (and optionally the digits of that output)
+//   XDIG    x arrives as pre-built digits (a.xq) instead of f32 (a.x)
+template <int WPT, int R, bool GATEUP, bool XDIG>
 HH_DEV void hh_q4k_body(const hh_q4k_args& a) {
     extern __shared__ __attribute__((aligned(16))) char hh_smem[];
     constexpr int TEAM = WPT * HH_WAVE;
     constexpr int TPW = HH_Q4K_WAVES / WPT;  // teams per workgroup
     constexpr int NV = GATEUP ? 2 : 1;
-    const hh_xdig xd = hh_q4k_stage_x(a.x, a.n, hh_smem);
-    __syncthreads();
-
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % TEAM;
-    const uint32_t team = tid / TEAM;
-    const uint32_t wave = tid / HH_WAVE;
+    const uint32_t team = __builtin_amdgcn_readfirstlane(tid / TEAM);  // wave-uniform
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / HH_WAVE);
     const uint32_t P = a.n / 64;
     const bool act = lane < P;
-    hh_q4k_x xr;
-    if (act) hh_q4k_load_lane_x(xd, lane, xr);
 
-    // contiguous row range of this workgroup
-    const uint32_t r0 = (uint32_t)(((uint64_t)blockIdx.x * a.m) / gridDim.x);
-    const uint32_t r1 = (uint32_t)(((uint64_t)(blockIdx.x + 1) * a.m) / gridDim.x);
+    // Contiguous row range of this workgroup.  When gate/up also emits the digits of h it
+    // splits 32-row sub-blocks, so each workgroup owns whole sub-blocks of h.
+    uint32_t r0, r1;
+    if (GATEUP && a.hq.q1 != nullptr) {
+        const uint32_t S = (a.m + 31) / 32;
+        r0 = 32u * (uint32_t)(((uint64_t)blockIdx.x * S) / gridDim.x);
+        r1 = min(a.m, 32u * (uint32_t)(((uint64_t)(blockIdx.x + 1) * S) / gridDim.x));
+    } else {
+        r0 = (uint32_t)(((uint64_t)blockIdx.x * a.m) / gridDim.x);
+        r1 = (uint32_t)(((uint64_t)(blockIdx.x + 1) * a.m) / gridDim.x);
+    }
     constexpr uint32_t ROWS_PER_STEP = TPW * R;
     const uint32_t nsteps = (r1 - r0 + ROWS_PER_STEP - 1) / ROWS_PER_STEP;
 
+    // LDS: [x digits (f32 input mode)] [h rows (gate/up)] [team reduction slots]
+    char* lds = hh_smem;
+    hh_digits_ptr xd = a.xq;
+    if constexpr (!XDIG) {
+        xd.q1 = reinterpret_cast<int8_t*>(lds);
+        xd.q2 = xd.q1 + a.n;
+        xd.sc = reinterpret_cast<float*>(xd.q2 + a.n);
+        xd.sum = xd.sc + a.n / 32;
+        lds = reinterpret_cast<char*>(xd.sum + a.n / 32);
+    }
+    float* hl = reinterpret_cast<float*>(lds);  // gate/up: h of rows [r0, r1)
+    float* red = hl + (GATEUP ? a.hrows : 0);
+
+    hh_q4k_x xr;
     auto row_of = [&](uint32_t k, int r) -> uint32_t { return r0 + k * ROWS_PER_STEP + team * R + r; };
     auto load_step = [&](uint32_t k, hh_q4k_data (&buf)[NV][R]) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const uint32_t row = row_of(k, r);
-            if (act && row < r1) {
-                hh_q4k_load<true>(a.w0 + (size_t)row * a.row_bytes, lane, buf[0][r]);
-                if constexpr (GATEUP) hh_q4k_load<true>(a.w1 + (size_t)row * a.row_bytes, lane, buf[NV - 1][r]);
+            if (row < r1) {
+                const size_t off = (size_t)row * a.row_bytes;  // scalar
+                if (act) {
+                    hh_q4k_load(a.w0 + off, lane, buf[0][r]);
+                    if constexpr (GATEUP) hh_q4k_load(a.w1 + off, lane, buf[NV - 1][r]);
+                }
             }
         }
     };
@@ -246,7 +285,6 @@ HH_DEV void hh_q4k_body(const hh_q4k_args& a) {
 #pragma unroll
         for (int i = 0; i < NV * R; i++) v[i] = hh_wave_sum(v[i]);
         if constexpr (WPT > 1) {
-            float* red = xd.red;
             if ((tid % HH_WAVE) == 0) {
 #pragma unroll
                 for (int i = 0; i < NV * R; i++) red[wave * (NV * R) + i] = v[i];
@@ -270,12 +308,24 @@ HH_DEV void hh_q4k_body(const hh_q4k_args& a) {
                     val2 = v[(NV - 1) * R + r];
                 }
             const uint32_t row = row_of(k, (int)lane);
-            if (row < r1) a.y[row] = GATEUP ? hh_act_mul(val, val2, a.act) : val;
+            if (row < r1) {
+                const float out = GATEUP ? hh_act_mul(val, val2, a.act) : val;
+                a.y[row] = out;
+                if constexpr (GATEUP) hl[row - r0] = out;
+            }
         }
     };
 
+    // The first row step's weights do not depend on x: put them in flight before the
+    // x prologue so HBM latency overlaps the digit conversion.
     hh_q4k_data A[NV][R], B[NV][R];
     if (nsteps > 0) load_step(0, A);
+    if constexpr (!XDIG) {
+        hh_quantize_digits(a.x, a.n, xd);
+        __syncthreads();
+    }
+    if (act) hh_q4k_load_lane_x(xd, lane, xr);
+
     for (uint32_t k = 0; k < nsteps; k += 2) {
         if (k + 1 < nsteps) load_step(k + 1, B);
         compute_step(k, A);
@@ -283,18 +333,30 @@ HH_DEV void hh_q4k_body(const hh_q4k_args& a) {
         if (k + 2 < nsteps) load_step(k + 2, A);
         compute_step(k + 1, B);
     }
+
+    if constexpr (GATEUP) {
+        // Digits of this workgroup's slice of h for the down projection.
+        if (a.hq.q1 != nullptr && r1 > r0) {
+            __syncthreads();
+            const hh_digits_ptr dst{a.hq.q1 + r0, a.hq.q2 + r0, a.hq.sc + r0 / 32, a.hq.sum + r0 / 32};
+            hh_quantize_digits(hl, r1 - r0, dst);
+        }
+    }
 }
 
-#define HH_Q4K_KERNELS(WPT, R)                                                                     \
-    extern "C" __global__ void __launch_bounds__(HH_Q4K_BLOCK) hh_q4k_gemv_w##WPT(const hh_q4k_args a) { \
-        hh_q4k_body<WPT, R, false>(a);                                                             \
-    }                                                                                              \
-    extern "C" __global__ void __launch_bounds__(HH_Q4K_BLOCK)                                     \
-        hh_q4k_gateup_w##WPT(const hh_q4k_args a) {                                                \
-        hh_q4k_body<WPT, (R > 1 ? R / 2 : 1), true>(a);                                           \
+// Kernel names: hh_q4k_{gemv,gemvq,gateup}_w<WPT>.  WPT = waves per team (row width up to
+// 64*WPT units); gemvq takes x as pre-built digits.  Rows per team step: 2 for a GEMV,
+// 1 for gate/up (two matrices), which measured best on MI355X.
+#define HH_Q4K_KERNEL(KIND, GU, XD, WPT, R)                                                  \
+    extern "C" __global__ void __launch_bounds__(HH_Q4K_BLOCK) hh_q4k_##KIND##_w##WPT(const hh_q4k_args a) { \
+        hh_q4k_body<WPT, R, GU, XD>(a);                                                      \
     }
+#define HH_Q4K_WPT(WPT)                          \
+    HH_Q4K_KERNEL(gemv, false, false, WPT, 2)    \
+    HH_Q4K_KERNEL(gemvq, false, true, WPT, 2)    \
+    HH_Q4K_KERNEL(gateup, true, false, WPT, 1)
 
-HH_Q4K_KERNELS(1, 2)
-HH_Q4K_KERNELS(2, 2)
-HH_Q4K_KERNELS(4, 2)
-HH_Q4K_KERNELS(8, 2)
+HH_Q4K_WPT(1)
+HH_Q4K_WPT(2)
+HH_Q4K_WPT(4)
+HH_Q4K_WPT(8)

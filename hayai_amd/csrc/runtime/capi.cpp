@@ -190,6 +190,20 @@ hh_status hh_buf_read(hh_engine* e, const hh_buf* src, size_t off, void* dst, si
     return HH_OK;
 }
 
+hh_status hh_buf_copy(hh_engine* e, hh_buf* dst, size_t dst_off, const hh_buf* src, size_t src_off, size_t bytes) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(check_engine(e, dst, "hh_buf_copy"));
+    HH_TRY(check_engine(e, src, "hh_buf_copy"));
+    HH_TRY(check_range(dst, dst_off, bytes, "hh_buf_copy dst"));
+    HH_TRY(check_range(src, src_off, bytes, "hh_buf_copy src"));
+    if (bytes == 0) return HH_OK;
+    HH_TRY(e->select());
+    HH_TRY_HIP(hipMemcpyAsync((char*)dst->ptr + dst_off, (const char*)src->ptr + src_off, bytes, hipMemcpyDefault,
+                              e->stream),
+               "hipMemcpyAsync(copy)");
+    return HH_OK;
+}
+
 hh_status hh_buf_fill(hh_engine* e, hh_buf* dst, size_t off, uint8_t value, size_t bytes) {
     HH_NOT_NULL(e, "engine");
     HH_TRY(check_engine(e, dst, "hh_buf_fill"));

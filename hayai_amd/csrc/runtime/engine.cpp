@@ -148,48 +148,83 @@ hh_status hh_engine::grow(void** p, size_t* cap, size_t need) {
 }
 
 // Kernel argument block of q4k.hip (same layout).
+struct hh_digits_ptr {
+    int8_t* q1;
+    int8_t* q2;
+    float* sc;
+    float* sum;
+};
 struct hh_q4k_args {
     const uint8_t* w0;
     const uint8_t* w1;
     const float* x;
     float* y;
+    hh_digits_ptr xq;
+    hh_digits_ptr hq;
     uint32_t m;
     uint32_t n;
     uint64_t row_bytes;
     int32_t act;
-    int32_t pad;
+    uint32_t hrows;
 };
 
+// Digit layout of an n-element activation in one buffer (see q4k.hip).
+static hh_digits_ptr digits_at(void* base, size_t n) {
+    int8_t* q1 = (int8_t*)base;
+    int8_t* q2 = q1 + n;
+    float* sc = (float*)(q2 + n);
+    return hh_digits_ptr{q1, q2, sc, sc + n / 32};
+}
+
+size_t hh_digits_bytes(size_t n) { return 2 * n + (n / 32) * 8; }
+
 hh_status hh_engine::enqueue_q4k(size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const float* x, float* y,
-                                 int act, bool gateup) {
+                                 int act, bool gateup, const void* xdigits, void* hdigits) {
     const size_t units = n / 64;
     const size_t rb = (n / 256) * 144;
-    if (q4k_generic || units == 0 || units > 512 || ((uintptr_t)x & 15u) || ((uintptr_t)w0 & 15u) ||
-        (gateup && ((uintptr_t)w1 & 15u)))
+    if (q4k_generic || units == 0 || units > 512 || ((uintptr_t)w0 & 15u) || (gateup && ((uintptr_t)w1 & 15u)) ||
+        (!xdigits && ((uintptr_t)x & 15u)) || (hdigits && (m % 256 != 0)))
         return HH_ERR_UNSUPPORTED_DEVICE;
     int wpt = 1;
     while ((size_t)wpt * 64 < units) wpt *= 2;
     const int waves = 8, tpw = waves / wpt;
     const int rows_per_team_step = gateup ? 1 : 2;
-    const std::string name = std::string(gateup ? "hh_q4k_gateup_w" : "hh_q4k_gemv_w") + std::to_string(wpt);
+    const char* kind = gateup ? "hh_q4k_gateup_w" : (xdigits ? "hh_q4k_gemvq_w" : "hh_q4k_gemv_w");
+    const std::string name = std::string(kind) + std::to_string(wpt);
     hipFunction_t fn;
     HH_TRY(kernel(name, &fn));
-    const size_t smem = 2 * n + (n / 32) * 8 + (size_t)waves * 4 * sizeof(float);
+    // Occupancy with the largest LDS this kernel asks for (gate/up h rows bounded below).
+    const size_t xbytes = xdigits ? 0 : hh_digits_bytes(n);
+    const size_t red_bytes = (size_t)waves * 4 * sizeof(float);
     int occ = blocks_per_cu_override;
     if (occ <= 0) {
         auto it = blocks_per_cu.find(name);
         if (it != blocks_per_cu.end()) {
             occ = it->second;
         } else {
-            if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, waves * 64, smem) != hipSuccess || occ < 1)
+            const size_t probe = xbytes + red_bytes + (gateup ? 64 * sizeof(float) : 0);
+            if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, waves * 64, probe) != hipSuccess ||
+                occ < 1)
                 occ = 1;
             blocks_per_cu[name] = occ;
         }
     }
-    const size_t rows_per_wg_step = (size_t)tpw * rows_per_team_step;
-    const size_t need = (m + rows_per_wg_step - 1) / rows_per_wg_step;
-    const size_t grid = std::max<size_t>(1, std::min(need, (size_t)props.multiProcessorCount * occ));
-    hh_q4k_args a{w0, w1, x, y, (uint32_t)m, (uint32_t)n, (uint64_t)rb, act, 0};
+    const size_t cap = (size_t)props.multiProcessorCount * occ;
+    size_t grid;
+    uint32_t hrows = 0;
+    if (gateup && hdigits) {
+        const size_t S = (m + 31) / 32;  // 32-row sub-blocks of h
+        grid = std::max<size_t>(1, std::min(S, cap));
+        hrows = (uint32_t)(32 * ((S + grid - 1) / grid));
+    } else {
+        const size_t rows_per_wg_step = (size_t)tpw * rows_per_team_step;
+        grid = std::max<size_t>(1, std::min((m + rows_per_wg_step - 1) / rows_per_wg_step, cap));
+        if (gateup) hrows = (uint32_t)((m + grid - 1) / grid + 3) & ~3u;
+    }
+    const size_t smem = xbytes + (size_t)hrows * sizeof(float) + red_bytes;
+    hh_q4k_args a{w0, w1, x, y, hh_digits_ptr{}, hh_digits_ptr{}, (uint32_t)m, (uint32_t)n, (uint64_t)rb, act, hrows};
+    if (xdigits) a.xq = digits_at(const_cast<void*>(xdigits), n);
+    if (hdigits) a.hq = digits_at(hdigits, m);
     void* params[] = {&a};
     hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, waves * 64, 1, 1, (unsigned)smem, stream, params,
                                            nullptr);
@@ -212,7 +247,7 @@ hh_status hh_engine::enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w
         return fail(HH_ERR_INVALID, "ggml_gemv_%s: weight address must be 2-byte aligned", f->name);
     const bool aligned16 = (((uintptr_t)w & 15u) == 0) && (rb % 16 == 0);
     if (type == HH_TYPE_Q4_K && aligned16) {
-        hh_status st = enqueue_q4k(m, n, w, nullptr, x, y, 0, false);
+        hh_status st = enqueue_q4k(m, n, w, nullptr, x, y, 0, false, nullptr, nullptr);
         if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
     }
     std::string name;
@@ -251,7 +286,7 @@ hh_status hh_engine::enqueue_gateup(int tg, int tu, size_t d_ff, size_t d_model,
     size_t rb;
     HH_TRY(row_bytes(tg, d_model, &rb));
     if (tg == HH_TYPE_Q4_K && tu == HH_TYPE_Q4_K) {
-        hh_status st = enqueue_q4k(d_ff, d_model, wg, wu, x, h, act, true);
+        hh_status st = enqueue_q4k(d_ff, d_model, wg, wu, x, h, act, true, nullptr, nullptr);
         if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
     }
     if (tg == tu && f->fused_gateup) {
@@ -287,9 +322,23 @@ hh_status hh_engine::enqueue_gateup(int tg, int tu, size_t d_ff, size_t d_model,
 
 hh_status hh_engine::enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y) {
     HH_TRY(grow(&ws_h, &ws_h_cap, d->d_ff * sizeof(float)));
-    HH_TRY(enqueue_gateup(d->type_gate, d->type_up, d->d_ff, d->d_model, pack + d->gate_off, pack + d->up_off, x,
-                          (float*)ws_h, d->act));
-    HH_TRY(enqueue_gemv(d->type_down, d->d_model, d->d_ff, pack + d->down_off, (const float*)ws_h, y));
+    const uint8_t* wg = pack + d->gate_off;
+    const uint8_t* wu = pack + d->up_off;
+    const uint8_t* wd = pack + d->down_off;
+    if (d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K && d->type_down == HH_TYPE_Q4_K) {
+        // Gate/up writes h and its int8 digits; down consumes the digits directly.
+        HH_TRY(grow(&ws_hq, &ws_hq_cap, hh_digits_bytes(d->d_ff)));
+        hh_status st = enqueue_q4k(d->d_ff, d->d_model, wg, wu, x, (float*)ws_h, d->act, true, nullptr, ws_hq);
+        if (st == HH_OK) {
+            st = enqueue_q4k(d->d_model, d->d_ff, wd, nullptr, nullptr, y, 0, false, ws_hq, nullptr);
+            if (st == HH_ERR_UNSUPPORTED_DEVICE) st = enqueue_gemv(d->type_down, d->d_model, d->d_ff, wd, (const float*)ws_h, y);
+            if (st == HH_OK) ffn_calls += 3;
+            return st;
+        }
+        if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
+    }
+    HH_TRY(enqueue_gateup(d->type_gate, d->type_up, d->d_ff, d->d_model, wg, wu, x, (float*)ws_h, d->act));
+    HH_TRY(enqueue_gemv(d->type_down, d->d_model, d->d_ff, wd, (const float*)ws_h, y));
     ffn_calls += 3;
     return HH_OK;
 }
@@ -307,10 +356,11 @@ static std::vector<std::string> required_kernels() {
     }
     for (const char* s : {"hh_gemv_f32_plain", "hh_gemv_f16_plain", "hh_act_mul_kernel", "hh_dequant_q4_0",
                           "hh_dequant_q4_k", "hh_dequant_iq2_xxs", "hh_dequant_iq3_xxs", "hh_dequant_f16",
-                          "hh_synth_bytes", "hh_synth_scales", "hh_q4k_gemv_w1", "hh_q4k_gemv_w2", "hh_q4k_gemv_w4",
-                          "hh_q4k_gemv_w8", "hh_q4k_gateup_w1", "hh_q4k_gateup_w2", "hh_q4k_gateup_w4",
-                          "hh_q4k_gateup_w8"})
+                          "hh_synth_bytes", "hh_synth_scales"})
         k.push_back(s);
+    for (int w : {1, 2, 4, 8})
+        for (const char* kind : {"hh_q4k_gemv_w", "hh_q4k_gemvq_w", "hh_q4k_gateup_w"})
+            k.push_back(std::string(kind) + std::to_string(w));
     return k;
 }
 
@@ -351,6 +401,7 @@ hh_status engine_create(int device, hh_engine** out) {
     }
     if (const char* b = getenv("HAYAI_HIP_BLOCKS_PER_CU")) e->blocks_per_cu_override = atoi(b);
     if (const char* g = getenv("HAYAI_HIP_Q4K_GENERIC")) e->q4k_generic = atoi(g) != 0;
+
     *out = e;
     return HH_OK;
 }
@@ -360,7 +411,7 @@ void engine_destroy(hh_engine* e) {
     hipSetDevice(e->device);
     if (e->stream) hipStreamSynchronize(e->stream);
     if (e->copy_stream) hipStreamSynchronize(e->copy_stream);
-    for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w})
+    for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq})
         if (p) hipFree(p);
     if (e->stream) hipStreamDestroy(e->stream);
     if (e->copy_stream) hipStreamDestroy(e->copy_stream);

@@ -99,6 +99,8 @@ struct hh_engine {
     size_t ws_u_cap = 0;
     void* ws_w = nullptr;
     size_t ws_w_cap = 0;
+    void* ws_hq = nullptr;  // int8 digits of the FFN intermediate (gate/up -> down)
+    size_t ws_hq_cap = 0;
     int blocks_per_cu_override = 0;  // HAYAI_HIP_BLOCKS_PER_CU
     bool q4k_generic = false;        // HAYAI_HIP_Q4K_GENERIC=1: skip the int8-digit Q4_K kernels
 
@@ -121,9 +123,10 @@ struct hh_engine {
                              const uint8_t* wu, const float* x, float* h, int act);
     hh_status enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y);
     // Q4_K batch-1 kernels (q4k.hip); returns HH_ERR_UNSUPPORTED_DEVICE when the shape or
-    // alignment needs the generic kernels instead (the caller then falls back).
+    // alignment needs the generic kernels instead (the caller then falls back).  xdigits:
+    // x given as int8 digits (then x is unused); hdigits: gate/up also writes h's digits.
     hh_status enqueue_q4k(size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const float* x, float* y,
-                          int act, bool gateup);
+                          int act, bool gateup, const void* xdigits, void* hdigits);
 };
 
 #endif

@@ -91,6 +91,10 @@ class DeviceBuffer:
         n = self.nbytes - offset if nbytes is None else nbytes
         _check(self.engine.lib.hh_buf_fill(self.engine.handle, self.handle, offset, value, n))
 
+    def copy_from(self, src: "DeviceBuffer", nbytes: int, dst_off: int = 0, src_off: int = 0) -> None:
+        """Enqueue a buffer-to-buffer copy on the engine's compute stream."""
+        _check(self.engine.lib.hh_buf_copy(self.engine.handle, self.handle, dst_off, src.handle, src_off, nbytes))
+
     def host_view(self) -> np.ndarray:
         """numpy view of a pinned buffer (HH_BUF_PINNED_HOST only)."""
         p = self.engine.lib.hh_buf_host_ptr(self.handle)

@@ -138,6 +138,8 @@ void* hh_buf_host_ptr(hh_buf* b);
  * CL_BLOCKING).  Ordered after all work already queued on the compute stream. */
 hh_status hh_buf_write(hh_engine* e, hh_buf* dst, size_t dst_off, const void* src, size_t bytes);
 hh_status hh_buf_read(hh_engine* e, const hh_buf* src, size_t src_off, void* dst, size_t bytes);
+/* Buffer-to-buffer copy (device or pinned), enqueued on the compute stream. */
+hh_status hh_buf_copy(hh_engine* e, hh_buf* dst, size_t dst_off, const hh_buf* src, size_t src_off, size_t bytes);
 /* Device fill with a byte value (enqueued on the compute stream). */
 hh_status hh_buf_fill(hh_engine* e, hh_buf* dst, size_t off, uint8_t value, size_t bytes);
 
