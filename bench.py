@@ -13,10 +13,14 @@ packed weights read once (99,090,432 B) + x in (16,384 B) + y out (16,384 B); th
 d_ff intermediate is excluded.  FFN tok/s = 1 / time per step.
 
 roofline: the fused gate/up kernel (2/3 of the bytes, the dominant kernel), timed with HIP
-events recorded on the compute stream around each of its launches in a second timed
-region; achieved = its algorithmic bytes per launch (W_gate + W_up + x + h) / its mean
-launch duration.  cpu_baseline: the oracle's fp32 restatement of hayai-model's gemv_q4_k
-FFN (oracle/, OpenMP over rows) on a bounded sample of the same layers, host cores.
+events on the compute stream around a region of its launches alone (32 layers x up to 50
+steps, issued through the FFN's two-call form hh_ffn_begin_dev / hh_ffn_finish_dev, which
+runs the same kernels as hh_ffn_dev); achieved = its algorithmic bytes per launch
+(W_gate + W_up + x + h) / its mean launch duration.  traffic = HBM bytes per launch of that kernel measured with
+rocprofv3 FETCH_SIZE / WRITE_SIZE passes (each scaled by what the counter reads for a
+256 MiB device copy, --copy-calibration), read from profiles/ when present.
+cpu_baseline: the oracle's fp32 restatement of hayai-model's gemv_q4_k FFN (oracle/,
+OpenMP over rows) on a bounded sample of the same layers, host cores.
 """
 from __future__ import annotations
 
@@ -36,6 +40,7 @@ D_MODEL, D_FF, LAYERS = 4096, 14336, 32
 Q4_K = 12
 PEAK_HBM_GBS = 8000.0
 CONFIG_ID = 2
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gateup_8b_bs1_traffic.json")
 
 
 def log(*a):
@@ -117,6 +122,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run one 256 MiB device copy before timing (reference point for HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the FFN path would shard "
@@ -151,6 +158,11 @@ def main() -> int:
         for l in range(LAYERS):
             eng.ffn_dev(desc, pack, l * stride, xbuf, 4 * D_MODEL * l, ybuf, 4 * D_MODEL * l)
 
+    if args.copy_calibration:
+        cal = eng.alloc(256 << 20)
+        cal.copy_from(pack, 256 << 20)
+        eng.sync()
+        cal.free()
     for _ in range(args.warmup):
         step()
     eng.sync()
@@ -167,29 +179,27 @@ def main() -> int:
     gbs = bytes_step / (ms / 1e3) / 1e9
     log(f"[bench] {ms * 1e3:.1f} us/step (event), wall {wall / args.steps * 1e6:.1f} us/step, {gbs:.1f} GB/s")
 
-    # Per-kernel durations: a second timed region issuing the same two kernels per layer
-    # through the gate/up and GEMV entry points, with events recorded between launches.
+    # Per-kernel durations: further timed regions issuing the same kernels through the FFN's
+    # two-call form -- gate/up launches alone over all layers, then gate/up + down -- each
+    # bracketed by events on the compute stream (events between single launches would add
+    # their own overhead to every launch).  down = (gate/up + down) - gate/up.
     n_prof = max(1, min(args.steps, 50))
-    evs = [[eng.event() for _ in range(3)] for _ in range(LAYERS)]
-    gu_ms, dn_ms = [], []
-    hbuf = eng.alloc(4 * D_FF)
-    for s in range(n_prof):
-        for l in range(LAYERS):
-            a, b, c = evs[l]
-            base = l * stride
-            a.record()
-            eng.gateup_dev((Q4_K, Q4_K), D_FF, D_MODEL, pack, base + lay.gate_off, pack, base + lay.up_off,
-                           xbuf, 4 * D_MODEL * l, hbuf, 0)
-            b.record()
-            eng.gemv_dev(Q4_K, D_MODEL, D_FF, pack, base + lay.down_off, hbuf, 0, ybuf, 4 * D_MODEL * l)
-            c.record()
+
+    def region(with_down: bool) -> float:
+        a, b = eng.event(), eng.event()
+        a.record()
+        for _ in range(n_prof):
+            for l in range(LAYERS):
+                base = l * stride
+                eng.ffn_begin_dev(desc, pack, base, xbuf, 4 * D_MODEL * l)
+                if with_down:
+                    eng.ffn_finish_dev(desc, pack, base, ybuf, 4 * D_MODEL * l)
+        b.record()
         eng.sync()
-        for l in range(LAYERS):
-            a, b, c = evs[l]
-            gu_ms.append(a.elapsed_ms(b))
-            dn_ms.append(b.elapsed_ms(c))
-    gu = statistics.mean(gu_ms)
-    dn = statistics.mean(dn_ms)
+        return a.elapsed_ms(b) / (n_prof * LAYERS)
+
+    gu = region(False)
+    dn = region(True) - gu
     gu_gbs = gateup_bytes() / (gu / 1e3) / 1e9
     dn_gbs = (D_MODEL * hayai_amd.row_bytes(Q4_K, D_FF) + 4 * D_FF + 4 * D_MODEL) / (dn / 1e3) / 1e9
     log(f"[bench] gate/up kernel {gu * 1e3:.2f} us ({gu_gbs:.0f} GB/s), down kernel {dn * 1e3:.2f} us ({dn_gbs:.0f} GB/s)")
@@ -199,6 +209,11 @@ def main() -> int:
         cpu = cpu_baseline(eng, pack, lay, stride, xs, args.cpu_budget)
         log(f"[bench] cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
 
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        traffic = int(t["hbm_bytes_per_launch"])
     out = {
         "metric": "FFN GEMV achieved HBM GB/s (% of peak) + FFN tok/s, 8B-shape Q4_K bs=1",
         "value": round(gbs, 2),
@@ -217,7 +232,8 @@ def main() -> int:
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "ffn_tok_s": round(1e3 / ms, 2),
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes": gateup_bytes(),
                      "kernel": "fused gate/up + SwiGLU (Q4_K, 14336x4096 x2)", "mean_us": round(gu * 1e3, 3),
                      "down_kernel_us": round(dn * 1e3, 3), "down_kernel_gbs": round(dn_gbs, 1)},
         "cpu_baseline": cpu,

@@ -95,9 +95,20 @@ HH_DEV void hh_digits8(const float (&v)[8], float scale, float inv, uint2& o1, u
     o2 = make_uint2(p2[0], p2[1]);
 }
 
+// Device-coherent (agent scope) 32/64-bit accesses: they go to the device coherence point
+// (sc1), so data written by one XCD is seen by another without flushing any L2.
+HH_DEV void hh_store_coherent(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+HH_DEV uint64_t hh_load_coherent(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Quantize n f32 values (n % 32 == 0) into digits: 4 lanes per 32-element sub-block,
 // chunk c = 8 elements.  All threads of the workgroup must call it (quads stay whole
-// because the stride is a multiple of 4 and n/8 is a multiple of 4).
+// because the stride is a multiple of 4 and n/8 is a multiple of 4).  COHERENT: write with
+// device-coherent stores (the digits are read by other workgroups in the same launch).
+template <bool COHERENT = false>
 HH_DEV void hh_quantize_digits(const float* src, uint32_t n, const hh_digits_ptr& dst) {
     for (uint32_t c = threadIdx.x; c < n / 8; c += blockDim.x) {
         const float4 t0 = reinterpret_cast<const float4*>(src)[2 * c];
@@ -115,11 +126,24 @@ HH_DEV void hh_quantize_digits(const float* src, uint32_t n, const hh_digits_ptr
         const float inv = amax > 0.f ? 127.0f / amax : 0.f;
         uint2 o1, o2;
         hh_digits8(v, scale, inv, o1, o2);
-        reinterpret_cast<uint2*>(dst.q1)[c] = o1;
-        reinterpret_cast<uint2*>(dst.q2)[c] = o2;
-        if ((c & 3u) == 0) {
-            dst.sc[c / 4] = scale;
-            dst.sum[c / 4] = s;
+        if constexpr (COHERENT) {
+            uint32_t* q1 = reinterpret_cast<uint32_t*>(dst.q1) + 2 * c;
+            uint32_t* q2 = reinterpret_cast<uint32_t*>(dst.q2) + 2 * c;
+            hh_store_coherent(q1, o1.x);
+            hh_store_coherent(q1 + 1, o1.y);
+            hh_store_coherent(q2, o2.x);
+            hh_store_coherent(q2 + 1, o2.y);
+            if ((c & 3u) == 0) {
+                hh_store_coherent(reinterpret_cast<uint32_t*>(dst.sc) + c / 4, __float_as_uint(scale));
+                hh_store_coherent(reinterpret_cast<uint32_t*>(dst.sum) + c / 4, __float_as_uint(s));
+            }
+        } else {
+            reinterpret_cast<uint2*>(dst.q1)[c] = o1;
+            reinterpret_cast<uint2*>(dst.q2)[c] = o2;
+            if ((c & 3u) == 0) {
+                dst.sc[c / 4] = scale;
+                dst.sum[c / 4] = s;
+            }
         }
     }
 }
@@ -219,8 +243,14 @@ HH_DEV float hh_q4k_unit(const hh_q4k_data& d, const hh_q4k_x& xr) {
 //   R       rows per team step
 //   GATEUP  two matrices, output act(gate)*up (and optionally the digits of that output)
 //   XDIG    x arrives as pre-built digits (a.xq) instead of f32 (a.x)
-template <int WPT, int R, bool GATEUP, bool XDIG>
-HH_DEV void hh_q4k_body(const hh_q4k_args& a) {
+//   COH     digits exchanged with other workgroups of the same launch (fused FFN): the h
+//           digits are written and read with device-coherent accesses
+struct hh_no_gate {
+    HH_DEV bool operator()() const { return true; }
+};
+
+template <int WPT, int R, bool GATEUP, bool XDIG, bool COH = false, class Gate = hh_no_gate>
+HH_DEV void hh_q4k_body(const hh_q4k_args& a, Gate gate = {}) {
     extern __shared__ __attribute__((aligned(16))) char hh_smem[];
     constexpr int TEAM = WPT * HH_WAVE;
     constexpr int TPW = HH_Q4K_WAVES / WPT;  // teams per workgroup
@@ -246,9 +276,18 @@ HH_DEV void hh_q4k_body(const hh_q4k_args& a) {
     constexpr uint32_t ROWS_PER_STEP = TPW * R;
     const uint32_t nsteps = (r1 - r0 + ROWS_PER_STEP - 1) / ROWS_PER_STEP;
 
-    // LDS: [x digits (f32 input mode)] [h rows (gate/up)] [team reduction slots]
+    // LDS: [x digits (f32 input mode, or staged copies of digits from other workgroups)]
+    //      [h rows (gate/up)] [team reduction slots]
     char* lds = hh_smem;
     hh_digits_ptr xd = a.xq;
+    if constexpr (XDIG && COH) {
+        // Staged copy of digits written by other workgroups of this launch (filled below).
+        xd.q1 = reinterpret_cast<int8_t*>(lds);
+        xd.q2 = xd.q1 + a.n;
+        xd.sc = reinterpret_cast<float*>(xd.q2 + a.n);
+        xd.sum = xd.sc + a.n / 32;
+        lds = reinterpret_cast<char*>(xd.sum + a.n / 32);
+    }
     if constexpr (!XDIG) {
         xd.q1 = reinterpret_cast<int8_t*>(lds);
         xd.q2 = xd.q1 + a.n;
@@ -320,6 +359,18 @@ HH_DEV void hh_q4k_body(const hh_q4k_args& a) {
     // x prologue so HBM latency overlaps the digit conversion.
     hh_q4k_data A[NV][R], B[NV][R];
     if (nsteps > 0) load_step(0, A);
+    if constexpr (XDIG && COH) {
+        // Digits produced by other workgroups: the first two row steps' weights are in
+        // flight while this workgroup waits for them (gate), then they are copied once into
+        // LDS with coalesced device-coherent loads (q1, q2, sc, sum are contiguous).
+        if (nsteps > 1) load_step(1, B);
+        if (!gate()) return;
+        const uint32_t words = (2 * a.n + (a.n / 32) * 8) / 8;
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(a.xq.q1);
+        uint64_t* dst = reinterpret_cast<uint64_t*>(xd.q1);
+        for (uint32_t i = tid; i < words; i += blockDim.x) dst[i] = hh_load_coherent(src + i);
+        __syncthreads();
+    }
     if constexpr (!XDIG) {
         hh_quantize_digits(a.x, a.n, xd);
         __syncthreads();
@@ -327,7 +378,7 @@ HH_DEV void hh_q4k_body(const hh_q4k_args& a) {
     if (act) hh_q4k_load_lane_x(xd, lane, xr);
 
     for (uint32_t k = 0; k < nsteps; k += 2) {
-        if (k + 1 < nsteps) load_step(k + 1, B);
+        if (k + 1 < nsteps && !(XDIG && COH && k == 0)) load_step(k + 1, B);
         compute_step(k, A);
         if (k + 1 >= nsteps) break;
         if (k + 2 < nsteps) load_step(k + 2, A);
@@ -339,7 +390,7 @@ HH_DEV void hh_q4k_body(const hh_q4k_args& a) {
         if (a.hq.q1 != nullptr && r1 > r0) {
             __syncthreads();
             const hh_digits_ptr dst{a.hq.q1 + r0, a.hq.q2 + r0, a.hq.sc + r0 / 32, a.hq.sum + r0 / 32};
-            hh_quantize_digits(hl, r1 - r0, dst);
+            hh_quantize_digits<COH>(hl, r1 - r0, dst);
         }
     }
 }
@@ -360,3 +411,103 @@ HH_Q4K_WPT(1)
 HH_Q4K_WPT(2)
 HH_Q4K_WPT(4)
 HH_Q4K_WPT(8)
+
+// ----------------------------------------------------------------------------------------
+// One launch per FFN layer: gate/up phase, grid-wide barrier, down phase.
+//
+// All workgroups are co-resident (the host sizes the grid from the occupancy API), so a
+// grid barrier is safe; it is still bounded: a wait that exceeds ~2^20 sleeps gives up,
+// records the failure in the error word and the kernel finishes (the host reports that
+// error, sticky, at its next synchronizing call and then clears the barrier state).
+//
+// Barrier state (hh_bar_*, one 128-byte line each so arrivals and polls spread over memory
+// channels instead of serializing on one address):
+//   line g      (g < 16)  arrival counter of group g = workgroups with blockIdx % 16 == g
+//   line 16 + g           release flag of group g (holds the generation of the last release)
+//   line 32               arrival counter of groups
+//   line 33               error word
+// The last arriver of a group resets its group counter and counts the group; the last
+// group resets that counter and writes the launch's generation (a host-side counter,
+// never 0) into every release flag.  Counters therefore return to zero at every release
+// and flags need no reset.  The h digits cross workgroups (and XCDs) through device-
+// coherent stores and loads, ordered by s_waitcnt before the arrival and by the barrier.
+#define HH_BAR_GROUPS 16
+#define HH_BAR_LINE 32  // u32 words per 128-byte line
+#define HH_BAR_WORDS (HH_BAR_LINE * (2 * HH_BAR_GROUPS + 2))
+
+struct hh_q4k_ffn_args {
+    hh_q4k_args gu;  // gate/up: writes h (f32) and the digits of h
+    hh_q4k_args dn;  // down: reads the digits of h
+    unsigned* bar;   // HH_BAR_WORDS words
+    unsigned gen;    // generation of this launch (!= 0)
+    unsigned pad;
+};
+
+HH_DEV unsigned hh_atomic_add_agent(unsigned* p, unsigned v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+HH_DEV void hh_store_agent(unsigned* p, unsigned v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+HH_DEV unsigned hh_load_agent(unsigned* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The caller has completed (s_waitcnt + workgroup barrier) every store that other
+// workgroups read after this barrier.
+HH_DEV bool hh_grid_barrier(unsigned* bar, unsigned gen) {
+    __shared__ int ok;
+    if (threadIdx.x == 0) {
+        const unsigned G = gridDim.x < HH_BAR_GROUPS ? gridDim.x : HH_BAR_GROUPS;
+        const unsigned g = blockIdx.x % HH_BAR_GROUPS;
+        const unsigned members = (gridDim.x - g + HH_BAR_GROUPS - 1) / HH_BAR_GROUPS;
+        unsigned* cnt = bar + g * HH_BAR_LINE;
+        unsigned* flag = bar + (HH_BAR_GROUPS + g) * HH_BAR_LINE;
+        unsigned* top = bar + 2 * HH_BAR_GROUPS * HH_BAR_LINE;
+        unsigned* err = top + HH_BAR_LINE;
+        if (hh_atomic_add_agent(cnt, 1u) == members - 1) {
+            hh_store_agent(cnt, 0u);
+            if (hh_atomic_add_agent(top, 1u) == G - 1) {
+                hh_store_agent(top, 0u);
+                __builtin_amdgcn_s_waitcnt(0);
+                for (unsigned k = 0; k < G; k++) hh_store_agent(bar + (HH_BAR_GROUPS + k) * HH_BAR_LINE, gen);
+            }
+        }
+        int good = 1;
+        for (unsigned spins = 0; hh_load_agent(flag) != gen; spins++) {
+            __builtin_amdgcn_s_sleep(4);
+            if (spins > (1u << 20)) {
+                good = 0;
+                hh_store_agent(err, 1u);
+                break;
+            }
+        }
+        ok = good;
+    }
+    __syncthreads();  // later device-coherent loads are issued after the wait completed
+    return ok != 0;
+}
+
+template <int WPT_GU, int WPT_D>
+HH_DEV void hh_q4k_ffn_body(const hh_q4k_ffn_args& a) {
+    hh_q4k_body<WPT_GU, 1, true, false, true>(a.gu);
+    // Every thread's device-coherent h-digit stores are complete before the workgroup
+    // arrives (vmcnt covers stores on this architecture).  No fence: a release/acquire
+    // fence at agent scope writes back and invalidates the whole L2 of the XCD.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // The down phase issues its first weight loads, then waits at the grid barrier.
+    hh_q4k_body<WPT_D, 2, false, true, true>(a.dn, [&]() { return hh_grid_barrier(a.bar, a.gen); });
+}
+
+// hh_q4k_ffn_g<WPT gate/up>_d<WPT down>
+#define HH_Q4K_FFN(G, D)                                                                     \
+    extern "C" __global__ void __launch_bounds__(HH_Q4K_BLOCK) hh_q4k_ffn_g##G##_d##D(const hh_q4k_ffn_args a) { \
+        hh_q4k_ffn_body<G, D>(a);                                                            \
+    }
+HH_Q4K_FFN(1, 1)
+HH_Q4K_FFN(1, 2)
+HH_Q4K_FFN(1, 4)
+HH_Q4K_FFN(2, 4)
+HH_Q4K_FFN(2, 8)
+HH_Q4K_FFN(4, 8)

@@ -114,7 +114,7 @@ hh_status hh_engine_sync(hh_engine* e) {
     HH_TRY(e->select());
     HH_TRY_HIP(hipStreamSynchronize(e->stream), "hipStreamSynchronize(compute)");
     HH_TRY_HIP(hipStreamSynchronize(e->copy_stream), "hipStreamSynchronize(copy)");
-    return HH_OK;
+    return e->check_device_error();
 }
 
 uint64_t hh_engine_ffn_calls(const hh_engine* e) { return e ? e->ffn_calls.load() : 0; }
@@ -186,8 +186,7 @@ hh_status hh_buf_read(hh_engine* e, const hh_buf* src, size_t off, void* dst, si
     HH_TRY(e->select());
     HH_TRY_HIP(hipMemcpyAsync(dst, (const char*)src->ptr + off, bytes, hipMemcpyDefault, e->stream),
                "hipMemcpyAsync(D2H)");
-    HH_TRY_HIP(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
-    return HH_OK;
+    return e->check_device_error();  // syncs the stream
 }
 
 hh_status hh_buf_copy(hh_engine* e, hh_buf* dst, size_t dst_off, const hh_buf* src, size_t src_off, size_t bytes) {
@@ -396,6 +395,28 @@ hh_status hh_ffn_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, siz
                           (float*)((char*)y->ptr + y_off));
 }
 
+hh_status hh_ffn_begin_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off, const hh_buf* x,
+                           size_t x_off) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_ffn(e, d, pack, pack_off));
+    HH_TRY(check_engine(e, x, "x"));
+    HH_TRY(check_range(x, x_off, d->d_model * sizeof(float), "x"));
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    return e->enqueue_ffn_begin(d, (const uint8_t*)pack->ptr + pack_off, (const float*)((const char*)x->ptr + x_off));
+}
+
+hh_status hh_ffn_finish_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off, hh_buf* y,
+                            size_t y_off) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_ffn(e, d, pack, pack_off));
+    HH_TRY(check_engine(e, y, "y"));
+    HH_TRY(check_range(y, y_off, d->d_model * sizeof(float), "y"));
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    return e->enqueue_ffn_finish(d, (const uint8_t*)pack->ptr + pack_off, (float*)((char*)y->ptr + y_off));
+}
+
 hh_status hh_ffn(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off, const float* x, float* y) {
     HH_NOT_NULL(e, "engine");
     HH_TRY(validate_ffn(e, d, pack, pack_off));
@@ -410,8 +431,7 @@ hh_status hh_ffn(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t 
     HH_TRY(e->enqueue_ffn(d, (const uint8_t*)pack->ptr + pack_off, (const float*)e->ws_x, (float*)e->ws_y));
     HH_TRY_HIP(hipMemcpyAsync(y, e->ws_y, d->d_model * sizeof(float), hipMemcpyDeviceToHost, e->stream),
                "hipMemcpyAsync(y)");
-    HH_TRY_HIP(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
-    return HH_OK;
+    return e->check_device_error();
 }
 
 hh_status hh_gateup_dev(hh_engine* e, int tg, int tu, size_t d_ff, size_t d_model, const hh_buf* wg, size_t wg_off,

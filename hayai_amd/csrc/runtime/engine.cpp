@@ -320,27 +320,141 @@ hh_status hh_engine::enqueue_gateup(int tg, int tu, size_t d_ff, size_t d_model,
     return launch(fn, (uint32_t)((d_ff + 255) / 256), 256, a);
 }
 
-hh_status hh_engine::enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y) {
+// Fused FFN kernel arguments and grid-barrier state (q4k.hip): 16 arrival-counter lines,
+// 16 release-flag lines, the group counter and the error word, 128 bytes each.
+struct hh_q4k_ffn_args {
+    hh_q4k_args gu;
+    hh_q4k_args dn;
+    unsigned* bar;
+    unsigned gen;
+    unsigned pad;
+};
+constexpr size_t kBarLine = 128;
+constexpr size_t kBarBytes = kBarLine * (2 * 16 + 2);
+constexpr size_t kBarErrOffset = kBarLine * (2 * 16 + 1);
+
+hh_status hh_engine::enqueue_q4k_ffn(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
+                                     const float* x, float* y) {
+    const size_t dm = d->d_model, df = d->d_ff;
+    if (!ffn_fused || q4k_generic || dm % 256 || df % 256 || dm / 64 > 512 || df / 64 > 512 ||
+        (((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd | (uintptr_t)x) & 15u))
+        return HH_ERR_UNSUPPORTED_DEVICE;
+    int wg_t = 1, wd_t = 1;
+    while ((size_t)wg_t * 64 < dm / 64) wg_t *= 2;
+    while ((size_t)wd_t * 64 < df / 64) wd_t *= 2;
+    const std::string name = "hh_q4k_ffn_g" + std::to_string(wg_t) + "_d" + std::to_string(wd_t);
+    hipFunction_t fn;
+    if (fns.find(name) == fns.end() && hipModuleGetFunction(&fn, module, name.c_str()) != hipSuccess)
+        return HH_ERR_UNSUPPORTED_DEVICE;
+    HH_TRY(kernel(name, &fn));
+    HH_TRY(grow(&ws_h, &ws_h_cap, df * sizeof(float)));
+    HH_TRY(grow(&ws_hq, &ws_hq_cap, hh_digits_bytes(df)));
+    const int waves = 8;
+    const size_t xbytes = hh_digits_bytes(dm);
+    const size_t red_bytes = (size_t)waves * 4 * sizeof(float);
+    int occ = blocks_per_cu_override;
+    if (occ <= 0) {
+        auto it = blocks_per_cu.find(name);
+        if (it != blocks_per_cu.end()) {
+            occ = it->second;
+        } else {
+            if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(
+                    &occ, fn, waves * 64, std::max(xbytes + 64 * sizeof(float), hh_digits_bytes(df)) + red_bytes) !=
+                    hipSuccess ||
+                occ < 1)
+                occ = 1;
+            blocks_per_cu[name] = occ;
+        }
+    }
+    const size_t S = df / 32;
+    const size_t grid = std::max<size_t>(1, std::min((size_t)props.multiProcessorCount * occ, S));
+    const uint32_t hrows = (uint32_t)(32 * ((S + grid - 1) / grid));
+    // gate/up phase: x digits + h rows + reduction; down phase: staged h digits + reduction
+    const size_t smem = std::max(xbytes + (size_t)hrows * sizeof(float), hh_digits_bytes(df)) + red_bytes;
+    hh_q4k_ffn_args a{};
+    a.gu = hh_q4k_args{wg, wu, x, (float*)ws_h, hh_digits_ptr{}, digits_at(ws_hq, df), (uint32_t)df, (uint32_t)dm,
+                       (uint64_t)((dm / 256) * 144), d->act, hrows};
+    a.dn = hh_q4k_args{wd, nullptr, nullptr, y, digits_at(ws_hq, df), hh_digits_ptr{}, (uint32_t)dm, (uint32_t)df,
+                       (uint64_t)((df / 256) * 144), 0, 0};
+    a.bar = (unsigned*)grid_sync;
+    if (++ffn_gen == 0) ffn_gen = 1;
+    a.gen = ffn_gen;
+    void* params[] = {&a};
+    hipError_t err;
+    if (coop_launch)
+        err = hipModuleLaunchCooperativeKernel(fn, (uint32_t)grid, 1, 1, waves * 64, 1, 1, (unsigned)smem, stream,
+                                               params);
+    else
+        err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, waves * 64, 1, 1, (unsigned)smem, stream, params,
+                                    nullptr);
+    if (err != hipSuccess) return hip_fail(err, "launch(fused q4k ffn)");
+    return HH_OK;
+}
+
+hh_status hh_engine::check_device_error() {
+    unsigned flag = 0;
+    HH_TRY_HIP(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    HH_TRY_HIP(hipMemcpy(&flag, (char*)grid_sync + kBarErrOffset, sizeof flag, hipMemcpyDeviceToHost),
+               "hipMemcpy(err)");
+    if (flag) {
+        HH_TRY_HIP(hipMemset(grid_sync, 0, kBarBytes), "hipMemset(grid_sync)");
+        return fail(HH_ERR_RUNTIME, "fused FFN grid barrier timed out (workgroups not co-resident)");
+    }
+    return HH_OK;
+}
+
+static bool same_ffn(const hh_ffn_desc* a, const hh_ffn_desc* b) {
+    return a->type_gate == b->type_gate && a->type_up == b->type_up && a->type_down == b->type_down &&
+           a->act == b->act && a->d_model == b->d_model && a->d_ff == b->d_ff;
+}
+
+hh_status hh_engine::enqueue_ffn_begin(const hh_ffn_desc* d, const uint8_t* pack, const float* x) {
+    ffn_stage_valid = false;
     HH_TRY(grow(&ws_h, &ws_h_cap, d->d_ff * sizeof(float)));
     const uint8_t* wg = pack + d->gate_off;
     const uint8_t* wu = pack + d->up_off;
-    const uint8_t* wd = pack + d->down_off;
+    bool digits = false;
+    hh_status st = HH_ERR_UNSUPPORTED_DEVICE;
     if (d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K && d->type_down == HH_TYPE_Q4_K) {
-        // Gate/up writes h and its int8 digits; down consumes the digits directly.
+        // Gate/up writes h and its int8 digits; the down projection consumes the digits.
         HH_TRY(grow(&ws_hq, &ws_hq_cap, hh_digits_bytes(d->d_ff)));
-        hh_status st = enqueue_q4k(d->d_ff, d->d_model, wg, wu, x, (float*)ws_h, d->act, true, nullptr, ws_hq);
-        if (st == HH_OK) {
-            st = enqueue_q4k(d->d_model, d->d_ff, wd, nullptr, nullptr, y, 0, false, ws_hq, nullptr);
-            if (st == HH_ERR_UNSUPPORTED_DEVICE) st = enqueue_gemv(d->type_down, d->d_model, d->d_ff, wd, (const float*)ws_h, y);
-            if (st == HH_OK) ffn_calls += 3;
-            return st;
-        }
-        if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
+        st = enqueue_q4k(d->d_ff, d->d_model, wg, wu, x, (float*)ws_h, d->act, true, nullptr, ws_hq);
+        digits = st == HH_OK;
     }
-    HH_TRY(enqueue_gateup(d->type_gate, d->type_up, d->d_ff, d->d_model, wg, wu, x, (float*)ws_h, d->act));
-    HH_TRY(enqueue_gemv(d->type_down, d->d_model, d->d_ff, wd, (const float*)ws_h, y));
-    ffn_calls += 3;
+    if (st == HH_ERR_UNSUPPORTED_DEVICE)
+        st = enqueue_gateup(d->type_gate, d->type_up, d->d_ff, d->d_model, wg, wu, x, (float*)ws_h, d->act);
+    if (st != HH_OK) return st;
+    ffn_stage = *d;
+    ffn_stage_digits = digits;
+    ffn_stage_valid = true;
+    ffn_calls += 2;
     return HH_OK;
+}
+
+hh_status hh_engine::enqueue_ffn_finish(const hh_ffn_desc* d, const uint8_t* pack, float* y) {
+    if (!ffn_stage_valid || !same_ffn(d, &ffn_stage))
+        return fail(HH_ERR_INVALID, "ffn finish: no gate/up of this FFN shape is pending (call the begin step first)");
+    ffn_stage_valid = false;
+    const uint8_t* wd = pack + d->down_off;
+    hh_status st = HH_ERR_UNSUPPORTED_DEVICE;
+    if (ffn_stage_digits) st = enqueue_q4k(d->d_model, d->d_ff, wd, nullptr, nullptr, y, 0, false, ws_hq, nullptr);
+    if (st == HH_ERR_UNSUPPORTED_DEVICE) st = enqueue_gemv(d->type_down, d->d_model, d->d_ff, wd, (const float*)ws_h, y);
+    if (st == HH_OK) ffn_calls += 1;
+    return st;
+}
+
+hh_status hh_engine::enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y) {
+    if (d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K && d->type_down == HH_TYPE_Q4_K) {
+        hh_status fst = enqueue_q4k_ffn(d, pack + d->gate_off, pack + d->up_off, pack + d->down_off, x, y);
+        if (fst == HH_OK) {
+            ffn_stage_valid = false;
+            ffn_calls += 3;
+            return HH_OK;
+        }
+        if (fst != HH_ERR_UNSUPPORTED_DEVICE) return fst;
+    }
+    HH_TRY(enqueue_ffn_begin(d, pack, x));
+    return enqueue_ffn_finish(d, pack, y);
 }
 
 // ---------------------------------------------------------------- bring-up -----------
@@ -373,6 +487,7 @@ hh_status engine_create(int device, hh_engine** out) {
     hh_engine* e = new hh_engine();
     e->device = device;
     auto bail = [&](hh_status st) {
+        if (e->grid_sync) hipFree(e->grid_sync);
         if (e->stream) hipStreamDestroy(e->stream);
         if (e->copy_stream) hipStreamDestroy(e->copy_stream);
         if (e->module) hipModuleUnload(e->module);
@@ -401,6 +516,11 @@ hh_status engine_create(int device, hh_engine** out) {
     }
     if (const char* b = getenv("HAYAI_HIP_BLOCKS_PER_CU")) e->blocks_per_cu_override = atoi(b);
     if (const char* g = getenv("HAYAI_HIP_Q4K_GENERIC")) e->q4k_generic = atoi(g) != 0;
+    if (const char* f = getenv("HAYAI_HIP_FFN_FUSED")) e->ffn_fused = atoi(f) != 0;
+    if (const char* c = getenv("HAYAI_HIP_COOP")) e->coop_launch = atoi(c) != 0;
+    err = hipMalloc(&e->grid_sync, kBarBytes);
+    if (err == hipSuccess) err = hipMemset(e->grid_sync, 0, kBarBytes);
+    if (err != hipSuccess) return bail(hip_fail(err, "hipMalloc(grid_sync)"));
 
     *out = e;
     return HH_OK;
@@ -411,7 +531,7 @@ void engine_destroy(hh_engine* e) {
     hipSetDevice(e->device);
     if (e->stream) hipStreamSynchronize(e->stream);
     if (e->copy_stream) hipStreamSynchronize(e->copy_stream);
-    for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq})
+    for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq, e->grid_sync})
         if (p) hipFree(p);
     if (e->stream) hipStreamDestroy(e->stream);
     if (e->copy_stream) hipStreamDestroy(e->copy_stream);

@@ -101,6 +101,13 @@ struct hh_engine {
     size_t ws_w_cap = 0;
     void* ws_hq = nullptr;  // int8 digits of the FFN intermediate (gate/up -> down)
     size_t ws_hq_cap = 0;
+    void* grid_sync = nullptr;  // fused FFN grid-barrier state (counters, flags, error word)
+    uint32_t ffn_gen = 0;       // generation of the last fused FFN launch
+    hh_ffn_desc ffn_stage{};    // FFN whose gate/up output is pending in ws_h (/ws_hq)
+    bool ffn_stage_valid = false;
+    bool ffn_stage_digits = false;  // ws_hq holds the digits of ws_h
+    bool ffn_fused = false;     // HAYAI_HIP_FFN_FUSED=1: one-launch Q4_K FFN (grid barrier)
+    bool coop_launch = false;   // HAYAI_HIP_COOP=1: cooperative launch API for the fused kernel
     int blocks_per_cu_override = 0;  // HAYAI_HIP_BLOCKS_PER_CU
     bool q4k_generic = false;        // HAYAI_HIP_Q4K_GENERIC=1: skip the int8-digit Q4_K kernels
 
@@ -122,11 +129,21 @@ struct hh_engine {
     hh_status enqueue_gateup(int type_g, int type_u, size_t d_ff, size_t d_model, const uint8_t* wg,
                              const uint8_t* wu, const float* x, float* h, int act);
     hh_status enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y);
+    // The two halves of enqueue_ffn's two-launch path: gate/up(+act) into the engine's FFN
+    // intermediate, then the down projection of that intermediate.
+    hh_status enqueue_ffn_begin(const hh_ffn_desc* d, const uint8_t* pack, const float* x);
+    hh_status enqueue_ffn_finish(const hh_ffn_desc* d, const uint8_t* pack, float* y);
     // Q4_K batch-1 kernels (q4k.hip); returns HH_ERR_UNSUPPORTED_DEVICE when the shape or
     // alignment needs the generic kernels instead (the caller then falls back).  xdigits:
     // x given as int8 digits (then x is unused); hdigits: gate/up also writes h's digits.
     hh_status enqueue_q4k(size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const float* x, float* y,
                           int act, bool gateup, const void* xdigits, void* hdigits);
+    // One-launch Q4_K FFN layer (gate/up, grid barrier, down); HH_ERR_UNSUPPORTED_DEVICE when
+    // the shape has no fused instantiation.
+    hh_status enqueue_q4k_ffn(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
+                              const float* x, float* y);
+    // Reports (and clears) a grid-barrier timeout recorded by a fused kernel.  Syncs.
+    hh_status check_device_error();
 };
 
 #endif

@@ -353,6 +353,18 @@ class HipEngine:
         _check(self.lib.hh_ffn_dev(self.handle, C.byref(desc), pack.handle, pack_off, x.handle, x_off, y.handle,
                                    y_off))
 
+    def ffn_begin_dev(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, x: DeviceBuffer,
+                      x_off: int) -> None:
+        """ffn_begin_gate_up_scratch (stream_infer.rs:3752-3808): gate/up + activation into
+        the engine's FFN intermediate, enqueue only."""
+        _check(self.lib.hh_ffn_begin_dev(self.handle, C.byref(desc), pack.handle, pack_off, x.handle, x_off))
+
+    def ffn_finish_dev(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, y: DeviceBuffer,
+                       y_off: int) -> None:
+        """ffn_finish_scratch (stream_infer.rs:3809-3864): down projection of the pending
+        intermediate, enqueue only."""
+        _check(self.lib.hh_ffn_finish_dev(self.handle, C.byref(desc), pack.handle, pack_off, y.handle, y_off))
+
     def gateup_dev(self, types, d_ff: int, d_model: int, wg: DeviceBuffer, wg_off: int, wu: DeviceBuffer,
                    wu_off: int, x: DeviceBuffer, x_off: int, h: DeviceBuffer, h_off: int, act: int = ACT_SILU) -> None:
         """h = act(W_gate . x) * (W_up . x) (gate/up half of the FFN op), enqueue only."""

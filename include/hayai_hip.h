@@ -202,6 +202,17 @@ hh_status hh_ffn(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t 
 hh_status hh_ffn_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
                      const hh_buf* x, size_t x_off, hh_buf* y, size_t y_off);
 
+/* hh_ffn_dev as the reference's two calls (the same kernels hh_ffn_dev runs in its
+ * two-launch form).  hh_ffn_begin_dev: ffn_begin_gate_up_scratch (stream_infer.rs:3752-3808)
+ * -- gate/up and the activation into the engine's FFN intermediate.  hh_ffn_finish_dev:
+ * ffn_finish_scratch (stream_infer.rs:3809-3864) -- the down projection of the
+ * intermediate left by the last begin of the same FFN shape; HH_ERR_INVALID when none is
+ * pending (a finish consumes it).  Enqueue only. */
+hh_status hh_ffn_begin_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                           const hh_buf* x, size_t x_off);
+hh_status hh_ffn_finish_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off, hh_buf* y,
+                            size_t y_off);
+
 /* The first half of the FFN op: ffn_begin_gate_up_scratch (stream_infer.rs:3752-3806)
  * fused with the activation of ffn_finish_scratch (:3836-3840):
  * h[d_ff] = act(W_gate . x) * (W_up . x), one kernel when gate and up share a format.

@@ -101,3 +101,67 @@ def test_ffn_rejects_bad_pack(engine):
     before = engine.ffn_calls
     engine.ffn(desc, pack, 0, synth.normal(1, d_model))
     assert engine.ffn_calls == before + 3
+
+
+def test_ffn_fused_one_launch_matches_two_launches(engine, monkeypatch):
+    # The one-launch Q4_K FFN (gate/up, grid barrier, down; HAYAI_HIP_FFN_FUSED=1) computes
+    # every row with the same team arithmetic as the two-launch path, so results are equal
+    # bit for bit; repeated launches exercise the barrier's generation flags.
+    types, d_model, d_ff = (12, 12, 12), 4096, 14336
+    print(f"[case] fused ffn {d_model}x{d_ff}", flush=True)
+    monkeypatch.setenv("HAYAI_HIP_FFN_FUSED", "1")
+    fused = hayai_amd.HipEngine(0)
+    try:
+        lay, (wg, wu, wd), pack = make_pack(engine, types, d_model, d_ff, 2)
+        fpack = fused.alloc(lay.total)
+        fpack.write(wg, lay.gate_off)
+        fpack.write(wu, lay.up_off)
+        fpack.write(wd, lay.down_off)
+        desc = engine.ffn_desc(types, d_model, d_ff, lay)
+        fdesc = fused.ffn_desc(types, d_model, d_ff, lay)
+        for k in range(3):
+            x = synth.normal(synth.seed_for(2, k, synth.ACT), d_model)
+            y2 = engine.ffn(desc, pack, 0, x)
+            y1 = fused.ffn(fdesc, fpack, 0, x)
+            np.testing.assert_array_equal(y1, y2)
+        ref = oracle.ffn(types, d_model, d_ff, wg, wu, wd, x)
+        assert rel_err(y1, ref) <= REL_TOL
+        # device chain of 4 launches without a host sync in between
+        xb = fused.upload(x)
+        bufs = [fused.alloc(4 * d_model) for _ in range(2)]
+        src = xb
+        for k in range(4):
+            fused.ffn_dev(fdesc, fpack, 0, src, 0, bufs[k % 2], 0)
+            src = bufs[k % 2]
+        yc = src.read(np.float32, d_model)
+        r = x
+        for k in range(4):
+            r = engine.ffn(desc, pack, 0, r)
+        np.testing.assert_array_equal(yc, r)
+    finally:
+        fused.close()
+
+
+@pytest.mark.parametrize("types,d_model,d_ff", [((12, 12, 12), 4096, 14336), ((2, 2, 2), 576, 1536),
+                                                 ((12, 2, 18), 1024, 2048)])
+def test_ffn_begin_finish_equals_ffn(engine, types, d_model, d_ff):
+    # the reference's two-call seam (ffn_begin_gate_up_scratch / ffn_finish_scratch) runs the
+    # same kernels as the one-call op: identical bits
+    print(f"[case] begin/finish types={types} {d_model}x{d_ff}", flush=True)
+    lay, _, pack = make_pack(engine, types, d_model, d_ff, 13)
+    desc = engine.ffn_desc(types, d_model, d_ff, lay)
+    x = synth.normal(77, d_model)
+    xb = engine.upload(x)
+    y1 = engine.alloc(4 * d_model)
+    y2 = engine.alloc(4 * d_model)
+    engine.ffn_dev(desc, pack, 0, xb, 0, y1, 0)
+    engine.ffn_begin_dev(desc, pack, 0, xb, 0)
+    engine.ffn_finish_dev(desc, pack, 0, y2, 0)
+    np.testing.assert_array_equal(y1.read(np.float32, d_model), y2.read(np.float32, d_model))
+    # a finish consumes the pending intermediate; a second one (or one for another shape) fails
+    with pytest.raises(hayai_amd.HipError):
+        engine.ffn_finish_dev(desc, pack, 0, y2, 0)
+    engine.ffn_begin_dev(desc, pack, 0, xb, 0)
+    other = engine.ffn_desc(types, d_model, d_ff, lay, 1)
+    with pytest.raises(hayai_amd.HipError):
+        engine.ffn_finish_dev(other, pack, 0, y2, 0)
