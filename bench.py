@@ -115,6 +115,85 @@ def cpu_baseline(engine, pack, lay, stride, xs, budget_s: float) -> dict:
     }
 
 
+def bench_batched(eng, pack, lay, stride, desc, args) -> int:
+    """the 8B Q4_K FFN for B tokens per step (all 32 layers
+    resident), gate/up(+SiLU) and down on the matrix cores.  value = algorithmic bytes per
+    step (weights once per layer + B tokens' f32 x in and y out) / step time."""
+    import hayai_amd
+    from hayai_amd import synth
+
+    B = args.batch
+    X = synth.normal(synth.seed_for(3, B, synth.ACT), B * D_MODEL * LAYERS).reshape(LAYERS, B, D_MODEL)
+    xbuf = eng.upload(X)
+    ybuf = eng.alloc(X.nbytes)
+    row = 4 * B * D_MODEL
+
+    def step():
+        for l in range(LAYERS):
+            eng.ffn_batched_dev(desc, pack, l * stride, xbuf, l * row, B, ybuf, l * row)
+
+    for _ in range(args.warmup):
+        step()
+    eng.sync()
+    e0, e1 = eng.event(), eng.event()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    eng.sync()
+    ms = e0.elapsed_ms(e1) / args.steps
+    wbytes = 2 * D_FF * hayai_amd.row_bytes(Q4_K, D_MODEL) + D_MODEL * hayai_amd.row_bytes(Q4_K, D_FF)
+    bytes_step = LAYERS * (wbytes + 2 * 4 * B * D_MODEL)
+    gbs = bytes_step / (ms / 1e3) / 1e9
+    flops = LAYERS * 2.0 * B * 3 * D_MODEL * D_FF
+    tflops = flops / (ms / 1e3) / 1e12
+    log(f"[bench] batched B={B}: {ms * 1e3:.1f} us/step, {gbs:.1f} GB/s, {tflops:.1f} TFLOP/s, "
+        f"{B * 1e3 / ms:.0f} tok/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+
+        oracle.build()
+        cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+        threads = max(1, min(16, cores))
+        oracle.set_threads(threads)
+        rg, rd = hayai_amd.row_bytes(Q4_K, D_MODEL), hayai_amd.row_bytes(Q4_K, D_FF)
+        wg = pack.read(np.uint8, D_FF * rg, lay.gate_off)
+        wu = pack.read(np.uint8, D_FF * rg, lay.up_off)
+        wd = pack.read(np.uint8, D_MODEL * rd, lay.down_off)
+        n, t_end, t0 = 0, time.time() + args.cpu_budget, time.perf_counter()
+        while time.time() < t_end or n < 2:
+            oracle.ffn((Q4_K, Q4_K, Q4_K), D_MODEL, D_FF, wg, wu, wd, X[0][n % B])
+            n += 1
+        t_tok = (time.perf_counter() - t0) / n
+        cpu = {"value": round(1.0 / (t_tok * LAYERS), 3), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"oracle fp32 FFN of layer 0, {n} tokens one at a time in {n * t_tok:.1f}s "
+                         f"({t_tok * 1e3:.1f} ms per token-layer), {threads} OpenMP threads; tok/s for 32 layers"}
+    out = {
+        "metric": "FFN GEMV achieved HBM GB/s (% of peak) + FFN tok/s, 8B-shape Q4_K batched",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 MFMA operands (x as hi+lo pair), f32 accumulate",
+        "data": "synthetic (seeded Q4_K blocks, N(0,1) f32 activations)",
+        "config": {"workload": f"llama3-8b-ffn-q4_k-batch{B}-32layers-resident", "d_model": D_MODEL, "d_ff": D_FF,
+                   "layers": LAYERS, "batch": B, "weights": "Q4_K", "act": "silu"},
+        "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "ffn_tok_s": round(B * 1e3 / ms, 2),
+        "tflops": round(tflops, 2),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    eng.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -124,6 +203,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 256 MiB device copy before timing (reference point for HBM counters)")
+    ap.add_argument("--workload", default="bs1", choices=["bs1", "batched"],
+                    help="bs1: BASELINE.json configs[1] (the headline); batched: configs[2], --batch tokens per step")
+    ap.add_argument("--batch", type=int, default=16, help="tokens per step for --workload batched")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the FFN path would shard "
@@ -153,6 +235,8 @@ def main() -> int:
     eng.sync()
     log(f"[bench] {LAYERS} layers resident: {stride * LAYERS / 2**30:.2f} GiB of Q4_K weights")
     desc = eng.ffn_desc((Q4_K, Q4_K, Q4_K), D_MODEL, D_FF, lay)
+    if args.workload == "batched":
+        return bench_batched(eng, pack, lay, stride, desc, args)
 
     def step():
         for l in range(LAYERS):

@@ -92,6 +92,10 @@ SIGNATURES = {
     "hh_dequant_dev": (ST, [P, I, P, SZ, SZ, P, SZ]),
     "hh_ffn": (ST, [P, C.POINTER(FfnDesc), P, SZ, P, P]),
     "hh_ffn_dev": (ST, [P, C.POINTER(FfnDesc), P, SZ, P, SZ, P, SZ]),
+    "hh_gemv_batched": (ST, [P, I, SZ, SZ, P, SZ, P, P, SZ]),
+    "hh_gemv_batched_dev": (ST, [P, I, SZ, SZ, P, SZ, P, SZ, SZ, P, SZ]),
+    "hh_ffn_batched_dev": (ST, [P, C.POINTER(FfnDesc), P, SZ, P, SZ, SZ, P, SZ]),
+    "hh_ffn_batched": (ST, [P, C.POINTER(FfnDesc), P, SZ, P, P, SZ]),
     "hh_ffn_begin_dev": (ST, [P, C.POINTER(FfnDesc), P, SZ, P, SZ]),
     "hh_ffn_finish_dev": (ST, [P, C.POINTER(FfnDesc), P, SZ, P, SZ]),
     "hh_gateup_dev": (ST, [P, I, I, SZ, SZ, P, SZ, P, SZ, P, SZ, P, SZ, I]),

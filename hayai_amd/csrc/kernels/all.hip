@@ -1,5 +1,6 @@
 // Single translation unit for the gfx950 code object (hayai_kernels.hsaco).
 #include "gemv.hip"
 #include "q4k.hip"
+#include "q4k_mm.hip"
 #include "dequant.hip"
 #include "synth.hip"

@@ -278,6 +278,59 @@ hh_status hh_gemv(hh_engine* e, int t, size_t m, size_t n, const uint8_t* weight
     return gemv_host_io(e, t, m, n, (const uint8_t*)e->ws_w, x, y);
 }
 
+static hh_status batch_bytes(size_t batch, size_t len, size_t* out) {
+    if (len != 0 && batch > SIZE_MAX / (len * sizeof(float))) return fail(HH_ERR_INVALID, "batch size overflow");
+    *out = batch * len * sizeof(float);
+    return HH_OK;
+}
+
+hh_status hh_gemv_batched(hh_engine* e, int t, size_t m, size_t n, const uint8_t* weights, size_t weights_len,
+                          const float* inputs, float* outputs, size_t batch) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_shape(t, m, n));
+    HH_TRY(validate_weights(t, m, n, weights_len));
+    size_t xb, yb, rb;
+    HH_TRY(batch_bytes(batch, n, &xb));
+    HH_TRY(batch_bytes(batch, m, &yb));
+    HH_TRY(row_bytes(t, n, &rb));
+    if (batch == 0) return HH_OK;
+    HH_NOT_NULL(weights, "weights");
+    HH_NOT_NULL(inputs, "inputs");
+    HH_NOT_NULL(outputs, "outputs");
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    HH_TRY(e->grow(&e->ws_w, &e->ws_w_cap, m * rb));
+    HH_TRY(e->grow(&e->ws_x, &e->ws_x_cap, xb));
+    HH_TRY(e->grow(&e->ws_y, &e->ws_y_cap, yb));
+    HH_TRY_HIP(hipMemcpyAsync(e->ws_w, weights, m * rb, hipMemcpyHostToDevice, e->stream), "hipMemcpyAsync(w)");
+    HH_TRY_HIP(hipMemcpyAsync(e->ws_x, inputs, xb, hipMemcpyHostToDevice, e->stream), "hipMemcpyAsync(x)");
+    HH_TRY(e->enqueue_gemv_batched(t, m, n, (const uint8_t*)e->ws_w, (const float*)e->ws_x, batch, (float*)e->ws_y));
+    HH_TRY_HIP(hipMemcpyAsync(outputs, e->ws_y, yb, hipMemcpyDeviceToHost, e->stream), "hipMemcpyAsync(y)");
+    return e->check_device_error();
+}
+
+hh_status hh_gemv_batched_dev(hh_engine* e, int t, size_t m, size_t n, const hh_buf* w, size_t w_off, const hh_buf* x,
+                              size_t x_off, size_t batch, hh_buf* y, size_t y_off) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_shape(t, m, n));
+    size_t xb, yb, rb;
+    HH_TRY(batch_bytes(batch, n, &xb));
+    HH_TRY(batch_bytes(batch, m, &yb));
+    HH_TRY(row_bytes(t, n, &rb));
+    HH_TRY(check_engine(e, w, "weights"));
+    HH_TRY(check_engine(e, x, "x"));
+    HH_TRY(check_engine(e, y, "y"));
+    HH_TRY(check_range(w, w_off, m * rb, "weights"));
+    HH_TRY(check_range(x, x_off, xb, "x"));
+    HH_TRY(check_range(y, y_off, yb, "y"));
+    if (((x_off | y_off) & 3u) != 0) return fail(HH_ERR_INVALID, "gemv_batched: x/y offsets must be 4-byte aligned");
+    if (batch == 0) return HH_OK;
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    return e->enqueue_gemv_batched(t, m, n, (const uint8_t*)w->ptr + w_off, (const float*)((const char*)x->ptr + x_off),
+                                   batch, (float*)((char*)y->ptr + y_off));
+}
+
 hh_status hh_gemv_begin(hh_engine* e, int t, size_t m, size_t n, const hh_buf* w, size_t w_off, const float* x,
                         hh_pending** out) {
     HH_NOT_NULL(e, "engine");
@@ -393,6 +446,44 @@ hh_status hh_ffn_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, siz
     std::lock_guard<std::mutex> lk(e->ws_mutex);
     return e->enqueue_ffn(d, (const uint8_t*)pack->ptr + pack_off, (const float*)((const char*)x->ptr + x_off),
                           (float*)((char*)y->ptr + y_off));
+}
+
+hh_status hh_ffn_batched_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off, const hh_buf* x,
+                             size_t x_off, size_t batch, hh_buf* y, size_t y_off) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_ffn(e, d, pack, pack_off));
+    size_t xb;
+    HH_TRY(batch_bytes(batch, d->d_model, &xb));
+    HH_TRY(check_engine(e, x, "x"));
+    HH_TRY(check_engine(e, y, "y"));
+    HH_TRY(check_range(x, x_off, xb, "x"));
+    HH_TRY(check_range(y, y_off, xb, "y"));
+    if (((x_off | y_off) & 3u) != 0) return fail(HH_ERR_INVALID, "ffn_batched: x/y offsets must be 4-byte aligned");
+    if (batch == 0) return HH_OK;
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    return e->enqueue_ffn_batched(d, (const uint8_t*)pack->ptr + pack_off, (const float*)((const char*)x->ptr + x_off),
+                                  batch, (float*)((char*)y->ptr + y_off));
+}
+
+hh_status hh_ffn_batched(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off, const float* x,
+                         float* y, size_t batch) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_ffn(e, d, pack, pack_off));
+    size_t xb;
+    HH_TRY(batch_bytes(batch, d->d_model, &xb));
+    if (batch == 0) return HH_OK;
+    HH_NOT_NULL(x, "x");
+    HH_NOT_NULL(y, "y");
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    HH_TRY(e->grow(&e->ws_x, &e->ws_x_cap, xb));
+    HH_TRY(e->grow(&e->ws_y, &e->ws_y_cap, xb));
+    HH_TRY_HIP(hipMemcpyAsync(e->ws_x, x, xb, hipMemcpyHostToDevice, e->stream), "hipMemcpyAsync(x)");
+    HH_TRY(e->enqueue_ffn_batched(d, (const uint8_t*)pack->ptr + pack_off, (const float*)e->ws_x, batch,
+                                  (float*)e->ws_y));
+    HH_TRY_HIP(hipMemcpyAsync(y, e->ws_y, xb, hipMemcpyDeviceToHost, e->stream), "hipMemcpyAsync(y)");
+    return e->check_device_error();
 }
 
 hh_status hh_ffn_begin_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off, const hh_buf* x,

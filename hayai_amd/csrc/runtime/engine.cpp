@@ -457,6 +457,131 @@ hh_status hh_engine::enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, cons
     return enqueue_ffn_finish(d, pack, y);
 }
 
+// ---------------------------------------------------------------- batched (MFMA) ------
+
+// Kernel argument blocks of q4k_mm.hip (same layout).
+struct hh_mm_args {
+    const uint8_t* w0;
+    const uint8_t* w1;
+    const void* xop;
+    float* y;
+    void* hop;
+    float* part;
+    unsigned* cnt;
+    uint32_t m, n, b, ksg;
+    uint64_t row_bytes;
+    int32_t act;
+    uint32_t pad;
+};
+struct hh_mm_prep_args {
+    const float* x;
+    void* xop;
+    uint32_t b, n, T, pad;
+};
+constexpr size_t kMmMaxTokens = 64;  // tokens per MFMA launch (4 tiles of 16)
+constexpr int kMmBlock = 256;        // 4 waves, one row pair each
+constexpr size_t kMmStage = 17408;   // bytes of one (16-token tile, superblock) operand stage
+
+static size_t mm_tiles(size_t b) { return b <= 16 ? 1 : (b <= 32 ? 2 : 4); }
+static size_t mm_stage_bytes(size_t n, size_t tt) { return tt * (n / 256) * kMmStage; }
+
+hh_status hh_engine::enqueue_mm_prep(const float* x, size_t b, size_t n, size_t tt) {
+    HH_TRY(grow(&ws_xop, &ws_xop_cap, mm_stage_bytes(n, tt)));
+    hipFunction_t fn;
+    HH_TRY(kernel("hh_mm_prep", &fn));
+    const size_t T = 16 * tt;
+    hh_mm_prep_args a{x, ws_xop, (uint32_t)b, (uint32_t)n, (uint32_t)T, 0};
+    const size_t threads = T * (n / 16);
+    return launch(fn, (uint32_t)((threads + 255) / 256), 256, a);
+}
+
+hh_status hh_engine::enqueue_q4k_mm(size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* xop,
+                                    size_t b, size_t tt, float* y, bool ffn, int act) {
+    const size_t nsb = n / 256;
+    const size_t T = 16 * tt;
+    const size_t pairs = ffn ? (m + 15) / 16 : (m + 31) / 32;
+    const size_t groups = (pairs + 3) / 4;
+    // Split the superblocks over workgroups until every CU has one (each keeps >= 2).
+    const size_t cus = (size_t)props.multiProcessorCount;
+    const size_t ksg = std::max<size_t>(1, std::min((cus + groups - 1) / groups, std::max<size_t>(1, nsb / 2)));
+    if (ksg > 1) {
+        HH_TRY(grow(&ws_part, &ws_part_cap, groups * ksg * 2 * T * 64 * sizeof(float)));
+        if (ws_cnt_cap < groups * sizeof(unsigned)) {
+            HH_TRY(grow(&ws_cnt, &ws_cnt_cap, groups * sizeof(unsigned)));
+            HH_TRY_HIP(hipMemsetAsync(ws_cnt, 0, ws_cnt_cap, stream), "hipMemsetAsync(counters)");
+        }
+    }
+    if (ffn) HH_TRY(grow(&ws_hop, &ws_hop_cap, mm_stage_bytes(m, tt)));
+    const std::string name = std::string(ffn ? "hh_q4k_mm_gateup_t" : "hh_q4k_mm_t") + std::to_string(tt);
+    hipFunction_t fn;
+    HH_TRY(kernel(name, &fn));
+    hh_mm_args a{};
+    a.w0 = w0;
+    a.w1 = w1;
+    a.xop = xop;
+    a.y = y;
+    a.hop = ws_hop;
+    a.part = (float*)ws_part;
+    a.cnt = (unsigned*)ws_cnt;
+    a.m = (uint32_t)m;
+    a.n = (uint32_t)n;
+    a.b = (uint32_t)b;
+    a.ksg = (uint32_t)ksg;
+    a.row_bytes = (uint64_t)(nsb * 144);
+    a.act = act;
+    return launch(fn, (uint32_t)(groups * ksg), kMmBlock, a);
+}
+
+hh_status hh_engine::enqueue_gemv_batched(int type, size_t m, size_t n, const uint8_t* w, const float* x, size_t batch,
+                                          float* y) {
+    if (batch == 0) return HH_OK;
+    const bool mfma = type == HH_TYPE_Q4_K && batch >= 2 && !q4k_generic && ((uintptr_t)w & 15u) == 0 &&
+                      ((uintptr_t)x & 15u) == 0 && m <= 0xFFFFFFFFu && n <= 0xFFFFFFFFu;
+    if (!mfma) {
+        for (size_t b = 0; b < batch; b++) HH_TRY(enqueue_gemv(type, m, n, w, x + b * n, y + b * m));
+        return HH_OK;
+    }
+    for (size_t b0 = 0; b0 < batch; b0 += kMmMaxTokens) {
+        const size_t nb = std::min(kMmMaxTokens, batch - b0);
+        if (nb == 1) {
+            HH_TRY(enqueue_gemv(type, m, n, w, x + b0 * n, y + b0 * m));
+            continue;
+        }
+        const size_t tt = mm_tiles(nb);
+        HH_TRY(enqueue_mm_prep(x + b0 * n, nb, n, tt));
+        HH_TRY(enqueue_q4k_mm(m, n, w, nullptr, ws_xop, nb, tt, y + b0 * m, false, 0));
+    }
+    return HH_OK;
+}
+
+hh_status hh_engine::enqueue_ffn_batched(const hh_ffn_desc* d, const uint8_t* pack, const float* x, size_t batch,
+                                         float* y) {
+    if (batch == 0) return HH_OK;
+    const size_t dm = d->d_model, df = d->d_ff;
+    const uint8_t* wg = pack + d->gate_off;
+    const uint8_t* wu = pack + d->up_off;
+    const uint8_t* wd = pack + d->down_off;
+    const bool mfma = d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K && d->type_down == HH_TYPE_Q4_K &&
+                      batch >= 2 && !q4k_generic && (((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd | (uintptr_t)x) & 15u) == 0;
+    if (!mfma) {
+        for (size_t b = 0; b < batch; b++) HH_TRY(enqueue_ffn(d, pack, x + b * dm, y + b * dm));
+        return HH_OK;
+    }
+    for (size_t b0 = 0; b0 < batch; b0 += kMmMaxTokens) {
+        const size_t nb = std::min(kMmMaxTokens, batch - b0);
+        if (nb == 1) {
+            HH_TRY(enqueue_ffn(d, pack, x + b0 * dm, y + b0 * dm));
+            continue;
+        }
+        const size_t tt = mm_tiles(nb);
+        HH_TRY(enqueue_mm_prep(x + b0 * dm, nb, dm, tt));
+        HH_TRY(enqueue_q4k_mm(df, dm, wg, wu, ws_xop, nb, tt, nullptr, true, d->act));
+        HH_TRY(enqueue_q4k_mm(dm, df, wd, nullptr, ws_hop, nb, tt, y + b0 * dm, false, 0));
+        ffn_calls += 3 * nb;
+    }
+    return HH_OK;
+}
+
 // ---------------------------------------------------------------- bring-up -----------
 
 static std::vector<std::string> required_kernels() {
@@ -475,6 +600,9 @@ static std::vector<std::string> required_kernels() {
     for (int w : {1, 2, 4, 8})
         for (const char* kind : {"hh_q4k_gemv_w", "hh_q4k_gemvq_w", "hh_q4k_gateup_w"})
             k.push_back(std::string(kind) + std::to_string(w));
+    for (int tt : {1, 2, 4})
+        for (const char* kind : {"hh_q4k_mm_t", "hh_q4k_mm_gateup_t"}) k.push_back(std::string(kind) + std::to_string(tt));
+    k.push_back("hh_mm_prep");
     return k;
 }
 
@@ -531,7 +659,8 @@ void engine_destroy(hh_engine* e) {
     hipSetDevice(e->device);
     if (e->stream) hipStreamSynchronize(e->stream);
     if (e->copy_stream) hipStreamSynchronize(e->copy_stream);
-    for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq, e->grid_sync})
+    for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq, e->ws_xop, e->ws_hop, e->ws_part,
+                    e->ws_cnt, e->grid_sync})
         if (p) hipFree(p);
     if (e->stream) hipStreamDestroy(e->stream);
     if (e->copy_stream) hipStreamDestroy(e->copy_stream);

@@ -101,6 +101,17 @@ struct hh_engine {
     size_t ws_w_cap = 0;
     void* ws_hq = nullptr;  // int8 digits of the FFN intermediate (gate/up -> down)
     size_t ws_hq_cap = 0;
+    // Batched (MFMA) path: tokens as MFMA operand stages (f16 hi/lo pairs + 16-element
+    // sums), the FFN intermediate in the same form, split-K partials and their per-row-group
+    // arrival counters.
+    void* ws_xop = nullptr;
+    size_t ws_xop_cap = 0;
+    void* ws_hop = nullptr;
+    size_t ws_hop_cap = 0;
+    void* ws_part = nullptr;
+    size_t ws_part_cap = 0;
+    void* ws_cnt = nullptr;  // zeroed when allocated; every launch leaves it zero
+    size_t ws_cnt_cap = 0;
     void* grid_sync = nullptr;  // fused FFN grid-barrier state (counters, flags, error word)
     uint32_t ffn_gen = 0;       // generation of the last fused FFN launch
     hh_ffn_desc ffn_stage{};    // FFN whose gate/up output is pending in ws_h (/ws_hq)
@@ -142,6 +153,20 @@ struct hh_engine {
     // the shape has no fused instantiation.
     hh_status enqueue_q4k_ffn(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                               const float* x, float* y);
+    // Batched GEMV Y[b][m] = W . X[b] (x, y device pointers, row-major by token).  Q4_K with
+    // 2 <= batch uses the MFMA kernels in chunks of up to 64 tokens; other formats (and
+    // batch 1) run one GEMV per token, as the reference's orchestrator does
+    // (orchestrator.rs:258-260).
+    hh_status enqueue_gemv_batched(int type, size_t m, size_t n, const uint8_t* w, const float* x, size_t batch,
+                                   float* y);
+    // Batched FFN: per token y[b] = FFN(x[b]); all-Q4_K FFNs run gate/up and down on MFMA.
+    hh_status enqueue_ffn_batched(const hh_ffn_desc* d, const uint8_t* pack, const float* x, size_t batch, float* y);
+    // Tokens [b][n] f32 -> operand stages in ws_xop for 16 * tt token slots.
+    hh_status enqueue_mm_prep(const float* x, size_t b, size_t n, size_t tt);
+    // One MFMA launch: GEMM mode (ffn == false; w0, y) or gate/up mode (w0 = gate, w1 = up,
+    // act, writing the stages of h into ws_hop).  xop holds 16 * tt tokens of n columns.
+    hh_status enqueue_q4k_mm(size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* xop, size_t b,
+                             size_t tt, float* y, bool ffn, int act);
     // Reports (and clears) a grid-barrier timeout recorded by a fused kernel.  Syncs.
     hh_status check_device_error();
 };

@@ -300,6 +300,26 @@ class HipEngine:
     def ggml_gemv_iq3_xxs(self, m, n, weights, inp):
         return self.ggml_gemv_dispatch(IQ3_XXS, m, n, weights, inp)
 
+    def ggml_gemv_batched(self, ggml_type: int, m: int, n: int, weights: np.ndarray, inputs: np.ndarray,
+                          batch: int) -> np.ndarray:
+        """ggml_gemv_batched_q4_k (compute.rs:179-257), any type: inputs = batch*n floats,
+        returns batch*m floats (token-major)."""
+        w = np.ascontiguousarray(weights, dtype=np.uint8)
+        x = np.ascontiguousarray(inputs, dtype=np.float32).reshape(-1)
+        if x.size != batch * n:
+            raise HipError(2, f"inputs have {x.size} floats, expected batch*n={batch * n}")
+        y = np.empty(batch * m, np.float32)
+        _check(self.lib.hh_gemv_batched(self.handle, ggml_type, m, n, _ptr(w), w.nbytes, _ptr(x), _ptr(y), batch))
+        return y
+
+    def ggml_gemv_batched_q4_k(self, m: int, n: int, weights: np.ndarray, inputs: np.ndarray, batch: int) -> np.ndarray:
+        return self.ggml_gemv_batched(Q4_K, m, n, weights, inputs, batch)
+
+    def gemv_batched_dev(self, ggml_type, m, n, w: DeviceBuffer, w_off, x: DeviceBuffer, x_off, batch,
+                         y: DeviceBuffer, y_off) -> None:
+        _check(self.lib.hh_gemv_batched_dev(self.handle, ggml_type, m, n, w.handle, w_off, x.handle, x_off, batch,
+                                            y.handle, y_off))
+
     def ggml_gemv_dispatch_bound(self, ggml_type: int, m: int, n: int, weights: DeviceBuffer, weight_off: int,
                                  inp: np.ndarray) -> np.ndarray:
         """compute.rs:388-461: resident weights at a byte offset."""
@@ -347,6 +367,20 @@ class HipEngine:
         y = np.empty(desc.d_model, np.float32)
         _check(self.lib.hh_ffn(self.handle, C.byref(desc), pack.handle, pack_off, _ptr(x), _ptr(y)))
         return y
+
+    def ffn_batched(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, x: np.ndarray) -> np.ndarray:
+        """The FFN op for a batch of tokens (rows of x), blocking; prefill_wave.rs:577-584."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim != 2 or x.shape[1] != desc.d_model:
+            raise HipError(2, f"x must be (batch, d_model={desc.d_model}), got {x.shape}")
+        y = np.empty_like(x)
+        _check(self.lib.hh_ffn_batched(self.handle, C.byref(desc), pack.handle, pack_off, _ptr(x), _ptr(y), x.shape[0]))
+        return y
+
+    def ffn_batched_dev(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, x: DeviceBuffer, x_off: int,
+                        batch: int, y: DeviceBuffer, y_off: int) -> None:
+        _check(self.lib.hh_ffn_batched_dev(self.handle, C.byref(desc), pack.handle, pack_off, x.handle, x_off, batch,
+                                           y.handle, y_off))
 
     def ffn_dev(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, x: DeviceBuffer, x_off: int,
                 y: DeviceBuffer, y_off: int) -> None:

@@ -164,6 +164,18 @@ hh_status hh_pending_wait(hh_pending* p, float* y, size_t m);
 /* Drop for PendingGemv (async_gemv.rs:48-57): waits for the kernel, then frees. */
 void hh_pending_destroy(hh_pending* p);
 
+/* ggml_gemv_batched_q4_k (crates/hayai-opencl/src/compute.rs:179-257) generalised to every
+ * type, as execute_quant_gemv_batched does (crates/hayai-core/src/orchestrator.rs:240-269):
+ * outputs[b*m + r] = W[r] . inputs[b*n .. b*n+n) for b < batch.  Host weights and
+ * activations, blocking.  Q4_K with batch >= 2 runs on the matrix cores (f16 operands, f32
+ * accumulation) in chunks of up to 64 tokens; other types loop over tokens. */
+hh_status hh_gemv_batched(hh_engine* e, int ggml_type, size_t m, size_t n, const uint8_t* weights,
+                          size_t weights_len, const float* inputs, float* outputs, size_t batch);
+/* Same with device buffers (weights at w_off; x: batch*n floats, y: batch*m floats);
+ * enqueue only. */
+hh_status hh_gemv_batched_dev(hh_engine* e, int ggml_type, size_t m, size_t n, const hh_buf* w, size_t w_off,
+                              const hh_buf* x, size_t x_off, size_t batch, hh_buf* y, size_t y_off);
+
 /* Device-resident GEMV: x and y are device buffers (byte offsets), enqueue only. */
 hh_status hh_gemv_dev(hh_engine* e, int ggml_type, size_t m, size_t n, const hh_buf* w,
                       size_t w_off, const hh_buf* x, size_t x_off, hh_buf* y, size_t y_off);
@@ -201,6 +213,16 @@ hh_status hh_ffn(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t 
  * The d_ff intermediate lives in an engine workspace. */
 hh_status hh_ffn_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
                      const hh_buf* x, size_t x_off, hh_buf* y, size_t y_off);
+
+/* The FFN op for `batch` tokens (x, y: batch rows of d_model floats): the batched-prefill
+ * form of the op (prefill_wave.rs:577-584 drives execute_quant_gemv_batched for FFN
+ * matrices).  All-Q4_K FFNs run gate/up(+act) and down on the matrix cores; other formats
+ * run the single-token op per token.  _dev: device buffers, enqueue only; without: host
+ * x / y, blocking. */
+hh_status hh_ffn_batched_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                             const hh_buf* x, size_t x_off, size_t batch, hh_buf* y, size_t y_off);
+hh_status hh_ffn_batched(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                         const float* x, float* y, size_t batch);
 
 /* hh_ffn_dev as the reference's two calls (the same kernels hh_ffn_dev runs in its
  * two-launch form).  hh_ffn_begin_dev: ffn_begin_gate_up_scratch (stream_infer.rs:3752-3808)

@@ -1,0 +1,134 @@
+"""Batched GEMV / FFN on the matrix cores against the oracle.
+
+ggml_gemv_batched_q4_k (crates/hayai-opencl/src/compute.rs:179-257) computes B GEMVs that
+share W; execute_quant_gemv_batched (crates/hayai-core/src/orchestrator.rs:240-269) runs
+other types token by token.  The MFMA path rounds x (and the FFN intermediate) to f16, so
+parity is held to the FFN tolerance (max |y - ref| / max |ref| <= 1e-3 per token) against
+the oracle's f32 restatement fed the original f32 inputs.
+"""
+import numpy as np
+import pytest
+
+import hayai_amd
+import oracle
+from hayai_amd import synth
+
+pytestmark = pytest.mark.gpu
+REL_TOL = 1e-3
+Q4_0, Q4_K = 2, 12
+
+
+def rel_err(y, ref):
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(y - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def per_token_err(Y, R):
+    return max(rel_err(Y[b], R[b]) for b in range(Y.shape[0]))
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _threads():
+    oracle.set_threads(min(16, oracle.max_threads()))
+
+
+def test_reference_batched_fixture(engine):
+    # compute.rs:1648-1670: m=32, n=256, batch=3, bytes (i*131+17)&0x1F, inputs i*0.003-0.2
+    m, n, batch = 32, 256, 3
+    w = ((np.arange(m * 144) * 131 + 17) & 0x1F).astype(np.uint8)
+    x = (np.arange(batch * n, dtype=np.float32) * np.float32(0.003) - np.float32(0.2)).astype(np.float32)
+    y = engine.ggml_gemv_batched_q4_k(m, n, w, x, batch)
+    ref = oracle.gemv_batched(Q4_K, m, n, w, x.reshape(batch, n)).reshape(-1)
+    assert np.max(np.abs(y - ref)) < 1e-3
+    assert per_token_err(y.reshape(batch, m), ref.reshape(batch, m)) <= REL_TOL
+
+
+@pytest.mark.parametrize("m,n,batch", [
+    (14336, 4096, 2), (14336, 4096, 4), (14336, 4096, 16), (14336, 4096, 17), (14336, 4096, 64),
+    (4096, 14336, 16), (4096, 14336, 64),   # down shape: superblocks split over workgroups
+    (4096, 14336, 33), (768, 2048, 8), (100, 512, 5), (48, 256, 70),  # ragged rows, > 64 tokens
+])
+def test_q4_k_batched_matches_oracle(engine, m, n, batch):
+    print(f"[case] batched q4_k m={m} n={n} batch={batch}", flush=True)
+    w = synth.matrix(Q4_K, m, n, synth.seed_for(3, batch, m))
+    X = synth.normal(synth.seed_for(3, batch, n), batch * n).reshape(batch, n)
+    Y = engine.ggml_gemv_batched_q4_k(m, n, w, X, batch).reshape(batch, m)
+    R = oracle.gemv_batched(Q4_K, m, n, w, X)
+    err = per_token_err(Y, R)
+    print(f"  per-token max rel err {err:.3e}", flush=True)
+    assert np.isfinite(Y).all()
+    assert err <= REL_TOL
+
+
+def test_batched_is_deterministic_and_batch1_is_gemv(engine):
+    m, n, batch = 4096, 14336, 16
+    w = synth.matrix(Q4_K, m, n, 91)
+    X = synth.normal(92, batch * n).reshape(batch, n)
+    a = engine.ggml_gemv_batched_q4_k(m, n, w, X, batch)
+    b = engine.ggml_gemv_batched_q4_k(m, n, w, X, batch)
+    np.testing.assert_array_equal(a, b)
+    y1 = engine.ggml_gemv_batched_q4_k(m, n, w, X[:1], 1)
+    np.testing.assert_array_equal(y1, engine.ggml_gemv_q4_k(m, n, w, X[0]))
+    assert engine.ggml_gemv_batched_q4_k(m, n, w, X[:0], 0).size == 0
+
+
+def test_other_types_run_per_token(engine):
+    m, n, batch = 1536, 576, 3
+    w = synth.matrix(Q4_0, m, n, 5)
+    X = synth.normal(6, batch * n).reshape(batch, n)
+    Y = engine.ggml_gemv_batched(Q4_0, m, n, w, X, batch).reshape(batch, m)
+    for b in range(batch):
+        np.testing.assert_array_equal(Y[b], engine.ggml_gemv_q4_0(m, n, w, X[b]))
+
+
+def test_batched_dev_offsets(engine):
+    m, n, batch = 2048, 768, 8
+    rb = hayai_amd.row_bytes(Q4_K, n)
+    w = synth.matrix(Q4_K, m, n, 31)
+    X = synth.normal(32, batch * n).reshape(batch, n)
+    wbuf = engine.alloc(256 + m * rb)
+    wbuf.write(w, 256)
+    xbuf = engine.alloc(64 + X.nbytes)
+    xbuf.write(X, 64)
+    ybuf = engine.alloc(128 + 4 * batch * m)
+    engine.gemv_batched_dev(Q4_K, m, n, wbuf, 256, xbuf, 64, batch, ybuf, 128)
+    Y = ybuf.read(np.float32, batch * m, 128).reshape(batch, m)
+    assert per_token_err(Y, oracle.gemv_batched(Q4_K, m, n, w, X)) <= REL_TOL
+    with pytest.raises(hayai_amd.HipError):
+        engine.gemv_batched_dev(Q4_K, m, n, wbuf, 256, xbuf, 64, batch + 1, ybuf, 128)  # x too short
+
+
+def make_pack(engine, types, d_model, d_ff, cfg):
+    tg, tu, td = types
+    gate = hayai_amd.QuantMatrix("ffn_gate", d_model, d_ff, tg)
+    up = hayai_amd.QuantMatrix("ffn_up", d_model, d_ff, tu)
+    down = hayai_amd.QuantMatrix("ffn_down", d_ff, d_model, td)
+    lay = hayai_amd.LayerPackLayout.ffn_only(gate, up, down)
+    wg = synth.matrix(tg, d_ff, d_model, synth.seed_for(cfg, 0, synth.GATE))
+    wu = synth.matrix(tu, d_ff, d_model, synth.seed_for(cfg, 0, synth.UP))
+    wd = synth.matrix(td, d_model, d_ff, synth.seed_for(cfg, 0, synth.DOWN))
+    pack = engine.alloc(lay.total)
+    pack.write(wg, lay.gate_off)
+    pack.write(wu, lay.up_off)
+    pack.write(wd, lay.down_off)
+    return lay, (wg, wu, wd), pack
+
+
+@pytest.mark.parametrize("types,d_model,d_ff,batch,act", [
+    ((12, 12, 12), 4096, 14336, 4, 0), ((12, 12, 12), 4096, 14336, 16, 0), ((12, 12, 12), 4096, 14336, 64, 0),
+    ((12, 12, 12), 2048, 768, 32, 0), ((12, 12, 12), 1024, 2048, 9, 1), ((2, 2, 2), 576, 1536, 3, 0),
+])
+def test_ffn_batched_matches_oracle(engine, types, d_model, d_ff, batch, act):
+    print(f"[case] ffn batched types={types} {d_model}x{d_ff} batch={batch} act={act}", flush=True)
+    lay, (wg, wu, wd), pack = make_pack(engine, types, d_model, d_ff, 30 + batch)
+    desc = engine.ffn_desc(types, d_model, d_ff, lay, act)
+    X = synth.normal(synth.seed_for(3, batch, synth.ACT), batch * d_model).reshape(batch, d_model)
+    Y = engine.ffn_batched(desc, pack, 0, X)
+    R = np.stack([oracle.ffn(types, d_model, d_ff, wg, wu, wd, X[b], act=act) for b in range(batch)])
+    err = per_token_err(Y, R)
+    print(f"  per-token max rel err {err:.3e}", flush=True)
+    assert err <= REL_TOL
+    if types == (2, 2, 2):
+        for b in range(batch):  # non-Q4_K formats: the single-token op per token
+            np.testing.assert_array_equal(Y[b], engine.ffn(desc, pack, 0, X[b]))
