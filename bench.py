@@ -194,6 +194,88 @@ def bench_batched(eng, pack, lay, stride, desc, args) -> int:
     return 0
 
 
+def bench_moe(eng, args) -> int:
+    """Qwen3-30B-A3B-shaped MoE layer (128 experts, top-8 softmax
+    routing with renormalisation, d_model 2048, expert d_ff 768, Q4_K), T tokens per step.
+    4 MoE layers are resident (4 x 340 MB, beyond the 256 MB last-level cache) and each step
+    cycles through 16 router-logit sets, so the experts a step reads are not cache-resident.
+    value = algorithmic bytes per step / step time, where the bytes count every DISTINCT
+    expert a layer's tokens select once (gate + up + down = 2,654,208 B) plus f32 x in, y
+    out and the logits."""
+    import hayai_amd
+    from hayai_amd import synth
+
+    T = args.batch
+    E, K, DM, DF, L, SETS = 128, 8, 2048, 768, 4, 16
+    rin, rff = hayai_amd.row_bytes(Q4_K, DM), hayai_amd.row_bytes(Q4_K, DF)
+    offs = (0, DF * rin, 2 * DF * rin)
+    stride = 2 * DF * rin + DM * rff
+    experts = eng.alloc(L * E * stride)
+    lo, hi = synth.SCALE_RANGE[Q4_K]
+    for l in range(L):
+        for e in range(E):
+            base = (l * E + e) * stride
+            for mat, off, rows, cols in ((synth.GATE, offs[0], DF, DM), (synth.UP, offs[1], DF, DM),
+                                         (synth.DOWN, offs[2], DM, DF)):
+                eng.synth_weights_dev(Q4_K, experts, base + off, rows * cols // 256,
+                                      synth.seed_for(4, l * E + e, mat), lo, hi)
+    desc = eng.moe_desc(DM, DF, E, K, stride, offs, norm_topk_prob=True)
+    rng = np.random.default_rng(4)
+    logits = rng.standard_normal((SETS, L, T, E)).astype(np.float32)
+    x = synth.normal(synth.seed_for(4, T, synth.ACT), L * T * DM).reshape(L, T, DM)
+    lbuf, xbuf = eng.upload(logits), eng.upload(x)
+    ybuf = eng.alloc(4 * L * T * DM)
+    # distinct experts per (set, layer) from the routing itself
+    ids, _ = eng.route_experts(desc, logits.reshape(-1, E))
+    ids = ids.reshape(SETS, L, T, K)
+    distinct = [[len(set(ids[s, l].reshape(-1).tolist()) - {-1}) for l in range(L)] for s in range(SETS)]
+    eng.sync()
+    log(f"[bench] moe T={T}: mean distinct experts per layer {np.mean(distinct):.1f}")
+    lstride, xstride = 4 * T * E, 4 * T * DM
+
+    def step(s):
+        for l in range(L):
+            eng.moe_dev(desc, experts, l * E * stride, lbuf, ((s % SETS) * L + l) * lstride, None, 0, xbuf,
+                        l * xstride, T, ybuf, l * xstride)
+
+    for i in range(args.warmup):
+        step(i)
+    eng.sync()
+    e0, e1 = eng.event(), eng.event()
+    e0.record()
+    for i in range(args.steps):
+        step(i)
+    e1.record()
+    eng.sync()
+    ms = e0.elapsed_ms(e1) / args.steps
+    bytes_step = np.mean([sum(distinct[i % SETS]) for i in range(args.steps)]) * stride + L * T * (2 * 4 * DM + 4 * E)
+    gbs = bytes_step / (ms / 1e3) / 1e9
+    log(f"[bench] moe T={T}: {ms * 1e3:.1f} us/step ({ms * 1e3 / L:.1f} us/layer), {gbs:.1f} GB/s")
+    out = {
+        "metric": "FFN GEMV achieved HBM GB/s (% of peak), Qwen3-30B-A3B-shaped MoE layer",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Q4_K experts, N(0,1) router logits and activations)",
+        "config": {"workload": f"qwen3-30b-a3b-moe-q4_k-T{T}", "experts": E, "top_k": K, "d_model": DM,
+                   "expert_d_ff": DF, "layers_resident": L, "tokens": T},
+        "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "us_per_layer": round(ms * 1e3 / L, 3),
+        "mean_distinct_experts_per_layer": round(float(np.mean(distinct)), 2),
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+    eng.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -203,8 +285,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 256 MiB device copy before timing (reference point for HBM counters)")
-    ap.add_argument("--workload", default="bs1", choices=["bs1", "batched"],
-                    help="bs1: BASELINE.json configs[1] (the headline); batched: configs[2], --batch tokens per step")
+    ap.add_argument("--workload", default="bs1", choices=["bs1", "batched", "moe"],
+                    help="bs1: BASELINE.json configs[1] (the headline); batched: configs[2], --batch tokens per "
+                         "step; moe: configs[3], --batch tokens per step")
     ap.add_argument("--batch", type=int, default=16, help="tokens per step for --workload batched")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -217,6 +300,8 @@ def main() -> int:
 
     eng = hayai_amd.HipEngine(0)
     log(f"[bench] device {eng.device_name} {eng.arch} CUs={eng.device_info.compute_units}")
+    if args.workload == "moe":
+        return bench_moe(eng, args)
     gate = hayai_amd.QuantMatrix("ffn_gate", D_MODEL, D_FF, Q4_K)
     up = hayai_amd.QuantMatrix("ffn_up", D_MODEL, D_FF, Q4_K)
     down = hayai_amd.QuantMatrix("ffn_down", D_FF, D_MODEL, Q4_K)

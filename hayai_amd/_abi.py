@@ -61,6 +61,26 @@ class FfnDesc(C.Structure):
     ]
 
 
+class MoeDesc(C.Structure):
+    _fields_ = [
+        ("type", C.c_int),
+        ("act", C.c_int),
+        ("d_model", C.c_size_t),
+        ("d_ff", C.c_size_t),
+        ("n_experts", C.c_size_t),
+        ("top_k", C.c_size_t),
+        ("expert_stride", C.c_size_t),
+        ("gate_off", C.c_size_t),
+        ("up_off", C.c_size_t),
+        ("down_off", C.c_size_t),
+        ("n_group", C.c_size_t),
+        ("topk_group", C.c_size_t),
+        ("gating", C.c_int),
+        ("norm_topk_prob", C.c_int),
+        ("routed_scaling_factor", C.c_float),
+    ]
+
+
 SIGNATURES = {
     "hh_abi_version": (C.c_int, []),
     "hh_last_error": (C.c_char_p, []),
@@ -99,6 +119,10 @@ SIGNATURES = {
     "hh_ffn_begin_dev": (ST, [P, C.POINTER(FfnDesc), P, SZ, P, SZ]),
     "hh_ffn_finish_dev": (ST, [P, C.POINTER(FfnDesc), P, SZ, P, SZ]),
     "hh_gateup_dev": (ST, [P, I, I, SZ, SZ, P, SZ, P, SZ, P, SZ, P, SZ, I]),
+    "hh_route_experts_dev": (ST, [P, C.POINTER(MoeDesc), P, SZ, P, SZ, SZ, P, SZ, P, SZ]),
+    "hh_route_experts": (ST, [P, C.POINTER(MoeDesc), P, P, SZ, P, P]),
+    "hh_moe_ffn_dev": (ST, [P, C.POINTER(MoeDesc), P, SZ, P, SZ, SZ, P, SZ, P, SZ, P, SZ]),
+    "hh_moe_dev": (ST, [P, C.POINTER(MoeDesc), P, SZ, P, SZ, P, SZ, P, SZ, SZ, P, SZ]),
     "hh_event_create": (ST, [P, PP]),
     "hh_event_destroy": (None, [P]),
     "hh_event_record": (ST, [P, P]),

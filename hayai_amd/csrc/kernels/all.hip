@@ -2,5 +2,6 @@
 #include "gemv.hip"
 #include "q4k.hip"
 #include "q4k_mm.hip"
+#include "moe.hip"
 #include "dequant.hip"
 #include "synth.hip"

@@ -547,6 +547,155 @@ hh_status hh_gateup_dev(hh_engine* e, int tg, int tu, size_t d_ff, size_t d_mode
                              (const float*)((const char*)x->ptr + x_off), (float*)((char*)h->ptr + h_off), act);
 }
 
+// ---------------------------------------------------------------- MoE ----------------
+
+static hh_status validate_moe_desc(const hh_moe_desc* d) {
+    HH_NOT_NULL(d, "moe desc");
+    if (d->type != HH_TYPE_Q4_K)
+        return fail(HH_ERR_KERNEL_MISSING, "moe: experts of GGML type %d have no MoE kernel (Q4_K only)", d->type);
+    if (d->act != HH_ACT_SILU && d->act != HH_ACT_GELU_TANH) return fail(HH_ERR_INVALID, "moe: unknown act %d", d->act);
+    if (d->n_experts < 1 || d->n_experts > 512)
+        return fail(HH_ERR_INVALID, "moe: n_experts=%zu outside 1..512", d->n_experts);
+    if (d->top_k < 1 || d->top_k > 64) return fail(HH_ERR_INVALID, "moe: top_k=%zu outside 1..64", d->top_k);
+    if (d->n_group > 64) return fail(HH_ERR_INVALID, "moe: n_group=%zu > 64", d->n_group);
+    return HH_OK;
+}
+
+static hh_status validate_moe_experts(hh_engine* e, const hh_moe_desc* d, const hh_buf* experts, size_t off) {
+    HH_TRY(validate_shape(d->type, d->d_ff, d->d_model));
+    HH_TRY(validate_shape(d->type, d->d_model, d->d_ff));
+    size_t rin, rff;
+    HH_TRY(row_bytes(d->type, d->d_model, &rin));
+    HH_TRY(row_bytes(d->type, d->d_ff, &rff));
+    // LDS of the expert kernels holds the digits of x (d_model) and of the k intermediates
+    const size_t lds_in = 2 * d->d_model + d->d_model / 4, lds_ff = 2 * d->top_k * d->d_ff + d->top_k * d->d_ff / 4;
+    if (lds_in > 65536 || lds_ff > 65536)
+        return fail(HH_ERR_INVALID, "moe: d_model=%zu / top_k*d_ff=%zu too large for the expert kernels", d->d_model,
+                    d->top_k * d->d_ff);
+    HH_TRY(check_engine(e, experts, "experts"));
+    const size_t pack_end = std::max({d->gate_off + d->d_ff * rin, d->up_off + d->d_ff * rin,
+                                      d->down_off + d->d_model * rff});
+    if (d->expert_stride != 0 && d->n_experts - 1 > (SIZE_MAX - pack_end) / d->expert_stride)
+        return fail(HH_ERR_INVALID, "moe: expert layout overflows");
+    HH_TRY(check_range(experts, off, (d->n_experts - 1) * d->expert_stride + pack_end, "moe experts"));
+    if (((uintptr_t)experts->ptr + off) % 16 || d->expert_stride % 16 || d->gate_off % 16 || d->up_off % 16 ||
+        d->down_off % 16)
+        return fail(HH_ERR_INVALID, "moe: expert packs and tensor offsets must be 16-byte aligned");
+    return HH_OK;
+}
+
+hh_status hh_route_experts_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* logits, size_t logits_off,
+                               const hh_buf* bias, size_t bias_off, size_t T, hh_buf* ids, size_t ids_off,
+                               hh_buf* weights, size_t weights_off) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_moe_desc(d));
+    size_t lb, kb;
+    HH_TRY(batch_bytes(T, d->n_experts, &lb));
+    HH_TRY(batch_bytes(T, d->top_k, &kb));
+    HH_TRY(check_engine(e, logits, "logits"));
+    HH_TRY(check_engine(e, ids, "ids"));
+    HH_TRY(check_engine(e, weights, "weights"));
+    HH_TRY(check_range(logits, logits_off, lb, "logits"));
+    HH_TRY(check_range(ids, ids_off, kb, "ids"));
+    HH_TRY(check_range(weights, weights_off, kb, "weights"));
+    if (bias) {
+        HH_TRY(check_engine(e, bias, "bias"));
+        HH_TRY(check_range(bias, bias_off, d->n_experts * sizeof(float), "bias"));
+    }
+    if ((logits_off | ids_off | weights_off | bias_off) & 3u)
+        return fail(HH_ERR_INVALID, "route_experts: offsets must be 4-byte aligned");
+    if (T == 0) return HH_OK;
+    HH_TRY(e->select());
+    return e->enqueue_moe_route(d, (const float*)((const char*)logits->ptr + logits_off),
+                                bias ? (const float*)((const char*)bias->ptr + bias_off) : nullptr, T,
+                                (int32_t*)((char*)ids->ptr + ids_off), (float*)((char*)weights->ptr + weights_off));
+}
+
+hh_status hh_route_experts(hh_engine* e, const hh_moe_desc* d, const float* logits, const float* bias, size_t T,
+                           int32_t* ids, float* weights) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_moe_desc(d));
+    size_t lb, kb;
+    HH_TRY(batch_bytes(T, d->n_experts, &lb));
+    HH_TRY(batch_bytes(T, d->top_k, &kb));
+    if (T == 0) return HH_OK;
+    HH_NOT_NULL(logits, "logits");
+    HH_NOT_NULL(ids, "ids");
+    HH_NOT_NULL(weights, "weights");
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    // x workspace: logits then bias; y workspace: ids then weights
+    const size_t bb = bias ? d->n_experts * sizeof(float) : 0;
+    HH_TRY(e->grow(&e->ws_x, &e->ws_x_cap, lb + bb));
+    HH_TRY(e->grow(&e->ws_y, &e->ws_y_cap, 2 * kb));
+    HH_TRY_HIP(hipMemcpyAsync(e->ws_x, logits, lb, hipMemcpyHostToDevice, e->stream), "hipMemcpyAsync(logits)");
+    if (bias)
+        HH_TRY_HIP(hipMemcpyAsync((char*)e->ws_x + lb, bias, bb, hipMemcpyHostToDevice, e->stream),
+                   "hipMemcpyAsync(bias)");
+    HH_TRY(e->enqueue_moe_route(d, (const float*)e->ws_x, bias ? (const float*)((char*)e->ws_x + lb) : nullptr, T,
+                                (int32_t*)e->ws_y, (float*)((char*)e->ws_y + kb)));
+    HH_TRY_HIP(hipMemcpyAsync(ids, e->ws_y, kb, hipMemcpyDeviceToHost, e->stream), "hipMemcpyAsync(ids)");
+    HH_TRY_HIP(hipMemcpyAsync(weights, (char*)e->ws_y + kb, kb, hipMemcpyDeviceToHost, e->stream),
+               "hipMemcpyAsync(weights)");
+    return e->check_device_error();
+}
+
+hh_status hh_moe_ffn_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* experts, size_t experts_off,
+                         const hh_buf* x, size_t x_off, size_t T, const hh_buf* ids, size_t ids_off,
+                         const hh_buf* weights, size_t weights_off, hh_buf* y, size_t y_off) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_moe_desc(d));
+    HH_TRY(validate_moe_experts(e, d, experts, experts_off));
+    size_t xb, kb;
+    HH_TRY(batch_bytes(T, d->d_model, &xb));
+    HH_TRY(batch_bytes(T, d->top_k, &kb));
+    for (const hh_buf* b : {x, ids, weights, (const hh_buf*)y}) HH_TRY(check_engine(e, b, "moe"));
+    HH_TRY(check_range(x, x_off, xb, "x"));
+    HH_TRY(check_range(y, y_off, xb, "y"));
+    HH_TRY(check_range(ids, ids_off, kb, "ids"));
+    HH_TRY(check_range(weights, weights_off, kb, "weights"));
+    if ((x_off & 15u) || ((y_off | ids_off | weights_off) & 3u))
+        return fail(HH_ERR_INVALID, "moe_ffn: x offset must be 16-byte aligned, y/ids/weights 4-byte");
+    if (T == 0) return HH_OK;
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    return e->enqueue_moe_ffn(d, (const uint8_t*)experts->ptr + experts_off, (const float*)((const char*)x->ptr + x_off),
+                              T, (int32_t*)((char*)ids->ptr + ids_off), (float*)((char*)weights->ptr + weights_off),
+                              (float*)((char*)y->ptr + y_off));
+}
+
+hh_status hh_moe_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* experts, size_t experts_off,
+                     const hh_buf* logits, size_t logits_off, const hh_buf* bias, size_t bias_off, const hh_buf* x,
+                     size_t x_off, size_t T, hh_buf* y, size_t y_off) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_moe_desc(d));
+    HH_TRY(validate_moe_experts(e, d, experts, experts_off));
+    size_t xb, kb, lb;
+    HH_TRY(batch_bytes(T, d->d_model, &xb));
+    HH_TRY(batch_bytes(T, d->top_k, &kb));
+    HH_TRY(batch_bytes(T, d->n_experts, &lb));
+    for (const hh_buf* b : {logits, x, (const hh_buf*)y}) HH_TRY(check_engine(e, b, "moe"));
+    HH_TRY(check_range(logits, logits_off, lb, "logits"));
+    HH_TRY(check_range(x, x_off, xb, "x"));
+    HH_TRY(check_range(y, y_off, xb, "y"));
+    if (bias) {
+        HH_TRY(check_engine(e, bias, "bias"));
+        HH_TRY(check_range(bias, bias_off, d->n_experts * sizeof(float), "bias"));
+    }
+    if ((x_off & 15u) || ((y_off | logits_off | bias_off) & 3u))
+        return fail(HH_ERR_INVALID, "moe: x offset must be 16-byte aligned, y/logits/bias 4-byte");
+    if (T == 0) return HH_OK;
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    HH_TRY(e->grow(&e->ws_moe_ids, &e->ws_moe_ids_cap, kb));
+    HH_TRY(e->grow(&e->ws_moe_w, &e->ws_moe_w_cap, kb));
+    // routing runs inside the gate/up kernel
+    return e->enqueue_moe_ffn(d, (const uint8_t*)experts->ptr + experts_off, (const float*)((const char*)x->ptr + x_off),
+                              T, (int32_t*)e->ws_moe_ids, (float*)e->ws_moe_w, (float*)((char*)y->ptr + y_off),
+                              (const float*)((const char*)logits->ptr + logits_off),
+                              bias ? (const float*)((const char*)bias->ptr + bias_off) : nullptr);
+}
+
 // ---------------------------------------------------------------- events -------------
 
 hh_status hh_event_create(hh_engine* e, hh_event** out) {

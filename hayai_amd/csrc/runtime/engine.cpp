@@ -582,6 +582,108 @@ hh_status hh_engine::enqueue_ffn_batched(const hh_ffn_desc* d, const uint8_t* pa
     return HH_OK;
 }
 
+// ---------------------------------------------------------------- MoE ----------------
+
+// Kernel argument blocks of moe.hip (same layout).
+struct hh_route_args {
+    const float* logits;
+    const float* bias;
+    int32_t* ids;
+    float* wts;
+    uint32_t T, E, top_k, k_out;
+    uint32_t n_group, topk_group;
+    int32_t gating, norm;
+    float scale;
+    uint32_t pad;
+};
+struct hh_moe_args {
+    const uint8_t* experts;
+    uint64_t expert_stride;
+    uint64_t gate_off, up_off, down_off;
+    uint64_t rb_in, rb_ff;
+    int32_t* ids;
+    float* wts;
+    const float* x;
+    float* h;
+    float* y;
+    uint32_t d_model, d_ff, k, n_experts;
+    int32_t act;
+    uint32_t route;
+    hh_route_args r;
+};
+constexpr int kMoeBlock = 256;
+constexpr size_t kMoeDownRows = 4;  // output rows per down workgroup (moe.hip)
+
+static int moe_team(size_t units) { return units <= 16 ? 16 : (units <= 32 ? 32 : 64); }
+
+static hh_route_args route_args(const hh_moe_desc* d, const float* logits, const float* bias, size_t T, int32_t* ids,
+                                float* wts) {
+    return hh_route_args{logits, bias, ids, wts, (uint32_t)T, (uint32_t)d->n_experts, (uint32_t)d->top_k,
+                         (uint32_t)d->top_k, (uint32_t)d->n_group, (uint32_t)d->topk_group, d->gating,
+                         d->norm_topk_prob, d->routed_scaling_factor, 0};
+}
+
+hh_status hh_engine::enqueue_moe_route(const hh_moe_desc* d, const float* logits, const float* bias, size_t T,
+                                       int32_t* ids, float* wts) {
+    if (T == 0) return HH_OK;
+    hipFunction_t fn;
+    HH_TRY(kernel("hh_moe_route", &fn));
+    const hh_route_args a = route_args(d, logits, bias, T, ids, wts);
+    return launch(fn, (uint32_t)((T + 3) / 4), kMoeBlock, a);
+}
+
+hh_status hh_engine::enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* experts, const float* x, size_t T,
+                                     int32_t* ids, float* wts, float* y, const float* logits, const float* bias) {
+    if (T == 0) return HH_OK;
+    const size_t k = d->top_k, dm = d->d_model, df = d->d_ff;
+    HH_TRY(grow(&ws_moe_h, &ws_moe_h_cap, T * k * df * sizeof(float)));
+    hh_moe_args a{};
+    a.experts = experts;
+    a.expert_stride = d->expert_stride;
+    a.gate_off = d->gate_off;
+    a.up_off = d->up_off;
+    a.down_off = d->down_off;
+    a.rb_in = (dm / 256) * 144;
+    a.rb_ff = (df / 256) * 144;
+    a.ids = ids;
+    a.wts = wts;
+    a.x = x;
+    a.h = (float*)ws_moe_h;
+    a.y = y;
+    a.d_model = (uint32_t)dm;
+    a.d_ff = (uint32_t)df;
+    a.k = (uint32_t)k;
+    a.n_experts = (uint32_t)d->n_experts;
+    a.act = d->act;
+    a.route = logits != nullptr;
+    if (logits) a.r = route_args(d, logits, bias, T, ids, wts);
+    const size_t cap = std::max<size_t>(1, ((size_t)props.multiProcessorCount * 2 + T - 1) / T);
+    void* params[] = {&a};
+    {
+        const int team = moe_team(dm / 64);
+        const size_t tpb = kMoeBlock / team;
+        const size_t gx = std::max<size_t>(1, std::min((k * df + tpb - 1) / tpb, cap));
+        const std::string name = "hh_moe_gateup_t" + std::to_string(team);
+        hipFunction_t fn;
+        HH_TRY(kernel(name, &fn));
+        HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)gx, (uint32_t)T, 1, kMoeBlock, 1, 1,
+                                         (unsigned)hh_digits_bytes(dm), stream, params, nullptr),
+                   "launch(moe gate/up)");
+    }
+    {
+        const int team = moe_team(df / 64);
+        const size_t gx = (dm + kMoeDownRows - 1) / kMoeDownRows;
+        const std::string name = "hh_moe_down_t" + std::to_string(team);
+        hipFunction_t fn;
+        HH_TRY(kernel(name, &fn));
+        HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)gx, (uint32_t)T, 1, kMoeBlock, 1, 1,
+                                         (unsigned)hh_digits_bytes(k * df), stream, params, nullptr),
+                   "launch(moe down)");
+    }
+    ffn_calls += 3 * T;
+    return HH_OK;
+}
+
 // ---------------------------------------------------------------- bring-up -----------
 
 static std::vector<std::string> required_kernels() {
@@ -603,6 +705,9 @@ static std::vector<std::string> required_kernels() {
     for (int tt : {1, 2, 4})
         for (const char* kind : {"hh_q4k_mm_t", "hh_q4k_mm_gateup_t"}) k.push_back(std::string(kind) + std::to_string(tt));
     k.push_back("hh_mm_prep");
+    k.push_back("hh_moe_route");
+    for (int t : {16, 32, 64})
+        for (const char* kind : {"hh_moe_gateup_t", "hh_moe_down_t"}) k.push_back(std::string(kind) + std::to_string(t));
     return k;
 }
 
@@ -660,7 +765,7 @@ void engine_destroy(hh_engine* e) {
     if (e->stream) hipStreamSynchronize(e->stream);
     if (e->copy_stream) hipStreamSynchronize(e->copy_stream);
     for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq, e->ws_xop, e->ws_hop, e->ws_part,
-                    e->ws_cnt, e->grid_sync})
+                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->grid_sync})
         if (p) hipFree(p);
     if (e->stream) hipStreamDestroy(e->stream);
     if (e->copy_stream) hipStreamDestroy(e->copy_stream);

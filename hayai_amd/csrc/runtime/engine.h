@@ -112,6 +112,13 @@ struct hh_engine {
     size_t ws_part_cap = 0;
     void* ws_cnt = nullptr;  // zeroed when allocated; every launch leaves it zero
     size_t ws_cnt_cap = 0;
+    // MoE: expert intermediates [T][k][d_ff], ids and weights of hh_moe_dev.
+    void* ws_moe_h = nullptr;
+    size_t ws_moe_h_cap = 0;
+    void* ws_moe_ids = nullptr;
+    size_t ws_moe_ids_cap = 0;
+    void* ws_moe_w = nullptr;
+    size_t ws_moe_w_cap = 0;
     void* grid_sync = nullptr;  // fused FFN grid-barrier state (counters, flags, error word)
     uint32_t ffn_gen = 0;       // generation of the last fused FFN launch
     hh_ffn_desc ffn_stage{};    // FFN whose gate/up output is pending in ws_h (/ws_hq)
@@ -167,6 +174,13 @@ struct hh_engine {
     // act, writing the stages of h into ws_hop).  xop holds 16 * tt tokens of n columns.
     hh_status enqueue_q4k_mm(size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* xop, size_t b,
                              size_t tt, float* y, bool ffn, int act);
+    // MoE routing of T tokens (device pointers) and the grouped expert FFN.
+    hh_status enqueue_moe_route(const hh_moe_desc* d, const float* logits, const float* bias, size_t T,
+                                int32_t* ids, float* wts);
+    // With logits, the gate/up kernel routes each token first and writes ids / wts itself.
+    hh_status enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* experts, const float* x, size_t T,
+                              int32_t* ids, float* wts, float* y, const float* logits = nullptr,
+                              const float* bias = nullptr);
     // Reports (and clears) a grid-barrier timeout recorded by a fused kernel.  Syncs.
     hh_status check_device_error();
 };

@@ -359,6 +359,47 @@ class HipEngine:
         tg, tu, td = types
         return _abi.FfnDesc(tg, tu, td, act, d_model, d_ff, layout.gate_off, layout.up_off, layout.down_off)
 
+    # ---------------------------------------------------------------- MoE
+    @staticmethod
+    def moe_desc(d_model: int, d_ff: int, n_experts: int, top_k: int, expert_stride: int, offs,
+                 ggml_type: int = Q4_K, act: int = ACT_SILU, n_group: int = 0, topk_group: int = 0,
+                 gating: int = 0, norm_topk_prob: bool = False,
+                 routed_scaling_factor: float = 1.0) -> _abi.MoeDesc:
+        """MoeMeta (exec_plan.rs:244-271) + the resident expert layout (moe_infer.rs:330-339)."""
+        g, u, dn = offs
+        return _abi.MoeDesc(ggml_type, act, d_model, d_ff, n_experts, top_k, expert_stride, g, u, dn, n_group,
+                            topk_group, gating, int(norm_topk_prob), routed_scaling_factor)
+
+    def route_experts(self, desc: _abi.MoeDesc, logits: np.ndarray, bias=None):
+        """route_experts (moe_infer.rs:865-934) for logits of shape (T, n_experts): returns
+        ids (T, top_k) int32 (-1 = empty slot) and weights (T, top_k) f32."""
+        lg = np.ascontiguousarray(logits, dtype=np.float32).reshape(-1, desc.n_experts)
+        T = lg.shape[0]
+        ids = np.empty((T, desc.top_k), np.int32)
+        w = np.empty((T, desc.top_k), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        _check(self.lib.hh_route_experts(self.handle, C.byref(desc), _ptr(lg), None if b is None else _ptr(b), T,
+                                         _ptr(ids), _ptr(w)))
+        return ids, w
+
+    def route_experts_dev(self, desc, logits: DeviceBuffer, logits_off, bias, bias_off, T, ids: DeviceBuffer,
+                          ids_off, weights: DeviceBuffer, weights_off) -> None:
+        _check(self.lib.hh_route_experts_dev(self.handle, C.byref(desc), logits.handle, logits_off,
+                                             None if bias is None else bias.handle, bias_off, T, ids.handle, ids_off,
+                                             weights.handle, weights_off))
+
+    def moe_ffn_dev(self, desc, experts: DeviceBuffer, experts_off, x: DeviceBuffer, x_off, T, ids: DeviceBuffer,
+                    ids_off, weights: DeviceBuffer, weights_off, y: DeviceBuffer, y_off) -> None:
+        """The routed-expert FFN + combine (moe_infer.rs:342-455), enqueue only."""
+        _check(self.lib.hh_moe_ffn_dev(self.handle, C.byref(desc), experts.handle, experts_off, x.handle, x_off, T,
+                                       ids.handle, ids_off, weights.handle, weights_off, y.handle, y_off))
+
+    def moe_dev(self, desc, experts: DeviceBuffer, experts_off, logits: DeviceBuffer, logits_off, bias, bias_off,
+                x: DeviceBuffer, x_off, T, y: DeviceBuffer, y_off) -> None:
+        _check(self.lib.hh_moe_dev(self.handle, C.byref(desc), experts.handle, experts_off, logits.handle, logits_off,
+                                   None if bias is None else bias.handle, bias_off, x.handle, x_off, T, y.handle,
+                                   y_off))
+
     def ffn(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, x: np.ndarray) -> np.ndarray:
         """ffn_begin_gate_up_scratch + ffn_finish_scratch (stream_infer.rs:3752-3864), one call."""
         x = np.ascontiguousarray(x, dtype=np.float32)

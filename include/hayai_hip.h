@@ -243,6 +243,52 @@ hh_status hh_gateup_dev(hh_engine* e, int type_gate, int type_up, size_t d_ff, s
                         size_t wg_off, const hh_buf* wu, size_t wu_off, const hh_buf* x, size_t x_off, hh_buf* h,
                         size_t h_off, int act);
 
+/* ------------------------------------------------------------------ MoE ------------- */
+
+/* The routed experts of one MoE layer: MoeMeta (crates/hayai-core/src/exec_plan.rs:244-271)
+ * plus the resident expert layout of moe_infer.rs:330-339 (expert e's pack at
+ * e * expert_stride; its gate/up/down tensors at fixed offsets inside the pack). */
+typedef struct hh_moe_desc {
+    int type;             /* GGML type of every expert tensor; the MoE kernels take HH_TYPE_Q4_K */
+    int act;              /* HH_ACT_* */
+    size_t d_model;       /* expert input and output width */
+    size_t d_ff;          /* expert intermediate width */
+    size_t n_experts;     /* expert_count, 1..512 */
+    size_t top_k;         /* experts per token, 1..64 */
+    size_t expert_stride; /* bytes between consecutive expert packs (multiple of 16) */
+    size_t gate_off, up_off, down_off;
+    size_t n_group;       /* grouped routing: number of groups (0 = off, <= 64) */
+    size_t topk_group;    /* groups kept */
+    int gating;           /* 0 softmax over all experts, 1 sigmoid */
+    int norm_topk_prob;   /* renormalise the top_k weights */
+    float routed_scaling_factor;
+} hh_moe_desc;
+
+/* route_experts + top_k_indices (crates/hayai-core/src/moe_infer.rs:852-934) for T tokens:
+ * logits [T][n_experts] f32 (+ optional e_score_correction_bias [n_experts], NULL for none)
+ * -> ids [T][top_k] int32 and weights [T][top_k] f32.  Ids are exactly the reference's; the
+ * weights use the device expf (within a few ulp of libm).  Slots past the number selected
+ * (fewer candidates than top_k) hold id -1 and weight 0.  _dev: device buffers, enqueue
+ * only; without: host arrays, blocking. */
+hh_status hh_route_experts_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* logits, size_t logits_off,
+                               const hh_buf* bias, size_t bias_off, size_t T, hh_buf* ids, size_t ids_off,
+                               hh_buf* weights, size_t weights_off);
+hh_status hh_route_experts(hh_engine* e, const hh_moe_desc* d, const float* logits, const float* bias, size_t T,
+                           int32_t* ids, float* weights);
+
+/* The routed-expert FFN and combine of moe_infer.rs:342-455 for T tokens:
+ * y[t] = sum_s weights[t][s] * down_e(act(gate_e x[t]) * up_e x[t]), e = ids[t][s], in slot
+ * order.  Ids outside [0, n_experts) (the -1 of an empty slot) contribute nothing.  Experts
+ * live in one device buffer at experts_off.  Enqueue only. */
+hh_status hh_moe_ffn_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* experts, size_t experts_off,
+                         const hh_buf* x, size_t x_off, size_t T, const hh_buf* ids, size_t ids_off,
+                         const hh_buf* weights, size_t weights_off, hh_buf* y, size_t y_off);
+
+/* Routing and the expert FFN in one call (ids and weights stay in engine workspaces). */
+hh_status hh_moe_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* experts, size_t experts_off,
+                     const hh_buf* logits, size_t logits_off, const hh_buf* bias, size_t bias_off,
+                     const hh_buf* x, size_t x_off, size_t T, hh_buf* y, size_t y_off);
+
 /* ------------------------------------------------------------------ timing ---------- */
 
 hh_status hh_event_create(hh_engine* e, hh_event** out);
