@@ -23,6 +23,7 @@ from .engine import (  # noqa: F401
     LayerPackLayout,
     PendingGemv,
     QuantMatrix,
+    StreamingScratch,
     device_count,
     row_bytes,
     validate_gemv_shape,

@@ -110,6 +110,8 @@ SIGNATURES = {
     "hh_pending_destroy": (None, [P]),
     "hh_gemv_dev": (ST, [P, I, SZ, SZ, P, SZ, P, SZ, P, SZ]),
     "hh_dequant_dev": (ST, [P, I, P, SZ, SZ, P, SZ]),
+    "hh_lut_gemv": (ST, [P, SZ, SZ, P, SZ, P, P, P]),
+    "hh_lut_gemv_dev": (ST, [P, SZ, SZ, P, SZ, P, SZ, P, SZ, P, SZ]),
     "hh_ffn": (ST, [P, C.POINTER(FfnDesc), P, SZ, P, P]),
     "hh_ffn_dev": (ST, [P, C.POINTER(FfnDesc), P, SZ, P, SZ, P, SZ]),
     "hh_gemv_batched": (ST, [P, I, SZ, SZ, P, SZ, P, P, SZ]),
@@ -123,6 +125,13 @@ SIGNATURES = {
     "hh_route_experts": (ST, [P, C.POINTER(MoeDesc), P, P, SZ, P, P]),
     "hh_moe_ffn_dev": (ST, [P, C.POINTER(MoeDesc), P, SZ, P, SZ, SZ, P, SZ, P, SZ, P, SZ]),
     "hh_moe_dev": (ST, [P, C.POINTER(MoeDesc), P, SZ, P, SZ, P, SZ, P, SZ, SZ, P, SZ]),
+    "hh_streamer_create": (ST, [P, SZ, SZ, SZ, PP]),
+    "hh_streamer_destroy": (None, [P]),
+    "hh_streamer_slot_for": (ST, [P, SZ, C.POINTER(SZ)]),
+    "hh_streamer_weight_offset": (ST, [P, SZ, SZ, C.POINTER(SZ)]),
+    "hh_streamer_host_slot": (ST, [P, SZ, PP]),
+    "hh_streamer_dma": (ST, [P, SZ, SZ, SZ]),
+    "hh_streamer_bind": (ST, [P, SZ, PP, C.POINTER(SZ)]),
     "hh_event_create": (ST, [P, PP]),
     "hh_event_destroy": (None, [P]),
     "hh_event_record": (ST, [P, P]),

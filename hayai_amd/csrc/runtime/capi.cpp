@@ -393,6 +393,62 @@ void hh_pending_destroy(hh_pending* p) {
     delete p;
 }
 
+// ---------------------------------------------------------------- Q4 LUT GEMV ------
+
+// The reference asserts these (compute.rs:54-58, matmul.rs:61-66); here they are status codes.
+static hh_status lut_shape(size_t m, size_t n) {
+    if (m == 0 || n == 0) return fail(HH_ERR_INVALID, "lut_matmul_q4: empty shape m=%zu n=%zu", m, n);
+    if (n % 2 != 0) return fail(HH_ERR_INVALID, "lut_matmul_q4: N must be even for packed Q4 weights (n=%zu)", n);
+    if (m > SIZE_MAX / (n / 2)) return fail(HH_ERR_INVALID, "lut_matmul_q4: weight size overflow");
+    return HH_OK;
+}
+
+hh_status hh_lut_gemv(hh_engine* e, size_t m, size_t n, const uint8_t* weights_q4, size_t weights_len,
+                      const float* lut, const float* x, float* y) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(lut_shape(m, n));
+    HH_NOT_NULL(weights_q4, "weights_q4");
+    HH_NOT_NULL(lut, "lut");
+    HH_NOT_NULL(x, "x");
+    HH_NOT_NULL(y, "y");
+    const size_t wb = m * (n / 2);
+    if (weights_len != wb)
+        return fail(HH_ERR_INVALID, "lut_matmul_q4: weights_q4 has %zu bytes, expected m*n/2 = %zu", weights_len, wb);
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    // one staging buffer: [lut 64 B][x n*4 B][weights], x 16-byte aligned
+    const size_t xo = 64, wo = xo + ((n * sizeof(float) + 255) / 256) * 256;
+    HH_TRY(e->grow(&e->ws_w, &e->ws_w_cap, wo + wb));
+    HH_TRY(e->grow(&e->ws_y, &e->ws_y_cap, m * sizeof(float)));
+    char* base = (char*)e->ws_w;
+    HH_TRY_HIP(hipMemcpyAsync(base, lut, 16 * sizeof(float), hipMemcpyHostToDevice, e->stream), "hipMemcpyAsync(lut)");
+    HH_TRY_HIP(hipMemcpyAsync(base + xo, x, n * sizeof(float), hipMemcpyHostToDevice, e->stream), "hipMemcpyAsync(x)");
+    HH_TRY_HIP(hipMemcpyAsync(base + wo, weights_q4, wb, hipMemcpyHostToDevice, e->stream), "hipMemcpyAsync(w)");
+    HH_TRY(e->enqueue_lut(m, n, (const uint8_t*)(base + wo), (const float*)base, (const float*)(base + xo),
+                          (float*)e->ws_y));
+    HH_TRY_HIP(hipMemcpyAsync(y, e->ws_y, m * sizeof(float), hipMemcpyDeviceToHost, e->stream), "hipMemcpyAsync(y)");
+    HH_TRY_HIP(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
+    return HH_OK;
+}
+
+hh_status hh_lut_gemv_dev(hh_engine* e, size_t m, size_t n, const hh_buf* w, size_t w_off, const hh_buf* lut,
+                          size_t lut_off, const hh_buf* x, size_t x_off, hh_buf* y, size_t y_off) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(lut_shape(m, n));
+    HH_TRY(check_engine(e, w, "weights"));
+    HH_TRY(check_engine(e, lut, "lut"));
+    HH_TRY(check_engine(e, x, "x"));
+    HH_TRY(check_engine(e, y, "y"));
+    HH_TRY(check_range(w, w_off, m * (n / 2), "weights"));
+    HH_TRY(check_range(lut, lut_off, 16 * sizeof(float), "lut"));
+    HH_TRY(check_range(x, x_off, n * sizeof(float), "x"));
+    HH_TRY(check_range(y, y_off, m * sizeof(float), "y"));
+    if (lut_off % 4 || x_off % 4 || y_off % 4) return fail(HH_ERR_INVALID, "lut_matmul_q4: f32 offsets must be 4-byte aligned");
+    HH_TRY(e->select());
+    return e->enqueue_lut(m, n, (const uint8_t*)w->ptr + w_off, (const float*)((const char*)lut->ptr + lut_off),
+                          (const float*)((const char*)x->ptr + x_off), (float*)((char*)y->ptr + y_off));
+}
+
 hh_status hh_dequant_dev(hh_engine* e, int t, const hh_buf* w, size_t w_off, size_t n, hh_buf* out, size_t out_off) {
     HH_NOT_NULL(e, "engine");
     const Format* f = format_of(t);

@@ -232,6 +232,28 @@ hh_status hh_engine::enqueue_q4k(size_t m, size_t n, const uint8_t* w0, const ui
     return HH_OK;
 }
 
+// Must match struct hh_lut_args in kernels/lut.hip.
+struct LutArgs {
+    const uint8_t* w;
+    const float* lut;
+    const float* x;
+    float* y;
+    uint32_t m, n, vec, pad;
+};
+
+hh_status hh_engine::enqueue_lut(size_t m, size_t n, const uint8_t* w, const float* lut, const float* x, float* y) {
+    if (m > UINT32_MAX || n > UINT32_MAX) return fail(HH_ERR_INVALID, "lut_matmul_q4: %zux%zu exceeds 32-bit sizes", m, n);
+    hipFunction_t f;
+    HH_TRY(kernel("hh_lut_gemv", &f));
+    const size_t pc = n / 2;
+    // dword weight loads need every row start 4-aligned; float4 x loads need x 16-aligned.
+    const bool vec = pc % 4 == 0 && ((uintptr_t)w & 3u) == 0 && ((uintptr_t)x & 15u) == 0;
+    LutArgs a{w, lut, x, y, (uint32_t)m, (uint32_t)n, vec ? 1u : 0u, 0u};
+    const size_t cap = (size_t)props.multiProcessorCount * 8;
+    const size_t grid = std::max<size_t>(1, std::min(cap, (m + 3) / 4));
+    return launch(f, (uint32_t)grid, 256, a);
+}
+
 hh_status hh_engine::enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w, const float* x, float* y) {
     const Format* f = format_of(type);
     if (!f) return fail(HH_ERR_KERNEL_MISSING, "no GEMV kernel for GGML type %d", type);
@@ -705,6 +727,7 @@ static std::vector<std::string> required_kernels() {
     for (int tt : {1, 2, 4})
         for (const char* kind : {"hh_q4k_mm_t", "hh_q4k_mm_gateup_t"}) k.push_back(std::string(kind) + std::to_string(tt));
     k.push_back("hh_mm_prep");
+    k.push_back("hh_lut_gemv");
     k.push_back("hh_moe_route");
     for (int t : {16, 32, 64})
         for (const char* kind : {"hh_moe_gateup_t", "hh_moe_down_t"}) k.push_back(std::string(kind) + std::to_string(t));

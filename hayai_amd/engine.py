@@ -114,6 +114,73 @@ class DeviceBuffer:
             pass
 
 
+class MirrorView:
+    """Non-owning handle of a streamer's device mirror slot (usable wherever a
+    DeviceBuffer is: ``handle`` and ``nbytes``); the streamer frees it."""
+
+    def __init__(self, engine: "HipEngine", handle, nbytes: int):
+        self.engine, self.handle, self.nbytes, self.kind = engine, handle, nbytes, BUF_DEVICE
+
+    def read(self, dtype, count: int, offset: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        _check(self.engine.lib.hh_buf_read(self.engine.handle, self.handle, offset, _ptr(out), out.nbytes))
+        return out
+
+
+class StreamingScratch:
+    """Pinned-host ping-pong weight slots + device mirrors: StreamingScratch
+    (crates/hayai-opencl/src/hetero_scratch.rs:48-71) on the pinned path."""
+
+    def __init__(self, engine: "HipEngine", layer_bytes: int, k_chunk: int = 1, n_slots: int = 2):
+        self.engine = engine
+        self.layer_bytes = int(layer_bytes)
+        self.block_k = max(1, int(k_chunk))
+        self.n_slots = max(2, int(n_slots))
+        h = C.c_void_p()
+        _check(engine.lib.hh_streamer_create(engine.handle, self.layer_bytes, self.block_k, self.n_slots, C.byref(h)))
+        self.handle = h
+        engine._children.add(self)
+
+    def slot_for(self, layer: int) -> int:
+        out = C.c_size_t(0)
+        _check(self.engine.lib.hh_streamer_slot_for(self.handle, layer, C.byref(out)))
+        return out.value
+
+    def weight_offset(self, layer: int, tensor_off: int) -> int:
+        out = C.c_size_t(0)
+        _check(self.engine.lib.hh_streamer_weight_offset(self.handle, layer, tensor_off, C.byref(out)))
+        return out.value
+
+    def host_slot(self, layer: int) -> np.ndarray:
+        """prepare_host_write + host_slot: writable uint8 view of the layer's pinned region."""
+        p = C.c_void_p()
+        _check(self.engine.lib.hh_streamer_host_slot(self.handle, layer, C.byref(p)))
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint8)), shape=(self.layer_bytes,))
+
+    def dma(self, layer: int, off: int = 0, length: int | None = None) -> None:
+        """dma_ffn_keep_mapped: async copy of [off, off+length) of the layer into its mirror."""
+        n = self.layer_bytes - off if length is None else length
+        _check(self.engine.lib.hh_streamer_dma(self.handle, layer, off, n))
+
+    def weight_bind(self, layer: int) -> tuple[MirrorView, int]:
+        """(mirror slot, byte offset of the layer in it); compute waits for the slot's DMA."""
+        b = C.c_void_p()
+        off = C.c_size_t(0)
+        _check(self.engine.lib.hh_streamer_bind(self.handle, layer, C.byref(b), C.byref(off)))
+        return MirrorView(self.engine, b, self.block_k * self.layer_bytes), off.value
+
+    def free(self) -> None:
+        if self.handle:
+            self.engine.lib.hh_streamer_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class PendingGemv:
     """In-flight GEMV; ``wait()`` returns y.  Dropping it waits first (async_gemv.rs:48-57)."""
 
@@ -342,6 +409,25 @@ class HipEngine:
 
     def gemv_dev(self, ggml_type, m, n, w: DeviceBuffer, w_off, x: DeviceBuffer, x_off, y: DeviceBuffer, y_off):
         _check(self.lib.hh_gemv_dev(self.handle, ggml_type, m, n, w.handle, w_off, x.handle, x_off, y.handle, y_off))
+
+    def lut_matmul_q4(self, m: int, n: int, weights_q4: np.ndarray, lut, inp: np.ndarray) -> np.ndarray:
+        """OpenClEngine::lut_matmul_q4 (compute.rs:45-128): Hayai's 4-bit LUT format, m rows of
+        n/2 packed bytes indexing a 16-entry f32 LUT; host arrays, blocking."""
+        w = np.ascontiguousarray(weights_q4, dtype=np.uint8)
+        t = np.ascontiguousarray(lut, dtype=np.float32)
+        x = np.ascontiguousarray(inp, dtype=np.float32)
+        if t.size != 16:
+            raise HipError(2, f"lut has {t.size} entries, expected 16")
+        if x.size != n:
+            raise HipError(2, f"input has {x.size} floats, expected n={n}")
+        y = np.empty(m, np.float32)
+        _check(self.lib.hh_lut_gemv(self.handle, m, n, _ptr(w), w.nbytes, _ptr(t), _ptr(x), _ptr(y)))
+        return y
+
+    def lut_gemv_dev(self, m, n, w: DeviceBuffer, w_off, lut: DeviceBuffer, lut_off, x: DeviceBuffer, x_off,
+                     y: DeviceBuffer, y_off) -> None:
+        _check(self.lib.hh_lut_gemv_dev(self.handle, m, n, w.handle, w_off, lut.handle, lut_off, x.handle, x_off,
+                                        y.handle, y_off))
 
     def dequant_dev(self, ggml_type, w: DeviceBuffer, w_off, n, out: DeviceBuffer, out_off=0):
         _check(self.lib.hh_dequant_dev(self.handle, ggml_type, w.handle, w_off, n, out.handle, out_off))

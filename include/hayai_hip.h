@@ -180,6 +180,20 @@ hh_status hh_gemv_batched_dev(hh_engine* e, int ggml_type, size_t m, size_t n, c
 hh_status hh_gemv_dev(hh_engine* e, int ggml_type, size_t m, size_t n, const hh_buf* w,
                       size_t w_off, const hh_buf* x, size_t x_off, hh_buf* y, size_t y_off);
 
+/* Q4 LUT MatMul, Hayai's own 4-bit dictionary format: weights_q4 holds m rows of n/2
+ * bytes (low nibble = even column, high nibble = odd column), each nibble an index into
+ * the 16-entry f32 `lut`; y[r] = sum_c x[2c]*lut[lo] + x[2c+1]*lut[hi].
+ * OpenClEngine::lut_matmul_q4 (crates/hayai-opencl/src/compute.rs:45-128), kernel
+ * lut_matmul_q4_v1 (crates/hayai-kernels/kernels/lut_matmul.cl:14-54), CPU twin
+ * cpu_lut_matmul_q4 (crates/hayai-cpu/src/matmul.rs:48-82).  The reference's assertions
+ * (n even, weights_q4.len() == m*n/2) become HH_ERR_INVALID.  Host arrays, blocking. */
+hh_status hh_lut_gemv(hh_engine* e, size_t m, size_t n, const uint8_t* weights_q4, size_t weights_len,
+                      const float* lut, const float* x, float* y);
+/* Same with device buffers (lut: 16 floats at lut_off; f32 offsets 4-byte aligned);
+ * enqueue only. */
+hh_status hh_lut_gemv_dev(hh_engine* e, size_t m, size_t n, const hh_buf* w, size_t w_off, const hh_buf* lut,
+                          size_t lut_off, const hh_buf* x, size_t x_off, hh_buf* y, size_t y_off);
+
 /* Dequant probe: n weights of a packed tensor at (w, w_off) -> f32 at (out, out_off),
  * bit-identical to hayai-model's dequant (gguf.rs:348-372, q4k.rs:162-203,
  * iq2.rs:504-523, iq3.rs:147-173; F16: gguf.rs:521-545).  Enqueue only. */
@@ -288,6 +302,43 @@ hh_status hh_moe_ffn_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* exper
 hh_status hh_moe_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* experts, size_t experts_off,
                      const hh_buf* logits, size_t logits_off, const hh_buf* bias, size_t bias_off,
                      const hh_buf* x, size_t x_off, size_t T, hh_buf* y, size_t y_off);
+
+/* ------------------------------------------------------------------ streaming ------- */
+
+/* Pinned-host ping-pong weight streaming: StreamingScratch
+ * (crates/hayai-opencl/src/hetero_scratch.rs:48-71) with PinnedHostBuffer host slots
+ * (crates/hayai-opencl/src/memory.rs:72-147) and a device mirror per slot.  n_slots slots
+ * (at least 2 = classic ping-pong) of block_k * layer_bytes; layer L lives in slot
+ * (L / block_k) % n_slots at offset (L % block_k) * layer_bytes (slot_for / weight_offset,
+ * hetero_scratch.rs:565-571,915-925).  DMAs run on the engine's copy stream with
+ * hipMemcpyAsync; the FFN kernels read the mirror on the compute stream; events order the
+ * two, so DMA of layer L+1 overlaps the FFN of layer L. */
+typedef struct hh_streamer hh_streamer;
+
+/* StreamingScratch::allocate_for_pool (hetero_scratch.rs:87-236), pinned-host path:
+ * block_k 0 is taken as 1 and n_slots below 2 as 2, as the reference does. */
+hh_status hh_streamer_create(hh_engine* e, size_t layer_bytes, size_t block_k, size_t n_slots, hh_streamer** out);
+/* Waits for both engine streams, then frees slots, mirrors and events. */
+void hh_streamer_destroy(hh_streamer* s);
+/* slot_for (hetero_scratch.rs:565-571). */
+hh_status hh_streamer_slot_for(const hh_streamer* s, size_t layer, size_t* slot);
+/* weight_offset (hetero_scratch.rs:915-925): byte offset of a tensor of `layer` inside the
+ * mirror that hh_streamer_bind returns. */
+hh_status hh_streamer_weight_offset(const hh_streamer* s, size_t layer, size_t tensor_off, size_t* off);
+/* prepare_host_write + host_slot (hetero_scratch.rs:611-656): the pinned host address of
+ * `layer`'s region (layer_bytes writable bytes), after any DMA still reading that slot has
+ * completed. */
+hh_status hh_streamer_host_slot(hh_streamer* s, size_t layer, void** host_ptr);
+/* dma_ffn_keep_mapped / dma_ffn_slices_mapped (hetero_scratch.rs:678-849): enqueue the copy
+ * of bytes [off, off+len) of `layer`'s host region into its mirror on the copy stream.  The
+ * copy first waits for all work already enqueued on the compute stream (the FFN of the layer
+ * that held the slot before).  Marks the slot as staged for `layer`'s block. */
+hh_status hh_streamer_dma(hh_streamer* s, size_t layer, size_t off, size_t len);
+/* weight_bind (hetero_scratch.rs:853-908): the device mirror holding `layer` (owned by the
+ * streamer; never pass it to hh_buf_free) and the layer's byte offset in it; the compute
+ * stream waits for the slot's last DMA, so FFN calls enqueued after this read the new bytes.
+ * HH_ERR_INVALID when the slot's last DMA was for another block. */
+hh_status hh_streamer_bind(hh_streamer* s, size_t layer, hh_buf** mirror, size_t* layer_off);
 
 /* ------------------------------------------------------------------ timing ---------- */
 
