@@ -3,22 +3,22 @@
 
 Workload: Llama-3-8B-shaped SwiGLU FFN, d_model=4096,
 d_ff=14336, 32 layers resident in HBM, batch 1, gate/up/down in Q4_K.  One step = one
-token through the FFN of all 32 layers: per layer one fused gate/up+SwiGLU kernel and one
-down kernel, all enqueued on the engine's compute stream.  Inputs are synthetic (seeded
-splitmix64 Q4_K blocks generated on the device, N(0,1) f32 activations per layer) and are
-resident in HBM before the timed region starts.
+token through the FFN of all 32 layers: one launch per layer of the persistent FFN kernel
+(gate/up + SwiGLU, grid barrier, down; hh_ffn_dev), all on the engine's compute stream.
+Inputs are synthetic (seeded splitmix64 Q4_K blocks generated on the device, N(0,1) f32
+activations per layer) and are resident in HBM before the timed region starts.
 
 value = algorithmic bytes per step / time per step, where algorithmic bytes per layer =
-packed weights read once (99,090,432 B) + x in (16,384 B) + y out (16,384 B); the fused
-d_ff intermediate is excluded.  FFN tok/s = 1 / time per step.
+packed weights read once (99,090,432 B) + x in (16,384 B) + y out (16,384 B); the d_ff
+intermediate is excluded.  FFN tok/s = 1 / time per step.
 
-roofline: the fused gate/up kernel (2/3 of the bytes, the dominant kernel), timed with HIP
-events on the compute stream around a region of its launches alone (32 layers x up to 50
-steps, issued through the FFN's two-call form hh_ffn_begin_dev / hh_ffn_finish_dev, which
-runs the same kernels as hh_ffn_dev); achieved = its algorithmic bytes per launch
-(W_gate + W_up + x + h) / its mean launch duration.  traffic = HBM bytes per launch of that kernel measured with
+roofline: the persistent FFN kernel (the only kernel of the step), timed with HIP events on
+the compute stream over the timed region: achieved = algorithmic bytes per launch (one
+layer) / mean launch duration.  traffic = HBM bytes per launch of that kernel from
 rocprofv3 FETCH_SIZE / WRITE_SIZE passes (each scaled by what the counter reads for a
-256 MiB device copy, --copy-calibration), read from profiles/ when present.
+256 MiB device copy, --copy-calibration), read from profiles/ when present.  The
+two-launch form (hh_ffn_begin_dev / hh_ffn_finish_dev: gate/up kernel, then down kernel)
+is timed in further regions and reported beside it.
 cpu_baseline: the oracle's fp32 restatement of hayai-model's gemv_q4_k FFN (oracle/,
 OpenMP over rows) on a bounded sample of the same layers, host cores.
 """
@@ -40,7 +40,7 @@ D_MODEL, D_FF, LAYERS = 4096, 14336, 32
 Q4_K = 12
 PEAK_HBM_GBS = 8000.0
 CONFIG_ID = 2
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gateup_8b_bs1_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_ffnp_8b_bs1_traffic.json")
 
 
 def log(*a):
@@ -535,10 +535,10 @@ def main() -> int:
     gbs = bytes_step / (ms / 1e3) / 1e9
     log(f"[bench] {ms * 1e3:.1f} us/step (event), wall {wall / args.steps * 1e6:.1f} us/step, {gbs:.1f} GB/s")
 
-    # Per-kernel durations: further timed regions issuing the same kernels through the FFN's
-    # two-call form -- gate/up launches alone over all layers, then gate/up + down -- each
-    # bracketed by events on the compute stream (events between single launches would add
-    # their own overhead to every launch).  down = (gate/up + down) - gate/up.
+    # The two-launch form of the same op for comparison: further timed regions issuing its
+    # kernels through the FFN's two-call form -- gate/up launches alone over all layers,
+    # then gate/up + down -- each bracketed by events on the compute stream.
+    # down = (gate/up + down) - gate/up.
     n_prof = max(1, min(args.steps, 50))
 
     def region(with_down: bool) -> float:
@@ -558,7 +558,10 @@ def main() -> int:
     dn = region(True) - gu
     gu_gbs = gateup_bytes() / (gu / 1e3) / 1e9
     dn_gbs = (D_MODEL * hayai_amd.row_bytes(Q4_K, D_FF) + 4 * D_FF + 4 * D_MODEL) / (dn / 1e3) / 1e9
-    log(f"[bench] gate/up kernel {gu * 1e3:.2f} us ({gu_gbs:.0f} GB/s), down kernel {dn * 1e3:.2f} us ({dn_gbs:.0f} GB/s)")
+    log(f"[bench] two-launch form: gate/up kernel {gu * 1e3:.2f} us ({gu_gbs:.0f} GB/s), down kernel "
+        f"{dn * 1e3:.2f} us ({dn_gbs:.0f} GB/s)")
+    layer_us = ms * 1e3 / LAYERS
+    layer_gbs = layer_bytes() / (layer_us / 1e6) / 1e9
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -587,11 +590,13 @@ def main() -> int:
                    "layers": LAYERS, "batch": 1, "weights": "Q4_K", "act": "silu"},
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "ffn_tok_s": round(1e3 / ms, 2),
-        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes": gateup_bytes(),
-                     "kernel": "fused gate/up + SwiGLU (Q4_K, 14336x4096 x2)", "mean_us": round(gu * 1e3, 3),
-                     "down_kernel_us": round(dn * 1e3, 3), "down_kernel_gbs": round(dn_gbs, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(layer_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(layer_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes": layer_bytes(),
+                     "kernel": "hh_q4k_ffnp_g1_d4: persistent FFN layer (gate/up + SwiGLU, grid barrier, down)",
+                     "mean_us": round(layer_us, 3)},
+        "two_launch_form": {"gateup_kernel_us": round(gu * 1e3, 3), "gateup_kernel_gbs": round(gu_gbs, 1),
+                            "down_kernel_us": round(dn * 1e3, 3), "down_kernel_gbs": round(dn_gbs, 1)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -2,6 +2,7 @@
 #include "gemv.hip"
 #include "q4k.hip"
 #include "lut.hip"
+#include "q4k_ffn.hip"
 #include "q4k_mm.hip"
 #include "moe.hip"
 #include "dequant.hip"

@@ -105,12 +105,14 @@ HH_DEV uint64_t hh_load_coherent(const uint64_t* p) {
 }
 
 // Quantize n f32 values (n % 32 == 0) into digits: 4 lanes per 32-element sub-block,
-// chunk c = 8 elements.  All threads of the workgroup must call it (quads stay whole
-// because the stride is a multiple of 4 and n/8 is a multiple of 4).  COHERENT: write with
+// chunk c = 8 elements.  Threads first, first + stride, ... take chunks (by default the
+// whole workgroup; quads stay whole because first and stride are multiples of 4 and n/8
+// is a multiple of 4).  COHERENT: write with
 // device-coherent stores (the digits are read by other workgroups in the same launch).
 template <bool COHERENT = false>
-HH_DEV void hh_quantize_digits(const float* src, uint32_t n, const hh_digits_ptr& dst) {
-    for (uint32_t c = threadIdx.x; c < n / 8; c += blockDim.x) {
+HH_DEV void hh_quantize_digits(const float* src, uint32_t n, const hh_digits_ptr& dst, uint32_t first = threadIdx.x,
+                               uint32_t stride = blockDim.x) {
+    for (uint32_t c = first; c < n / 8; c += stride) {
         const float4 t0 = reinterpret_cast<const float4*>(src)[2 * c];
         const float4 t1 = reinterpret_cast<const float4*>(src)[2 * c + 1];
         const float v[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};

@@ -413,6 +413,69 @@ hh_status hh_engine::enqueue_q4k_ffn(const hh_ffn_desc* d, const uint8_t* wg, co
     return HH_OK;
 }
 
+// Must match struct hh_ffnp_args in kernels/q4k_ffn.hip.
+struct FfnpArgs {
+    const uint8_t* wg;
+    const uint8_t* wu;
+    const uint8_t* wd;
+    const float* x;
+    float* y;
+    uint8_t* hx;
+    unsigned* bar;
+    uint64_t rb1, rb2;
+    uint32_t d_model, d_ff, gen;
+    int32_t act;
+};
+
+hh_status hh_engine::enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu,
+                                      const uint8_t* wd, const float* x, float* y) {
+    const size_t dm = d->d_model, df = d->d_ff;
+    if (!ffnp || q4k_generic || dm % 256 || df % 256 || dm > 8192 || df > 32768 ||
+        (((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd | (uintptr_t)x) & 15u))
+        return HH_ERR_UNSUPPORTED_DEVICE;
+    const int w1 = dm <= 4096 ? 1 : 2;
+    int w2 = 1;
+    while ((size_t)w2 * 64 < df / 64) w2 *= 2;
+    if (w2 < w1) w2 = w1;  // instantiated pairs: g1 with d1..d8, g2 with d2..d8
+    const std::string name = "hh_q4k_ffnp_g" + std::to_string(w1) + "_d" + std::to_string(w2);
+    hipFunction_t fn;
+    HH_TRY(kernel(name, &fn));
+    const int block = 9 * 64;  // 8 compute waves + the exchange wave
+    const size_t G0 = (size_t)props.multiProcessorCount;
+    // LDS: digits (x, then h) + gate/up row sums + down lane partials + 128 B staging (the
+    // kernel's layout)
+    const size_t NG = df / 8;
+    const size_t rr_max = 2 * 8 * ((NG + G0 - 1) / G0);
+    const size_t rows2_max = (dm + G0 - 1) / G0;
+    const size_t dig = std::max(2 * dm + (dm / 32) * 8, 2 * df + (df / 8) * 4);
+    const size_t smem = ((dig + 15) & ~size_t(15)) + ((rr_max * w1 + 3) & ~size_t(3)) * 4 +
+                        rows2_max * (size_t)w2 * 64 * 4 + 128;
+    if (smem > props.sharedMemPerBlock) return HH_ERR_UNSUPPORTED_DEVICE;
+    int occ = 0;
+    auto it = blocks_per_cu.find(name);
+    if (it != blocks_per_cu.end()) {
+        occ = it->second;
+    } else {
+        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, block, smem) != hipSuccess) occ = 0;
+        blocks_per_cu[name] = occ;
+    }
+    // Every workgroup must be resident at once (grid barrier): one per CU.  Never more, even
+    // when the occupancy calculator reports room for two: it counts wave slots per CU, but a
+    // 9-wave workgroup puts 3 waves on one SIMD, so a second one may not fit beside it.
+    if (occ < 1) return HH_ERR_UNSUPPORTED_DEVICE;
+    const size_t grid = G0;
+    HH_TRY(grow(&ws_hq, &ws_hq_cap, 3 * df + 16));
+    FfnpArgs a{wg, wu, wd, x, y, (uint8_t*)ws_hq, (unsigned*)grid_sync, (uint64_t)((dm / 256) * 144),
+               (uint64_t)((df / 256) * 144), (uint32_t)dm, (uint32_t)df, 0u, d->act};
+    if (++ffn_gen == 0) ffn_gen = 1;
+    a.gen = ffn_gen;
+    void* params[] = {&a};
+    hipError_t err =
+        hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
+    if (err != hipSuccess) return hip_fail(err, "launch(persistent q4k ffn)");
+    return HH_OK;
+}
+
 hh_status hh_engine::check_device_error() {
     unsigned flag = 0;
     HH_TRY_HIP(hipStreamSynchronize(stream), "hipStreamSynchronize");
@@ -467,7 +530,9 @@ hh_status hh_engine::enqueue_ffn_finish(const hh_ffn_desc* d, const uint8_t* pac
 
 hh_status hh_engine::enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y) {
     if (d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K && d->type_down == HH_TYPE_Q4_K) {
-        hh_status fst = enqueue_q4k_ffn(d, pack + d->gate_off, pack + d->up_off, pack + d->down_off, x, y);
+        hh_status fst = enqueue_q4k_ffnp(d, pack + d->gate_off, pack + d->up_off, pack + d->down_off, x, y);
+        if (fst == HH_ERR_UNSUPPORTED_DEVICE)
+            fst = enqueue_q4k_ffn(d, pack + d->gate_off, pack + d->up_off, pack + d->down_off, x, y);
         if (fst == HH_OK) {
             ffn_stage_valid = false;
             ffn_calls += 3;
@@ -728,6 +793,8 @@ static std::vector<std::string> required_kernels() {
         for (const char* kind : {"hh_q4k_mm_t", "hh_q4k_mm_gateup_t"}) k.push_back(std::string(kind) + std::to_string(tt));
     k.push_back("hh_mm_prep");
     k.push_back("hh_lut_gemv");
+    for (const char* f : {"g1_d1", "g1_d2", "g1_d4", "g1_d8", "g2_d2", "g2_d4", "g2_d8"})
+        k.push_back(std::string("hh_q4k_ffnp_") + f);
     k.push_back("hh_moe_route");
     for (int t : {16, 32, 64})
         for (const char* kind : {"hh_moe_gateup_t", "hh_moe_down_t"}) k.push_back(std::string(kind) + std::to_string(t));
@@ -773,6 +840,7 @@ hh_status engine_create(int device, hh_engine** out) {
     if (const char* b = getenv("HAYAI_HIP_BLOCKS_PER_CU")) e->blocks_per_cu_override = atoi(b);
     if (const char* g = getenv("HAYAI_HIP_Q4K_GENERIC")) e->q4k_generic = atoi(g) != 0;
     if (const char* f = getenv("HAYAI_HIP_FFN_FUSED")) e->ffn_fused = atoi(f) != 0;
+    if (const char* f = getenv("HAYAI_HIP_FFNP")) e->ffnp = atoi(f) != 0;
     if (const char* c = getenv("HAYAI_HIP_COOP")) e->coop_launch = atoi(c) != 0;
     err = hipMalloc(&e->grid_sync, kBarBytes);
     if (err == hipSuccess) err = hipMemset(e->grid_sync, 0, kBarBytes);

@@ -125,6 +125,7 @@ struct hh_engine {
     bool ffn_stage_valid = false;
     bool ffn_stage_digits = false;  // ws_hq holds the digits of ws_h
     bool ffn_fused = false;     // HAYAI_HIP_FFN_FUSED=1: one-launch Q4_K FFN (grid barrier)
+    bool ffnp = true;           // HAYAI_HIP_FFNP=0: skip the persistent pipelined Q4_K FFN
     bool coop_launch = false;   // HAYAI_HIP_COOP=1: cooperative launch API for the fused kernel
     int blocks_per_cu_override = 0;  // HAYAI_HIP_BLOCKS_PER_CU
     bool q4k_generic = false;        // HAYAI_HIP_Q4K_GENERIC=1: skip the int8-digit Q4_K kernels
@@ -160,6 +161,11 @@ struct hh_engine {
     // the shape has no fused instantiation.
     hh_status enqueue_q4k_ffn(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                               const float* x, float* y);
+    // Persistent one-launch Q4_K FFN layer with the down weights prefetched across the grid
+    // barrier (q4k_ffn.hip); HH_ERR_UNSUPPORTED_DEVICE when the shape, alignment or
+    // occupancy does not allow it.
+    hh_status enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
+                               const float* x, float* y);
     // Batched GEMV Y[b][m] = W . X[b] (x, y device pointers, row-major by token).  Q4_K with
     // 2 <= batch uses the MFMA kernels in chunks of up to 64 tokens; other formats (and
     // batch 1) run one GEMV per token, as the reference's orchestrator does
