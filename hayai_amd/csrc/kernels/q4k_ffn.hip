@@ -196,7 +196,7 @@ HH_DEV bool hh_barrier_wait(unsigned* bar, unsigned gen) {
 }
 
 
-template <int WPT1, int WPT2, int D>
+template <int WPT1, int WPT2, int D, int P>
 HH_DEV void hh_ffnp_body(const hh_ffnp_args& a) {
     extern __shared__ __attribute__((aligned(16))) char hh_smem[];
     constexpr uint32_t TEAM1 = WPT1 * HH_WAVE, TPW1 = HH_FFNP_CW / WPT1;
@@ -270,9 +270,14 @@ HH_DEV void hh_ffnp_body(const hh_ffnp_args& a) {
 
     // Prologue: every compute thread first loads its 8 elements of x, then (after a
     // workgroup barrier, so all of the CU's x requests are queued before any ring request)
-    // the ring's first D items go out, and x is quantized into per-32 digits in LDS while
-    // the ring is in flight (a wave's loads return in issue order: x arrives first).
+    // the ring's first P items go out, x is quantized into per-32 digits in LDS, and only
+    // then the rest of the ring: a deep ring burst at start would delay x (its requests
+    // share the memory queues with every CU's ring), while a short one gets x back fast.
     hh_q4k_data ring[D];
+    auto fill = [&](int s) {
+        if ((uint32_t)s < n1p) issue1((uint32_t)s, ring[s]);
+        else issue2((uint32_t)s - n1p, ring[s]);
+    };
     const uint32_t c = tid;  // chunk of 8 elements (d_model <= 8 * 512 per pass)
     const bool has = !xw && c < dm / 8;
     const float4* x4 = reinterpret_cast<const float4*>(a.x);
@@ -284,15 +289,14 @@ HH_DEV void hh_ffnp_body(const hh_ffnp_args& a) {
     __syncthreads();
     if (!xw) {
 #pragma unroll
-        for (int s = 0; s < D; s++) {
-            if ((uint32_t)s < n1p) issue1((uint32_t)s, ring[s]);
-            else issue2((uint32_t)s - n1p, ring[s]);
-        }
+        for (int s = 0; s < P; s++) fill(s);
         hh_ffnp_digits_chunk(t0, t1, c, has, xd);
         for (uint32_t c2 = c + HH_FFNP_CW * HH_WAVE; c2 < dm / 8; c2 += HH_FFNP_CW * HH_WAVE) {
             const float4 u0 = x4[2 * c2], u1 = x4[2 * c2 + 1];  // d_model > 4096: later passes
             hh_ffnp_digits_chunk(u0, u1, c2, true, xd);
         }
+#pragma unroll
+        for (int s = P; s < D; s++) fill(s);
     }
     __syncthreads();
 
@@ -423,15 +427,15 @@ HH_DEV void hh_ffnp_body(const hh_ffnp_args& a) {
 }
 
 // hh_q4k_ffnp_g<WPT1>_d<WPT2>: WPT1 waves per gate/up row (d_model <= 4096 * WPT1),
-// WPT2 waves per down row (d_ff <= 4096 * WPT2), ring depth D.
-#define HH_FFNP(G1, G2, D)                                                                      \
+// WPT2 waves per down row (d_ff <= 4096 * WPT2), ring depth D, P ring items issued before x.
+#define HH_FFNP(G1, G2, D, P)                                                                   \
     extern "C" __global__ void __launch_bounds__(HH_FFNP_BLOCK) hh_q4k_ffnp_g##G1##_d##G2(const hh_ffnp_args a) { \
-        hh_ffnp_body<G1, G2, D>(a);                                                             \
+        hh_ffnp_body<G1, G2, D, P>(a);                                                          \
     }
-HH_FFNP(1, 1, 3)
-HH_FFNP(1, 2, 3)
-HH_FFNP(1, 4, 3)
-HH_FFNP(1, 8, 3)
-HH_FFNP(2, 2, 3)
-HH_FFNP(2, 4, 3)
-HH_FFNP(2, 8, 3)
+HH_FFNP(1, 1, 3, 1)
+HH_FFNP(1, 2, 3, 1)
+HH_FFNP(1, 4, 3, 1)
+HH_FFNP(1, 8, 3, 1)
+HH_FFNP(2, 2, 3, 1)
+HH_FFNP(2, 4, 3, 1)
+HH_FFNP(2, 8, 3, 1)
