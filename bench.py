@@ -3,22 +3,24 @@
 
 Workload: Llama-3-8B-shaped SwiGLU FFN, d_model=4096,
 d_ff=14336, 32 layers resident in HBM, batch 1, gate/up/down in Q4_K.  One step = one
-token through the FFN of all 32 layers: one launch per layer of the persistent FFN kernel
-(gate/up + SwiGLU, grid barrier, down; hh_ffn_dev), all on the engine's compute stream.
+token through the FFN of all 32 layers (hh_ffn_dev per layer: the ring gate/up kernel, which
+writes h as int8 digits, then the ring down kernel), all on the engine's compute stream.
 Inputs are synthetic (seeded splitmix64 Q4_K blocks generated on the device, N(0,1) f32
 activations per layer) and are resident in HBM before the timed region starts.
 
+The step is timed eagerly (one dispatch per kernel; value) and also as a HIP graph of the
+same 32-layer step captured once and replayed (hh_graph_*), reported beside it.
 value = algorithmic bytes per step / time per step, where algorithmic bytes per layer =
 packed weights read once (99,090,432 B) + x in (16,384 B) + y out (16,384 B); the d_ff
 intermediate is excluded.  FFN tok/s = 1 / time per step.
 
-roofline: the persistent FFN kernel (the only kernel of the step), timed with HIP events on
-the compute stream over the timed region: achieved = algorithmic bytes per launch (one
-layer) / mean launch duration.  traffic = HBM bytes per launch of that kernel from
+roofline: the dominant kernel, the ring gate/up kernel (66 MB of the layer's 99 MB), timed
+with HIP events on the compute stream around a region of its launches alone (32 layers x
+50, back to back): achieved = its algorithmic bytes (W_gate + W_up + x + h as f32) / time per
+launch.  traffic = HBM bytes per launch of that kernel from
 rocprofv3 FETCH_SIZE / WRITE_SIZE passes (each scaled by what the counter reads for a
-256 MiB device copy, --copy-calibration), read from profiles/ when present.  The
-two-launch form (hh_ffn_begin_dev / hh_ffn_finish_dev: gate/up kernel, then down kernel)
-is timed in further regions and reported beside it.
+256 MiB device copy, --copy-calibration), read from profiles/ when present.  The down kernel
+is timed the same way and reported beside it.
 cpu_baseline: the oracle's fp32 restatement of hayai-model's gemv_q4_k FFN (oracle/,
 OpenMP over rows) on a bounded sample of the same layers, host cores.
 """
@@ -40,7 +42,7 @@ D_MODEL, D_FF, LAYERS = 4096, 14336, 32
 Q4_K = 12
 PEAK_HBM_GBS = 8000.0
 CONFIG_ID = 2
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_ffnp_8b_bs1_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gu_ring_8b_bs1_traffic.json")
 
 
 def log(*a):
@@ -519,49 +521,57 @@ def main() -> int:
         cal.copy_from(pack, 256 << 20)
         eng.sync()
         cal.free()
+    def timed(run, n) -> float:  # ms per call of run(), events on the compute stream
+        e0, e1 = eng.event(), eng.event()
+        e0.record()
+        for _ in range(n):
+            run()
+        e1.record()
+        eng.sync()
+        return e0.elapsed_ms(e1) / n
+
     for _ in range(args.warmup):
         step()
     eng.sync()
-    e0, e1 = eng.event(), eng.event()
     t0 = time.perf_counter()
-    e0.record()
-    for _ in range(args.steps):
-        step()
-    e1.record()
-    eng.sync()
+    ms_eager = timed(step, args.steps)
     wall = time.perf_counter() - t0
-    ms = e0.elapsed_ms(e1) / args.steps
+    graph = eng.capture(step)
+    for _ in range(3):
+        graph.launch()
+    eng.sync()
+    ms_graph = timed(graph.launch, args.steps)
+    graph.free()
+    ms = ms_eager
     bytes_step = layer_bytes() * LAYERS
     gbs = bytes_step / (ms / 1e3) / 1e9
-    log(f"[bench] {ms * 1e3:.1f} us/step (event), wall {wall / args.steps * 1e6:.1f} us/step, {gbs:.1f} GB/s")
+    gbs_graph = bytes_step / (ms_graph / 1e3) / 1e9
+    log(f"[bench] {ms * 1e3:.1f} us/step (event), wall {wall / args.steps * 1e6:.1f} us/step, {gbs:.1f} GB/s; "
+        f"graph replay {ms_graph * 1e3:.1f} us/step, {gbs_graph:.1f} GB/s")
 
-    # The two-launch form of the same op for comparison: further timed regions issuing its
-    # kernels through the FFN's two-call form -- gate/up launches alone over all layers,
-    # then gate/up + down -- each bracketed by events on the compute stream.
-    # down = (gate/up + down) - gate/up.
+    # Each kernel of the step on its own, through the FFN's two-call form (it issues exactly
+    # the kernels of the one-call op): a region of gate/up launches alone over all layers,
+    # then one of gate/up + down, each bracketed by events on the compute stream;
+    # down = (gate/up + down) - gate/up.  Back-to-back launches of one kernel: the time per
+    # launch includes the dispatch gap between launches.
     n_prof = max(1, min(args.steps, 50))
 
     def region(with_down: bool) -> float:
-        a, b = eng.event(), eng.event()
-        a.record()
-        for _ in range(n_prof):
+        def run():
             for l in range(LAYERS):
                 base = l * stride
                 eng.ffn_begin_dev(desc, pack, base, xbuf, 4 * D_MODEL * l)
                 if with_down:
                     eng.ffn_finish_dev(desc, pack, base, ybuf, 4 * D_MODEL * l)
-        b.record()
-        eng.sync()
-        return a.elapsed_ms(b) / (n_prof * LAYERS)
+        return timed(run, n_prof) / LAYERS
 
     gu = region(False)
     dn = region(True) - gu
     gu_gbs = gateup_bytes() / (gu / 1e3) / 1e9
     dn_gbs = (D_MODEL * hayai_amd.row_bytes(Q4_K, D_FF) + 4 * D_FF + 4 * D_MODEL) / (dn / 1e3) / 1e9
-    log(f"[bench] two-launch form: gate/up kernel {gu * 1e3:.2f} us ({gu_gbs:.0f} GB/s), down kernel "
-        f"{dn * 1e3:.2f} us ({dn_gbs:.0f} GB/s)")
+    log(f"[bench] per kernel: gate/up {gu * 1e3:.2f} us ({gu_gbs:.0f} GB/s), down {dn * 1e3:.2f} us "
+        f"({dn_gbs:.0f} GB/s)")
     layer_us = ms * 1e3 / LAYERS
-    layer_gbs = layer_bytes() / (layer_us / 1e6) / 1e9
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -587,16 +597,19 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic (seeded Q4_K blocks, N(0,1) f32 activations)",
         "config": {"workload": "llama3-8b-ffn-q4_k-bs1-32layers-resident", "d_model": D_MODEL, "d_ff": D_FF,
-                   "layers": LAYERS, "batch": 1, "weights": "Q4_K", "act": "silu"},
+                   "layers": LAYERS, "batch": 1, "weights": "Q4_K", "act": "silu",
+                   "launch": "eager, 2 kernels per layer"},
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "ffn_tok_s": round(1e3 / ms, 2),
-        "roofline": {"bound": "hbm", "achieved": round(layer_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(layer_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes": layer_bytes(),
-                     "kernel": "hh_q4k_ffnp_g1_d4: persistent FFN layer (gate/up + SwiGLU, grid barrier, down)",
-                     "mean_us": round(layer_us, 3)},
-        "two_launch_form": {"gateup_kernel_us": round(gu * 1e3, 3), "gateup_kernel_gbs": round(gu_gbs, 1),
-                            "down_kernel_us": round(dn * 1e3, 3), "down_kernel_gbs": round(dn_gbs, 1)},
+        "us_per_layer": round(layer_us, 3),
+        "graph_replay": {"ms_per_step": round(ms_graph, 5), "value": round(gbs_graph, 2),
+                         "ffn_tok_s": round(1e3 / ms_graph, 2)},
+        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes": gateup_bytes(),
+                     "kernel": "hh_q4k_gu_ring_g1: ring gate/up + SwiGLU, h as int8 digits",
+                     "mean_us": round(gu * 1e3, 3)},
+        "down_kernel": {"kernel": "hh_q4k_dn_ring_d4", "us": round(dn * 1e3, 3), "gbs": round(dn_gbs, 1)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

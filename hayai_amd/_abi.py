@@ -136,6 +136,10 @@ SIGNATURES = {
     "hh_event_destroy": (None, [P]),
     "hh_event_record": (ST, [P, P]),
     "hh_event_elapsed_ms": (ST, [P, P, C.POINTER(C.c_float)]),
+    "hh_graph_begin": (ST, [P]),
+    "hh_graph_end": (ST, [P, PP]),
+    "hh_graph_launch": (ST, [P]),
+    "hh_graph_destroy": (None, [P]),
     "hh_synth_weights_dev": (ST, [P, I, P, SZ, SZ, C.c_uint64, C.c_float, C.c_float]),
 }
 

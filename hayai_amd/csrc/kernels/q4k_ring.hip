@@ -1,0 +1,278 @@
+// The Q4_K FFN at batch 1 as two streaming launches (gfx950):
+//   hh_q4k_gu_ring_g<W1>:  h = act(W_gate . x) * (W_up . x), written as int8 digits
+//                          (ffn_begin_gate_up_scratch, crates/hayai-core/src/
+//                          stream_infer.rs:3752-3808, with the activation of :3836-3840)
+//   hh_q4k_dn_ring_d<W2>:  y = W_down . h from those digits (ffn_finish_scratch, :3809-3864)
+// (Compiled after q4k_ffn.hip in the same translation unit; uses its ring and digit helpers.)
+//
+// Each launch is one weight stream with nothing else on its path: a kernel boundary costs
+// less than any exchange of h inside one launch (see q4k_ffn.hip), so the layer is split
+// there.  Both kernels use the persistent kernel's ring: every compute wave keeps D items
+// (one 64-column Q4_K unit of one row per lane: 16-byte block header + 32 qs bytes) in
+// flight, addressed by a wave-uniform row base plus fixed lane offsets, so the wait counts
+// are static and HBM never waits for the math.
+//
+// Intermediate: q1[d_ff] | q2[d_ff] int8 | scale[d_ff/8] f32, h ~ scale * (q1 + q2/256) per
+// granule of 8 rows (granules never straddle workgroups).
+
+#define HH_RING_BLOCK (HH_FFNP_CW * HH_WAVE)
+
+struct hh_gur_args {
+    const uint8_t* wg;  // W_gate [d_ff][rb1]
+    const uint8_t* wu;  // W_up   [d_ff][rb1]
+    const float* x;     // d_model f32, 16-byte aligned
+    uint8_t* hx;        // intermediate (above)
+    uint64_t rb1;       // row bytes of gate/up
+    uint32_t d_model;
+    uint32_t d_ff;
+    int32_t act;
+    uint32_t pad;
+};
+
+struct hh_dnr_args {
+    const uint8_t* wd;  // W_down [d_model][rb2]
+    const uint8_t* hx;  // intermediate (above), 16-byte aligned
+    float* y;           // d_model f32
+    uint64_t rb2;       // row bytes of down
+    uint32_t d_model;
+    uint32_t d_ff;
+};
+
+// Gate/up: workgroup w owns the 8-row granules [w*NG/G, (w+1)*NG/G) of W_gate and W_up; a
+// team of WPT1 waves reads one row (lane = unit, x as per-32 digits in registers).  After
+// the last row, wave 0 applies the activation to the workgroup's rows and writes their
+// digits.
+template <int WPT1, int D, int P>
+HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
+    extern __shared__ __attribute__((aligned(16))) char hh_smem[];
+    constexpr uint32_t TEAM1 = WPT1 * HH_WAVE, TPW1 = HH_FFNP_CW / WPT1;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid % HH_WAVE;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / HH_WAVE);
+    const uint32_t G = gridDim.x, w = blockIdx.x;
+    const uint32_t dm = a.d_model, dff = a.d_ff;
+    const uint32_t NG = dff / 8;
+    const uint32_t r0 = 8u * (uint32_t)(((uint64_t)w * NG) / G);
+    const uint32_t r1 = 8u * (uint32_t)(((uint64_t)(w + 1) * NG) / G);
+    const uint32_t RR = 2u * (r1 - r0);  // row reads: (gate, up) of each row
+    const uint32_t n1 = (RR + TPW1 - 1) / TPW1;
+    const uint32_t n1p = (n1 + D - 1) / D * D;
+
+    // LDS: [x digits][gate/up row sums][staging 128 B]
+    const uint32_t xbytes = 2u * dm + (dm / 32u) * 8u;
+    hh_digits_ptr xd;
+    xd.q1 = reinterpret_cast<int8_t*>(hh_smem);
+    xd.q2 = xd.q1 + dm;
+    xd.sc = reinterpret_cast<float*>(xd.q2 + dm);
+    xd.sum = xd.sc + dm / 32;
+    float* gu = reinterpret_cast<float*>(hh_smem + ((xbytes + 15u) & ~15u));  // [RR][WPT1]
+    uint8_t* stage = reinterpret_cast<uint8_t*>(gu + ((RR * WPT1 + 3u) & ~3u));
+
+    const uint32_t lane1 = tid % TEAM1, team1 = (wave / WPT1) % TPW1;
+    const bool act1 = lane1 < dm / 64;
+    const uint32_t u1 = act1 ? lane1 : 0u;
+    const uint8_t* const wgp = a.wg;
+    const uint8_t* const wup = a.wu;
+    const uint32_t oh = (u1 >> 2) * 144u, oq = oh + 16u + (u1 & 3u) * 32u;
+    // item j of this team: row read i = team1 + j*TPW1 (gate and up rows interleaved); reads
+    // past the workgroup's rows (ring padding) re-read the start of W_gate
+    auto issue = [&](uint32_t j, hh_q4k_data& s) {
+        const uint32_t i = team1 + j * TPW1;
+        const uint8_t* row = i < RR ? ((i & 1u) ? wup : wgp) + (size_t)(r0 + (i >> 1)) * a.rb1 : wgp;
+        s.h = hh_ld16(row + oh);
+        s.q0 = hh_ld16(row + oq);
+        s.q1 = hh_ld16(row + oq + 16);
+    };
+
+    // prologue: x loads first, then P ring items, x -> per-32 digits in LDS, the rest of the
+    // ring (x is not queued behind a burst of weight requests)
+    hh_q4k_data ring[D];
+    const uint32_t c = tid;  // chunk of 8 elements (d_model <= 8 * 512 per pass)
+    const bool has = c < dm / 8;
+    const float4* x4 = reinterpret_cast<const float4*>(a.x);
+    const float4 t0 = x4[2 * min(c, dm / 8 - 1)];
+    const float4 t1 = x4[2 * min(c, dm / 8 - 1) + 1];
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < P; s++) issue((uint32_t)s, ring[s]);
+    hh_ffnp_digits_chunk(t0, t1, c, has, xd);
+    for (uint32_t c2 = c + HH_RING_BLOCK; c2 < dm / 8; c2 += HH_RING_BLOCK) {
+        const float4 v0 = x4[2 * c2], v1 = x4[2 * c2 + 1];  // d_model > 4096: later passes
+        hh_ffnp_digits_chunk(v0, v1, c2, true, xd);
+    }
+#pragma unroll
+    for (int s = P; s < D; s++) issue((uint32_t)s, ring[s]);
+    __syncthreads();
+
+    {
+        hh_q4k_x xr;
+        hh_q4k_load_lane_x(xd, u1, xr);
+        for (uint32_t j0 = 0; j0 < n1p; j0 += D) {
+#pragma unroll
+            for (int s = 0; s < D; s++) {
+                const uint32_t j = j0 + (uint32_t)s;
+                const uint32_t i = team1 + j * TPW1;
+                if (i < RR) {  // wave-uniform
+                    float v = hh_q4k_unit(ring[s], xr);
+                    v = hh_wave_sum(act1 ? v : 0.f);
+                    if (lane == 0) gu[i * WPT1 + wave % WPT1] = v;
+                }
+                issue(j + D, ring[s]);
+            }
+        }
+    }
+    __syncthreads();  // row sums are in LDS
+
+    if (wave == 0) {
+        // h = act(g) * u, two int8 digits per element, one scale per granule of 8 rows
+        int8_t* gq1 = reinterpret_cast<int8_t*>(a.hx);
+        int8_t* gq2 = gq1 + dff;
+        float* gsc = reinterpret_cast<float*>(gq2 + dff);
+        for (uint32_t rho0 = 0; rho0 < r1 - r0; rho0 += HH_WAVE) {
+            const uint32_t rho = rho0 + lane;
+            const bool ok = rho < r1 - r0;  // granule-aligned: whole 8-lane groups agree
+            float hv = 0.f;
+            if (ok) {
+                float g = 0.f, u = 0.f;
+#pragma unroll
+                for (int k = 0; k < WPT1; k++) {
+                    g += gu[(2 * rho) * WPT1 + k];
+                    u += gu[(2 * rho + 1) * WPT1 + k];
+                }
+                hv = hh_act_mul(g, u, a.act);
+            }
+            float amax = fabsf(hv);
+#pragma unroll
+            for (int m = 1; m < 8; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, HH_WAVE));
+            const float scale = amax * (1.0f / 127.0f);
+            const float inv = amax > 0.f ? 127.0f / amax : 0.f;
+            const float d1 = fminf(fmaxf(rintf(hv * inv), -127.f), 127.f);
+            const float rr = hv - d1 * scale;
+            const float d2 = fminf(fmaxf(rintf(rr * inv * 256.0f), -127.f), 127.f);
+            stage[lane] = (uint8_t)(int8_t)(int)d1;
+            stage[64 + lane] = (uint8_t)(int8_t)(int)d2;
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): staged bytes visible to the wave
+            __builtin_amdgcn_wave_barrier();
+            if (ok && (lane & 7u) == 0) {
+                const uint32_t r = r0 + rho;
+                *reinterpret_cast<uint64_t*>(gq1 + r) = *reinterpret_cast<const uint64_t*>(stage + lane);
+                *reinterpret_cast<uint64_t*>(gq2 + r) = *reinterpret_cast<const uint64_t*>(stage + 64 + lane);
+                gsc[r / 8] = scale;
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+}
+
+// Down: workgroup w owns output rows [w*M/G, (w+1)*M/G); a team of WPT2 waves covers one row
+// (lane = unit).  A ninth wave copies the intermediate into LDS (global->LDS DMA) while the
+// compute waves' rings are already in flight, so neither waits behind the other's requests;
+// lane partials meet in LDS and a 32-lane DPP reduction per row writes y (fixed order:
+// deterministic).
+#define HH_DN_BLOCK ((HH_FFNP_CW + 1) * HH_WAVE)
+template <int WPT2, int D>
+HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
+    extern __shared__ __attribute__((aligned(16))) char hh_smem[];
+    constexpr uint32_t TEAM2 = WPT2 * HH_WAVE, TPW2 = HH_FFNP_CW / WPT2;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid % HH_WAVE;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / HH_WAVE);
+    const uint32_t G = gridDim.x, w = blockIdx.x;
+    const uint32_t dm = a.d_model, dff = a.d_ff;
+    const uint32_t q0 = (uint32_t)(((uint64_t)w * dm) / G);
+    const uint32_t q1 = (uint32_t)(((uint64_t)(w + 1) * dm) / G);
+    const uint32_t n2 = (q1 - q0 + TPW2 - 1) / TPW2;
+    const uint32_t n2p = (n2 + D - 1) / D * D;
+
+    // LDS: [intermediate][lane partials: rows x TEAM2]
+    const uint32_t hbytes = 2u * dff + (dff / 8u) * 4u;
+    int8_t* hq1 = reinterpret_cast<int8_t*>(hh_smem);
+    int8_t* hq2 = hq1 + dff;
+    float* hsc = reinterpret_cast<float*>(hq2 + dff);
+    float* part = reinterpret_cast<float*>(hh_smem + ((hbytes + 15u) & ~15u));
+
+    const uint32_t lane2 = tid % TEAM2, team2 = (wave / WPT2) % TPW2;
+    const bool act2 = lane2 < dff / 64;
+    const uint32_t u2 = act2 ? lane2 : 0u;
+    const uint8_t* const wdp = a.wd;
+    const uint32_t oh = (u2 >> 2) * 144u, oq = oh + 16u + (u2 & 3u) * 32u;
+    auto issue = [&](uint32_t k, hh_q4k_data& s) {  // item k: row team2 + k*TPW2
+        const uint32_t r = q0 + team2 + k * TPW2;
+        const uint8_t* row = r < q1 ? wdp + (size_t)r * a.rb2 : wdp;
+        s.h = hh_ld16(row + oh);
+        s.q0 = hh_ld16(row + oq);
+        s.q1 = hh_ld16(row + oq + 16);
+    };
+
+    hh_q4k_data ring[D];
+    if (wave < HH_FFNP_CW) {
+#pragma unroll
+        for (int s = 0; s < D; s++) issue((uint32_t)s, ring[s]);
+    } else {
+        // the intermediate -> LDS, every 16-byte chunk in flight at once
+        const uint32_t chunks = hbytes / 16u;
+        for (uint32_t c0 = 0; c0 < chunks; c0 += HH_WAVE) {
+            if (c0 + lane < chunks)
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void*)(a.hx + (size_t)(c0 + lane) * 16),
+                    (__attribute__((address_space(3))) void*)(hh_smem + (size_t)c0 * 16), 16, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+    __syncthreads();  // the intermediate is in LDS (the rings stay in flight)
+
+    if (wave < HH_FFNP_CW) {
+        hh_ffnp_h hr;
+        hh_ffnp_load_h(hq1, hq2, hsc, u2, hr);
+        for (uint32_t j0 = 0; j0 < n2p; j0 += D) {
+#pragma unroll
+            for (int s = 0; s < D; s++) {
+                const uint32_t k = j0 + (uint32_t)s;
+                const uint32_t rl = team2 + k * TPW2;  // local row
+                if (q0 + rl < q1) {                    // wave-uniform
+                    const float v = hh_ffnp_unit_g8(ring[s], hr);
+                    part[rl * TEAM2 + lane2] = act2 ? v : 0.f;  // reduced after the loop
+                }
+                issue(k + D, ring[s]);
+            }
+        }
+    }
+    __syncthreads();  // lane partials are in LDS
+    // y[q0 + rl] = sum over the TEAM2 lane partials of row rl: 32 threads per row, each sums
+    // TEAM2/32 consecutive partials, then a 32-lane DPP reduction (rows never straddle the
+    // 32-lane halves of a wave)
+    {
+        constexpr uint32_t PER = TEAM2 / 32;
+        const uint32_t nrows = q1 - q0;
+        for (uint32_t rl0 = 0; rl0 < nrows; rl0 += HH_DN_BLOCK / 32) {
+            const uint32_t rl = rl0 + tid / 32, seg = tid % 32;
+            float s = 0.f;
+            if (rl < nrows) {
+                const float* p = part + rl * TEAM2 + seg * PER;
+#pragma unroll
+                for (uint32_t i = 0; i < PER; i++) s += p[i];
+            }
+            s += hh_dpp<0xB1>(s);        // quad_perm [1,0,3,2]
+            s += hh_dpp<0x4E>(s);        // quad_perm [2,3,0,1]
+            s += hh_dpp<0x124>(s);       // row_ror:4
+            s += hh_dpp<0x128>(s);       // row_ror:8 -> each row of 16 holds its sum
+            s += hh_dpp<0x142, 0xA>(s);  // row_bcast:15 -> lanes 31 and 63 hold their half's sum
+            if (rl < nrows && seg == 31) a.y[q0 + rl] = s;
+        }
+    }
+}
+
+#define HH_GU_RING(G1)                                                                          \
+    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_q4k_gu_ring_g##G1(const hh_gur_args a) { \
+        hh_gu_ring_body<G1, 3, 1>(a);                                                           \
+    }
+#define HH_DN_RING(G2)                                                                          \
+    extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) hh_q4k_dn_ring_d##G2(const hh_dnr_args a) { \
+        hh_dn_ring_body<G2, 3>(a);                                                              \
+    }
+HH_GU_RING(1)
+HH_GU_RING(2)
+HH_DN_RING(1)
+HH_DN_RING(2)
+HH_DN_RING(4)
+HH_DN_RING(8)

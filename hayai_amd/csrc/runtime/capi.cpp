@@ -312,6 +312,7 @@ hh_status hh_gemv_batched(hh_engine* e, int t, size_t m, size_t n, const uint8_t
 hh_status hh_gemv_batched_dev(hh_engine* e, int t, size_t m, size_t n, const hh_buf* w, size_t w_off, const hh_buf* x,
                               size_t x_off, size_t batch, hh_buf* y, size_t y_off) {
     HH_NOT_NULL(e, "engine");
+    HH_TRY(e->no_capture("gemv_batched_dev"));
     HH_TRY(validate_shape(t, m, n));
     size_t xb, yb, rb;
     HH_TRY(batch_bytes(batch, n, &xb));
@@ -507,6 +508,7 @@ hh_status hh_ffn_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, siz
 hh_status hh_ffn_batched_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off, const hh_buf* x,
                              size_t x_off, size_t batch, hh_buf* y, size_t y_off) {
     HH_NOT_NULL(e, "engine");
+    HH_TRY(e->no_capture("ffn_batched_dev"));
     HH_TRY(validate_ffn(e, d, pack, pack_off));
     size_t xb;
     HH_TRY(batch_bytes(batch, d->d_model, &xb));
@@ -644,6 +646,7 @@ hh_status hh_route_experts_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf*
                                const hh_buf* bias, size_t bias_off, size_t T, hh_buf* ids, size_t ids_off,
                                hh_buf* weights, size_t weights_off) {
     HH_NOT_NULL(e, "engine");
+    HH_TRY(e->no_capture("route_experts_dev"));
     HH_TRY(validate_moe_desc(d));
     size_t lb, kb;
     HH_TRY(batch_bytes(T, d->n_experts, &lb));
@@ -700,6 +703,7 @@ hh_status hh_moe_ffn_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* exper
                          const hh_buf* x, size_t x_off, size_t T, const hh_buf* ids, size_t ids_off,
                          const hh_buf* weights, size_t weights_off, hh_buf* y, size_t y_off) {
     HH_NOT_NULL(e, "engine");
+    HH_TRY(e->no_capture("moe_ffn_dev"));
     HH_TRY(validate_moe_desc(d));
     HH_TRY(validate_moe_experts(e, d, experts, experts_off));
     size_t xb, kb;
@@ -724,6 +728,7 @@ hh_status hh_moe_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* experts, 
                      const hh_buf* logits, size_t logits_off, const hh_buf* bias, size_t bias_off, const hh_buf* x,
                      size_t x_off, size_t T, hh_buf* y, size_t y_off) {
     HH_NOT_NULL(e, "engine");
+    HH_TRY(e->no_capture("moe_dev"));
     HH_TRY(validate_moe_desc(d));
     HH_TRY(validate_moe_experts(e, d, experts, experts_off));
     size_t xb, kb, lb;
@@ -791,6 +796,67 @@ hh_status hh_event_elapsed_ms(hh_event* a, hh_event* b, float* ms) {
     HH_TRY_HIP(hipEventSynchronize(b->ev), "hipEventSynchronize");
     HH_TRY_HIP(hipEventElapsedTime(ms, a->ev, b->ev), "hipEventElapsedTime");
     return HH_OK;
+}
+
+// ---------------------------------------------------------------- graphs -------------
+
+struct hh_graph {
+    hh_engine* engine;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+hh_status hh_graph_begin(hh_engine* e) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    if (e->capturing) return fail(HH_ERR_INVALID, "graph_begin: a capture is already open on this engine");
+    HH_TRY_HIP(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    e->capturing = true;
+    return HH_OK;
+}
+
+hh_status hh_graph_end(hh_engine* e, hh_graph** out) {
+    HH_NOT_NULL(e, "engine");
+    HH_NOT_NULL(out, "out");
+    *out = nullptr;
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    if (!e->capturing) return fail(HH_ERR_INVALID, "graph_end: no capture is open on this engine");
+    e->capturing = false;
+    hipGraph_t g = nullptr;
+    HH_TRY_HIP(hipStreamEndCapture(e->stream, &g), "hipStreamEndCapture");
+    hipGraphExec_t x = nullptr;
+    hipError_t err = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    if (err != hipSuccess) {
+        hipGraphDestroy(g);
+        return hip_fail(err, "hipGraphInstantiate");
+    }
+    hh_graph* h = new (std::nothrow) hh_graph{e, g, x};
+    if (!h) {
+        hipGraphExecDestroy(x);
+        hipGraphDestroy(g);
+        return fail(HH_ERR_OUT_OF_MEMORY, "host allocation failed");
+    }
+    *out = h;
+    return HH_OK;
+}
+
+hh_status hh_graph_launch(hh_graph* g) {
+    HH_NOT_NULL(g, "graph");
+    HH_TRY(g->engine->select());
+    std::lock_guard<std::mutex> lk(g->engine->ws_mutex);
+    if (g->engine->capturing) return fail(HH_ERR_INVALID, "graph_launch: the engine's stream is being captured");
+    HH_TRY_HIP(hipGraphLaunch(g->exec, g->engine->stream), "hipGraphLaunch");
+    return HH_OK;
+}
+
+void hh_graph_destroy(hh_graph* g) {
+    if (!g) return;
+    g->engine->select();
+    hipGraphExecDestroy(g->exec);
+    hipGraphDestroy(g->graph);
+    delete g;
 }
 
 // ---------------------------------------------------------------- synthetic data -----

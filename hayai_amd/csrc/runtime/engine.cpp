@@ -131,8 +131,16 @@ int hh_engine::resident_blocks(const std::string& name, int block) {
     return nb;
 }
 
+hh_status hh_engine::no_capture(const char* what) const {
+    if (capturing) return fail(HH_ERR_INVALID, "%s cannot be captured into a graph", what);
+    return HH_OK;
+}
+
 hh_status hh_engine::grow(void** p, size_t* cap, size_t need) {
     if (need <= *cap && *p) return HH_OK;
+    if (capturing)
+        return fail(HH_ERR_INVALID,
+                    "a workspace would grow during graph capture: run the sequence once before capturing it");
     if (*p) {
         hipError_t e1 = hipStreamSynchronize(stream);
         if (e1 != hipSuccess) return hip_fail(e1, "hipStreamSynchronize");
@@ -358,7 +366,8 @@ constexpr size_t kBarErrOffset = kBarLine * (2 * 16 + 1);
 hh_status hh_engine::enqueue_q4k_ffn(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                                      const float* x, float* y) {
     const size_t dm = d->d_model, df = d->d_ff;
-    if (!ffn_fused || q4k_generic || dm % 256 || df % 256 || dm / 64 > 512 || df / 64 > 512 ||
+    // (its grid barrier carries a per-launch generation: a graph replay would reuse it)
+    if (capturing || !ffn_fused || q4k_generic || dm % 256 || df % 256 || dm / 64 > 512 || df / 64 > 512 ||
         (((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd | (uintptr_t)x) & 15u))
         return HH_ERR_UNSUPPORTED_DEVICE;
     int wg_t = 1, wd_t = 1;
@@ -430,7 +439,8 @@ struct FfnpArgs {
 hh_status hh_engine::enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu,
                                       const uint8_t* wd, const float* x, float* y) {
     const size_t dm = d->d_model, df = d->d_ff;
-    if (!ffnp || q4k_generic || dm % 256 || df % 256 || dm > 8192 || df > 32768 ||
+    // (its grid barrier carries a per-launch generation: a graph replay would reuse it)
+    if (capturing || !ffnp || q4k_generic || dm % 256 || df % 256 || dm > 8192 || df > 32768 ||
         (((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd | (uintptr_t)x) & 15u))
         return HH_ERR_UNSUPPORTED_DEVICE;
     const int w1 = dm <= 4096 ? 1 : 2;
@@ -476,6 +486,95 @@ hh_status hh_engine::enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, c
     return HH_OK;
 }
 
+// Must match struct hh_gur_args / hh_dnr_args in kernels/q4k_ring.hip.
+struct GurArgs {
+    const uint8_t* wg;
+    const uint8_t* wu;
+    const float* x;
+    uint8_t* hx;
+    uint64_t rb1;
+    uint32_t d_model, d_ff;
+    int32_t act;
+    uint32_t pad;
+};
+struct DnrArgs {
+    const uint8_t* wd;
+    const uint8_t* hx;
+    float* y;
+    uint64_t rb2;
+    uint32_t d_model, d_ff;
+};
+
+// The ring kernels' grid: `per_cu` workgroups per CU when the occupancy allows it.
+static size_t ring_grid(int occ, int per_cu, size_t cus) { return cus * (size_t)std::max(1, std::min(occ, per_cu)); }
+
+bool hh_engine::ring_ok(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
+                        const float* x) const {
+    const size_t dm = d->d_model, df = d->d_ff;
+    return ring && !q4k_generic && d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K &&
+           d->type_down == HH_TYPE_Q4_K && dm % 256 == 0 && df % 256 == 0 && dm <= 8192 && df <= 32768 &&
+           ((((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd | (uintptr_t)x) & 15u) == 0);
+}
+
+hh_status hh_engine::enqueue_q4k_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu,
+                                         const float* x) {
+    const size_t dm = d->d_model, df = d->d_ff;
+    const int w1 = dm <= 4096 ? 1 : 2;
+    const std::string name = "hh_q4k_gu_ring_g" + std::to_string(w1);
+    hipFunction_t fn;
+    HH_TRY(kernel(name, &fn));
+    const int block = 8 * 64;
+    int occ = 0;
+    const size_t cus = (size_t)props.multiProcessorCount;
+    // LDS: x digits + gate/up row sums + 128 B staging (the kernel's layout), sized for the
+    // smallest grid it may run with
+    const size_t rr_max = 2 * 8 * ((df / 8 + cus - 1) / cus);
+    const size_t smem = (((2 * dm + (dm / 32) * 8) + 15) & ~size_t(15)) + ((rr_max * w1 + 3) & ~size_t(3)) * 4 + 128;
+    auto it = blocks_per_cu.find(name);
+    if (it != blocks_per_cu.end()) {
+        occ = it->second;
+    } else {
+        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, block, smem) != hipSuccess) occ = 1;
+        blocks_per_cu[name] = occ;
+    }
+    const size_t grid = ring_grid(occ, ring_gu_per_cu, cus);
+    HH_TRY(grow(&ws_hq, &ws_hq_cap, 2 * df + (df / 8) * 4 + 16));
+    GurArgs a{wg, wu, x, (uint8_t*)ws_hq, (uint64_t)((dm / 256) * 144), (uint32_t)dm, (uint32_t)df, d->act, 0u};
+    void* params[] = {&a};
+    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
+    if (err != hipSuccess) return hip_fail(err, "launch(ring q4k gate/up)");
+    return HH_OK;
+}
+
+hh_status hh_engine::enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd, float* y) {
+    const size_t dm = d->d_model, df = d->d_ff;
+    int w2 = 1;
+    while ((size_t)w2 * 64 < df / 64) w2 *= 2;
+    const std::string name = "hh_q4k_dn_ring_d" + std::to_string(w2);
+    hipFunction_t fn;
+    HH_TRY(kernel(name, &fn));
+    const int block = 9 * 64;  // 8 compute waves + the wave that copies the intermediate
+    int occ = 0;
+    const size_t cus = (size_t)props.multiProcessorCount;
+    // LDS: the intermediate + lane partials (rows x 64*w2), sized for the smallest grid
+    const size_t rows_max = (dm + cus - 1) / cus;
+    const size_t smem = (((2 * df + (df / 8) * 4) + 15) & ~size_t(15)) + rows_max * (size_t)w2 * 64 * 4;
+    if (smem > props.sharedMemPerBlock) return HH_ERR_UNSUPPORTED_DEVICE;
+    auto it = blocks_per_cu.find(name);
+    if (it != blocks_per_cu.end()) {
+        occ = it->second;
+    } else {
+        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, block, smem) != hipSuccess) occ = 1;
+        blocks_per_cu[name] = occ;
+    }
+    const size_t grid = ring_grid(occ, ring_dn_per_cu, cus);
+    DnrArgs a{wd, (const uint8_t*)ws_hq, y, (uint64_t)((df / 256) * 144), (uint32_t)dm, (uint32_t)df};
+    void* params[] = {&a};
+    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
+    if (err != hipSuccess) return hip_fail(err, "launch(ring q4k down)");
+    return HH_OK;
+}
+
 hh_status hh_engine::check_device_error() {
     unsigned flag = 0;
     HH_TRY_HIP(hipStreamSynchronize(stream), "hipStreamSynchronize");
@@ -500,6 +599,16 @@ hh_status hh_engine::enqueue_ffn_begin(const hh_ffn_desc* d, const uint8_t* pack
     const uint8_t* wu = pack + d->up_off;
     bool digits = false;
     hh_status st = HH_ERR_UNSUPPORTED_DEVICE;
+    if (ring_ok(d, wg, wu, pack + d->down_off, x)) {
+        // the ring kernels: gate/up writes h's granule digits, the finish step reads them
+        HH_TRY(enqueue_q4k_ring_gu(d, wg, wu, x));
+        ffn_stage = *d;
+        ffn_stage_digits = false;
+        ffn_stage_ring = true;
+        ffn_stage_valid = true;
+        ffn_calls += 2;
+        return HH_OK;
+    }
     if (d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K && d->type_down == HH_TYPE_Q4_K) {
         // Gate/up writes h and its int8 digits; the down projection consumes the digits.
         HH_TRY(grow(&ws_hq, &ws_hq_cap, hh_digits_bytes(d->d_ff)));
@@ -511,6 +620,7 @@ hh_status hh_engine::enqueue_ffn_begin(const hh_ffn_desc* d, const uint8_t* pack
     if (st != HH_OK) return st;
     ffn_stage = *d;
     ffn_stage_digits = digits;
+    ffn_stage_ring = false;
     ffn_stage_valid = true;
     ffn_calls += 2;
     return HH_OK;
@@ -522,13 +632,21 @@ hh_status hh_engine::enqueue_ffn_finish(const hh_ffn_desc* d, const uint8_t* pac
     ffn_stage_valid = false;
     const uint8_t* wd = pack + d->down_off;
     hh_status st = HH_ERR_UNSUPPORTED_DEVICE;
-    if (ffn_stage_digits) st = enqueue_q4k(d->d_model, d->d_ff, wd, nullptr, nullptr, y, 0, false, ws_hq, nullptr);
+    if (ffn_stage_ring) st = enqueue_q4k_ring_dn(d, wd, y);
+    else if (ffn_stage_digits) st = enqueue_q4k(d->d_model, d->d_ff, wd, nullptr, nullptr, y, 0, false, ws_hq, nullptr);
     if (st == HH_ERR_UNSUPPORTED_DEVICE) st = enqueue_gemv(d->type_down, d->d_model, d->d_ff, wd, (const float*)ws_h, y);
     if (st == HH_OK) ffn_calls += 1;
     return st;
 }
 
 hh_status hh_engine::enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y) {
+    if (ring_ok(d, pack + d->gate_off, pack + d->up_off, pack + d->down_off, x)) {
+        HH_TRY(enqueue_q4k_ring_gu(d, pack + d->gate_off, pack + d->up_off, x));
+        HH_TRY(enqueue_q4k_ring_dn(d, pack + d->down_off, y));
+        ffn_stage_valid = false;
+        ffn_calls += 3;
+        return HH_OK;
+    }
     if (d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K && d->type_down == HH_TYPE_Q4_K) {
         hh_status fst = enqueue_q4k_ffnp(d, pack + d->gate_off, pack + d->up_off, pack + d->down_off, x, y);
         if (fst == HH_ERR_UNSUPPORTED_DEVICE)
@@ -795,6 +913,8 @@ static std::vector<std::string> required_kernels() {
     k.push_back("hh_lut_gemv");
     for (const char* f : {"g1_d1", "g1_d2", "g1_d4", "g1_d8", "g2_d2", "g2_d4", "g2_d8"})
         k.push_back(std::string("hh_q4k_ffnp_") + f);
+    for (const char* f : {"gu_ring_g1", "gu_ring_g2", "dn_ring_d1", "dn_ring_d2", "dn_ring_d4", "dn_ring_d8"})
+        k.push_back(std::string("hh_q4k_") + f);
     k.push_back("hh_moe_route");
     for (int t : {16, 32, 64})
         for (const char* kind : {"hh_moe_gateup_t", "hh_moe_down_t"}) k.push_back(std::string(kind) + std::to_string(t));
@@ -841,6 +961,9 @@ hh_status engine_create(int device, hh_engine** out) {
     if (const char* g = getenv("HAYAI_HIP_Q4K_GENERIC")) e->q4k_generic = atoi(g) != 0;
     if (const char* f = getenv("HAYAI_HIP_FFN_FUSED")) e->ffn_fused = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_FFNP")) e->ffnp = atoi(f) != 0;
+    if (const char* f = getenv("HAYAI_HIP_RING")) e->ring = atoi(f) != 0;
+    if (const char* f = getenv("HAYAI_HIP_RING_GU_PER_CU")) e->ring_gu_per_cu = std::max(1, atoi(f));
+    if (const char* f = getenv("HAYAI_HIP_RING_DN_PER_CU")) e->ring_dn_per_cu = std::max(1, atoi(f));
     if (const char* c = getenv("HAYAI_HIP_COOP")) e->coop_launch = atoi(c) != 0;
     err = hipMalloc(&e->grid_sync, kBarBytes);
     if (err == hipSuccess) err = hipMemset(e->grid_sync, 0, kBarBytes);

@@ -124,13 +124,21 @@ struct hh_engine {
     hh_ffn_desc ffn_stage{};    // FFN whose gate/up output is pending in ws_h (/ws_hq)
     bool ffn_stage_valid = false;
     bool ffn_stage_digits = false;  // ws_hq holds the digits of ws_h
+    bool ffn_stage_ring = false;    // ws_hq holds the ring kernels' granule digits of h
     bool ffn_fused = false;     // HAYAI_HIP_FFN_FUSED=1: one-launch Q4_K FFN (grid barrier)
     bool ffnp = true;           // HAYAI_HIP_FFNP=0: skip the persistent pipelined Q4_K FFN
+    bool ring = true;           // HAYAI_HIP_RING=0: skip the two-launch ring Q4_K FFN
+    int ring_gu_per_cu = 1;     // HAYAI_HIP_RING_GU_PER_CU: ring gate/up workgroups per CU
+    int ring_dn_per_cu = 1;     // HAYAI_HIP_RING_DN_PER_CU: ring down workgroups per CU
     bool coop_launch = false;   // HAYAI_HIP_COOP=1: cooperative launch API for the fused kernel
     int blocks_per_cu_override = 0;  // HAYAI_HIP_BLOCKS_PER_CU
     bool q4k_generic = false;        // HAYAI_HIP_Q4K_GENERIC=1: skip the int8-digit Q4_K kernels
 
     hh_status select();  // hipSetDevice(device)
+    // Between hh_graph_begin and hh_graph_end the compute stream is being captured into a
+    // HIP graph: nothing may allocate, synchronize, or bake per-launch state into a kernel.
+    bool capturing = false;
+    hh_status no_capture(const char* what) const;
     hh_status kernel(const std::string& name, hipFunction_t* out);
     int resident_blocks(const std::string& name, int block);
     template <class A>
@@ -164,6 +172,9 @@ struct hh_engine {
     // Persistent one-launch Q4_K FFN layer with the down weights prefetched across the grid
     // barrier (q4k_ffn.hip); HH_ERR_UNSUPPORTED_DEVICE when the shape, alignment or
     // occupancy does not allow it.
+    bool ring_ok(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd, const float* x) const;
+    hh_status enqueue_q4k_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const float* x);
+    hh_status enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd, float* y);
     hh_status enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                                const float* x, float* y);
     // Batched GEMV Y[b][m] = W . X[b] (x, y device pointers, row-major by token).  Q4_K with

@@ -236,6 +236,31 @@ class Event:
             pass
 
 
+class Graph:
+    """A captured sequence of enqueue-only calls (HipEngine.capture), replayed by launch()."""
+
+    def __init__(self, engine: "HipEngine", handle: C.c_void_p):
+        self.engine = engine
+        self.handle = handle
+        engine._children.add(self)
+
+    def launch(self) -> None:
+        _check(self.engine.lib.hh_graph_launch(self.handle))
+
+    def free(self) -> None:
+        if self.handle:
+            self.engine.lib.hh_graph_destroy(self.handle)
+            self.handle = None
+
+    close = free
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 @dataclass
 class QuantMatrix:
     """Weight descriptor (quant.rs:31-54): y[nrows] = W . x[ncols] in GGML layout."""
@@ -343,6 +368,23 @@ class HipEngine:
 
     def event(self) -> Event:
         return Event(self)
+
+    # ---------------------------------------------------------------- graphs
+    def capture(self, fn) -> Graph:
+        """Capture the enqueue-only calls fn() makes on this engine into a replayable graph
+        (hh_graph_begin / hh_graph_end); the capture is closed even when fn raises."""
+        _check(self.lib.hh_graph_begin(self.handle))
+        try:
+            fn()
+        except BaseException:
+            h = C.c_void_p()
+            self.lib.hh_graph_end(self.handle, C.byref(h))
+            if h:
+                self.lib.hh_graph_destroy(h)
+            raise
+        h = C.c_void_p()
+        _check(self.lib.hh_graph_end(self.handle, C.byref(h)))
+        return Graph(self, h)
 
     # ---------------------------------------------------------------- GEMV (compute.rs)
     def ggml_gemv_dispatch(self, ggml_type: int, m: int, n: int, weights: np.ndarray, inp: np.ndarray) -> np.ndarray:

@@ -348,6 +348,25 @@ void hh_event_destroy(hh_event* ev);
 hh_status hh_event_record(hh_engine* e, hh_event* ev);
 hh_status hh_event_elapsed_ms(hh_event* start, hh_event* stop, float* ms);
 
+/* ------------------------------------------------------------------ graphs ---------- */
+
+/* No counterpart in the reference (its OpenCL queue replays nothing): capture a fixed
+ * sequence of enqueue-only (*_dev) calls on the engine's compute stream into a HIP graph and
+ * replay it, for decode loops whose launches are the same every token (one graph launch
+ * instead of one dispatch per kernel).  Between hh_graph_begin and hh_graph_end only *_dev
+ * calls may be made, and none may need a larger workspace than an earlier call did (run the
+ * sequence once eagerly first); calls whose kernels carry per-launch state (the persistent
+ * one-launch FFN form, batched and MoE FFNs) are refused or routed to graph-safe kernels.
+ * A replay reads and writes the buffers the captured calls named, with their contents at
+ * replay time. */
+typedef struct hh_graph hh_graph;
+hh_status hh_graph_begin(hh_engine* e);
+/* Ends the capture (also after a refused call) and instantiates the graph. */
+hh_status hh_graph_end(hh_engine* e, hh_graph** out);
+/* Enqueue one replay on the engine's compute stream. */
+hh_status hh_graph_launch(hh_graph* g);
+void hh_graph_destroy(hh_graph* g);
+
 /* ------------------------------------------------------------------ synthetic data -- */
 
 /* Fill n_blocks GGUF blocks of ggml_type at (dst, off) with the seeded synthetic stream

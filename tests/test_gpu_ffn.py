@@ -103,21 +103,35 @@ def test_ffn_rejects_bad_pack(engine):
     assert engine.ffn_calls == before + 3
 
 
-@pytest.fixture(scope="module")
-def two_launch_engine():
-    """An engine with the persistent one-launch Q4_K FFN switched off (HAYAI_HIP_FFNP=0):
-    every FFN runs as the two-launch gate/up(+act) then down path."""
+def engine_with_env(**env):
+    """A HipEngine created with the given HAYAI_HIP_* switches set (read at creation)."""
     import os
 
-    old = os.environ.get("HAYAI_HIP_FFNP")
-    os.environ["HAYAI_HIP_FFNP"] = "0"
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
     try:
-        eng = hayai_amd.HipEngine(0)
+        return hayai_amd.HipEngine(0)
     finally:
-        if old is None:
-            del os.environ["HAYAI_HIP_FFNP"]
-        else:
-            os.environ["HAYAI_HIP_FFNP"] = old
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+
+
+@pytest.fixture(scope="module")
+def persistent_engine():
+    """An engine whose Q4_K FFN is the persistent one-launch form (ring form off)."""
+    eng = engine_with_env(HAYAI_HIP_RING="0")
+    yield eng
+    eng.close()
+
+
+@pytest.fixture(scope="module")
+def two_launch_engine():
+    """An engine with the ring and persistent Q4_K FFN forms off: every FFN runs as the first
+    two-launch kernels (gate/up + activation with per-32 digits of h, then down)."""
+    eng = engine_with_env(HAYAI_HIP_RING="0", HAYAI_HIP_FFNP="0")
     yield eng
     eng.close()
 
@@ -130,35 +144,43 @@ PERSISTENT_CASES = [
 ]
 
 
+@pytest.mark.parametrize("form", ["ring", "persistent"])
 @pytest.mark.parametrize("d_model,d_ff", PERSISTENT_CASES)
-def test_persistent_ffn_matches_oracle_and_two_launch(engine, two_launch_engine, d_model, d_ff):
-    # The persistent kernel (gate/up, grid barrier, down with its weights already in flight)
-    # against the oracle and against the two-launch kernels on the same bytes.
+def test_q4k_ffn_forms_match_oracle_and_two_launch(engine, persistent_engine, two_launch_engine, form, d_model,
+                                                   d_ff):
+    # The ring form (two streaming launches, h as granule digits in between) and the
+    # persistent one-launch form (gate/up, grid barrier, down with its weights already in
+    # flight) against the oracle and against the first two-launch kernels on the same bytes.
     types = (12, 12, 12)
-    print(f"[case] persistent ffn {d_model}x{d_ff}", flush=True)
+    eng = engine if form == "ring" else persistent_engine
+    print(f"[case] q4_k ffn ({form}) {d_model}x{d_ff}", flush=True)
     oracle.set_threads(min(16, oracle.max_threads()))
-    lay, (wg, wu, wd), pack = make_pack(engine, types, d_model, d_ff, 20)
+    lay, (wg, wu, wd), pack = make_pack(eng, types, d_model, d_ff, 20)
     pack2 = two_launch_engine.alloc(lay.total)
     pack2.write(wg, lay.gate_off)
     pack2.write(wu, lay.up_off)
     pack2.write(wd, lay.down_off)
-    desc = engine.ffn_desc(types, d_model, d_ff, lay)
+    desc = eng.ffn_desc(types, d_model, d_ff, lay)
     for k in range(2):
         x = synth.normal(synth.seed_for(20, k, synth.ACT), d_model)
-        y = engine.ffn(desc, pack, 0, x)
+        y = eng.ffn(desc, pack, 0, x)
         y2 = two_launch_engine.ffn(desc, pack2, 0, x)
         ref = oracle.ffn(types, d_model, d_ff, wg, wu, wd, x)
         assert rel_err(y, ref) <= REL_TOL, rel_err(y, ref)
         assert rel_err(y, y2) <= REL_TOL
         print(f"  rel_err vs oracle {rel_err(y, ref):.2e}, vs two-launch {rel_err(y, y2):.2e}", flush=True)
+    eng.sync()  # reports a timed-out wait if one was recorded
 
 
-def test_persistent_ffn_chain_is_deterministic(engine):
-    # 6 dependent launches with no host sync in between (each launch's grid barrier uses a new
-    # generation; the h exchange buffer is reused), then the same chain call by call: the
-    # results are identical bit for bit, and every step is within tolerance of the oracle.
+@pytest.mark.parametrize("form", ["ring", "persistent"])
+def test_q4k_ffn_chain_is_deterministic(engine, persistent_engine, form):
+    # 6 dependent launches with no host sync in between (the persistent form uses a new
+    # barrier generation per launch; the h buffer is reused), then the same chain call by
+    # call: the results are identical bit for bit, and every step is within tolerance of the
+    # oracle.
     types, d_model, d_ff = (12, 12, 12), 4096, 14336
-    print(f"[case] persistent ffn chain {d_model}x{d_ff}", flush=True)
+    engine = engine if form == "ring" else persistent_engine
+    print(f"[case] q4_k ffn chain ({form}) {d_model}x{d_ff}", flush=True)
     lay, (wg, wu, wd), pack = make_pack(engine, types, d_model, d_ff, 2)
     desc = engine.ffn_desc(types, d_model, d_ff, lay)
     x = synth.normal(synth.seed_for(2, 9, synth.ACT), d_model)
@@ -182,10 +204,10 @@ def test_persistent_ffn_chain_is_deterministic(engine):
                                                  ((12, 2, 18), 1024, 2048)])
 def test_ffn_begin_finish_equals_ffn(engine, two_launch_engine, types, d_model, d_ff):
     # The reference's two-call seam (ffn_begin_gate_up_scratch / ffn_finish_scratch) runs the
-    # same kernels as the two-launch form of the one-call op: identical bits.  (With the
-    # persistent Q4_K kernel the one-call op differs from it only by rounding.)
+    # same kernels as the one-call op (the ring kernels for Q4_K, or the first two-launch
+    # kernels): identical bits.
     print(f"[case] begin/finish types={types} {d_model}x{d_ff}", flush=True)
-    for eng, exact in ((two_launch_engine, True), (engine, types != (12, 12, 12))):
+    for eng in (engine, two_launch_engine):
         lay, _, pack = make_pack(eng, types, d_model, d_ff, 13)
         desc = eng.ffn_desc(types, d_model, d_ff, lay)
         x = synth.normal(77, d_model)
@@ -196,10 +218,7 @@ def test_ffn_begin_finish_equals_ffn(engine, two_launch_engine, types, d_model, 
         eng.ffn_begin_dev(desc, pack, 0, xb, 0)
         eng.ffn_finish_dev(desc, pack, 0, y2, 0)
         a, b = y1.read(np.float32, d_model), y2.read(np.float32, d_model)
-        if exact:
-            np.testing.assert_array_equal(a, b)
-        else:
-            assert rel_err(a, b) <= REL_TOL
+        np.testing.assert_array_equal(a, b)
         # a finish consumes the pending intermediate; a second one (or one for another shape) fails
         with pytest.raises(hayai_amd.HipError):
             eng.ffn_finish_dev(desc, pack, 0, y2, 0)
