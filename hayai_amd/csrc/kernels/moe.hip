@@ -106,15 +106,23 @@ HH_DEV void hh_wave_sync() {
     __builtin_amdgcn_wave_barrier();
 }
 
-// One wave routes token t.  Lane r < kk returns the expert of slot r in *id and its weight in
-// *w; the return value is kk, the number of experts selected.
-HH_DEV uint32_t hh_route_token(const hh_route_args& a, uint32_t t, bool valid, hh_route_lds& L, int* id, float* w) {
+// Routing of token t by one wave, in three steps that hh_route_token runs back to back and
+// the one-token MoE kernel runs on two waves at once:
+//   hh_route_select_n:  the selection; lane r < kk gets the expert of slot r (return kk);
+//   hh_route_softmax_n: exp(score - max) of every expert into ex[], returns 1/sum (the sum
+//                       sequential in expert order, as the reference's iterator sum);
+//   hh_route_weight:    slot weights (softmax or sigmoid), renormalisation, scaling.
+// EPL = experts per lane held in registers (E <= 64 * EPL); every EPL gives the same
+// selections and bit-identical weights (the same operations in the same order on the same
+// candidates; lanes' extra slots only ever hold non-candidates).
+template <int EPL>
+HH_DEV uint32_t hh_route_select_n(const hh_route_args& a, uint32_t t, bool valid, hh_route_lds& L, int* id) {
     const uint32_t lane = threadIdx.x % HH_WAVE;
     const uint32_t E = a.E;
-    float sc[HH_MOE_EPL], ch[HH_MOE_EPL];
-    int pos[HH_MOE_EPL];
+    float sc[EPL], ch[EPL];
+    int pos[EPL];
 #pragma unroll
-    for (int i = 0; i < HH_MOE_EPL; i++) {
+    for (int i = 0; i < EPL; i++) {
         const uint32_t e = lane + HH_WAVE * i;
         const bool in = e < E;
         const float s = (in && valid) ? a.logits[(size_t)t * E + e] : 0.f;
@@ -158,7 +166,7 @@ HH_DEV uint32_t hh_route_token(const hh_route_args& a, uint32_t t, bool valid, h
         hh_wave_sync();
         const uint32_t keep = a.topk_group < G ? a.topk_group : G;
 #pragma unroll
-        for (int i = 0; i < HH_MOE_EPL; i++) {
+        for (int i = 0; i < EPL; i++) {
             const uint32_t e = lane + HH_WAVE * i;
             if (e < E) {
                 const uint32_t g = e / gs;
@@ -182,7 +190,7 @@ HH_DEV uint32_t hh_route_token(const hh_route_args& a, uint32_t t, bool valid, h
     for (uint32_t r = 0; r < kk; r++) {
         uint64_t best = 0;
 #pragma unroll
-        for (int i = 0; i < HH_MOE_EPL; i++) {
+        for (int i = 0; i < EPL; i++) {
             const uint64_t key = pos[i] >= 0 ? hh_route_key(ch[i], pos[i]) : 0ull;
             best = key > best ? key : best;
         }
@@ -190,39 +198,57 @@ HH_DEV uint32_t hh_route_token(const hh_route_args& a, uint32_t t, bool valid, h
         const int p = best ? (int)~(uint32_t)best : 0;
         const int be = grouped ? L.group_of_rank[p / (int)gsz] * (int)gsz + p % (int)gsz : p;
 #pragma unroll
-        for (int i = 0; i < HH_MOE_EPL; i++)
+        for (int i = 0; i < EPL; i++)
             if ((int)(lane + HH_WAVE * i) == be) pos[i] = -1;
         if (lane == r) sel = be;
     }
+    *id = sel;
+    return kk;
+}
 
+template <int EPL>
+HH_DEV float hh_route_softmax_n(const hh_route_args& a, uint32_t t, bool valid, float* ex) {
+    const uint32_t lane = threadIdx.x % HH_WAVE;
+    const uint32_t E = a.E;
+    float sc[EPL];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        const uint32_t e = lane + HH_WAVE * i;
+        sc[i] = (e < E && valid) ? a.logits[(size_t)t * E + e] : 0.f;
+        if (e < E) mx = fmaxf(mx, sc[i]);
+    }
+    mx = hh_wave_max_f(mx);
+    hh_wave_sync();  // (ex may be the selection's scratch, done with by now)
+#pragma unroll
+    for (int i = 0; i < EPL; i++)
+        if (lane + HH_WAVE * i < E) ex[lane + HH_WAVE * i] = expf(sc[i] - mx);
+    hh_wave_sync();
+    // sequential sum in expert order (every lane computes it; the loads are broadcasts)
+    float sum = 0.f;
+    uint32_t e = 0;
+#pragma unroll 8
+    for (; e + 4 <= E; e += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(&ex[e]);
+        sum += v.x;
+        sum += v.y;
+        sum += v.z;
+        sum += v.w;
+    }
+    for (; e < E; e++) sum += ex[e];
+    return sum > 0.f ? 1.0f / sum : 0.f;
+}
+
+// Lane r < kk: the weight of slot r (expert sel); sc = raw scores, ex / inv from
+// hh_route_softmax_n (unused for sigmoid gating).
+HH_DEV float hh_route_weight(const hh_route_args& a, const float* sc, const float* ex, float inv, int sel,
+                             uint32_t kk) {
+    const uint32_t lane = threadIdx.x % HH_WAVE;
     float wv = 0.f;
     if (a.gating == 1) {
-        if (lane < kk) wv = 1.0f / (1.0f + expf(-L.sc[sel]));
+        if (lane < kk) wv = 1.0f / (1.0f + expf(-sc[sel]));
     } else {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < HH_MOE_EPL; i++)
-            if (lane + HH_WAVE * i < E) mx = fmaxf(mx, sc[i]);
-        mx = hh_wave_max_f(mx);
-        hh_wave_sync();  // the grouped pass is done with L.ex
-#pragma unroll
-        for (int i = 0; i < HH_MOE_EPL; i++)
-            if (lane + HH_WAVE * i < E) L.ex[lane + HH_WAVE * i] = expf(sc[i] - mx);
-        hh_wave_sync();
-        // sequential sum in expert order (every lane computes it; the loads are broadcasts)
-        float sum = 0.f;
-        uint32_t e = 0;
-#pragma unroll 8
-        for (; e + 4 <= E; e += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(&L.ex[e]);
-            sum += v.x;
-            sum += v.y;
-            sum += v.z;
-            sum += v.w;
-        }
-        for (; e < E; e++) sum += L.ex[e];
-        const float inv = sum > 0.f ? 1.0f / sum : 0.f;
-        if (lane < kk) wv = L.ex[sel] * inv;
+        if (lane < kk) wv = ex[sel] * inv;
     }
     if (a.norm) {
         float s = 0.f;
@@ -231,9 +257,38 @@ HH_DEV uint32_t hh_route_token(const hh_route_args& a, uint32_t t, bool valid, h
         if (s > 0.f) wv = wv / s;
     }
     if (fabsf(a.scale - 1.0f) > 1e-9f) wv = wv * a.scale;
+    return wv;
+}
+
+template <int EPL>
+HH_DEV uint32_t hh_route_token_n(const hh_route_args& a, uint32_t t, bool valid, hh_route_lds& L, int* id, float* w) {
+    int sel;
+    const uint32_t kk = hh_route_select_n<EPL>(a, t, valid, L, &sel);
+    const float inv = a.gating == 1 ? 0.f : hh_route_softmax_n<EPL>(a, t, valid, L.ex);
     *id = sel;
-    *w = wv;
+    *w = hh_route_weight(a, L.sc, L.ex, inv, sel, kk);
     return kk;
+}
+
+HH_DEV uint32_t hh_route_select(const hh_route_args& a, uint32_t t, bool valid, hh_route_lds& L, int* id) {
+    if (a.E <= 64) return hh_route_select_n<1>(a, t, valid, L, id);
+    if (a.E <= 128) return hh_route_select_n<2>(a, t, valid, L, id);
+    if (a.E <= 256) return hh_route_select_n<4>(a, t, valid, L, id);
+    return hh_route_select_n<HH_MOE_EPL>(a, t, valid, L, id);
+}
+
+HH_DEV float hh_route_softmax(const hh_route_args& a, uint32_t t, bool valid, float* ex) {
+    if (a.E <= 64) return hh_route_softmax_n<1>(a, t, valid, ex);
+    if (a.E <= 128) return hh_route_softmax_n<2>(a, t, valid, ex);
+    if (a.E <= 256) return hh_route_softmax_n<4>(a, t, valid, ex);
+    return hh_route_softmax_n<HH_MOE_EPL>(a, t, valid, ex);
+}
+
+HH_DEV uint32_t hh_route_token(const hh_route_args& a, uint32_t t, bool valid, hh_route_lds& L, int* id, float* w) {
+    if (a.E <= 64) return hh_route_token_n<1>(a, t, valid, L, id, w);
+    if (a.E <= 128) return hh_route_token_n<2>(a, t, valid, L, id, w);
+    if (a.E <= 256) return hh_route_token_n<4>(a, t, valid, L, id, w);
+    return hh_route_token_n<HH_MOE_EPL>(a, t, valid, L, id, w);
 }
 
 extern "C" __global__ void __launch_bounds__(HH_MOE_BLOCK) hh_moe_route(const hh_route_args a) {

@@ -862,6 +862,43 @@ hh_status hh_engine::enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* expert
     a.act = d->act;
     a.route = logits != nullptr;
     if (logits) a.r = route_args(d, logits, bias, T, ids, wts);
+    // One token (decode): the ring kernels (moe_ring.hip), when the shape allows them.
+    const size_t K = k * df, uin = dm / 64;
+    if (T == 1 && ring && (uin == 16 || uin == 32 || uin == 64) && df % 256 == 0 && K / 64 <= 512 &&
+        ((d->expert_stride | d->gate_off | d->up_off | d->down_off | (uintptr_t)experts | (uintptr_t)x) & 15u) == 0) {
+        HH_TRY(grow(&ws_moe_hx, &ws_moe_hx_cap, 2 * K + (K / 8) * 4 + 16));
+        struct {
+            hh_moe_args m;
+            uint8_t* hx;
+        } ra{a, (uint8_t*)ws_moe_hx};
+        void* rparams[] = {&ra};
+        const size_t cus = (size_t)props.multiProcessorCount;
+        {
+            const std::string name = "hh_moe_gu_ring_u" + std::to_string(uin);
+            hipFunction_t fn;
+            HH_TRY(kernel(name, &fn));
+            const size_t rr_max = 2 * 8 * ((K / 8 + cus - 1) / cus);
+            const size_t smem = (((2 * dm + (dm / 32) * 8) + 15) & ~size_t(15)) + ((rr_max + 3) & ~size_t(3)) * 4 + 128;
+            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)cus, 1, 1, 8 * 64, 1, 1, (unsigned)smem, stream, rparams,
+                                             nullptr),
+                       "launch(moe ring gate/up)");
+        }
+        {
+            int w2 = 1;
+            while ((size_t)w2 * 64 < K / 64) w2 *= 2;
+            const std::string name = "hh_moe_dn_ring_d" + std::to_string(w2);
+            hipFunction_t fn;
+            HH_TRY(kernel(name, &fn));
+            const size_t rows_max = (dm + cus - 1) / cus;
+            const size_t smem = (((2 * K + (K / 8) * 4) + 15) & ~size_t(15)) + rows_max * (size_t)w2 * 64 * 4;
+            if (smem > props.sharedMemPerBlock) return fail(HH_ERR_INVALID, "moe: expert intermediate too large");
+            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)cus, 1, 1, 9 * 64, 1, 1, (unsigned)smem, stream, rparams,
+                                             nullptr),
+                       "launch(moe ring down)");
+        }
+        ffn_calls += 3;
+        return HH_OK;
+    }
     const size_t cap = std::max<size_t>(1, ((size_t)props.multiProcessorCount * 2 + T - 1) / T);
     void* params[] = {&a};
     {
@@ -915,6 +952,9 @@ static std::vector<std::string> required_kernels() {
         k.push_back(std::string("hh_q4k_ffnp_") + f);
     for (const char* f : {"gu_ring_g1", "gu_ring_g2", "dn_ring_d1", "dn_ring_d2", "dn_ring_d4", "dn_ring_d8"})
         k.push_back(std::string("hh_q4k_") + f);
+    for (const char* f : {"gu_ring_u16", "gu_ring_u32", "gu_ring_u64", "dn_ring_d1", "dn_ring_d2", "dn_ring_d4",
+                          "dn_ring_d8"})
+        k.push_back(std::string("hh_moe_") + f);
     k.push_back("hh_moe_route");
     for (int t : {16, 32, 64})
         for (const char* kind : {"hh_moe_gateup_t", "hh_moe_down_t"}) k.push_back(std::string(kind) + std::to_string(t));
@@ -979,7 +1019,7 @@ void engine_destroy(hh_engine* e) {
     if (e->stream) hipStreamSynchronize(e->stream);
     if (e->copy_stream) hipStreamSynchronize(e->copy_stream);
     for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq, e->ws_xop, e->ws_hop, e->ws_part,
-                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->grid_sync})
+                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->grid_sync})
         if (p) hipFree(p);
     if (e->stream) hipStreamDestroy(e->stream);
     if (e->copy_stream) hipStreamDestroy(e->copy_stream);

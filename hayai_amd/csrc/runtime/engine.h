@@ -115,6 +115,8 @@ struct hh_engine {
     // MoE: expert intermediates [T][k][d_ff], ids and weights of hh_moe_dev.
     void* ws_moe_h = nullptr;
     size_t ws_moe_h_cap = 0;
+    void* ws_moe_hx = nullptr;  // digits of the weighted expert intermediate (one-token MoE)
+    size_t ws_moe_hx_cap = 0;
     void* ws_moe_ids = nullptr;
     size_t ws_moe_ids_cap = 0;
     void* ws_moe_w = nullptr;

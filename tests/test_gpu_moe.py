@@ -95,8 +95,10 @@ def make_experts(engine, E, d_model, d_ff, seed):
 
 
 @pytest.mark.parametrize("E,k,d_model,d_ff,T", [
-    (32, 8, 2048, 768, 1),     # Qwen3-30B-A3B expert shape
+    (32, 8, 2048, 768, 1),     # Qwen3-30B-A3B expert shape (one token: the ring kernels)
     (32, 8, 2048, 768, 5),
+    (8, 2, 4096, 1024, 1),     # one token, 64 lanes per gate/up row
+    (16, 4, 1024, 512, 1),     # one token, 4 gate/up rows per wave item
     (8, 2, 4096, 1024, 3),     # wider rows: 64-lane teams, several units per lane on down
     (16, 4, 1024, 512, 2),
 ])
