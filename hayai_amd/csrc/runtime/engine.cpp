@@ -144,7 +144,7 @@ hh_status hh_engine::grow(void** p, size_t* cap, size_t need) {
     if (*p) {
         hipError_t e1 = hipStreamSynchronize(stream);
         if (e1 != hipSuccess) return hip_fail(e1, "hipStreamSynchronize");
-        hipFree(*p);
+        (void)hipFree(*p);
         *p = nullptr;
         *cap = 0;
     }
@@ -737,6 +737,107 @@ hh_status hh_engine::enqueue_q4k_mm(size_t m, size_t n, const uint8_t* w0, const
     return launch(fn, (uint32_t)(groups * ksg), kMmBlock, a);
 }
 
+// Kernel argument block of q4k_mmr.hip (same layout).
+struct hh_mmr_args {
+    const uint8_t* w0;
+    const uint8_t* w1;
+    const void* x;
+    float* y;
+    void* hop;
+    float* part;
+    unsigned* cnt;
+    uint64_t row_bytes;
+    uint32_t m, n, b, nw, kc;
+    int32_t act;
+};
+constexpr size_t kMmrMaxTokens = 16;
+
+// Work split of a weight-stream launch over nu 16-row units and nsb superblocks: chunks of
+// S superblocks (S x 17 KB of token stages in LDS) and nw units (one wave each) per
+// workgroup.  A CU holds res = min(LDS / stages, 8 / nw) workgroups at once (the kernels
+// need more than 128 VGPRs: at most two waves per SIMD); its stream rate is taken as
+// proportional to its resident waves (up to 8), plus a fixed start-up cost of about two
+// items per round (first-data latency, token staging).  Ties go to the split that fills
+// more of the CU slots, then to longer chunks (fewer partial sums).
+struct mmr_plan {
+    int S = 0;
+    uint32_t nw = 0, kc = 0, groups = 0;
+};
+static mmr_plan plan_mmr(size_t nu, size_t nsb, size_t cus, size_t lds) {
+    mmr_plan best;
+    double best_cost = 1e300, best_fill = 0;
+    for (int S : {8, 7, 4, 2}) {
+        if (S > 2 && (size_t)S > nsb) continue;
+        const size_t kc = (nsb + S - 1) / S;
+        const size_t by_lds = lds / ((size_t)S * kMmStage + 64);
+        if (by_lds == 0) continue;
+        for (size_t nw = 8; nw >= 1; nw--) {
+            const size_t groups = (nu + nw - 1) / nw;
+            const size_t wgs = groups * kc;
+            const size_t res = std::min(by_lds, 8 / nw);
+            const size_t rounds = (wgs + cus * res - 1) / (cus * res);
+            const double cost = (double)rounds * ((double)(res * nw * S) / (double)std::min<size_t>(nw * res, 8) + 2.0);
+            const double fill = (double)wgs / (double)(rounds * cus * res);
+            if (cost < best_cost - 1e-9 || (cost < best_cost + 1e-9 && fill > best_fill + 1e-9)) {
+                best_cost = cost;
+                best_fill = fill;
+                best.S = S;
+                best.nw = (uint32_t)nw;
+                best.kc = (uint32_t)kc;
+                best.groups = (uint32_t)groups;
+            }
+        }
+    }
+    return best;
+}
+
+bool hh_engine::mmr_ok(size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const {
+    return mmr && !q4k_generic && b >= 1 && b <= kMmrMaxTokens && m >= 1 && n >= 256 && n % 256 == 0 &&
+           m <= 0x7FFFFFFFu && n <= 0x7FFFFFFFu && ((((uintptr_t)w0 | (uintptr_t)w1 | (uintptr_t)x) & 15u) == 0);
+}
+
+hh_status hh_engine::enqueue_q4k_mmr(int kind, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* x,
+                                     size_t b, float* y, int act) {
+    if (!mmr_ok(m, n, b, w0, kind == MMR_GU ? w1 : w0, x) || (kind == MMR_GU && m % 256 != 0))
+        return HH_ERR_UNSUPPORTED_DEVICE;
+    const size_t nsb = n / 256, nu = (m + 15) / 16;
+    const mmr_plan pl = plan_mmr(nu, nsb, (size_t)props.multiProcessorCount, (size_t)props.sharedMemPerBlock);
+    if (pl.S == 0) return HH_ERR_UNSUPPORTED_DEVICE;
+    const size_t smem = (size_t)pl.S * kMmStage;
+    const size_t nt = kind == MMR_GU ? 2 : 1;
+    if (pl.kc > 1) {
+        HH_TRY(grow(&ws_part, &ws_part_cap, (size_t)pl.groups * pl.kc * pl.nw * nt * 256 * sizeof(float)));
+        if (ws_cnt_cap < pl.groups * sizeof(unsigned)) {
+            HH_TRY(grow(&ws_cnt, &ws_cnt_cap, pl.groups * sizeof(unsigned)));
+            HH_TRY_HIP(hipMemsetAsync(ws_cnt, 0, ws_cnt_cap, stream), "hipMemsetAsync(counters)");
+        }
+    }
+    if (kind == MMR_GU) HH_TRY(grow(&ws_hop, &ws_hop_cap, mm_stage_bytes(m, 1)));
+    static const char* kinds[] = {"hh_q4k_mmr_s", "hh_q4k_mmr_gu_s", "hh_q4k_mmr_dn_s"};
+    hipFunction_t fn;
+    HH_TRY(kernel(std::string(kinds[kind]) + std::to_string(pl.S), &fn));
+    hh_mmr_args a{};
+    a.w0 = w0;
+    a.w1 = kind == MMR_GU ? w1 : w0;
+    a.x = x;
+    a.y = y;
+    a.hop = ws_hop;
+    a.part = (float*)ws_part;
+    a.cnt = (unsigned*)ws_cnt;
+    a.row_bytes = (uint64_t)(nsb * 144);
+    a.m = (uint32_t)m;
+    a.n = (uint32_t)n;
+    a.b = (uint32_t)b;
+    a.nw = pl.nw;
+    a.kc = pl.kc;
+    a.act = act;
+    void* params[] = {&a};
+    hipError_t err = hipModuleLaunchKernel(fn, pl.groups * pl.kc, 1, 1, pl.nw * 64, 1, 1, (unsigned)smem, stream,
+                                           params, nullptr);
+    if (err != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel(q4k_mmr)");
+    return HH_OK;
+}
+
 hh_status hh_engine::enqueue_gemv_batched(int type, size_t m, size_t n, const uint8_t* w, const float* x, size_t batch,
                                           float* y) {
     if (batch == 0) return HH_OK;
@@ -750,6 +851,10 @@ hh_status hh_engine::enqueue_gemv_batched(int type, size_t m, size_t n, const ui
         const size_t nb = std::min(kMmMaxTokens, batch - b0);
         if (nb == 1) {
             HH_TRY(enqueue_gemv(type, m, n, w, x + b0 * n, y + b0 * m));
+            continue;
+        }
+        if (nb <= kMmrMaxTokens && mmr_ok(m, n, nb, w, w, x + b0 * n)) {
+            HH_TRY(enqueue_q4k_mmr(MMR_GEMM, m, n, w, nullptr, x + b0 * n, nb, y + b0 * m, 0));
             continue;
         }
         const size_t tt = mm_tiles(nb);
@@ -776,6 +881,13 @@ hh_status hh_engine::enqueue_ffn_batched(const hh_ffn_desc* d, const uint8_t* pa
         const size_t nb = std::min(kMmMaxTokens, batch - b0);
         if (nb == 1) {
             HH_TRY(enqueue_ffn(d, pack, x + b0 * dm, y + b0 * dm));
+            continue;
+        }
+        if (nb <= kMmrMaxTokens && df % 256 == 0 && mmr_ok(df, dm, nb, wg, wu, x + b0 * dm) &&
+            mmr_ok(dm, df, nb, wd, wd, wd)) {
+            HH_TRY(enqueue_q4k_mmr(MMR_GU, df, dm, wg, wu, x + b0 * dm, nb, nullptr, d->act));
+            HH_TRY(enqueue_q4k_mmr(MMR_DN, dm, df, wd, nullptr, ws_hop, nb, y + b0 * dm, 0));
+            ffn_calls += 3 * nb;
             continue;
         }
         const size_t tt = mm_tiles(nb);
@@ -947,6 +1059,9 @@ static std::vector<std::string> required_kernels() {
     for (int tt : {1, 2, 4})
         for (const char* kind : {"hh_q4k_mm_t", "hh_q4k_mm_gateup_t"}) k.push_back(std::string(kind) + std::to_string(tt));
     k.push_back("hh_mm_prep");
+    for (int S : {2, 4, 7, 8})
+        for (const char* kind : {"hh_q4k_mmr_s", "hh_q4k_mmr_gu_s", "hh_q4k_mmr_dn_s"})
+            k.push_back(std::string(kind) + std::to_string(S));
     k.push_back("hh_lut_gemv");
     for (const char* f : {"g1_d1", "g1_d2", "g1_d4", "g1_d8", "g2_d2", "g2_d4", "g2_d8"})
         k.push_back(std::string("hh_q4k_ffnp_") + f);
@@ -970,10 +1085,10 @@ hh_status engine_create(int device, hh_engine** out) {
     hh_engine* e = new hh_engine();
     e->device = device;
     auto bail = [&](hh_status st) {
-        if (e->grid_sync) hipFree(e->grid_sync);
-        if (e->stream) hipStreamDestroy(e->stream);
-        if (e->copy_stream) hipStreamDestroy(e->copy_stream);
-        if (e->module) hipModuleUnload(e->module);
+        if (e->grid_sync) (void)hipFree(e->grid_sync);
+        if (e->stream) (void)hipStreamDestroy(e->stream);
+        if (e->copy_stream) (void)hipStreamDestroy(e->copy_stream);
+        if (e->module) (void)hipModuleUnload(e->module);
         delete e;
         return st;
     };
@@ -1004,6 +1119,7 @@ hh_status engine_create(int device, hh_engine** out) {
     if (const char* f = getenv("HAYAI_HIP_RING")) e->ring = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_RING_GU_PER_CU")) e->ring_gu_per_cu = std::max(1, atoi(f));
     if (const char* f = getenv("HAYAI_HIP_RING_DN_PER_CU")) e->ring_dn_per_cu = std::max(1, atoi(f));
+    if (const char* f = getenv("HAYAI_HIP_MMR")) e->mmr = atoi(f) != 0;
     if (const char* c = getenv("HAYAI_HIP_COOP")) e->coop_launch = atoi(c) != 0;
     err = hipMalloc(&e->grid_sync, kBarBytes);
     if (err == hipSuccess) err = hipMemset(e->grid_sync, 0, kBarBytes);

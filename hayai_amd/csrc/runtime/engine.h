@@ -132,6 +132,7 @@ struct hh_engine {
     bool ring = true;           // HAYAI_HIP_RING=0: skip the two-launch ring Q4_K FFN
     int ring_gu_per_cu = 1;     // HAYAI_HIP_RING_GU_PER_CU: ring gate/up workgroups per CU
     int ring_dn_per_cu = 1;     // HAYAI_HIP_RING_DN_PER_CU: ring down workgroups per CU
+    bool mmr = true;            // HAYAI_HIP_MMR=0: batched Q4_K (<= 16 tokens) on the q4k_mm kernels
     bool coop_launch = false;   // HAYAI_HIP_COOP=1: cooperative launch API for the fused kernel
     int blocks_per_cu_override = 0;  // HAYAI_HIP_BLOCKS_PER_CU
     bool q4k_generic = false;        // HAYAI_HIP_Q4K_GENERIC=1: skip the int8-digit Q4_K kernels
@@ -193,6 +194,13 @@ struct hh_engine {
     // act, writing the stages of h into ws_hop).  xop holds 16 * tt tokens of n columns.
     hh_status enqueue_q4k_mm(size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* xop, size_t b,
                              size_t tt, float* y, bool ffn, int act);
+    // Weight-stream MFMA launch for 1..16 tokens (q4k_mmr.hip).  kind: MMR_GEMM (w0, f32 x,
+    // y), MMR_GU (w0 = gate, w1 = up, f32 x, act; h stages into ws_hop) or MMR_DN (w0, x =
+    // token stages, y).  HH_ERR_UNSUPPORTED_DEVICE when shape or alignment does not fit.
+    enum { MMR_GEMM = 0, MMR_GU = 1, MMR_DN = 2 };
+    bool mmr_ok(size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const;
+    hh_status enqueue_q4k_mmr(int kind, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* x,
+                              size_t b, float* y, int act);
     // MoE routing of T tokens (device pointers) and the grouped expert FFN.
     hh_status enqueue_moe_route(const hh_moe_desc* d, const float* logits, const float* bias, size_t T,
                                 int32_t* ids, float* wts);
