@@ -1,33 +1,43 @@
 // Batched Q4_K on the matrix cores as one weight stream per launch (gfx950), for up to 16
 // tokens (one 16-token tile):
-//   hh_q4k_mmr_gu_s<S>  FFN gate/up + act: h = act(W_gate . X) * (W_up . X), written as
+//   hh_q4k_mmr_gu_s<S>  FFN gate/up + act: h = act(W_gate . X) * (W_up . X), written as the
 //                       token stages of the down projection (prefill_batched's gate/up and
 //                       host SiLU*up, crates/hayai-core/src/prefill_wave.rs:569-584, fused)
 //   hh_q4k_mmr_dn_s<S>  Y = W_down . H from those stages (prefill_wave.rs:579-584)
-//   hh_q4k_mmr_s<S>     Y = W . X from f32 tokens (ggml_gemv_batched_q4_k,
-//                       crates/hayai-opencl/src/compute.rs:179-257)
-// (Compiled after q4k_mm.hip: the same MFMA arithmetic, tile decode and token-stage layout.)
+//   hh_q4k_mmr_s<S>     Y = W . X (ggml_gemv_batched_q4_k, crates/hayai-opencl/src/
+//                       compute.rs:179-257)
+// (Compiled after q4k_mm.hip: the same MFMA arithmetic, tile decode and token-stage layout;
+// hh_mm_prep writes the token stages of X once per call.)
+//
+// Token stages.  X enters as hi + lo f16 halves (the 17 KB stages of q4k_mm.hip: f32-level
+// accuracy; a single f16 rounding of the FFN input costs up to ~2e-3 of relative output
+// error).  h enters the down projection as one f16 per element plus hi/lo sums (9 KB stages:
+// [0, 8192) operands, [8192, 8704) sums hi, [8704, 9216) sums lo); its rounding costs at most
+// ~2.5e-4 of the output and halves the down projection's MFMAs and staging.
 //
 // Work split: rows in 16-row units (FFN: the gate tile and the up tile of the same 16
-// rows), superblocks in chunks of S.  A workgroup owns nw units of one chunk.  It builds the
-// chunk's S token stages in LDS once (S x 17 KB: from f32 tokens, or copied by LDS DMA from
-// stages in global memory), then each of its nw waves streams its own unit's S superblocks
-// through a ring of D items in flight.  An item is the lane's 48 bytes of each tile (block
-// header + 32 qs bytes, the operands of hh_mm_decode) at a wave-uniform base plus fixed
-// lane offsets, so wait counts are static and no barrier or exchange stands between the
-// weight stream and the MFMAs.
+// rows), superblocks in chunks of S.  A workgroup owns nw units of one chunk: it copies the
+// chunk's S token stages into LDS by DMA and waits for them before its first weight request
+// (a burst of weight requests would queue the copy behind it), then each of its nw waves
+// streams its unit's S superblocks through a ring of D items in flight.  An item is the
+// lane's 48 bytes of each tile (block header + 32 qs bytes) at a wave-uniform base plus fixed
+// lane offsets, so wait counts are static and nothing stands between the weight stream and
+// the MFMAs.  The MFMAs take the tokens as A and the weights as B, so each D lane holds four
+// tokens of its own weight row and the superblock's d and dmin apply lane by lane; each
+// weight operand is decoded right before its MFMA step (hh_mmr_wstep).
 // The chunks of one row group meet in a workspace: each workgroup writes its partial sums
 // with device-coherent stores, and the last to arrive (per-row-group counter, reset by it)
 // adds them in chunk order, so results do not depend on arrival order.
-// Token columns b..15 of the stages are never initialised: an MFMA output column depends
-// only on its own B column, so whatever they hold stays in outputs that are never stored.
+// Token slots b..15 of the stages are zero (hh_mm_prep) or whatever the gate/up kernel
+// computed for them: an MFMA output depends only on its own token, so they stay in outputs
+// that are never stored.
 
 struct hh_mmr_args {
     const uint8_t* w0;  // GEMM: W; FFN: W_gate   [m][row_bytes]
     const uint8_t* w1;  // FFN: W_up
-    const void* x;      // f32 tokens [b][n], or token stages [n/256] (down projection)
+    const uint8_t* xop; // token stages of the input [n/256]
     float* y;           // GEMM: [b][m] f32
-    uint8_t* hop;       // FFN: h as token stages [m/256]
+    uint8_t* hop;       // FFN: h as single-f16 token stages [m/256]
     float* part;        // kc > 1: [groups][kc][nw][tiles * 4 rows][64 lanes] partial sums
     unsigned* cnt;      // kc > 1: arrival counter per row group (zero between launches)
     uint64_t row_bytes;
@@ -40,55 +50,67 @@ struct hh_mmr_args {
 };
 
 #define HH_MMR_MAX_WAVES 8
-#define HH_MMR_XROUNDS 5  // token-staging jobs per thread kept in registers ahead of the ring
+#define HH_MMR_STAGE_HI 9216u  // single-f16 stage: operands, sums hi, sums lo
 
-// One staging job: token t, half-sub-block hs (16 elements) of the chunk, from 4 float4 of
-// f32 tokens into hi/lo f16 operands and the half's sum (as hh_mm_prep).
-HH_DEV void hh_mmr_stage_job(uint8_t* stages, uint32_t t, uint32_t hs, const float4* v) {
-    uint8_t* st = stages + (hs / 16u) * HH_MM_STAGE;
-    const uint32_t h = hs % 16u;
-    const float e[16] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w,
-                         v[2].x, v[2].y, v[2].z, v[2].w, v[3].x, v[3].y, v[3].z, v[3].w};
-    float s = 0.f;
-#pragma unroll
-    for (int half8 = 0; half8 < 2; half8++) {
-        hh_h8 hi, lo;
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            _Float16 vh, vl;
-            hh_split_f16(e[8 * half8 + k], vh, vl);
-            hi[k] = vh;
-            lo[k] = vl;
-            s += e[8 * half8 + k];
-        }
-        const uint32_t off = hh_mm_elem_off(t, h * 16 + 8 * half8);
-        *reinterpret_cast<hh_h8*>(st + off) = hi;
-        *reinterpret_cast<hh_h8*>(st + 8192 + off) = lo;
+// Superblock header of this lane's row, decoded for its group c: the sub-block scales as
+// (sc, -1024 sc) f16 pairs (for hh_mm_scq), the mins as the B operand of the min MFMA, d
+// and dmin (q4k.rs:34-43).
+struct hh_mmr_head {
+    hh_h2 sl, sh, nl, nh;
+    hh_h4 amin;
+    float d, dmin;
+};
+HH_DEV void hh_mmr_head_decode(const uint4& h, uint32_t c, hh_mmr_head& t) {
+    const uint32_t kk = 2u * (c & 1u);
+    const uint32_t sel_yz = kk | ((kk + 1u) << 8) | ((kk + 4u) << 16) | ((kk + 5u) << 24);
+    const uint32_t sel_w = kk | ((kk + 1u) << 8) | (kk << 16) | ((kk + 1u) << 24);
+    const uint32_t b = __builtin_amdgcn_perm(h.z, h.y, sel_yz);
+    const uint32_t lo = b & 0x3F3F3F3Fu;
+    const uint32_t wp = __builtin_amdgcn_perm(h.w, h.w, sel_w);
+    const uint32_t hi = (wp & 0x00000F0Fu) | ((wp >> 4) & 0x0F0F0000u) | ((b >> 2) & 0x30303030u);
+    const uint32_t s = c >= 2 ? hi : lo;
+    const float sc_lo = hh_ub0(s), sc_hi = hh_ub1(s);
+    t.d = hh_f16(h.x & 0xFFFFu);
+    t.dmin = hh_f16(h.x >> 16);
+    const _Float16 mlo = (_Float16)(-hh_ub2(s));
+    const _Float16 mhi = (_Float16)(-hh_ub3(s));
+    t.amin = hh_h4{mlo, mlo, mhi, mhi};
+    t.sl = hh_h2{(_Float16)sc_lo, (_Float16)sc_lo};
+    t.sh = hh_h2{(_Float16)sc_hi, (_Float16)sc_hi};
+    t.nl = hh_h2{(_Float16)(-1024.0f * sc_lo), (_Float16)(-1024.0f * sc_lo)};
+    t.nh = hh_h2{(_Float16)(-1024.0f * sc_hi), (_Float16)(-1024.0f * sc_hi)};
+}
+
+// Weight operand of MFMA step s (the k order of hh_mm_decode): s < 4 takes the low nibbles
+// of qs dwords 2s, 2s+1 of this lane's group, s >= 4 the high nibbles of dwords 2(s-4),
+// 2(s-4)+1; each weight becomes sc * q, exact in f16.
+template <int S_>
+HH_DEV hh_h8 hh_mmr_wstep(const uint4& q0, const uint4& q1, const hh_mmr_head& t) {
+    constexpr int s4 = S_ & 3;
+    const uint32_t w0 = s4 == 0 ? q0.x : s4 == 1 ? q0.z : s4 == 2 ? q1.x : q1.z;
+    const uint32_t w1 = s4 == 0 ? q0.y : s4 == 1 ? q0.w : s4 == 2 ? q1.y : q1.w;
+    hh_h2 r[4];
+    if constexpr (S_ < 4) {
+        hh_mm_scq(w0 & 0x0F0F0F0Fu, t.sl, t.nl, r);
+        hh_mm_scq(w1 & 0x0F0F0F0Fu, t.sl, t.nl, r + 2);
+    } else {
+        hh_mm_scq((w0 >> 4) & 0x0F0F0F0Fu, t.sh, t.nh, r);
+        hh_mm_scq((w1 >> 4) & 0x0F0F0F0Fu, t.sh, t.nh, r + 2);
     }
-    _Float16 sh, sl;
-    hh_split_f16(s, sh, sl);
-    const uint32_t so = hh_mm_sum_off(t, h);
-    *reinterpret_cast<_Float16*>(st + so) = sh;
-    *reinterpret_cast<_Float16*>(st + 512 + so) = sl;
+    return hh_h8{r[0].x, r[0].y, r[1].x, r[1].y, r[2].x, r[2].y, r[3].x, r[3].y};
 }
 
-HH_DEV void hh_mmr_load_job(const float* x, uint32_t n, uint32_t sb0, uint32_t per_tok, uint32_t job, float4* v,
-                            uint32_t& t, uint32_t& hs) {
-    t = job / per_tok;
-    hs = job % per_tok;
-    const float4* src = reinterpret_cast<const float4*>(x + (size_t)t * n + (size_t)sb0 * 256 + (size_t)hs * 16);
-#pragma unroll
-    for (int q = 0; q < 4; q++) v[q] = src[q];
-}
-
-// FFN: NT = 2 tiles per unit (gate, up); GEMM: 1.  XF32: tokens arrive as f32 (else as
-// stages in global memory).  S superblocks per chunk, D ring items in flight per wave, P of
-// them issued before the f32 tokens are converted.
-template <bool FFN, bool XF32, int S, int D, int P>
+// FFN: NT = 2 tiles per unit (gate, up); GEMM: 1.  LO: the input stages carry lo halves
+// (17 KB stages) or not (9 KB).  S superblocks per chunk, D ring items in flight per wave,
+// refilled RB at a time (RB consecutive superblocks of each row per request burst: longer
+// runs per DRAM page than one 144-byte block).
+template <bool FFN, bool LO, int S, int D, int RB>
 HH_DEV void hh_mmr_body(const hh_mmr_args& a) {
-    extern __shared__ __attribute__((aligned(16))) char hh_smem[];  // S token stages
+    extern __shared__ __attribute__((aligned(16))) char hh_smem[];  // S token stages [+ FFN tiles]
     __shared__ int last_flag;
     constexpr int NT = FFN ? 2 : 1;
+    constexpr uint32_t SB = LO ? HH_MM_STAGE : HH_MMR_STAGE_HI;  // stage bytes
+    constexpr uint32_t SUMS = LO ? 16384u : 8192u;               // offset of the sums
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % HH_WAVE;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / HH_WAVE);
@@ -124,46 +146,18 @@ HH_DEV void hh_mmr_body(const hh_mmr_args& a) {
     };
     constexpr int D0 = D < S ? D : S;
 
-    if constexpr (XF32) {
-        // f32 tokens: the first HH_MMR_XROUNDS jobs per thread are loaded before any weight
-        // request (surplus threads repeat the last job: identical bytes to the same place)
-        const float* x = reinterpret_cast<const float*>(a.x);
-        const uint32_t per_tok = ns * 16u;
-        const uint32_t jobs = a.b * per_tok;
-        float4 xv[HH_MMR_XROUNDS][4];
-        uint32_t jt[HH_MMR_XROUNDS], jh[HH_MMR_XROUNDS];
-#pragma unroll
-        for (int k = 0; k < HH_MMR_XROUNDS; k++)
-            hh_mmr_load_job(x, a.n, sb0, per_tok, min(tid + (uint32_t)k * nthr, jobs - 1), xv[k], jt[k], jh[k]);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int s = 0; s < (P < D0 ? P : D0); s++) issue(s, ring[s]);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int k = 0; k < HH_MMR_XROUNDS; k++) hh_mmr_stage_job(stages, jt[k], jh[k], xv[k]);
-        for (uint32_t job = tid + HH_MMR_XROUNDS * nthr; job < jobs; job += nthr) {  // few waves only
-            float4 v[4];
-            uint32_t t, hs;
-            hh_mmr_load_job(x, a.n, sb0, per_tok, job, v, t, hs);
-            hh_mmr_stage_job(stages, t, hs, v);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int s = (P < D0 ? P : D0); s < D0; s++) issue(s, ring[s]);
-    } else {
-        // stages in global memory: LDS DMA of the chunk (17 * 64 chunks of 16 bytes per
-        // stage), then the ring; the DMA is complete once at most the ring's loads remain
-        const uint8_t* src = reinterpret_cast<const uint8_t*>(a.x) + (size_t)sb0 * HH_MM_STAGE;
-        const uint32_t chunks = ns * (HH_MM_STAGE / 16u);
+    // the chunk's stages -> LDS (SB / 16 = 17 * 64 or 9 * 64 chunks of 16 bytes per stage),
+    // complete before the first weight request; then the ring
+    {
+        const uint8_t* src = a.xop + (size_t)sb0 * SB;
+        const uint32_t chunks = ns * (SB / 16u);
         for (uint32_t c0 = wave * HH_WAVE; c0 < chunks; c0 += nthr)
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + (size_t)(c0 + lane) * 16),
                                              (__attribute__((address_space(3))) void*)(stages + (size_t)c0 * 16), 16, 0, 0);
-#pragma unroll
-        for (int s = 0; s < D0; s++) issue(s, ring[s]);
-        constexpr uint32_t pend = (uint32_t)(D0 * NT * 3);  // vmcnt: only ring loads may remain
-        static_assert(pend < 64, "ring loads exceed the vmcnt range");
-        __builtin_amdgcn_s_waitcnt((pend & 0xFu) | (0x7u << 4) | (0xFu << 8) | ((pend >> 4) << 14));
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
+#pragma unroll
+    for (int s = 0; s < D0; s++) issue(s, ring[s]);
     __syncthreads();  // the chunk's token stages are in LDS
 
     hh_f4 acc[NT];
@@ -171,10 +165,20 @@ HH_DEV void hh_mmr_body(const hh_mmr_args& a) {
     for (int q = 0; q < NT; q++) acc[q] = hh_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < S; j++) {
-        hh_mm_tile t[NT];
+        hh_mmr_head hd[NT];
+        uint4 qa[NT], qb[NT];
 #pragma unroll
-        for (int q = 0; q < NT; q++) hh_mm_decode(ring[j % D][q].h, ring[j % D][q].q0, ring[j % D][q].q1, c, lane, t[q]);
-        if (j + D < S) issue(j + D, ring[j % D]);
+        for (int q = 0; q < NT; q++) {
+            hh_mmr_head_decode(ring[j % D][q].h, c, hd[q]);
+            qa[q] = ring[j % D][q].q0;
+            qb[q] = ring[j % D][q].q1;
+        }
+        static_assert(D % RB == 0, "refill batches must divide the ring");
+        if ((j + 1) % RB == 0) {
+#pragma unroll
+            for (int k = j + 1 - RB + D; k <= j + D; k++)
+                if (k < S) issue(k, ring[k % D]);
+        }
         // items past a short last chunk add nothing: their weights and token stage repeat
         // item 0's (finite values, scaled by zero)
         uint32_t jst = (uint32_t)j;
@@ -182,48 +186,58 @@ HH_DEV void hh_mmr_body(const hh_mmr_args& a) {
             jst = (uint32_t)j < ns ? (uint32_t)j : 0u;
             const float keep = (uint32_t)j < ns ? 1.f : 0.f;
 #pragma unroll
-            for (int q = 0; q < NT; q++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    t[q].d4[r] *= keep;
-                    t[q].dmin4[r] *= keep;
-                }
+            for (int q = 0; q < NT; q++) {
+                hd[q].d *= keep;
+                hd[q].dmin *= keep;
+            }
         }
-        const uint8_t* st = stages + jst * HH_MM_STAGE;
+        const uint8_t* st = stages + jst * SB;
+        // all token fragments of the item are requested at once, ahead of the decode
+        constexpr int NF = LO ? 16 : 8;
+        hh_h8 xf[NF];
+#pragma unroll
+        for (int i = 0; i < NF; i++) xf[i] = *reinterpret_cast<const hh_h8*>(st + (i >> 3) * 8192 + ((i & 7) * 64 + lane) * 16);
+        const hh_h4 shi = *reinterpret_cast<const hh_h4*>(st + SUMS + lane * 8);
+        const hh_h4 slo = *reinterpret_cast<const hh_h4*>(st + SUMS + 512 + lane * 8);
+        __builtin_amdgcn_sched_barrier(0);
         const hh_f4 z = hh_f4{0.f, 0.f, 0.f, 0.f};
-        hh_f4 sq[NT], sm[NT];
-#pragma unroll
-        for (int q = 0; q < NT; q++) sq[q] = z;
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const hh_h8 xh = *reinterpret_cast<const hh_h8*>(st + (s * 64 + lane) * 16);
-#pragma unroll
-            for (int q = 0; q < NT; q++) sq[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(t[q].a[s], xh, sq[q], 0, 0, 0);
-        }
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const hh_h8 xl = *reinterpret_cast<const hh_h8*>(st + 8192 + (s * 64 + lane) * 16);
-#pragma unroll
-            for (int q = 0; q < NT; q++) sq[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(t[q].a[s], xl, sq[q], 0, 0, 0);
-        }
-        const hh_h4 shi = *reinterpret_cast<const hh_h4*>(st + 16384 + lane * 8);
-        const hh_h4 slo = *reinterpret_cast<const hh_h4*>(st + 16896 + lane * 8);
+        hh_f4 ah[NT], al[NT], am[NT];
 #pragma unroll
         for (int q = 0; q < NT; q++) {
-            sm[q] = __builtin_amdgcn_mfma_f32_16x16x16f16(t[q].amin, shi, z, 0, 0, 0);
-            sm[q] = __builtin_amdgcn_mfma_f32_16x16x16f16(t[q].amin, slo, sm[q], 0, 0, 0);
+            ah[q] = z;
+            al[q] = z;
+        }
+#define HH_MMR_STEP(SS)                                                                     \
+    _Pragma("unroll") for (int q = 0; q < NT; q++) {                                         \
+        const hh_h8 w = hh_mmr_wstep<SS>(qa[q], qb[q], hd[q]);                               \
+        ah[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[SS], w, ah[q], 0, 0, 0);           \
+        if constexpr (LO) al[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[8 + ((SS) & 7)], w, al[q], 0, 0, 0); \
+    }
+        HH_MMR_STEP(0)
+        HH_MMR_STEP(1)
+        HH_MMR_STEP(2)
+        HH_MMR_STEP(3)
+        HH_MMR_STEP(4)
+        HH_MMR_STEP(5)
+        HH_MMR_STEP(6)
+        HH_MMR_STEP(7)
+#undef HH_MMR_STEP
+#pragma unroll
+        for (int q = 0; q < NT; q++) {
+            am[q] = __builtin_amdgcn_mfma_f32_16x16x16f16(shi, hd[q].amin, z, 0, 0, 0);
+            am[q] = __builtin_amdgcn_mfma_f32_16x16x16f16(slo, hd[q].amin, am[q], 0, 0, 0);
         }
 #pragma unroll
         for (int q = 0; q < NT; q++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                acc[q][r] = fmaf(t[q].d4[r], sq[q][r], acc[q][r]);
-                acc[q][r] = fmaf(t[q].dmin4[r], sm[q][r], acc[q][r]);
+                acc[q][r] = fmaf(hd[q].d, LO ? ah[q][r] + al[q][r] : ah[q][r], acc[q][r]);
+                acc[q][r] = fmaf(hd[q].dmin, am[q][r], acc[q][r]);
             }
     }
 
-    // D lane (token r16, quarter c) holds rows 4c..4c+3 of its unit.  Partials are laid out
-    // [tile][row r][lane] so every store and load instruction covers 256 contiguous bytes.
+    // Partials are laid out [tile][r][lane] so every store and load instruction covers 256
+    // contiguous bytes.
     if (a.kc > 1) {
         constexpr uint32_t PT = NT * 4u * HH_WAVE;
         float* my = a.part + (((size_t)grp * a.kc + kci) * a.nw + wave) * PT + lane;
@@ -266,73 +280,80 @@ HH_DEV void hh_mmr_body(const hh_mmr_args& a) {
     }
     if (!live) return;
 
-    const uint32_t rbase = unit * 16 + 4 * c;
+    // D lane (row r16, quarter c): acc[q][r] is token 4c + r of row R = unit * 16 + r16
+    const uint32_t R0 = unit * 16, R = R0 + r16;
     if constexpr (FFN) {
-        // h of rows rbase..rbase+3, token r16 -> the down projection's token stages (n = m).
-        // Lanes c and c^1 swap their rows, so each holds the 8-row run 8(c/2).. of its token and
-        // writes one 16-byte chunk of it: the hi halves (c even) or the lo halves (c odd).
-        float h[4];
-        float hsum = 0.f;
+        // h -> single-f16 token stages of the down projection (n = m).  The wave transposes
+        // its 16 x 16 tile through LDS (its own 512 bytes past the stages) so that lanes 0..31
+        // each write one 16-byte chunk: 8 consecutive rows of one token.
+        _Float16* tp = reinterpret_cast<_Float16*>(stages + (size_t)S * SB + wave * 512u);
+        float hsum[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            h[r] = hh_act_mul(acc[0][r], acc[1][r], a.act);
-            hsum += h[r];
+            const float h = hh_act_mul(acc[0][r], acc[1][r], a.act);
+            hsum[r] = h;
+            tp[(4 * c + (uint32_t)r) * 16 + r16] = (_Float16)h;
         }
-        float o[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) o[r] = __shfl_xor(h[r], 16, HH_WAVE);
-        const bool odd = (c & 1u) != 0;
-        hh_h8 run;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float first = odd ? o[r] : h[r];  // rows 8p + r
-            const float second = odd ? h[r] : o[r];  // rows 8p + 4 + r
-            _Float16 hi0, lo0, hi1, lo1;
-            hh_split_f16(first, hi0, lo0);
-            hh_split_f16(second, hi1, lo1);
-            run[r] = odd ? lo0 : hi0;
-            run[4 + r] = odd ? lo1 : hi1;
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the tile is in LDS
+        __builtin_amdgcn_wave_barrier();
+        if (lane < 32) {
+            const uint32_t run = lane >> 4, tok = lane & 15u;
+            const hh_h8 chunk = *reinterpret_cast<const hh_h8*>(tp + tok * 16 + 8 * run);
+            uint8_t* st = a.hop + (size_t)(R0 / 256) * HH_MMR_STAGE_HI;
+            *reinterpret_cast<hh_h8*>(st + hh_mm_elem_off(tok, (R0 & 255u) + 8 * run)) = chunk;
         }
-        const uint32_t e0 = unit * 16 + 8 * (c >> 1);  // first row of the run
-        uint8_t* st = a.hop + (size_t)(e0 / 256) * HH_MM_STAGE;
-        *reinterpret_cast<hh_h8*>(st + (odd ? 8192u : 0u) + hh_mm_elem_off(r16, e0 & 255u)) = run;
-        // the unit's 16 rows are one half-sub-block of h: their sum feeds the min term
-        hsum += __shfl_xor(hsum, 16, HH_WAVE);
-        hsum += __shfl_xor(hsum, 32, HH_WAVE);
-        if (c == 0) {
-            _Float16 hi, lo;
-            hh_split_f16(hsum, hi, lo);
-            uint8_t* ss = a.hop + (size_t)(unit * 16 / 256) * HH_MM_STAGE;
-            const uint32_t off = hh_mm_sum_off(r16, (unit * 16 & 255u) / 16);
-            *reinterpret_cast<_Float16*>(ss + off) = hi;
-            *reinterpret_cast<_Float16*>(ss + 512 + off) = lo;
+        // the unit's 16 rows are one half-sub-block of h: per token, their f32 sum (over the
+        // 16 lanes of the quarter) feeds the down projection's min term as hi + lo
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int m = 1; m < 16; m <<= 1) hsum[r] += __shfl_xor(hsum[r], m, HH_WAVE);
+        if (r16 == 0) {
+            uint8_t* ss = a.hop + (size_t)(R0 / 256) * HH_MMR_STAGE_HI;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                _Float16 hi, lo;
+                hh_split_f16(hsum[r], hi, lo);
+                const uint32_t off = hh_mm_sum_off(4 * c + (uint32_t)r, (R0 & 255u) / 16) - 16384u + 8192u;
+                *reinterpret_cast<_Float16*>(ss + off) = hi;
+                *reinterpret_cast<_Float16*>(ss + 512 + off) = lo;
+            }
         }
     } else {
-        if (r16 < a.b) {
-            float* yp = a.y + (size_t)r16 * a.m + rbase;
-            if (rbase + 4 <= a.m && ((uintptr_t)yp & 15u) == 0) {
-                *reinterpret_cast<float4*>(yp) = make_float4(acc[0][0], acc[0][1], acc[0][2], acc[0][3]);
-            } else {
+        if (R < a.m) {
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    if (rbase + r < a.m) yp[r] = acc[0][r];
+            for (int r = 0; r < 4; r++) {
+                const uint32_t tok = 4 * c + (uint32_t)r;
+                if (tok < a.b) a.y[(size_t)tok * a.m + R] = acc[0][r];
             }
         }
     }
 }
 
 #define HH_MMR_BLOCK (HH_MMR_MAX_WAVES * HH_WAVE)
-#define HH_MMR_KERNELS(S)                                                                               \
+#define HH_MMR_GU(S)                                                                                   \
     extern "C" __global__ void __launch_bounds__(HH_MMR_BLOCK) hh_q4k_mmr_gu_s##S(const hh_mmr_args a) { \
-        hh_mmr_body<true, true, S, 4, 2>(a);                                                            \
-    }                                                                                                   \
-    extern "C" __global__ void __launch_bounds__(HH_MMR_BLOCK) hh_q4k_mmr_dn_s##S(const hh_mmr_args a) { \
-        hh_mmr_body<false, false, S, S, S>(a);                                                          \
-    }                                                                                                   \
-    extern "C" __global__ void __launch_bounds__(HH_MMR_BLOCK) hh_q4k_mmr_s##S(const hh_mmr_args a) {    \
-        hh_mmr_body<false, true, S, S, 4>(a);                                                           \
+        hh_mmr_body<true, true, S, (S < 3 ? S : 3), 1>(a);                                                              \
     }
-HH_MMR_KERNELS(2)
-HH_MMR_KERNELS(4)
-HH_MMR_KERNELS(7)
-HH_MMR_KERNELS(8)
+#define HH_MMR_GEMM(S)                                                                                 \
+    extern "C" __global__ void __launch_bounds__(HH_MMR_BLOCK) hh_q4k_mmr_s##S(const hh_mmr_args a) {    \
+        hh_mmr_body<false, true, S, (S < 6 ? S : 6), 1>(a);                                               \
+    }
+#define HH_MMR_DN(S)                                                                                   \
+    extern "C" __global__ void __launch_bounds__(HH_MMR_BLOCK) hh_q4k_mmr_dn_s##S(const hh_mmr_args a) { \
+        hh_mmr_body<false, false, S, (S < 4 ? S : 4), (S < 4 ? 1 : 2)>(a);                                              \
+    }
+HH_MMR_GU(2)
+HH_MMR_GU(4)
+HH_MMR_GU(7)
+HH_MMR_GU(8)
+HH_MMR_GEMM(2)
+HH_MMR_GEMM(4)
+HH_MMR_GEMM(7)
+HH_MMR_GEMM(8)
+HH_MMR_DN(2)
+HH_MMR_DN(4)
+HH_MMR_DN(7)
+HH_MMR_DN(8)
+HH_MMR_DN(14)
+HH_MMR_DN(16)

@@ -741,7 +741,7 @@ hh_status hh_engine::enqueue_q4k_mm(size_t m, size_t n, const uint8_t* w0, const
 struct hh_mmr_args {
     const uint8_t* w0;
     const uint8_t* w1;
-    const void* x;
+    const void* xop;
     float* y;
     void* hop;
     float* part;
@@ -751,25 +751,34 @@ struct hh_mmr_args {
     int32_t act;
 };
 constexpr size_t kMmrMaxTokens = 16;
+constexpr size_t kMmrStageHi = 9216;     // single-f16 token stage (the down projection's h)
+constexpr size_t kMmrTileLds = 8 * 512;  // gate/up: per-wave 512-byte transposition tile after the stages
+
+static size_t mmr_stage_bytes(int kind) { return kind == hh_engine::MMR_DN ? kMmrStageHi : kMmStage; }
 
 // Work split of a weight-stream launch over nu 16-row units and nsb superblocks: chunks of
-// S superblocks (S x 17 KB of token stages in LDS) and nw units (one wave each) per
-// workgroup.  A CU holds res = min(LDS / stages, 8 / nw) workgroups at once (the kernels
-// need more than 128 VGPRs: at most two waves per SIMD); its stream rate is taken as
-// proportional to its resident waves (up to 8), plus a fixed start-up cost of about two
-// items per round (first-data latency, token staging).  Ties go to the split that fills
-// more of the CU slots, then to longer chunks (fewer partial sums).
+// S superblocks (their token stages in LDS) and nw units (one wave each) per workgroup.  A
+// CU holds res = min(LDS / stages, 8 / nw) workgroups at once (the kernels need more than
+// 128 VGPRs: at most two waves per SIMD); its stream rate is taken as proportional to its
+// resident waves (up to 8), plus a fixed start-up cost of about two items per round (stage
+// copy, first-data latency).  Ties go to the split that fills more of the CU slots, then to
+// longer chunks (fewer partial sums).
 struct mmr_plan {
     int S = 0;
     uint32_t nw = 0, kc = 0, groups = 0;
 };
-static mmr_plan plan_mmr(size_t nu, size_t nsb, size_t cus, size_t lds) {
+static mmr_plan plan_mmr(int kind, size_t nu, size_t nsb, size_t cus, size_t lds) {
+    static const int gu_s[] = {8, 7, 4, 2}, dn_s[] = {16, 14, 8, 7, 4, 2};
+    const int* ss = kind == hh_engine::MMR_DN ? dn_s : gu_s;
+    const size_t nss = kind == hh_engine::MMR_DN ? 6 : 4;
+    const size_t sb = mmr_stage_bytes(kind), extra = (kind == hh_engine::MMR_GU ? kMmrTileLds : 0) + 64;
     mmr_plan best;
     double best_cost = 1e300, best_fill = 0;
-    for (int S : {8, 7, 4, 2}) {
+    for (size_t si = 0; si < nss; si++) {
+        const int S = ss[si];
         if (S > 2 && (size_t)S > nsb) continue;
         const size_t kc = (nsb + S - 1) / S;
-        const size_t by_lds = lds / ((size_t)S * kMmStage + 64);
+        const size_t by_lds = lds / ((size_t)S * sb + extra);
         if (by_lds == 0) continue;
         for (size_t nw = 8; nw >= 1; nw--) {
             const size_t groups = (nu + nw - 1) / nw;
@@ -801,9 +810,9 @@ hh_status hh_engine::enqueue_q4k_mmr(int kind, size_t m, size_t n, const uint8_t
     if (!mmr_ok(m, n, b, w0, kind == MMR_GU ? w1 : w0, x) || (kind == MMR_GU && m % 256 != 0))
         return HH_ERR_UNSUPPORTED_DEVICE;
     const size_t nsb = n / 256, nu = (m + 15) / 16;
-    const mmr_plan pl = plan_mmr(nu, nsb, (size_t)props.multiProcessorCount, (size_t)props.sharedMemPerBlock);
+    const mmr_plan pl = plan_mmr(kind, nu, nsb, (size_t)props.multiProcessorCount, (size_t)props.sharedMemPerBlock);
     if (pl.S == 0) return HH_ERR_UNSUPPORTED_DEVICE;
-    const size_t smem = (size_t)pl.S * kMmStage;
+    const size_t smem = (size_t)pl.S * mmr_stage_bytes(kind) + (kind == MMR_GU ? kMmrTileLds : 0);
     const size_t nt = kind == MMR_GU ? 2 : 1;
     if (pl.kc > 1) {
         HH_TRY(grow(&ws_part, &ws_part_cap, (size_t)pl.groups * pl.kc * pl.nw * nt * 256 * sizeof(float)));
@@ -812,14 +821,21 @@ hh_status hh_engine::enqueue_q4k_mmr(int kind, size_t m, size_t n, const uint8_t
             HH_TRY_HIP(hipMemsetAsync(ws_cnt, 0, ws_cnt_cap, stream), "hipMemsetAsync(counters)");
         }
     }
-    if (kind == MMR_GU) HH_TRY(grow(&ws_hop, &ws_hop_cap, mm_stage_bytes(m, 1)));
+    // the input's token stages: f32 tokens are staged once per call (hi + lo halves); the down
+    // projection reads the gate/up kernel's single-f16 stages of h
+    const void* xop = x;
+    if (kind != MMR_DN) {
+        HH_TRY(enqueue_mm_prep((const float*)x, b, n, 1));
+        xop = ws_xop;
+    }
+    if (kind == MMR_GU) HH_TRY(grow(&ws_hop, &ws_hop_cap, (m / 256) * kMmrStageHi));
     static const char* kinds[] = {"hh_q4k_mmr_s", "hh_q4k_mmr_gu_s", "hh_q4k_mmr_dn_s"};
     hipFunction_t fn;
     HH_TRY(kernel(std::string(kinds[kind]) + std::to_string(pl.S), &fn));
     hh_mmr_args a{};
     a.w0 = w0;
     a.w1 = kind == MMR_GU ? w1 : w0;
-    a.x = x;
+    a.xop = xop;
     a.y = y;
     a.hop = ws_hop;
     a.part = (float*)ws_part;
@@ -1060,8 +1076,8 @@ static std::vector<std::string> required_kernels() {
         for (const char* kind : {"hh_q4k_mm_t", "hh_q4k_mm_gateup_t"}) k.push_back(std::string(kind) + std::to_string(tt));
     k.push_back("hh_mm_prep");
     for (int S : {2, 4, 7, 8})
-        for (const char* kind : {"hh_q4k_mmr_s", "hh_q4k_mmr_gu_s", "hh_q4k_mmr_dn_s"})
-            k.push_back(std::string(kind) + std::to_string(S));
+        for (const char* kind : {"hh_q4k_mmr_s", "hh_q4k_mmr_gu_s"}) k.push_back(std::string(kind) + std::to_string(S));
+    for (int S : {2, 4, 7, 8, 14, 16}) k.push_back("hh_q4k_mmr_dn_s" + std::to_string(S));
     k.push_back("hh_lut_gemv");
     for (const char* f : {"g1_d1", "g1_d2", "g1_d4", "g1_d8", "g2_d2", "g2_d4", "g2_d8"})
         k.push_back(std::string("hh_q4k_ffnp_") + f);
