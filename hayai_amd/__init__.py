@@ -17,6 +17,8 @@ from .engine import (  # noqa: F401
     IQ3_XXS,
     Q4_0,
     Q4_K,
+    Q6_K,
+    Q8_0,
     DeviceBuffer,
     HipEngine,
     HipError,

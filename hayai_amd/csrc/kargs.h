@@ -10,7 +10,9 @@
 #define HH_TYPE_F32 0
 #define HH_TYPE_F16 1
 #define HH_TYPE_Q4_0 2
+#define HH_TYPE_Q8_0 8
 #define HH_TYPE_Q4_K 12
+#define HH_TYPE_Q6_K 14
 #define HH_TYPE_IQ2_XXS 16
 #define HH_TYPE_IQ3_XXS 18
 

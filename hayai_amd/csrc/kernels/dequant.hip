@@ -3,6 +3,8 @@
 // -ffp-contract=off), so the output is bit-identical to hayai-model's dequant:
 //   Q4_0    (float)(q - 8) * d                                  gguf.rs:348-372
 //   Q4_K    (d*sc)*q - (dmin*m)                                 q4k.rs:178-203
+//   Q8_0    (float)(i8)q * d                                    gguf.rs:401-420
+//   Q6_K    (d*sc)*(q - 32)                                     q6k.rs:27-57
 //   IQ2_XXS ((d*(0.5+s))*0.25 * g) * (+-1)                      iq2.rs:504-523
 //   IQ3_XXS ((d*(0.5+s))*0.5 * g) * (+-1)                       iq3.rs:147-173
 //   F16     IEEE binary16 -> f32                                gguf.rs:521-545
@@ -48,6 +50,43 @@ extern "C" __global__ void __launch_bounds__(256) hh_dequant_q4_k(const hh_dequa
         const uint8_t* q = blk + 16 + 32 * g;
         for (int l = 0; l < 32; l++) y[64 * g + l] = d1 * (float)(q[l] & 0x0Fu) - m1v;
         for (int l = 0; l < 32; l++) y[64 * g + 32 + l] = d2 * (float)(q[l] >> 4) - m2v;
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) hh_dequant_q8_0(const hh_dequant_args a) {
+    const uint64_t b = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint64_t nblk = (a.n + 31) / 32;
+    if (b >= nblk) return;
+    const uint8_t* blk = a.w + b * 34;
+    const float d = hh_f16(hh_ld_u16(blk));
+    for (int j = 0; j < 32; j++) {
+        const uint64_t i = b * 32 + j;
+        if (i < a.n) a.out[i] = (float)(int8_t)blk[2 + j] * d;
+    }
+}
+
+// One thread per superblock; element order and products as dequant_q6_k_block.
+extern "C" __global__ void __launch_bounds__(256) hh_dequant_q6_k(const hh_dequant_args a) {
+    const uint64_t b = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= a.n / 256) return;
+    const uint8_t* blk = a.w + b * 210;
+    const float d = hh_f16(hh_ld_u16(blk + 208));
+    float* y = a.out + b * 256;
+    for (int h = 0; h < 2; h++) {
+        const uint8_t* ql = blk + 64 * h;
+        const uint8_t* qh = blk + 128 + 32 * h;
+        const int8_t* sc = reinterpret_cast<const int8_t*>(blk + 192 + 8 * h);
+        for (int l = 0; l < 32; l++) {
+            const int is = l / 16;
+            const int q1 = (int)((ql[l] & 0x0Fu) | (((qh[l] >> 0) & 3u) << 4)) - 32;
+            const int q2 = (int)((ql[l + 32] & 0x0Fu) | (((qh[l] >> 2) & 3u) << 4)) - 32;
+            const int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3u) << 4)) - 32;
+            const int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3u) << 4)) - 32;
+            y[128 * h + l] = d * (float)sc[is] * (float)q1;
+            y[128 * h + l + 32] = d * (float)sc[is + 2] * (float)q2;
+            y[128 * h + l + 64] = d * (float)sc[is + 4] * (float)q3;
+            y[128 * h + l + 96] = d * (float)sc[is + 6] * (float)q4;
+        }
     }
 }
 

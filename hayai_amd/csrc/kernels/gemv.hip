@@ -196,6 +196,8 @@ HH_TEAMS(HH_GEMV_KERNEL, q4_k_unaligned, QK4<false>)
 HH_TEAMS(HH_GEMV_KERNEL, q4_0, Q40)
 HH_TEAMS(HH_GEMV_KERNEL, iq2_xxs, QI2)
 HH_TEAMS(HH_GEMV_KERNEL, iq3_xxs, QI3)
+HH_TEAMS(HH_GEMV_KERNEL, q8_0, Q80)
+HH_TEAMS(HH_GEMV_KERNEL, q6_k, QK6)
 HH_TEAMS(HH_GEMV_KERNEL, f32, QF32)
 HH_TEAMS(HH_GEMV_KERNEL, f16, QF16)
 
@@ -204,6 +206,8 @@ HH_TEAMS(HH_GATEUP_KERNEL, q4_k_unaligned, QK4<false>)
 HH_TEAMS(HH_GATEUP_KERNEL, q4_0, Q40)
 HH_TEAMS(HH_GATEUP_KERNEL, iq2_xxs, QI2)
 HH_TEAMS(HH_GATEUP_KERNEL, iq3_xxs, QI3)
+HH_TEAMS(HH_GATEUP_KERNEL, q8_0, Q80)
+HH_TEAMS(HH_GATEUP_KERNEL, q6_k, QK6)
 
 // Element-wise act(g) * u, for FFNs whose gate and up formats differ (unfused path).
 extern "C" __global__ void __launch_bounds__(256) hh_act_mul_kernel(const hh_act_args a) {

@@ -8,6 +8,10 @@
 //           + qs[32g .. 32g+32); 64 columns: low nibbles -> sub-block 2g, high -> 2g+1
 //           (crates/hayai-model/src/q4k.rs:178-203)
 //   Q4_0    unit = one 18-byte block, 32 columns (gguf.rs:348-372)
+//   Q8_0    unit = one 34-byte block: d + 32 int8 codes (gguf.rs:401-420)
+//   Q6_K    unit = quarter (h, is) of a 210-byte superblock: 16 columns of each of the four
+//           32-column groups of half h, taken from ql[64h+16is..+16), ql[64h+32+16is..+16),
+//           qh[32h+16is..+16), scales[8h+is+{0,2,4,6}] and d (q6k.rs:27-57)
 //   IQ2_XXS unit = one 32-column sub-block ib of a 66-byte block: d + aux0/aux1
 //           (iq2.rs:504-523)
 //   IQ3_XXS unit = one 32-column sub-block ib of a 98-byte block: d + qs[8ib..8ib+8) +
@@ -195,6 +199,116 @@ struct Q40 {
             ah = fmaf(hh_ub3(h), xr.v[16 + 4 * i + 3], ah);
         }
         return hh_f16(d.d) * ((al + ah * 0.0625f) - 8.0f * xr.s);
+    }
+};
+
+// ------------------------------------------------------------------------ Q8_0 ------
+struct Q80 {
+    static constexpr uint32_t UNIT = 32;
+    static constexpr uint32_t BLOCK = 32;
+    static constexpr uint32_t BLOCK_BYTES = 34;
+    static constexpr bool TABLES = false;
+    struct Data {
+        uint32_t d;
+        uint32_t q[8];
+    };
+    struct X {
+        float v[32];
+    };
+    static HH_DEV Data load(const uint8_t* row, uint32_t u) {
+        const uint8_t* blk = row + (size_t)u * 34;  // 2-byte aligned
+        Data d;
+        d.d = hh_ld_u16(blk);
+#pragma unroll
+        for (int i = 0; i < 8; i++) d.q[i] = hh_ld_u32_a2(blk + 2 + 4 * i);
+        return d;
+    }
+    static HH_DEV void load_x(const float* x, uint32_t u, X& xr) {
+        const float* p = x + (size_t)u * 32;
+#pragma unroll
+        for (int i = 0; i < 32; i++) xr.v[i] = p[i];
+    }
+    // d * sum(q x) over the block's 32 signed codes
+    static HH_DEV float dot(const Data& d, const X& xr, uint32_t, const hh_tables*) {
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int32_t w = (int32_t)d.q[i];
+            float& a = (i & 1) ? a1 : a0;
+            a = fmaf((float)((w << 24) >> 24), xr.v[4 * i + 0], a);
+            a = fmaf((float)((w << 16) >> 24), xr.v[4 * i + 1], a);
+            a = fmaf((float)((w << 8) >> 24), xr.v[4 * i + 2], a);
+            a = fmaf((float)(w >> 24), xr.v[4 * i + 3], a);
+        }
+        return hh_f16(d.d) * (a0 + a1);
+    }
+};
+
+// ------------------------------------------------------------------------ Q6_K ------
+struct QK6 {
+    static constexpr uint32_t UNIT = 64;
+    static constexpr uint32_t BLOCK = 256;
+    static constexpr uint32_t BLOCK_BYTES = 210;
+    static constexpr bool TABLES = false;
+    struct Data {
+        uint32_t la[4], lb[4], h[4];  // ql run (groups 0, 2), ql run (groups 1, 3), qh run
+        uint32_t sc;                  // scales of groups 0..3 (i8 bytes)
+        uint32_t d;
+    };
+    struct X {
+        float v[64];  // 16 columns of each group, group r at v[16r..16r+16)
+    };
+    static HH_DEV Data load(const uint8_t* row, uint32_t u) {
+        const uint8_t* blk = row + (size_t)(u >> 2) * 210;  // 2-byte aligned
+        const uint32_t hh = (u >> 1) & 1u, is = u & 1u;
+        const uint8_t* qa = blk + 64 * hh + 16 * is;
+        const uint8_t* qh = blk + 128 + 32 * hh + 16 * is;
+        Data d;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            d.la[i] = hh_ld_u32_a2(qa + 4 * i);
+            d.lb[i] = hh_ld_u32_a2(qa + 32 + 4 * i);
+            d.h[i] = hh_ld_u32_a2(qh + 4 * i);
+        }
+        const uint8_t* sc = blk + 192 + 8 * hh + is;
+        d.sc = (uint32_t)sc[0] | ((uint32_t)sc[2] << 8) | ((uint32_t)sc[4] << 16) | ((uint32_t)sc[6] << 24);
+        d.d = hh_ld_u16(blk + 208);
+        return d;
+    }
+    static HH_DEV void load_x(const float* x, uint32_t u, X& xr) {
+        const float* p = x + (size_t)(u >> 2) * 256 + 128 * ((u >> 1) & 1u) + 16 * (u & 1u);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int l = 0; l < 16; l++) xr.v[16 * r + l] = p[32 * r + l];
+    }
+    // d * sum_r sc_r * sum_l (q - 32) x over the four groups (q = 4 low bits | 2 high bits)
+    static HH_DEV float dot(const Data& d, const X& xr, uint32_t, const hh_tables*) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t hb = d.h[i];
+            // groups 0..3 of 4 columns: (ql low, qh bits 0-1), (ql' low, bits 2-3),
+            // (ql high, bits 4-5), (ql' high, bits 6-7)
+            const uint32_t q0 = (d.la[i] & 0x0F0F0F0Fu) | ((hb << 4) & 0x30303030u);
+            const uint32_t q1 = (d.lb[i] & 0x0F0F0F0Fu) | ((hb << 2) & 0x30303030u);
+            const uint32_t q2 = ((d.la[i] >> 4) & 0x0F0F0F0Fu) | (hb & 0x30303030u);
+            const uint32_t q3 = ((d.lb[i] >> 4) & 0x0F0F0F0Fu) | ((hb >> 2) & 0x30303030u);
+            const uint32_t qq[4] = {q0, q1, q2, q3};
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float* xv = xr.v + 16 * r + 4 * i;
+                acc[r] = fmaf(hh_ub0(qq[r]) - 32.f, xv[0], acc[r]);
+                acc[r] = fmaf(hh_ub1(qq[r]) - 32.f, xv[1], acc[r]);
+                acc[r] = fmaf(hh_ub2(qq[r]) - 32.f, xv[2], acc[r]);
+                acc[r] = fmaf(hh_ub3(qq[r]) - 32.f, xv[3], acc[r]);
+            }
+        }
+        const int32_t sc = (int32_t)d.sc;
+        const float s =
+            (float)((sc << 24) >> 24) * acc[0] + (float)((sc << 16) >> 24) * acc[1] +
+            (float)((sc << 8) >> 24) * acc[2] + (float)(sc >> 24) * acc[3];
+        return hh_f16(d.d) * s;
     }
 };
 

@@ -47,8 +47,8 @@ HH_DEV void hh_put16(uint8_t* p, uint16_t v) {
     p[1] = (uint8_t)(v >> 8);
 }
 
-// Patch the f16 scale fields: Q4_K d (field 2b) and dmin (field 2b+1); Q4_0 / IQ2_XXS /
-// IQ3_XXS d (field b).
+// Patch the f16 scale fields: Q4_K d (field 2b) and dmin (field 2b+1); Q4_0 / Q8_0 /
+// IQ2_XXS / IQ3_XXS d (field b, at the block start); Q6_K d (field b, at byte 208).
 extern "C" __global__ void __launch_bounds__(256) hh_synth_scales(const hh_synth_args a) {
     const uint64_t b = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (b >= a.nblocks) return;
@@ -60,6 +60,8 @@ extern "C" __global__ void __launch_bounds__(256) hh_synth_scales(const hh_synth
     case HH_TYPE_Q4_0: hh_put16(a.dst + b * 18, hh_synth_scale(a, b)); break;
     case HH_TYPE_IQ2_XXS: hh_put16(a.dst + b * 66, hh_synth_scale(a, b)); break;
     case HH_TYPE_IQ3_XXS: hh_put16(a.dst + b * 98, hh_synth_scale(a, b)); break;
+    case HH_TYPE_Q8_0: hh_put16(a.dst + b * 34, hh_synth_scale(a, b)); break;
+    case HH_TYPE_Q6_K: hh_put16(a.dst + b * 210 + 208, hh_synth_scale(a, b)); break;
     default: break;
     }
 }

@@ -454,7 +454,7 @@ hh_status hh_dequant_dev(hh_engine* e, int t, const hh_buf* w, size_t w_off, siz
     HH_NOT_NULL(e, "engine");
     const Format* f = format_of(t);
     if (!f || t == HH_TYPE_F32) return fail(HH_ERR_KERNEL_MISSING, "no dequant kernel for GGML type %d", t);
-    if (t != HH_TYPE_Q4_0 && n % f->block != 0)
+    if (t != HH_TYPE_Q4_0 && t != HH_TYPE_Q8_0 && n % f->block != 0)
         return fail(HH_ERR_INVALID, "dequant_%s: n=%zu not a multiple of %u", f->name, n, f->block);
     const size_t nblk = (n + f->block - 1) / f->block;
     HH_TRY(check_engine(e, w, "weights"));

@@ -40,6 +40,8 @@ static const Format kFormats[] = {
     {HH_TYPE_Q4_K, "q4_k", 256, 144, 64, true},
     {HH_TYPE_IQ2_XXS, "iq2_xxs", 256, 66, 32, true},
     {HH_TYPE_IQ3_XXS, "iq3_xxs", 256, 98, 32, true},
+    {HH_TYPE_Q8_0, "q8_0", 32, 34, 32, true},
+    {HH_TYPE_Q6_K, "q6_k", 256, 210, 64, true},
 };
 
 const Format* format_of(int t) {
@@ -1058,15 +1060,16 @@ hh_status hh_engine::enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* expert
 
 static std::vector<std::string> required_kernels() {
     std::vector<std::string> k;
-    const char* gemv_fmts[] = {"q4_k", "q4_k_unaligned", "q4_0", "iq2_xxs", "iq3_xxs", "f32", "f16"};
-    const char* gateup_fmts[] = {"q4_k", "q4_k_unaligned", "q4_0", "iq2_xxs", "iq3_xxs"};
+    const char* gemv_fmts[] = {"q4_k", "q4_k_unaligned", "q4_0", "iq2_xxs", "iq3_xxs", "q8_0", "q6_k", "f32", "f16"};
+    const char* gateup_fmts[] = {"q4_k", "q4_k_unaligned", "q4_0", "iq2_xxs", "iq3_xxs", "q8_0", "q6_k"};
     for (int i = 0; i < kNumTeamCfgs; i++) {
         std::string suf = "_t" + std::to_string(kTeamCfgs[i].team) + "_u" + std::to_string(kTeamCfgs[i].upl);
         for (const char* f : gemv_fmts) k.push_back(std::string("hh_gemv_") + f + suf);
         for (const char* f : gateup_fmts) k.push_back(std::string("hh_gateup_") + f + suf);
     }
     for (const char* s : {"hh_gemv_f32_plain", "hh_gemv_f16_plain", "hh_act_mul_kernel", "hh_dequant_q4_0",
-                          "hh_dequant_q4_k", "hh_dequant_iq2_xxs", "hh_dequant_iq3_xxs", "hh_dequant_f16",
+                          "hh_dequant_q4_k", "hh_dequant_iq2_xxs", "hh_dequant_iq3_xxs", "hh_dequant_q8_0",
+                          "hh_dequant_q6_k", "hh_dequant_f16",
                           "hh_synth_bytes", "hh_synth_scales"})
         k.push_back(s);
     for (int w : {1, 2, 4, 8})

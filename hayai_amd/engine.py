@@ -23,10 +23,11 @@ import numpy as np
 
 from . import _abi
 
-F32, F16, Q4_0, Q4_K, IQ2_XXS, IQ3_XXS = 0, 1, 2, 12, 16, 18
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, IQ2_XXS, IQ3_XXS = 0, 1, 2, 8, 12, 14, 16, 18
 ACT_SILU, ACT_GELU_TANH = 0, 1
 BUF_DEVICE, BUF_PINNED_HOST = 0, 1
-TYPE_NAMES = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q4_K: "q4_k", IQ2_XXS: "iq2_xxs", IQ3_XXS: "iq3_xxs"}
+TYPE_NAMES = {F32: "f32", F16: "f16", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k", IQ2_XXS: "iq2_xxs",
+              IQ3_XXS: "iq3_xxs"}
 
 
 class HipError(RuntimeError):
@@ -408,6 +409,12 @@ class HipEngine:
 
     def ggml_gemv_iq3_xxs(self, m, n, weights, inp):
         return self.ggml_gemv_dispatch(IQ3_XXS, m, n, weights, inp)
+
+    def ggml_gemv_q8_0(self, m, n, weights, inp):
+        return self.ggml_gemv_dispatch(Q8_0, m, n, weights, inp)
+
+    def ggml_gemv_q6_k(self, m, n, weights, inp):
+        return self.ggml_gemv_dispatch(Q6_K, m, n, weights, inp)
 
     def ggml_gemv_batched(self, ggml_type: int, m: int, n: int, weights: np.ndarray, inputs: np.ndarray,
                           batch: int) -> np.ndarray:

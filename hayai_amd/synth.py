@@ -6,7 +6,8 @@ The byte recipe is shared with the device generator (csrc/kernels/synth.hip,
 * stream byte j of seed s = byte (j % 8), little endian, of
   ``mix64(s + (j // 8 + 1) * 0x9E3779B97F4A7C15)`` (splitmix64 evaluated at a counter);
 * every f16 scale field k of the format (Q4_K: d = field 2b, dmin = field 2b+1 of block b;
-  Q4_0 / IQ2_XXS / IQ3_XXS: d = field b) is then overwritten with
+  Q4_0 / Q8_0 / IQ2_XXS / IQ3_XXS: d = field b at the block start; Q6_K: d = field b at
+  byte 208) is then overwritten with
   ``f16_rne(f32(lo + (hi - lo) * u_k))``, ``u_k = (mix64 stream of s ^ SCALE_SALT at k) >> 11
   * 2**-53`` computed in double, lo/hi being f32 values.
 
@@ -23,10 +24,12 @@ SCALE_SALT = 0xD1B54A32D192ED03
 M64 = (1 << 64) - 1
 
 # GGML type ids
-F32, F16, Q4_0, Q4_K, IQ2_XXS, IQ3_XXS = 0, 1, 2, 12, 16, 18
-BLOCK = {Q4_0: (32, 18), Q4_K: (256, 144), IQ2_XXS: (256, 66), IQ3_XXS: (256, 98), F32: (1, 4), F16: (1, 2)}
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, IQ2_XXS, IQ3_XXS = 0, 1, 2, 8, 12, 14, 16, 18
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), IQ2_XXS: (256, 66),
+         IQ3_XXS: (256, 98), F32: (1, 4), F16: (1, 2)}
 # Default U(lo, hi) ranges of the f16 scales per format (project choices).
-SCALE_RANGE = {Q4_0: (0.001, 0.02), Q4_K: (2e-4, 2e-3), IQ2_XXS: (0.001, 0.01), IQ3_XXS: (0.001, 0.01)}
+SCALE_RANGE = {Q4_0: (0.001, 0.02), Q8_0: (0.001, 0.01), Q4_K: (2e-4, 2e-3), Q6_K: (5e-5, 5e-4),
+               IQ2_XXS: (0.001, 0.01), IQ3_XXS: (0.001, 0.01)}
 
 
 def _mix64(z: np.ndarray) -> np.ndarray:
@@ -75,6 +78,9 @@ def quant_weights(t: int, n_blocks: int, seed: int, lo: float | None = None, hi:
         dm = scale_values(seed, 2 * b + 1, lo, hi)
         view[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
         view[:, 2:4] = dm.view(np.uint8).reshape(-1, 2)
+    elif t == Q6_K:
+        d = scale_values(seed, b, lo, hi)
+        view[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
     else:
         d = scale_values(seed, b, lo, hi)
         view[:, 0:2] = d.view(np.uint8).reshape(-1, 2)

@@ -56,7 +56,9 @@ enum {
     HH_TYPE_F32 = 0,
     HH_TYPE_F16 = 1,
     HH_TYPE_Q4_0 = 2,
+    HH_TYPE_Q8_0 = 8,
     HH_TYPE_Q4_K = 12,
+    HH_TYPE_Q6_K = 14,
     HH_TYPE_IQ2_XXS = 16,
     HH_TYPE_IQ3_XXS = 18
 };

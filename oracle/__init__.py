@@ -18,8 +18,9 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "libhayai_oracle.so")
 
 # GGML type ids (crates/hayai-model/src/gguf_types.rs:6-78)
-F32, F16, Q4_0, Q4_K, IQ2_XXS, IQ3_XXS = 0, 1, 2, 12, 16, 18
-BLOCK = {Q4_0: (32, 18), Q4_K: (256, 144), IQ2_XXS: (256, 66), IQ3_XXS: (256, 98), F32: (1, 4), F16: (1, 2)}
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, IQ2_XXS, IQ3_XXS = 0, 1, 2, 8, 12, 14, 16, 18
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), IQ2_XXS: (256, 66),
+         IQ3_XXS: (256, 98), F32: (1, 4), F16: (1, 2)}
 
 
 def build(force: bool = False) -> str:

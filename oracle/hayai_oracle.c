@@ -20,7 +20,8 @@
  * Pinning (how each function is checked by tests/test_oracle.py):
  *   or_f16_to_f32        exhaustive over all 65536 codes vs numpy's IEEE conversion
  *   dequant (all types)  closed-form special cases from the reference's own tests
- *                        (Q4_K d=1,dmin=0,scales=1 -> w=nibble; Q4_0 d=0x2E66 -> (q-8)*d),
+ *                        (Q4_K d=1,dmin=0,scales=1 -> w=nibble; Q4_0 d=0x2E66 -> (q-8)*d;
+ *                        Q6_K d=1,scales=1 -> w=6-bit code-32; Q8_0 d=0x2E66 -> q*d),
  *                        the reference quantizer round trip (q4k.rs:319-350), scale
  *                        packing inverse over all 64x64 (sc,m), IQ sign parity and grid
  *                        invariants, golden fixtures in tests/golden/
@@ -38,7 +39,7 @@
 #include "iq_grids.inc"
 
 /* GGML type ids, crates/hayai-model/src/gguf_types.rs:6-78. */
-enum { OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q4_K = 12, OR_IQ2_XXS = 16, OR_IQ3_XXS = 18 };
+enum { OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q6_K = 14, OR_IQ2_XXS = 16, OR_IQ3_XXS = 18 };
 
 /* Status codes shared with the ctypes wrapper. */
 enum { OR_OK = 0, OR_EINVAL = 2 };
@@ -138,7 +139,9 @@ static inline float reduce_sum8(const float a[8]) {
 static int block_geom(int type, size_t* block, size_t* bytes) {
     switch (type) {
     case OR_Q4_0: *block = 32; *bytes = 18; return 1;
+    case OR_Q8_0: *block = 32; *bytes = 34; return 1;
     case OR_Q4_K: *block = 256; *bytes = 144; return 1;
+    case OR_Q6_K: *block = 256; *bytes = 210; return 1;
     case OR_IQ2_XXS: *block = 256; *bytes = 66; return 1;
     case OR_IQ3_XXS: *block = 256; *bytes = 98; return 1;
     case OR_F32: *block = 1; *bytes = 4; return 1;
@@ -189,6 +192,40 @@ static void dequant_q4_0_block(const uint8_t* blk, float* y) {
         int x1 = (int)(qs[j] >> 4) - 8;
         y[j] = (float)x0 * d;
         y[j + 16] = (float)x1 * d;
+    }
+}
+
+/* Q8_0 dequant: (i8 q) * d; crates/hayai-model/src/gguf.rs:401-420. */
+static void dequant_q8_0_block(const uint8_t* blk, float* y) {
+    float d = f16le(blk);
+    for (int j = 0; j < 32; j++) y[j] = (float)(int8_t)blk[2 + j] * d;
+}
+
+/* Q6_K dequant; crates/hayai-model/src/q6k.rs:27-57.  Block: ql[128] | qh[64] | scales[16]
+ * (i8) | d (f16).  Two halves of 128 elements; in half h, l in 0..32 gives the elements
+ * l, l+32, l+64, l+96 from ql[64h+l] / ql[64h+l+32] (low, then high nibbles) and bit pairs
+ * 0,2,4,6 of qh[32h+l], each minus 32, scaled by (d * scales[8h + l/16 + 0,2,4,6]). */
+static void dequant_q6_k_block(const uint8_t* blk, float* y) {
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    float d = f16le(blk + 208);
+    for (int h = 0; h < 2; h++) {
+        for (int l = 0; l < 32; l++) {
+            int is = l / 16;
+            int q1 = (int)(int8_t)((ql[l] & 0x0F) | (((qh[l] >> 0) & 3) << 4)) - 32;
+            int q2 = (int)(int8_t)((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32;
+            int q3 = (int)(int8_t)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+            int q4 = (int)(int8_t)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+            y[l] = d * (float)sc[is] * (float)q1;
+            y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+            y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+            y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+        }
+        y += 128;
+        ql += 64;
+        qh += 32;
+        sc += 8;
     }
 }
 
@@ -296,7 +333,7 @@ int or_dequant(int type, const uint8_t* bytes, size_t len, size_t n, float* out)
         for (size_t i = 0; i < n; i++) out[i] = f16le(bytes + 2 * i);
         return OR_OK;
     }
-    if (type != OR_Q4_0 && n % block != 0) return OR_EINVAL; /* q4k.rs:163, iq2.rs:577 */
+    if (type != OR_Q4_0 && type != OR_Q8_0 && n % block != 0) return OR_EINVAL; /* q4k.rs:163, iq2.rs:577, q6k.rs:12 */
     size_t nblk = (n + block - 1) / block;
     if (len < nblk * bb) return OR_EINVAL;
     float tmp[256];
@@ -304,11 +341,13 @@ int or_dequant(int type, const uint8_t* bytes, size_t len, size_t n, float* out)
         const uint8_t* blk = bytes + b * bb;
         switch (type) {
         case OR_Q4_0: dequant_q4_0_block(blk, tmp); break;
+        case OR_Q8_0: dequant_q8_0_block(blk, tmp); break;
         case OR_Q4_K: dequant_q4_k_block(blk, tmp); break;
+        case OR_Q6_K: dequant_q6_k_block(blk, tmp); break;
         case OR_IQ2_XXS: dequant_iq2_xxs_block(blk, tmp); break;
         case OR_IQ3_XXS: dequant_iq3_xxs_block(blk, tmp); break;
         }
-        size_t take = n - b * block < block ? n - b * block : block; /* Q4_0 tail, gguf.rs:363-368 */
+        size_t take = n - b * block < block ? n - b * block : block; /* Q4_0 / Q8_0 tail, gguf.rs:363-368,412-416 */
         memcpy(out + b * block, tmp, take * sizeof(float));
     }
     return OR_OK;
@@ -390,6 +429,32 @@ static float row_q4_k(const uint8_t* row, size_t nb, const float* x) {
     return sum;
 }
 
+/* gemv_q8_0 row: sum += (i8 q) * d * x, element by element in column order;
+ * crates/hayai-model/src/quant.rs:598-613. */
+static float row_q8_0(const uint8_t* row, size_t nb, const float* x) {
+    float sum = 0.0f;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = row + b * 34;
+        float d = f16le(blk);
+        const float* xb = x + b * 32;
+        for (int j = 0; j < 32; j++) sum += (float)(int8_t)blk[2 + j] * d * xb[j];
+    }
+    return sum;
+}
+
+/* gemv_q6_k row: dequant every block of the row, then sum += v[c] * x[c] in column order;
+ * crates/hayai-model/src/q6k.rs:59-88. */
+static float row_q6_k(const uint8_t* row, size_t nb, const float* x) {
+    float sum = 0.0f;
+    float tmp[256];
+    for (size_t b = 0; b < nb; b++) {
+        dequant_q6_k_block(row + b * 210, tmp);
+        const float* xb = x + b * 256;
+        for (int j = 0; j < 256; j++) sum += tmp[j] * xb[j];
+    }
+    return sum;
+}
+
 /* IQ GEMV row: dequant 256 into tmp, then scalar sum += tmp[j] * x[j];
  * crates/hayai-model/src/iq2.rs:591-626 (macro body) and iq3.rs:258-295. */
 static float row_iq(const uint8_t* row, size_t nb, const float* x, int type) {
@@ -440,7 +505,9 @@ int or_gemv(int type, size_t m, size_t n, const uint8_t* w, size_t wlen, const f
         float v;
         switch (type) {
         case OR_Q4_0: v = row_q4_0(row, nb, x); break;
+        case OR_Q8_0: v = row_q8_0(row, nb, x); break;
         case OR_Q4_K: v = row_q4_k(row, nb, x); break;
+        case OR_Q6_K: v = row_q6_k(row, nb, x); break;
         case OR_IQ2_XXS:
         case OR_IQ3_XXS: v = row_iq(row, nb, x, type); break;
         case OR_F32: v = row_f32(row, n, x); break;

@@ -9,7 +9,8 @@ What it writes (data only; no reference source text is copied):
                     plus the 128 sign-table bytes.  The oracle and the HIP library are
                     checked against these.
   ref_fixtures.npz  the inputs of the reference's own GPU-vs-CPU parity tests
-                    (crates/hayai-opencl/src/compute.rs:1034-1670; their byte/input formulas
+                    (crates/hayai-opencl/src/compute.rs:1034-1670, including the Q6_K and Q8_0
+                    tests at :1146-1190 and :1235-1272; their byte/input formulas
                     reproduced), with two expected outputs per case: the oracle's fp32 result
                     and an fp64 dot product of the oracle's bit-exact dequant.
 """
@@ -99,6 +100,38 @@ def q4_k_fixture():
     return oracle.Q4_K, m, n, w, x
 
 
+def q6_k_fixture():
+    """compute.rs:1146-1190: ql=(row+q)%256, qh=(row*3+q)%256 (q = byte index), scales=1,
+    d=1.0, x=i*0.005-0.2, m=32, n=256."""
+    m, n = 32, 256
+    w = np.zeros(m * 210, np.uint8)
+    for row in range(m):
+        base = row * 210
+        for q in range(128):
+            w[base + q] = (row + q) % 256
+        for q in range(128, 192):
+            w[base + q] = (row * 3 + q) % 256
+        w[base + 192:base + 208] = 1
+        w[base + 208], w[base + 209] = 0x00, 0x3C
+    x = (np.arange(n, dtype=np.float32) * np.float32(0.005) - np.float32(0.2)).astype(np.float32)
+    return oracle.Q6_K, m, n, w, x
+
+
+def q8_0_fixture():
+    """compute.rs:1235-1272: d=0x2E66, qs=(row+b+j)%256, x=i*0.01-0.4, m=32, n=256."""
+    m, n = 32, 256
+    nb = n // 32
+    w = np.zeros(m * nb * 34, np.uint8)
+    for row in range(m):
+        for b in range(nb):
+            base = (row * nb + b) * 34
+            w[base], w[base + 1] = 0x66, 0x2E
+            for j in range(32):
+                w[base + 2 + j] = (row + b + j) % 256
+    x = (np.arange(n, dtype=np.float32) * np.float32(0.01) - np.float32(0.4)).astype(np.float32)
+    return oracle.Q8_0, m, n, w, x
+
+
 def parity_fixture(t):
     """compute.rs:1370-1394 gemv_parity: bytes (i*131+17)&0x1F, x=i*0.003-0.2, m=32, n=256."""
     m, n = 32, 256
@@ -152,6 +185,8 @@ def main():
         "parity_iq2_xxs": parity_fixture(oracle.IQ2_XXS),
         "parity_iq3_xxs": parity_fixture(oracle.IQ3_XXS),
         "f16": f16_fixture(),
+        "q6_k": q6_k_fixture(),
+        "q8_0": q8_0_fixture(),
     }
     for name, (t, m, n, w, x) in cases.items():
         out[f"{name}/type"] = np.array([t, m, n], np.int64)

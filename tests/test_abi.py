@@ -76,7 +76,7 @@ def test_validation_errors():
     hayai_amd.validate_gemv_weights(hayai_amd.Q4_K, 4, 256, 576)
     # a type with no kernel is a hard error, never a fallback (orchestrator.rs:403-409)
     with pytest.raises(hayai_amd.HipError) as e:
-        hayai_amd.validate_gemv_shape(14, 4, 256)  # Q6_K
+        hayai_amd.validate_gemv_shape(13, 4, 256)  # Q5_K
     assert e.value.status_name == "HH_ERR_KERNEL_MISSING"
 
 
@@ -85,7 +85,7 @@ def test_validation_matches_oracle():
 
     rng = np.random.default_rng(0)
     for _ in range(300):
-        t = int(rng.choice([0, 1, 2, 12, 16, 18]))
+        t = int(rng.choice([0, 1, 2, 8, 12, 14, 16, 18]))
         m = int(rng.integers(0, 5))
         n = int(rng.choice([0, 1, 31, 32, 64, 255, 256, 512, 1000]))
         ok_shape = oracle.validate_shape(t, m, n)

@@ -44,6 +44,9 @@ FFN_CASES = [
     ((18, 18, 18), 4096, 14336, 0, 6),
     ((12, 12, 12), 4096, 14336, 1, 7),   # GELU(tanh) activation
     ((12, 2, 18), 1024, 2048, 0, 8),     # gate/up formats differ -> unfused gate/up path
+    ((12, 12, 14), 4096, 14336, 0, 9),   # Q4_K_M layout: gate/up Q4_K, down Q6_K
+    ((14, 14, 14), 1024, 2048, 0, 10),   # all Q6_K
+    ((8, 8, 8), 1024, 2048, 1, 11),      # all Q8_0, GELU
 ]
 
 

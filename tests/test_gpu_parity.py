@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 FIX = np.load(os.path.join(GOLDEN, "ref_fixtures.npz"))
 REL_TOL = 1e-3
-QTYPES = [hayai_amd.Q4_0, hayai_amd.Q4_K, hayai_amd.IQ2_XXS, hayai_amd.IQ3_XXS]
+QTYPES = [hayai_amd.Q4_0, hayai_amd.Q4_K, hayai_amd.IQ2_XXS, hayai_amd.IQ3_XXS, hayai_amd.Q8_0, hayai_amd.Q6_K]
 
 
 def rel_err(y, ref):
@@ -60,7 +60,9 @@ def test_dequant_bit_exact(engine, t):
     cases.append(((i * 131 + 17) & 0x1F).astype(np.uint8))  # compute.rs:1376-1380 bytes
     rng = np.random.default_rng(t)
     raw = rng.integers(0, 256, nblk * bb, dtype=np.uint8)
-    raw.reshape(nblk, bb)[:, 1] &= 0x7B  # keep the f16 scale finite (exponent < 31)
+    # keep the f16 scale finite (exponent < 31): d is bytes 0-1 (Q6_K: 208-209), Q4_K's
+    # dmin bytes 2-3
+    raw.reshape(nblk, bb)[:, 209 if t == hayai_amd.Q6_K else 1] &= 0x7B
     if t == hayai_amd.Q4_K:
         raw.reshape(nblk, bb)[:, 3] &= 0x7B
     cases.append(raw)
@@ -70,10 +72,11 @@ def test_dequant_bit_exact(engine, t):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
-def test_dequant_q4_0_tail(engine):
-    w = synth.quant_weights(hayai_amd.Q4_0, 3, seed=5)
-    got = engine.dequant(hayai_amd.Q4_0, w, 70)
-    assert np.array_equal(got.view(np.uint32), oracle.dequant(oracle.Q4_0, w, 70).view(np.uint32))
+@pytest.mark.parametrize("t", [hayai_amd.Q4_0, hayai_amd.Q8_0])
+def test_dequant_32_block_tail(engine, t):
+    w = synth.quant_weights(t, 3, seed=5)
+    got = engine.dequant(t, w, 70)
+    assert np.array_equal(got.view(np.uint32), oracle.dequant(t, w, 70).view(np.uint32))
 
 
 # ------------------------------------------------------------------ synthetic bytes
@@ -93,7 +96,8 @@ def test_device_synth_matches_host(engine, t):
 
 # ------------------------------------------------------------------ GEMV: reference fixtures
 
-GEMV_CASES = ["q4_0", "q4_k", "parity_q4_0", "parity_q4_k", "parity_iq2_xxs", "parity_iq3_xxs", "f16"]
+GEMV_CASES = ["q4_0", "q4_k", "parity_q4_0", "parity_q4_k", "parity_iq2_xxs", "parity_iq3_xxs", "f16", "q6_k",
+              "q8_0"]
 
 
 @pytest.mark.parametrize("name", GEMV_CASES)
@@ -124,13 +128,13 @@ def _width_cases():
     # cover every team bucket (units per row 1..1024) for each format
     out = []
     for t in QTYPES + [hayai_amd.F32, hayai_amd.F16]:
-        unit = 64 if t == hayai_amd.Q4_K else 32
+        unit = 64 if t in (hayai_amd.Q4_K, hayai_amd.Q6_K) else 32
         block = oracle.BLOCK[t][0]
         for units in (1, 9, 32, 64, 100, 256, 300, 512, 700, 1024):
             n = units * unit
             if n % block:
                 n = (n + block - 1) // block * block
-            if t in (hayai_amd.IQ2_XXS, hayai_amd.IQ3_XXS, hayai_amd.F32) and n > 16384:
+            if t in (hayai_amd.IQ2_XXS, hayai_amd.IQ3_XXS, hayai_amd.Q6_K, hayai_amd.F32) and n > 16384:
                 continue  # keep the oracle fast; wide IQ rows are covered at config 5 shape
             out.append((t, n))
     return out
@@ -200,7 +204,7 @@ def test_device_path_rejects_bad_ranges(engine):
         (hayai_amd.Q4_K, 4, 512, wb, 0, xb, 0, yb, 0),   # x too small
         (hayai_amd.Q4_K, 4, 300, wb, 0, xb, 0, yb, 0),   # n not a block multiple
         (hayai_amd.Q4_K, 0, 256, wb, 0, xb, 0, yb, 0),   # empty
-        (14, 4, 256, wb, 0, xb, 0, yb, 0),                # Q6_K: no kernel
+        (13, 4, 256, wb, 0, xb, 0, yb, 0),                # Q5_K: no kernel
     ]:
         with pytest.raises(hayai_amd.HipError) as e:
             engine.gemv_dev(*args)
@@ -222,7 +226,7 @@ def test_pending_dropped_without_wait(engine):
 
 CONFIG_GEMVS = [
     # (type, m, n): config 1 (SmolLM Q4_0), config 2 (8B Q4_K), config 4 experts (Q4_K),
-    # config 5 (70B IQ2_XXS gate/up and down), IQ3_XXS at the 8B shape
+    # config 5 (70B IQ2_XXS gate/up and down), IQ3_XXS, Q6_K and Q8_0 at the 8B shape
     (hayai_amd.Q4_0, 1536, 576),
     (hayai_amd.Q4_0, 576, 1536),
     (hayai_amd.Q4_K, 14336, 4096),
@@ -233,6 +237,10 @@ CONFIG_GEMVS = [
     (hayai_amd.IQ2_XXS, 1024, 28672),
     (hayai_amd.IQ3_XXS, 14336, 4096),
     (hayai_amd.IQ3_XXS, 4096, 14336),
+    # Q4_K_M files: ffn_down (and some ffn_up) in Q6_K; Q8_0 tensors at the 8B shape
+    (hayai_amd.Q6_K, 4096, 14336),
+    (hayai_amd.Q6_K, 14336, 4096),
+    (hayai_amd.Q8_0, 4096, 14336),
 ]
 
 

@@ -227,8 +227,70 @@ def test_iq_scale_nibble(t, bb, scale):
         assert np.array_equal(y[ib], (y0[ib] * np.float32(0.5 + s) * np.float32(2.0)).astype(np.float32))
 
 
+def test_q8_0_closed_form_d_0x2e66():
+    # compute.rs:1235-1272 fixture scale d = 0x2E66; gguf.rs:401-420: value = (i8 q) * d
+    rng = np.random.default_rng(21)
+    w = _blocks(8, 34, rng)
+    w.reshape(8, 34)[:, 0:2] = [0x66, 0x2E]
+    q = w.reshape(8, 34)[:, 2:].view(np.int8).astype(np.float32)
+    assert np.array_equal(oracle.dequant(oracle.Q8_0, w, 256), (q * np.float32(0.0999755859375)).reshape(-1))
+    # a tail block: n not a multiple of 32 writes only the first n values (gguf.rs:412-416)
+    assert np.array_equal(oracle.dequant(oracle.Q8_0, w, 40), oracle.dequant(oracle.Q8_0, w, 64)[:40])
+
+
+def _q6_k_encode(codes, scales, d_bits):
+    """Pack per-element 6-bit codes (256 per block), 16 i8 scales and an f16 d into Q6_K
+    blocks, walking the layout element by element: element e = 128h + 32r + l takes the low
+    (r = 0, 1) or high (r = 2, 3) nibble of ql[64h + l + 32(r & 1)] and bits 2r, 2r+1 of
+    qh[32h + l] (q6k.rs:31-55 read in the packing direction)."""
+    nb = codes.shape[0]
+    out = np.zeros((nb, 210), np.uint8)
+    for b in range(nb):
+        for e in range(256):
+            h, r, l = e // 128, (e % 128) // 32, e % 32
+            c = int(codes[b, e])
+            qi = 64 * h + l + 32 * (r & 1)
+            out[b, qi] |= (c & 15) << (4 if r >= 2 else 0)
+            out[b, 128 + 32 * h + l] |= (c >> 4) << (2 * r)
+        out[b, 192:208] = scales[b].astype(np.int8).view(np.uint8)
+        out[b, 208], out[b, 209] = d_bits & 0xFF, d_bits >> 8
+    return out.reshape(-1)
+
+
+def test_q6_k_codes_round_trip():
+    # scales = 1, d = 1: every element must come back as its 6-bit code - 32
+    rng = np.random.default_rng(22)
+    codes = rng.integers(0, 64, (4, 256))
+    w = _q6_k_encode(codes, np.ones((4, 16), np.int64), 0x3C00)
+    assert np.array_equal(oracle.dequant(oracle.Q6_K, w, 1024), (codes - 32).reshape(-1).astype(np.float32))
+
+
+def test_q6_k_scale_per_16_columns():
+    # code 33 (q = 1) everywhere, scales[k] = k + 1 (k = 0..15) and one negative: element
+    # e = 128h + 32r + l uses scales[8h + l/16 + 2r] (q6k.rs:36-48), d = 2 doubles it
+    codes = np.full((1, 256), 33)
+    sc = np.arange(1, 17)[None, :].copy()
+    sc[0, 5] = -7
+    w = _q6_k_encode(codes, sc, 0x4000)
+    e = np.arange(256)
+    idx = 8 * (e // 128) + (e % 32) // 16 + 2 * ((e % 128) // 32)
+    assert np.array_equal(oracle.dequant(oracle.Q6_K, w, 256), (2.0 * sc[0, idx]).astype(np.float32))
+
+
+def test_q6_k_reference_fixture_is_code_minus_32():
+    # compute.rs:1146-1190 bytes (scales 1, d 1): values are integers in [-32, 31], each
+    # equal to what the element-wise packing of those codes gives back
+    w = FIX["q6_k/w"]
+    y = oracle.dequant(oracle.Q6_K, w, 32 * 256).reshape(32, 256)
+    assert np.array_equal(y, np.round(y)) and y.min() >= -32 and y.max() <= 31
+    codes = (y + 32).astype(np.int64)
+    blk = w.reshape(32, 210)
+    again = _q6_k_encode(codes, np.ones((32, 16), np.int64), 0x3C00).reshape(32, 210)
+    assert np.array_equal(again[:, :192], blk[:, :192])
+
+
 FIX = np.load(os.path.join(GOLDEN, "ref_fixtures.npz"))
-CASES = ["q4_0", "q4_k", "parity_q4_0", "parity_q4_k", "parity_iq2_xxs", "parity_iq3_xxs", "f16"]
+CASES = ["q4_0", "q4_k", "parity_q4_0", "parity_q4_k", "parity_iq2_xxs", "parity_iq3_xxs", "f16", "q6_k", "q8_0"]
 
 
 @pytest.mark.parametrize("name", CASES)
@@ -245,7 +307,8 @@ def test_gemv_reference_fixtures(name):
     assert np.all(np.abs(y - y64) <= bound)
 
 
-@pytest.mark.parametrize("t", [oracle.Q4_0, oracle.Q4_K, oracle.IQ2_XXS, oracle.IQ3_XXS, oracle.F16, oracle.F32])
+@pytest.mark.parametrize("t", [oracle.Q4_0, oracle.Q4_K, oracle.IQ2_XXS, oracle.IQ3_XXS, oracle.Q8_0, oracle.Q6_K,
+                               oracle.F16, oracle.F32])
 def test_gemv_fp64_bound_and_linearity(t):
     import hayai_amd.synth as synth
 

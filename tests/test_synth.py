@@ -43,10 +43,20 @@ def test_normal_moments():
 
 
 def test_iq_formats_well_formed():
-    for t in (synth.IQ2_XXS, synth.IQ3_XXS, synth.Q4_0):
+    for t in (synth.IQ2_XXS, synth.IQ3_XXS, synth.Q4_0, synth.Q8_0, synth.Q6_K):
         w = synth.matrix(t, 8, 1024, seed=t)
         y = oracle.dequant(t, w, 8 * 1024)
         assert np.isfinite(y).all() and np.abs(y).max() > 0
+
+
+def test_scale_field_positions():
+    # d lands where each format keeps it: the block start, or byte 208 for Q6_K
+    for t, at in ((synth.Q8_0, 0), (synth.Q6_K, 208), (synth.Q4_0, 0)):
+        block, bb = synth.BLOCK[t]
+        w = synth.quant_weights(t, 64, seed=7).reshape(64, bb)
+        d = w[:, at:at + 2].copy().view(np.uint16).ravel().view(np.float16).astype(np.float32)
+        lo, hi = synth.SCALE_RANGE[t]
+        assert (d >= np.float32(lo) * 0.999).all() and (d <= np.float32(hi) * 1.001).all()
 
 
 def test_seed_for_distinct():
