@@ -460,6 +460,74 @@ def bench_smollm(eng, args) -> int:
     return 0
 
 
+def bench_q4km(eng, args) -> int:
+    """The 8B FFN in the Q4_K_M layout: gate/up Q4_K, down Q6_K (llama.cpp's Q4_K_M keeps
+    ffn_down of many layers in Q6_K), 32 layers resident, batch 1.  Not a BASELINE.json
+    config: it measures the path a real Q4_K_M file takes through the FFN op."""
+    import hayai_amd
+    from hayai_amd import synth
+
+    Q6_K = hayai_amd.Q6_K
+    gate = hayai_amd.QuantMatrix("ffn_gate", D_MODEL, D_FF, Q4_K)
+    up = hayai_amd.QuantMatrix("ffn_up", D_MODEL, D_FF, Q4_K)
+    down = hayai_amd.QuantMatrix("ffn_down", D_FF, D_MODEL, Q6_K)
+    lay = hayai_amd.LayerPackLayout.ffn_only(gate, up, down)
+    stride = (lay.total + 255) // 256 * 256
+    pack = eng.alloc(stride * LAYERS)
+    for l in range(LAYERS):
+        for t, mat, off, rows, cols in ((Q4_K, synth.GATE, lay.gate_off, D_FF, D_MODEL),
+                                        (Q4_K, synth.UP, lay.up_off, D_FF, D_MODEL),
+                                        (Q6_K, synth.DOWN, lay.down_off, D_MODEL, D_FF)):
+            lo, hi = synth.SCALE_RANGE[t]
+            eng.synth_weights_dev(t, pack, l * stride + off, rows * cols // 256, synth.seed_for(9, l, mat), lo, hi)
+    xs = [synth.normal(synth.seed_for(9, l, synth.ACT), D_MODEL) for l in range(LAYERS)]
+    xbuf = eng.upload(np.concatenate(xs))
+    ybuf = eng.alloc(4 * D_MODEL * LAYERS)
+    desc = eng.ffn_desc((Q4_K, Q4_K, Q6_K), D_MODEL, D_FF, lay)
+
+    def step():
+        for l in range(LAYERS):
+            eng.ffn_dev(desc, pack, l * stride, xbuf, 4 * D_MODEL * l, ybuf, 4 * D_MODEL * l)
+
+    for _ in range(args.warmup):
+        step()
+    eng.sync()
+    a, b = eng.event(), eng.event()
+    a.record()
+    for _ in range(args.steps):
+        step()
+    b.record()
+    eng.sync()
+    ms = a.elapsed_ms(b) / args.steps
+    wb = gate.nbytes + up.nbytes + down.nbytes
+    bytes_step = LAYERS * (wb + 2 * 4 * D_MODEL + 2 * 4 * D_FF)
+    gbs = bytes_step / (ms / 1e3) / 1e9
+    log(f"[bench] q4_k_m: {ms * 1e3:.1f} us/step ({ms * 1e3 / LAYERS:.2f} us/layer), {gbs:.1f} GB/s")
+    out = {
+        "metric": "FFN GEMV achieved HBM GB/s (% of peak) + FFN tok/s, 8B-shape Q4_K_M (Q6_K down) bs=1",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Q4_K / Q6_K blocks, N(0,1) f32 activations)",
+        "config": {"workload": "llama3-8b-ffn-q4_k_m-bs1-32layers-resident", "d_model": D_MODEL, "d_ff": D_FF,
+                   "layers": LAYERS, "batch": 1, "weights": "Q4_K gate/up, Q6_K down", "act": "silu"},
+        "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "ffn_tok_s": round(1e3 / ms, 2),
+        "us_per_layer": round(ms * 1e3 / LAYERS, 3),
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+    eng.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -469,10 +537,11 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 256 MiB device copy before timing (reference point for HBM counters)")
-    ap.add_argument("--workload", default="bs1", choices=["bs1", "batched", "moe", "stream", "smollm"],
+    ap.add_argument("--workload", default="bs1", choices=["bs1", "batched", "moe", "stream", "smollm", "q4km"],
                     help="bs1: BASELINE.json configs[1] (the headline); batched: configs[2], --batch tokens per "
                          "step; moe: configs[3], --batch tokens per step; stream: configs[4] (70B IQ2_XXS "
-                         "streamed from pinned host); smollm: configs[0]")
+                         "streamed from pinned host); smollm: configs[0]; q4km: the 8B FFN with a Q6_K down "
+                         "projection (Q4_K_M layout)")
     ap.add_argument("--batch", type=int, default=16, help="tokens per step for --workload batched")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -491,6 +560,8 @@ def main() -> int:
         return bench_stream(eng, args)
     if args.workload == "smollm":
         return bench_smollm(eng, args)
+    if args.workload == "q4km":
+        return bench_q4km(eng, args)
     gate = hayai_amd.QuantMatrix("ffn_gate", D_MODEL, D_FF, Q4_K)
     up = hayai_amd.QuantMatrix("ffn_up", D_MODEL, D_FF, Q4_K)
     down = hayai_amd.QuantMatrix("ffn_down", D_FF, D_MODEL, Q4_K)
