@@ -513,8 +513,11 @@ static size_t ring_grid(int occ, int per_cu, size_t cus) { return cus * (size_t)
 bool hh_engine::ring_ok(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                         const float* x) const {
     const size_t dm = d->d_model, df = d->d_ff;
-    return ring && !q4k_generic && d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K &&
-           d->type_down == HH_TYPE_Q4_K && dm % 256 == 0 && df % 256 == 0 && dm <= 8192 && df <= 32768 &&
+    // a Q6_K W_down (Q4_K_M files) needs an even number of 210-byte superblocks per row, so
+    // that its rows start 4-byte aligned
+    const bool down_ok = d->type_down == HH_TYPE_Q4_K || (d->type_down == HH_TYPE_Q6_K && df % 512 == 0);
+    return ring && !q4k_generic && d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K && down_ok &&
+           dm % 256 == 0 && df % 256 == 0 && dm <= 8192 && df <= 32768 &&
            ((((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd | (uintptr_t)x) & 15u) == 0);
 }
 
@@ -552,7 +555,8 @@ hh_status hh_engine::enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd
     const size_t dm = d->d_model, df = d->d_ff;
     int w2 = 1;
     while ((size_t)w2 * 64 < df / 64) w2 *= 2;
-    const std::string name = "hh_q4k_dn_ring_d" + std::to_string(w2);
+    const bool q6 = d->type_down == HH_TYPE_Q6_K;
+    const std::string name = std::string(q6 ? "hh_q6k_dn_ring_d" : "hh_q4k_dn_ring_d") + std::to_string(w2);
     hipFunction_t fn;
     HH_TRY(kernel(name, &fn));
     const int block = 9 * 64;  // 8 compute waves + the wave that copies the intermediate
@@ -570,7 +574,7 @@ hh_status hh_engine::enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd
         blocks_per_cu[name] = occ;
     }
     const size_t grid = ring_grid(occ, ring_dn_per_cu, cus);
-    DnrArgs a{wd, (const uint8_t*)ws_hq, y, (uint64_t)((df / 256) * 144), (uint32_t)dm, (uint32_t)df};
+    DnrArgs a{wd, (const uint8_t*)ws_hq, y, (uint64_t)((df / 256) * (q6 ? 210 : 144)), (uint32_t)dm, (uint32_t)df};
     void* params[] = {&a};
     hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
     if (err != hipSuccess) return hip_fail(err, "launch(ring q4k down)");
@@ -1086,6 +1090,7 @@ static std::vector<std::string> required_kernels() {
         k.push_back(std::string("hh_q4k_ffnp_") + f);
     for (const char* f : {"gu_ring_g1", "gu_ring_g2", "dn_ring_d1", "dn_ring_d2", "dn_ring_d4", "dn_ring_d8"})
         k.push_back(std::string("hh_q4k_") + f);
+    for (int w : {1, 2, 4, 8}) k.push_back("hh_q6k_dn_ring_d" + std::to_string(w));
     for (const char* f : {"gu_ring_u16", "gu_ring_u32", "gu_ring_u64", "dn_ring_d1", "dn_ring_d2", "dn_ring_d4",
                           "dn_ring_d8"})
         k.push_back(std::string("hh_moe_") + f);

@@ -175,6 +175,39 @@ def test_q4k_ffn_forms_match_oracle_and_two_launch(engine, persistent_engine, tw
     eng.sync()  # reports a timed-out wait if one was recorded
 
 
+Q4KM_CASES = [
+    # (d_model, d_ff): the 8B shape; d_model 8192; d_ff 28672 (8 waves per down row); a tiny
+    # layer (2 superblocks per down row); d_ff 1280 (an odd number of Q6_K superblocks per
+    # row: down rows are not 4-byte aligned, so the generic kernels run instead)
+    (4096, 14336), (8192, 4096), (1024, 28672), (256, 512), (512, 1280),
+]
+
+
+@pytest.mark.parametrize("d_model,d_ff", Q4KM_CASES)
+def test_q4k_m_ffn_matches_oracle_and_two_launch(engine, two_launch_engine, d_model, d_ff):
+    # Q4_K_M layout (gate/up Q4_K, down Q6_K): the ring gate/up kernel and the Q6_K ring down
+    # kernel (210-byte superblocks, half of them 2 bytes off a dword) against the oracle and
+    # against the generic gate/up + Q6_K GEMV kernels on the same bytes.
+    types = (12, 12, 14)
+    print(f"[case] q4_k_m ffn {d_model}x{d_ff}", flush=True)
+    oracle.set_threads(min(16, oracle.max_threads()))
+    lay, (wg, wu, wd), pack = make_pack(engine, types, d_model, d_ff, 21)
+    pack2 = two_launch_engine.alloc(lay.total)
+    pack2.write(wg, lay.gate_off)
+    pack2.write(wu, lay.up_off)
+    pack2.write(wd, lay.down_off)
+    desc = engine.ffn_desc(types, d_model, d_ff, lay)
+    for k in range(2):
+        x = synth.normal(synth.seed_for(21, k, synth.ACT), d_model)
+        y = engine.ffn(desc, pack, 0, x)
+        y2 = two_launch_engine.ffn(desc, pack2, 0, x)
+        ref = oracle.ffn(types, d_model, d_ff, wg, wu, wd, x)
+        assert np.isfinite(y).all()
+        assert rel_err(y, ref) <= REL_TOL, rel_err(y, ref)
+        assert rel_err(y, y2) <= REL_TOL
+        print(f"  rel_err vs oracle {rel_err(y, ref):.2e}, vs two-launch {rel_err(y, y2):.2e}", flush=True)
+
+
 @pytest.mark.parametrize("form", ["ring", "persistent"])
 def test_q4k_ffn_chain_is_deterministic(engine, persistent_engine, form):
     # 6 dependent launches with no host sync in between (the persistent form uses a new
@@ -204,7 +237,7 @@ def test_q4k_ffn_chain_is_deterministic(engine, persistent_engine, form):
 
 
 @pytest.mark.parametrize("types,d_model,d_ff", [((12, 12, 12), 4096, 14336), ((2, 2, 2), 576, 1536),
-                                                 ((12, 2, 18), 1024, 2048)])
+                                                 ((12, 2, 18), 1024, 2048), ((12, 12, 14), 4096, 14336)])
 def test_ffn_begin_finish_equals_ffn(engine, two_launch_engine, types, d_model, d_ff):
     # The reference's two-call seam (ffn_begin_gate_up_scratch / ffn_finish_scratch) runs the
     # same kernels as the one-call op (the ring kernels for Q4_K, or the first two-launch
