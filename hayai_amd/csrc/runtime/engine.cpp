@@ -1155,9 +1155,9 @@ hh_status engine_create(int device, hh_engine** out) {
 
 void engine_destroy(hh_engine* e) {
     if (!e) return;
-    hipSetDevice(e->device);
-    if (e->stream) hipStreamSynchronize(e->stream);
-    if (e->copy_stream) hipStreamSynchronize(e->copy_stream);
+    (void)hipSetDevice(e->device);
+    if (e->stream) (void)hipStreamSynchronize(e->stream);
+    if (e->copy_stream) (void)hipStreamSynchronize(e->copy_stream);
     for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq, e->ws_xop, e->ws_hop, e->ws_part,
                     e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->grid_sync})
         if (p) hipFree(p);
