@@ -528,6 +528,72 @@ def bench_q4km(eng, args) -> int:
     return 0
 
 
+def bench_block(eng, pack, lay, stride, desc, args) -> int:
+    """The 8B decode step's FFN half as a model runs it: 32 residual blocks chained in place
+    on one residual stream, x_{l+1} = x_l + FFN_l(rms_norm(x_l, norm_l)) (ffn_apply,
+    hybrid_infer.rs:883-936), the RMSNorm and the residual add fused into the ring kernels.
+    Reported beside the plain FFN op on the same weights (independent per-layer x)."""
+    from hayai_amd import synth
+
+    norms = eng.upload(np.concatenate([synth.normal(synth.seed_for(CONFIG_ID, l, 7), D_MODEL) * 0.1 + 1.0
+                                       for l in range(LAYERS)]).astype(np.float32))
+    x0 = synth.normal(synth.seed_for(CONFIG_ID, 0, synth.ACT), D_MODEL)
+    xres = eng.upload(x0)
+    xs = eng.upload(np.tile(x0, LAYERS))
+    ys = eng.alloc(4 * D_MODEL * LAYERS)
+
+    def block_step():
+        for l in range(LAYERS):
+            eng.ffn_block_dev(desc, pack, l * stride, norms, 4 * D_MODEL * l, 1e-5, xres, 0, xres, 0)
+
+    def ffn_step():
+        for l in range(LAYERS):
+            eng.ffn_dev(desc, pack, l * stride, xs, 4 * D_MODEL * l, ys, 4 * D_MODEL * l)
+
+    def timed(run, n):
+        e0, e1 = eng.event(), eng.event()
+        e0.record()
+        for _ in range(n):
+            run()
+        e1.record()
+        eng.sync()
+        return e0.elapsed_ms(e1) / n
+
+    for _ in range(args.warmup):
+        xres.write(x0)
+        block_step()
+        ffn_step()
+    eng.sync()
+    xres.write(x0)
+    ms_block = timed(block_step, args.steps)
+    ms_ffn = timed(ffn_step, args.steps)
+    bytes_step = LAYERS * (layer_bytes() + 4 * D_MODEL)  # + the norm weights
+    gbs = bytes_step / (ms_block / 1e3) / 1e9
+    log(f"[bench] block: {ms_block * 1e3:.1f} us/step ({ms_block * 1e3 / LAYERS:.2f} us/layer), {gbs:.1f} GB/s; "
+        f"plain FFN op {ms_ffn * 1e3 / LAYERS:.2f} us/layer")
+    out = {
+        "metric": "FFN residual block (RMSNorm + FFN + residual) achieved HBM GB/s, 8B-shape Q4_K bs=1",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_block, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Q4_K blocks, N(0,1) f32 residual stream, norm weights 1 + 0.1 N(0,1))",
+        "config": {"workload": "llama3-8b-ffn-block-q4_k-bs1-32layers-chained", "d_model": D_MODEL, "d_ff": D_FF,
+                   "layers": LAYERS, "batch": 1, "weights": "Q4_K", "act": "silu", "eps": 1e-5},
+        "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "us_per_layer": round(ms_block * 1e3 / LAYERS, 3),
+        "plain_ffn_us_per_layer": round(ms_ffn * 1e3 / LAYERS, 3),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -537,11 +603,12 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 256 MiB device copy before timing (reference point for HBM counters)")
-    ap.add_argument("--workload", default="bs1", choices=["bs1", "batched", "moe", "stream", "smollm", "q4km"],
+    ap.add_argument("--workload", default="bs1", choices=["bs1", "batched", "moe", "stream", "smollm", "q4km", "block"],
                     help="bs1: BASELINE.json configs[1] (the headline); batched: configs[2], --batch tokens per "
                          "step; moe: configs[3], --batch tokens per step; stream: configs[4] (70B IQ2_XXS "
                          "streamed from pinned host); smollm: configs[0]; q4km: the 8B FFN with a Q6_K down "
-                         "projection (Q4_K_M layout)")
+                         "projection (Q4_K_M layout); block: the 8B FFN residual block (RMSNorm + FFN + "
+                         "residual) chained over 32 layers")
     ap.add_argument("--batch", type=int, default=16, help="tokens per step for --workload batched")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -582,6 +649,8 @@ def main() -> int:
     desc = eng.ffn_desc((Q4_K, Q4_K, Q4_K), D_MODEL, D_FF, lay)
     if args.workload == "batched":
         return bench_batched(eng, pack, lay, stride, desc, args)
+    if args.workload == "block":
+        return bench_block(eng, pack, lay, stride, desc, args)
 
     def step():
         for l in range(LAYERS):

@@ -51,6 +51,24 @@ struct hh_act_args {
     int32_t act;
 };
 
+// y = RMSNorm(x) * w over n elements (one workgroup)
+struct hh_norm_args {
+    const float* x;
+    const float* w;
+    float* y;
+    uint32_t n;
+    float eps;
+};
+
+// y = a + b over n elements (the residual add)
+struct hh_add_args {
+    const float* a;
+    const float* b;
+    float* y;
+    uint32_t n;
+    uint32_t pad;
+};
+
 // out[n] = dequant(w[...]) for n elements (the dequant probe)
 struct hh_dequant_args {
     const uint8_t* w;

@@ -17,22 +17,40 @@
 
 #define HH_RING_BLOCK (HH_FFNP_CW * HH_WAVE)
 
+// sum of squares of 8 elements, and x * inv * weight in the reference's order
+// (simd_scale_mul, crates/hayai-cpu/src/simd_ops.rs:28-41)
+HH_DEV float hh_sq8(const float4& a, const float4& b) {
+    return a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w + b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w;
+}
+HH_DEV void hh_norm8(float4& a, float4& b, const float4& wa, const float4& wb, float inv) {
+    a.x = (a.x * inv) * wa.x;
+    a.y = (a.y * inv) * wa.y;
+    a.z = (a.z * inv) * wa.z;
+    a.w = (a.w * inv) * wa.w;
+    b.x = (b.x * inv) * wb.x;
+    b.y = (b.y * inv) * wb.y;
+    b.z = (b.z * inv) * wb.z;
+    b.w = (b.w * inv) * wb.w;
+}
+
 struct hh_gur_args {
     const uint8_t* wg;  // W_gate [d_ff][rb1]
     const uint8_t* wu;  // W_up   [d_ff][rb1]
     const float* x;     // d_model f32, 16-byte aligned
     uint8_t* hx;        // intermediate (above)
+    const float* nw;    // RMSNorm weight (d_model f32, 16-byte aligned), or null: x as given
     uint64_t rb1;       // row bytes of gate/up
     uint32_t d_model;
     uint32_t d_ff;
     int32_t act;
-    uint32_t pad;
+    float eps;          // RMSNorm epsilon (with nw)
 };
 
 struct hh_dnr_args {
     const uint8_t* wd;  // W_down [d_model][rb2]
     const uint8_t* hx;  // intermediate (above), 16-byte aligned
     float* y;           // d_model f32
+    const float* res;   // residual added to y (may be y itself), or null
     uint64_t rb2;       // row bytes of down
     uint32_t d_model;
     uint32_t d_ff;
@@ -42,7 +60,7 @@ struct hh_dnr_args {
 // team of WPT1 waves reads one row (lane = unit, x as per-32 digits in registers).  After
 // the last row, wave 0 applies the activation to the workgroup's rows and writes their
 // digits.
-template <int WPT1, int D, int P>
+template <int WPT1, int D, int P, bool NORM>
 HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
     extern __shared__ __attribute__((aligned(16))) char hh_smem[];
     constexpr uint32_t TEAM1 = WPT1 * HH_WAVE, TPW1 = HH_FFNP_CW / WPT1;
@@ -90,14 +108,38 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
     const uint32_t c = tid;  // chunk of 8 elements (d_model <= 8 * 512 per pass)
     const bool has = c < dm / 8;
     const float4* x4 = reinterpret_cast<const float4*>(a.x);
-    const float4 t0 = x4[2 * min(c, dm / 8 - 1)];
-    const float4 t1 = x4[2 * min(c, dm / 8 - 1) + 1];
+    float4 t0 = x4[2 * min(c, dm / 8 - 1)];
+    float4 t1 = x4[2 * min(c, dm / 8 - 1) + 1];
+    const float4* n4 = reinterpret_cast<const float4*>(a.nw);
+    float4 m0 = make_float4(1.f, 1.f, 1.f, 1.f), m1 = m0;
+    if constexpr (NORM) {
+        m0 = n4[2 * min(c, dm / 8 - 1)];
+        m1 = n4[2 * min(c, dm / 8 - 1) + 1];
+    }
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < P; s++) issue((uint32_t)s, ring[s]);
+    float inv = 1.f;
+    if constexpr (NORM) {
+        // RMSNorm (rms_norm, crates/hayai-cpu/src/attention.rs:142-147, applied before the
+        // FFN by ffn_apply, crates/hayai-core/src/hybrid_infer.rs:895-896): every workgroup
+        // forms sum(x^2) itself (d_model floats from L2), then x * inv * weight
+        float ss = has ? hh_sq8(t0, t1) : 0.f;
+        for (uint32_t c2 = c + HH_RING_BLOCK; c2 < dm / 8; c2 += HH_RING_BLOCK) ss += hh_sq8(x4[2 * c2], x4[2 * c2 + 1]);
+        ss = hh_wave_sum(ss);
+        float* red = reinterpret_cast<float*>(stage);  // free until the epilogue
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int k = 0; k < HH_FFNP_CW; k++) tot += red[k];
+        inv = 1.0f / sqrtf(tot / (float)dm + a.eps);
+        hh_norm8(t0, t1, m0, m1, inv);
+    }
     hh_ffnp_digits_chunk(t0, t1, c, has, xd);
     for (uint32_t c2 = c + HH_RING_BLOCK; c2 < dm / 8; c2 += HH_RING_BLOCK) {
-        const float4 v0 = x4[2 * c2], v1 = x4[2 * c2 + 1];  // d_model > 4096: later passes
+        float4 v0 = x4[2 * c2], v1 = x4[2 * c2 + 1];  // d_model > 4096: later passes
+        if constexpr (NORM) hh_norm8(v0, v1, n4[2 * c2], n4[2 * c2 + 1], inv);
         hh_ffnp_digits_chunk(v0, v1, c2, true, xd);
     }
 #pragma unroll
@@ -184,6 +226,10 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
     const uint32_t n2 = (q1 - q0 + TPW2 - 1) / TPW2;
     const uint32_t n2p = (n2 + D - 1) / D * D;
 
+    // the residual of the first row this thread stores, fetched now rather than on the tail
+    float res0 = 0.f;
+    if (a.res && tid % 32 == 31 && tid / 32 < q1 - q0) res0 = a.res[q0 + tid / 32];
+
     // LDS: [intermediate][lane partials: rows x TEAM2]
     const uint32_t hbytes = 2u * dff + (dff / 8u) * 4u;
     int8_t* hq1 = reinterpret_cast<int8_t*>(hh_smem);
@@ -257,14 +303,18 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
             s += hh_dpp<0x124>(s);       // row_ror:4
             s += hh_dpp<0x128>(s);       // row_ror:8 -> each row of 16 holds its sum
             s += hh_dpp<0x142, 0xA>(s);  // row_bcast:15 -> lanes 31 and 63 hold their half's sum
-            if (rl < nrows && seg == 31) a.y[q0 + rl] = s;
+            if (rl < nrows && seg == 31) a.y[q0 + rl] = a.res ? (rl0 == 0 ? res0 : a.res[q0 + rl]) + s : s;
         }
     }
 }
 
+// _n: with the RMSNorm prologue (the FFN residual block)
 #define HH_GU_RING(G1)                                                                          \
     extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_q4k_gu_ring_g##G1(const hh_gur_args a) { \
-        hh_gu_ring_body<G1, 3, 1>(a);                                                           \
+        hh_gu_ring_body<G1, 3, 1, false>(a);                                                    \
+    }                                                                                           \
+    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_q4k_gu_ring_g##G1##_n(const hh_gur_args a) { \
+        hh_gu_ring_body<G1, 3, 1, true>(a);                                                     \
     }
 #define HH_DN_RING(G2)                                                                          \
     extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) hh_q4k_dn_ring_d##G2(const hh_dnr_args a) { \

@@ -127,6 +127,10 @@ HH_DEV void hh_q6k_dn_ring_body(const hh_dnr_args& a) {
     const uint32_t n2 = (q1 - q0 + TPW2 - 1) / TPW2;
     const uint32_t n2p = (n2 + D - 1) / D * D;
 
+    // the residual of the first row this thread stores, fetched now rather than on the tail
+    float res0 = 0.f;
+    if (a.res && tid % 32 == 31 && tid / 32 < q1 - q0) res0 = a.res[q0 + tid / 32];
+
     // LDS: [intermediate][lane partials: rows x TEAM2]
     const uint32_t hbytes = 2u * dff + (dff / 8u) * 4u;
     int8_t* hq1 = reinterpret_cast<int8_t*>(hh_smem);
@@ -209,7 +213,7 @@ HH_DEV void hh_q6k_dn_ring_body(const hh_dnr_args& a) {
             s += hh_dpp<0x124>(s);       // row_ror:4
             s += hh_dpp<0x128>(s);       // row_ror:8 -> each row of 16 holds its sum
             s += hh_dpp<0x142, 0xA>(s);  // row_bcast:15 -> lanes 31 and 63 hold their half's sum
-            if (rl < nrows && seg == 31) a.y[q0 + rl] = s;
+            if (rl < nrows && seg == 31) a.y[q0 + rl] = a.res ? (rl0 == 0 ? res0 : a.res[q0 + rl]) + s : s;
         }
     }
 }

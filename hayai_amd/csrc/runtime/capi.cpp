@@ -137,9 +137,9 @@ hh_status hh_buf_alloc(hh_engine* e, size_t bytes, int kind, hh_buf** out) {
     hh_buf* b = new (std::nothrow) hh_buf{e, p, bytes, kind};
     if (!b) {
         if (kind == HH_BUF_DEVICE)
-            hipFree(p);
+            (void)hipFree(p);
         else
-            hipHostFree(p);
+            (void)hipHostFree(p);
         return fail(HH_ERR_OUT_OF_MEMORY, "host allocation failed");
     }
     *out = b;
@@ -148,14 +148,14 @@ hh_status hh_buf_alloc(hh_engine* e, size_t bytes, int kind, hh_buf** out) {
 
 void hh_buf_free(hh_buf* b) {
     if (!b) return;
-    hipSetDevice(b->engine->device);
+    (void)hipSetDevice(b->engine->device);
     // Work queued on the engine may still read the buffer.
-    hipStreamSynchronize(b->engine->stream);
-    hipStreamSynchronize(b->engine->copy_stream);
+    (void)hipStreamSynchronize(b->engine->stream);
+    (void)hipStreamSynchronize(b->engine->copy_stream);
     if (b->kind == HH_BUF_DEVICE)
-        hipFree(b->ptr);
+        (void)hipFree(b->ptr);
     else
-        hipHostFree(b->ptr);
+        (void)hipHostFree(b->ptr);
     delete b;
 }
 
@@ -347,9 +347,9 @@ hh_status hh_gemv_begin(hh_engine* e, int t, size_t m, size_t n, const hh_buf* w
     hh_pending* p = new (std::nothrow) hh_pending{e, nullptr, nullptr, m, nullptr, false};
     if (!p) return fail(HH_ERR_OUT_OF_MEMORY, "host allocation failed");
     auto bail = [&](hh_status st) {
-        if (p->dx) hipFree(p->dx);
-        if (p->dy) hipFree(p->dy);
-        if (p->done) hipEventDestroy(p->done);
+        if (p->dx) (void)hipFree(p->dx);
+        if (p->dy) (void)hipFree(p->dy);
+        if (p->done) (void)hipEventDestroy(p->done);
         delete p;
         return st;
     };
@@ -361,12 +361,12 @@ hh_status hh_gemv_begin(hh_engine* e, int t, size_t m, size_t n, const hh_buf* w
     e->ffn_calls++;
     hh_status st = e->enqueue_gemv(t, m, n, (const uint8_t*)w->ptr + w_off, (const float*)p->dx, (float*)p->dy);
     if (st != HH_OK) {
-        hipStreamSynchronize(e->stream);
+        (void)hipStreamSynchronize(e->stream);
         return bail(st);
     }
     err = hipEventRecord(p->done, e->stream);
     if (err != hipSuccess) {
-        hipStreamSynchronize(e->stream);
+        (void)hipStreamSynchronize(e->stream);
         return bail(hip_fail(err, "hipEventRecord"));
     }
     *out = p;
@@ -386,11 +386,11 @@ hh_status hh_pending_wait(hh_pending* p, float* y, size_t m) {
 
 void hh_pending_destroy(hh_pending* p) {
     if (!p) return;
-    hipSetDevice(p->engine->device);
-    hipEventSynchronize(p->done);  // never free buffers a queued kernel still uses
-    hipFree(p->dx);
-    hipFree(p->dy);
-    hipEventDestroy(p->done);
+    (void)hipSetDevice(p->engine->device);
+    (void)hipEventSynchronize(p->done);  // never free buffers a queued kernel still uses
+    (void)hipFree(p->dx);
+    (void)hipFree(p->dy);
+    (void)hipEventDestroy(p->done);
     delete p;
 }
 
@@ -503,6 +503,28 @@ hh_status hh_ffn_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, siz
     std::lock_guard<std::mutex> lk(e->ws_mutex);
     return e->enqueue_ffn(d, (const uint8_t*)pack->ptr + pack_off, (const float*)((const char*)x->ptr + x_off),
                           (float*)((char*)y->ptr + y_off));
+}
+
+hh_status hh_ffn_block_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                           const hh_buf* norm, size_t norm_off, float eps, const hh_buf* x, size_t x_off, hh_buf* y,
+                           size_t y_off) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_ffn(e, d, pack, pack_off));
+    HH_TRY(check_engine(e, norm, "norm"));
+    HH_TRY(check_engine(e, x, "x"));
+    HH_TRY(check_engine(e, y, "y"));
+    HH_TRY(check_range(norm, norm_off, d->d_model * sizeof(float), "norm"));
+    HH_TRY(check_range(x, x_off, d->d_model * sizeof(float), "x"));
+    HH_TRY(check_range(y, y_off, d->d_model * sizeof(float), "y"));
+    if (((norm_off | x_off | y_off) & 3u) != 0)
+        return fail(HH_ERR_INVALID, "ffn_block: norm/x/y offsets must be 4-byte aligned");
+    if (!(eps >= 0.f) || eps > 1.f) return fail(HH_ERR_INVALID, "ffn_block: eps=%g outside [0, 1]", (double)eps);
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    return e->enqueue_ffn_block(d, (const uint8_t*)pack->ptr + pack_off,
+                                (const float*)((const char*)x->ptr + x_off),
+                                (const float*)((const char*)norm->ptr + norm_off), eps,
+                                (float*)((char*)y->ptr + y_off));
 }
 
 hh_status hh_ffn_batched_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off, const hh_buf* x,
@@ -648,7 +670,7 @@ hh_status hh_route_experts_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf*
     HH_NOT_NULL(e, "engine");
     HH_TRY(e->no_capture("route_experts_dev"));
     HH_TRY(validate_moe_desc(d));
-    size_t lb, kb;
+    size_t lb = 0, kb = 0;
     HH_TRY(batch_bytes(T, d->n_experts, &lb));
     HH_TRY(batch_bytes(T, d->top_k, &kb));
     HH_TRY(check_engine(e, logits, "logits"));
@@ -674,7 +696,7 @@ hh_status hh_route_experts(hh_engine* e, const hh_moe_desc* d, const float* logi
                            int32_t* ids, float* weights) {
     HH_NOT_NULL(e, "engine");
     HH_TRY(validate_moe_desc(d));
-    size_t lb, kb;
+    size_t lb = 0, kb = 0;
     HH_TRY(batch_bytes(T, d->n_experts, &lb));
     HH_TRY(batch_bytes(T, d->top_k, &kb));
     if (T == 0) return HH_OK;
@@ -706,7 +728,7 @@ hh_status hh_moe_ffn_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* exper
     HH_TRY(e->no_capture("moe_ffn_dev"));
     HH_TRY(validate_moe_desc(d));
     HH_TRY(validate_moe_experts(e, d, experts, experts_off));
-    size_t xb, kb;
+    size_t xb = 0, kb = 0;
     HH_TRY(batch_bytes(T, d->d_model, &xb));
     HH_TRY(batch_bytes(T, d->top_k, &kb));
     for (const hh_buf* b : {x, ids, weights, (const hh_buf*)y}) HH_TRY(check_engine(e, b, "moe"));
@@ -731,7 +753,7 @@ hh_status hh_moe_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* experts, 
     HH_TRY(e->no_capture("moe_dev"));
     HH_TRY(validate_moe_desc(d));
     HH_TRY(validate_moe_experts(e, d, experts, experts_off));
-    size_t xb, kb, lb;
+    size_t xb = 0, kb = 0, lb = 0;
     HH_TRY(batch_bytes(T, d->d_model, &xb));
     HH_TRY(batch_bytes(T, d->top_k, &kb));
     HH_TRY(batch_bytes(T, d->n_experts, &lb));
@@ -776,8 +798,8 @@ hh_status hh_event_create(hh_engine* e, hh_event** out) {
 
 void hh_event_destroy(hh_event* ev) {
     if (!ev) return;
-    hipSetDevice(ev->device);
-    hipEventDestroy(ev->ev);
+    (void)hipSetDevice(ev->device);
+    (void)hipEventDestroy(ev->ev);
     delete ev;
 }
 
@@ -829,13 +851,13 @@ hh_status hh_graph_end(hh_engine* e, hh_graph** out) {
     hipGraphExec_t x = nullptr;
     hipError_t err = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
     if (err != hipSuccess) {
-        hipGraphDestroy(g);
+        (void)hipGraphDestroy(g);
         return hip_fail(err, "hipGraphInstantiate");
     }
     hh_graph* h = new (std::nothrow) hh_graph{e, g, x};
     if (!h) {
-        hipGraphExecDestroy(x);
-        hipGraphDestroy(g);
+        (void)hipGraphExecDestroy(x);
+        (void)hipGraphDestroy(g);
         return fail(HH_ERR_OUT_OF_MEMORY, "host allocation failed");
     }
     *out = h;
@@ -854,8 +876,8 @@ hh_status hh_graph_launch(hh_graph* g) {
 void hh_graph_destroy(hh_graph* g) {
     if (!g) return;
     g->engine->select();
-    hipGraphExecDestroy(g->exec);
-    hipGraphDestroy(g->graph);
+    (void)hipGraphExecDestroy(g->exec);
+    (void)hipGraphDestroy(g->graph);
     delete g;
 }
 

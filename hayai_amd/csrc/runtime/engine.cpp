@@ -494,15 +494,17 @@ struct GurArgs {
     const uint8_t* wu;
     const float* x;
     uint8_t* hx;
+    const float* nw;
     uint64_t rb1;
     uint32_t d_model, d_ff;
     int32_t act;
-    uint32_t pad;
+    float eps;
 };
 struct DnrArgs {
     const uint8_t* wd;
     const uint8_t* hx;
     float* y;
+    const float* res;
     uint64_t rb2;
     uint32_t d_model, d_ff;
 };
@@ -522,10 +524,10 @@ bool hh_engine::ring_ok(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* 
 }
 
 hh_status hh_engine::enqueue_q4k_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu,
-                                         const float* x) {
+                                         const float* x, const float* norm, float eps) {
     const size_t dm = d->d_model, df = d->d_ff;
     const int w1 = dm <= 4096 ? 1 : 2;
-    const std::string name = "hh_q4k_gu_ring_g" + std::to_string(w1);
+    const std::string name = "hh_q4k_gu_ring_g" + std::to_string(w1) + (norm ? "_n" : "");
     hipFunction_t fn;
     HH_TRY(kernel(name, &fn));
     const int block = 8 * 64;
@@ -544,14 +546,14 @@ hh_status hh_engine::enqueue_q4k_ring_gu(const hh_ffn_desc* d, const uint8_t* wg
     }
     const size_t grid = ring_grid(occ, ring_gu_per_cu, cus);
     HH_TRY(grow(&ws_hq, &ws_hq_cap, 2 * df + (df / 8) * 4 + 16));
-    GurArgs a{wg, wu, x, (uint8_t*)ws_hq, (uint64_t)((dm / 256) * 144), (uint32_t)dm, (uint32_t)df, d->act, 0u};
+    GurArgs a{wg, wu, x, (uint8_t*)ws_hq, norm, (uint64_t)((dm / 256) * 144), (uint32_t)dm, (uint32_t)df, d->act, eps};
     void* params[] = {&a};
     hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
     if (err != hipSuccess) return hip_fail(err, "launch(ring q4k gate/up)");
     return HH_OK;
 }
 
-hh_status hh_engine::enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd, float* y) {
+hh_status hh_engine::enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd, float* y, const float* res) {
     const size_t dm = d->d_model, df = d->d_ff;
     int w2 = 1;
     while ((size_t)w2 * 64 < df / 64) w2 *= 2;
@@ -574,7 +576,7 @@ hh_status hh_engine::enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd
         blocks_per_cu[name] = occ;
     }
     const size_t grid = ring_grid(occ, ring_dn_per_cu, cus);
-    DnrArgs a{wd, (const uint8_t*)ws_hq, y, (uint64_t)((df / 256) * (q6 ? 210 : 144)), (uint32_t)dm, (uint32_t)df};
+    DnrArgs a{wd, (const uint8_t*)ws_hq, y, res, (uint64_t)((df / 256) * (q6 ? 210 : 144)), (uint32_t)dm, (uint32_t)df};
     void* params[] = {&a};
     hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
     if (err != hipSuccess) return hip_fail(err, "launch(ring q4k down)");
@@ -666,6 +668,36 @@ hh_status hh_engine::enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, cons
     }
     HH_TRY(enqueue_ffn_begin(d, pack, x));
     return enqueue_ffn_finish(d, pack, y);
+}
+
+// The FFN residual block of one token: y = x + FFN(RMSNorm(x)) (ffn_apply,
+// crates/hayai-core/src/hybrid_infer.rs:883-936, with rms_norm of
+// crates/hayai-cpu/src/attention.rs:142-147).  The ring kernels fuse both neighbours: gate/up
+// normalizes x while quantizing it, down adds the residual as it stores y.  Other layouts
+// run RMSNorm, the FFN and the residual add as three steps.  y may be x.
+hh_status hh_engine::enqueue_ffn_block(const hh_ffn_desc* d, const uint8_t* pack, const float* x, const float* norm,
+                                       float eps, float* y) {
+    const uint8_t* wg = pack + d->gate_off;
+    const uint8_t* wu = pack + d->up_off;
+    const uint8_t* wd = pack + d->down_off;
+    if (ring_ok(d, wg, wu, wd, x) && ((uintptr_t)norm & 15u) == 0) {
+        HH_TRY(enqueue_q4k_ring_gu(d, wg, wu, x, norm, eps));
+        HH_TRY(enqueue_q4k_ring_dn(d, wd, y, x));
+        ffn_stage_valid = false;
+        ffn_calls += 3;
+        return HH_OK;
+    }
+    const size_t dm = d->d_model;
+    HH_TRY(grow(&ws_xn, &ws_xn_cap, dm * sizeof(float)));
+    HH_TRY(grow(&ws_f, &ws_f_cap, dm * sizeof(float)));
+    hipFunction_t fn;
+    HH_TRY(kernel("hh_rmsnorm_kernel", &fn));
+    hh_norm_args na{x, norm, (float*)ws_xn, (uint32_t)dm, eps};
+    HH_TRY(launch(fn, 1, 1024, na));
+    HH_TRY(enqueue_ffn(d, pack, (const float*)ws_xn, (float*)ws_f));
+    HH_TRY(kernel("hh_add_kernel", &fn));
+    hh_add_args aa{x, (const float*)ws_f, y, (uint32_t)dm, 0u};
+    return launch(fn, (uint32_t)((dm + 255) / 256), 256, aa);
 }
 
 // ---------------------------------------------------------------- batched (MFMA) ------
@@ -1088,13 +1120,15 @@ static std::vector<std::string> required_kernels() {
     k.push_back("hh_lut_gemv");
     for (const char* f : {"g1_d1", "g1_d2", "g1_d4", "g1_d8", "g2_d2", "g2_d4", "g2_d8"})
         k.push_back(std::string("hh_q4k_ffnp_") + f);
-    for (const char* f : {"gu_ring_g1", "gu_ring_g2", "dn_ring_d1", "dn_ring_d2", "dn_ring_d4", "dn_ring_d8"})
+    for (const char* f : {"gu_ring_g1", "gu_ring_g2", "gu_ring_g1_n", "gu_ring_g2_n", "dn_ring_d1", "dn_ring_d2", "dn_ring_d4", "dn_ring_d8"})
         k.push_back(std::string("hh_q4k_") + f);
     for (int w : {1, 2, 4, 8}) k.push_back("hh_q6k_dn_ring_d" + std::to_string(w));
     for (const char* f : {"gu_ring_u16", "gu_ring_u32", "gu_ring_u64", "dn_ring_d1", "dn_ring_d2", "dn_ring_d4",
                           "dn_ring_d8"})
         k.push_back(std::string("hh_moe_") + f);
     k.push_back("hh_moe_route");
+    k.push_back("hh_rmsnorm_kernel");
+    k.push_back("hh_add_kernel");
     for (int t : {16, 32, 64})
         for (const char* kind : {"hh_moe_gateup_t", "hh_moe_down_t"}) k.push_back(std::string(kind) + std::to_string(t));
     return k;
@@ -1159,10 +1193,10 @@ void engine_destroy(hh_engine* e) {
     if (e->stream) (void)hipStreamSynchronize(e->stream);
     if (e->copy_stream) (void)hipStreamSynchronize(e->copy_stream);
     for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq, e->ws_xop, e->ws_hop, e->ws_part,
-                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->grid_sync})
-        if (p) hipFree(p);
-    if (e->stream) hipStreamDestroy(e->stream);
-    if (e->copy_stream) hipStreamDestroy(e->copy_stream);
-    if (e->module) hipModuleUnload(e->module);
+                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->ws_xn, e->ws_f, e->grid_sync})
+        if (p) (void)hipFree(p);
+    if (e->stream) (void)hipStreamDestroy(e->stream);
+    if (e->copy_stream) (void)hipStreamDestroy(e->copy_stream);
+    if (e->module) (void)hipModuleUnload(e->module);
     delete e;
 }

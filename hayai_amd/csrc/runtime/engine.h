@@ -101,6 +101,10 @@ struct hh_engine {
     size_t ws_w_cap = 0;
     void* ws_hq = nullptr;  // int8 digits of the FFN intermediate (gate/up -> down)
     size_t ws_hq_cap = 0;
+    void* ws_xn = nullptr;  // FFN block (generic formats): RMSNorm(x), then the FFN output
+    size_t ws_xn_cap = 0;
+    void* ws_f = nullptr;
+    size_t ws_f_cap = 0;
     // Batched (MFMA) path: tokens as MFMA operand stages (f16 hi/lo pairs + 16-element
     // sums), the FFN intermediate in the same form, split-K partials and their per-row-group
     // arrival counters.
@@ -159,6 +163,8 @@ struct hh_engine {
     hh_status enqueue_gateup(int type_g, int type_u, size_t d_ff, size_t d_model, const uint8_t* wg,
                              const uint8_t* wu, const float* x, float* h, int act);
     hh_status enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y);
+    hh_status enqueue_ffn_block(const hh_ffn_desc* d, const uint8_t* pack, const float* x, const float* norm,
+                                float eps, float* y);
     // The two halves of enqueue_ffn's two-launch path: gate/up(+act) into the engine's FFN
     // intermediate, then the down projection of that intermediate.
     hh_status enqueue_ffn_begin(const hh_ffn_desc* d, const uint8_t* pack, const float* x);
@@ -176,8 +182,9 @@ struct hh_engine {
     // barrier (q4k_ffn.hip); HH_ERR_UNSUPPORTED_DEVICE when the shape, alignment or
     // occupancy does not allow it.
     bool ring_ok(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd, const float* x) const;
-    hh_status enqueue_q4k_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const float* x);
-    hh_status enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd, float* y);
+    hh_status enqueue_q4k_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const float* x,
+                                  const float* norm = nullptr, float eps = 0.f);
+    hh_status enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd, float* y, const float* res = nullptr);
     hh_status enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                                const float* x, float* y);
     // Batched GEMV Y[b][m] = W . X[b] (x, y device pointers, row-major by token).  Q4_K with

@@ -39,18 +39,18 @@ struct hh_streamer {
 static void streamer_free(hh_streamer* s) {
     if (!s) return;
     if (s->engine) {
-        hipSetDevice(s->engine->device);
-        hipStreamSynchronize(s->engine->copy_stream);
-        hipStreamSynchronize(s->engine->stream);
+        (void)hipSetDevice(s->engine->device);
+        (void)hipStreamSynchronize(s->engine->copy_stream);
+        (void)hipStreamSynchronize(s->engine->stream);
     }
     for (hipEvent_t ev : s->dma_done)
-        if (ev) hipEventDestroy(ev);
-    if (s->tail) hipEventDestroy(s->tail);
+        if (ev) (void)hipEventDestroy(ev);
+    if (s->tail) (void)hipEventDestroy(s->tail);
     for (void* p : s->host)
-        if (p) hipHostFree(p);
+        if (p) (void)hipHostFree(p);
     for (hh_buf* b : s->mirror)
         if (b) {
-            if (b->ptr) hipFree(b->ptr);
+            if (b->ptr) (void)hipFree(b->ptr);
             delete b;
         }
     delete s;
@@ -104,7 +104,7 @@ hh_status hh_streamer_create(hh_engine* e, size_t layer_bytes, size_t block_k, s
         }
         s->mirror[i] = new (std::nothrow) hh_buf{e, d, s->slot_bytes, HH_BUF_DEVICE};
         if (!s->mirror[i]) {
-            hipFree(d);
+            (void)hipFree(d);
             streamer_free(s);
             return fail(HH_ERR_OUT_OF_MEMORY, "host allocation failed");
         }
@@ -122,13 +122,13 @@ void hh_streamer_destroy(hh_streamer* s) { streamer_free(s); }
 
 hh_status hh_streamer_slot_for(const hh_streamer* s, size_t layer, size_t* slot) {
     if (!slot) return fail(HH_ERR_INVALID, "slot is NULL");
-    size_t in_slot;
+    size_t in_slot = 0;
     return check_layer(s, layer, slot, &in_slot);
 }
 
 hh_status hh_streamer_weight_offset(const hh_streamer* s, size_t layer, size_t tensor_off, size_t* off) {
     if (!off) return fail(HH_ERR_INVALID, "off is NULL");
-    size_t slot, in_slot;
+    size_t slot = 0, in_slot = 0;
     HH_TRY(check_layer(s, layer, &slot, &in_slot));
     *off = in_slot + tensor_off;
     return HH_OK;
@@ -137,7 +137,7 @@ hh_status hh_streamer_weight_offset(const hh_streamer* s, size_t layer, size_t t
 hh_status hh_streamer_host_slot(hh_streamer* s, size_t layer, void** host_ptr) {
     if (!host_ptr) return fail(HH_ERR_INVALID, "host_ptr is NULL");
     *host_ptr = nullptr;
-    size_t slot, in_slot;
+    size_t slot = 0, in_slot = 0;
     HH_TRY(check_layer(s, layer, &slot, &in_slot));
     HH_TRY(s->engine->select());
     if (s->dma_pending[slot]) {
@@ -150,7 +150,7 @@ hh_status hh_streamer_host_slot(hh_streamer* s, size_t layer, void** host_ptr) {
 }
 
 hh_status hh_streamer_dma(hh_streamer* s, size_t layer, size_t off, size_t len) {
-    size_t slot, in_slot;
+    size_t slot = 0, in_slot = 0;
     HH_TRY(check_layer(s, layer, &slot, &in_slot));
     if (off > s->layer_bytes || len > s->layer_bytes - off)
         return fail(HH_ERR_INVALID, "streamer dma: range [%zu, +%zu) outside a %zu-byte layer", off, len,
@@ -177,7 +177,7 @@ hh_status hh_streamer_dma(hh_streamer* s, size_t layer, size_t off, size_t len) 
 
 hh_status hh_streamer_bind(hh_streamer* s, size_t layer, hh_buf** mirror, size_t* layer_off) {
     if (!mirror || !layer_off) return fail(HH_ERR_INVALID, "mirror / layer_off is NULL");
-    size_t slot, in_slot;
+    size_t slot = 0, in_slot = 0;
     HH_TRY(check_layer(s, layer, &slot, &in_slot));
     const long long block = (long long)(layer / s->block_k);
     if (s->staged[slot] != block)

@@ -563,6 +563,28 @@ class HipEngine:
         _check(self.lib.hh_ffn_dev(self.handle, C.byref(desc), pack.handle, pack_off, x.handle, x_off, y.handle,
                                    y_off))
 
+    def ffn_block_dev(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, norm: DeviceBuffer,
+                      norm_off: int, eps: float, x: DeviceBuffer, x_off: int, y: DeviceBuffer, y_off: int) -> None:
+        """The FFN residual block (ffn_apply, hybrid_infer.rs:883-936): y = x + FFN(rms_norm(x,
+        norm, eps)); y may be x.  Enqueue only."""
+        _check(self.lib.hh_ffn_block_dev(self.handle, C.byref(desc), pack.handle, pack_off, norm.handle, norm_off,
+                                         eps, x.handle, x_off, y.handle, y_off))
+
+    def ffn_block(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, norm: np.ndarray, eps: float,
+                  x: np.ndarray) -> np.ndarray:
+        """ffn_apply on host activations: returns x + FFN(rms_norm(x, norm, eps)), blocking."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        norm = np.ascontiguousarray(norm, dtype=np.float32)
+        if x.size != desc.d_model or norm.size != desc.d_model:
+            raise HipError(2, f"x and norm must hold d_model={desc.d_model} floats")
+        xb, nb = self.upload(x), self.upload(norm)
+        try:
+            self.ffn_block_dev(desc, pack, pack_off, nb, 0, eps, xb, 0, xb, 0)
+            return xb.read(np.float32, desc.d_model)
+        finally:
+            xb.free()
+            nb.free()
+
     def ffn_begin_dev(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, x: DeviceBuffer,
                       x_off: int) -> None:
         """ffn_begin_gate_up_scratch (stream_infer.rs:3752-3808): gate/up + activation into

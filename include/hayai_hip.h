@@ -230,6 +230,16 @@ hh_status hh_ffn(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t 
 hh_status hh_ffn_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
                      const hh_buf* x, size_t x_off, hh_buf* y, size_t y_off);
 
+/* The FFN residual block of one token (ffn_apply, crates/hayai-core/src/hybrid_infer.rs:
+ * 883-936): y = x + FFN(RMSNorm(x)), RMSNorm as rms_norm (crates/hayai-cpu/src/attention.rs:
+ * 142-147): x * (1 / sqrt(mean(x^2) + eps)) * norm.  norm: d_model floats; y may be x (the
+ * reference updates x in place).  All-Q4_K and Q4_K_M layers fuse the norm into gate/up and
+ * the residual into down; other layouts run norm, FFN and add as separate kernels.
+ * Device buffers, enqueue only. */
+hh_status hh_ffn_block_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                           const hh_buf* norm, size_t norm_off, float eps, const hh_buf* x, size_t x_off, hh_buf* y,
+                           size_t y_off);
+
 /* The FFN op for `batch` tokens (x, y: batch rows of d_model floats): the batched-prefill
  * form of the op (prefill_wave.rs:577-584 drives execute_quant_gemv_batched for FFN
  * matrices).  All-Q4_K FFNs run gate/up(+act) and down on the matrix cores; other formats

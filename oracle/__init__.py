@@ -57,6 +57,9 @@ def lib():
         L.or_swiglu.argtypes = [P, P, P, sz]
         L.or_gelu_tanh.argtypes = [P, P, P, sz]
         L.or_ffn.argtypes = [C.c_int, C.c_int, C.c_int, sz, sz, P, sz, P, sz, P, sz, C.c_int, P, P, P]
+        L.or_rms_norm.argtypes = [P, P, C.c_float, P, sz]
+        L.or_ffn_block.argtypes = [C.c_int, C.c_int, C.c_int, sz, sz, P, sz, P, sz, P, sz, C.c_int, P, C.c_float,
+                                   P, P]
         L.or_route_experts.argtypes = [P, C.c_int, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                        C.c_float, P, P]
         L.or_moe_token.argtypes = [C.c_int, sz, sz, P, sz, sz, sz, sz, C.c_int, P, P, P, P]
@@ -185,6 +188,29 @@ def ffn(types, d_model: int, d_ff: int, wg, wu, wd, x, act: int = 0, return_h: b
     _check(lib().or_ffn(tg, tu, td, d_model, d_ff, _p(wg), wg.size, _p(wu), wu.size, _p(wd), wd.size,
                         act, _p(x), _p(y), _p(h)), "ffn")
     return (y, h) if return_h else y
+
+
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    """rms_norm (crates/hayai-cpu/src/attention.rs:142-147), out of place."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    if x.size != w.size:
+        raise ValueError("x and w differ in length")
+    y = np.empty_like(x)
+    lib().or_rms_norm(_p(x), _p(w), eps, _p(y), x.size)
+    return y
+
+
+def ffn_block(types, d_model: int, d_ff: int, wg, wu, wd, norm, eps: float, x, act: int = 0) -> np.ndarray:
+    """ffn_apply (crates/hayai-core/src/hybrid_infer.rs:883-936): x + FFN(rms_norm(x))."""
+    tg, tu, td = types
+    wg, wu, wd = (np.ascontiguousarray(a, dtype=np.uint8) for a in (wg, wu, wd))
+    norm = np.ascontiguousarray(norm, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(d_model, np.float32)
+    _check(lib().or_ffn_block(tg, tu, td, d_model, d_ff, _p(wg), wg.size, _p(wu), wu.size, _p(wd), wd.size, act,
+                              _p(norm), eps, _p(x), _p(y)), "ffn_block")
+    return y
 
 
 def route_experts(scores, top_k: int, bias=None, n_group: int = 0, topk_group: int = 0, gating: int = 0,

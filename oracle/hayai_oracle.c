@@ -592,6 +592,24 @@ void or_gelu_tanh(const float* g, const float* u, float* h, size_t n) {
     }
 }
 
+/* RMSNorm; rms_norm, crates/hayai-cpu/src/attention.rs:142-147: the mean square as
+ * simd_mean_square (crates/hayai-cpu/src/simd_ops.rs:10-24: f32x8 lane sums of v*v, ordered
+ * reduce_sum, scalar tail, / n), inv = 1 / sqrt(ms + eps), then simd_scale_mul (:28-41):
+ * (x * inv) * w over whole f32x8s, x * (inv * w) on the tail. */
+void or_rms_norm(const float* x, const float* w, float eps, float* y, size_t n) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    size_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; l++) acc[l] = acc[l] + x[i + l] * x[i + l];
+    float ms = reduce_sum8(acc);
+    for (; i < n; i++) ms = ms + x[i] * x[i];
+    ms = ms / (float)n;
+    const float inv = 1.0f / sqrtf(ms + eps);
+    for (i = 0; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; l++) y[i + l] = (x[i + l] * inv) * w[i + l];
+    for (; i < n; i++) y[i] = x[i] * (inv * w[i]);
+}
+
 /* The FFN op: gate & up GEMV -> act(gate)*up -> down GEMV;
  * ffn_begin_gate_up_scratch + ffn_finish_scratch, stream_infer.rs:3752-3864.
  * act 0 = SiLU, 1 = GELU(tanh).  h (d_ff floats) is optional scratch output. */
@@ -615,6 +633,27 @@ out:
     free(u);
     if (!h_out) free(h);
     return rc;
+}
+
+/* The FFN residual block of one token; ffn_apply, crates/hayai-core/src/hybrid_infer.rs:
+ * 883-936: xn = rms_norm(x), y = x + FFN(xn) (x[i] += ws_down[i]). */
+int or_ffn_block(int tg, int tu, int td, size_t d_model, size_t d_ff, const uint8_t* wg, size_t lg,
+                 const uint8_t* wu, size_t lu, const uint8_t* wd, size_t ld, int act, const float* norm, float eps,
+                 const float* x, float* y) {
+    float* xn = (float*)malloc(d_model * sizeof(float));
+    float* f = (float*)malloc(d_model * sizeof(float));
+    if (!xn || !f) {
+        free(xn);
+        free(f);
+        return OR_EINVAL;
+    }
+    or_rms_norm(x, norm, eps, xn, d_model);
+    int st = or_ffn(tg, tu, td, d_model, d_ff, wg, lg, wu, lu, wd, ld, act, xn, f, NULL);
+    if (st == OR_OK)
+        for (size_t i = 0; i < d_model; i++) y[i] = x[i] + f[i];
+    free(xn);
+    free(f);
+    return st;
 }
 
 /* ------------------------------------------------------------- MoE routing ---------- */

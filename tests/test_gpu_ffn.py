@@ -262,3 +262,85 @@ def test_ffn_begin_finish_equals_ffn(engine, two_launch_engine, types, d_model, 
         other = eng.ffn_desc(types, d_model, d_ff, lay, 1)
         with pytest.raises(hayai_amd.HipError):
             eng.ffn_finish_dev(other, pack, 0, y2, 0)
+
+
+BLOCK_CASES = [
+    # (types, d_model, d_ff): the ring kernels with the norm and residual fused (8B Q4_K,
+    # Q4_K_M, d_model 8192: two x passes per thread), and the generic three-step path (SmolLM
+    # Q4_0, IQ2_XXS)
+    ((12, 12, 12), 4096, 14336), ((12, 12, 14), 4096, 14336), ((12, 12, 12), 8192, 4096),
+    ((2, 2, 2), 576, 1536), ((16, 16, 16), 1024, 2048),
+]
+
+
+@pytest.mark.parametrize("types,d_model,d_ff", BLOCK_CASES)
+def test_ffn_block_matches_oracle(engine, types, d_model, d_ff):
+    # ffn_apply (hybrid_infer.rs:883-936): y = x + FFN(rms_norm(x)).  The FFN part (y - x) is
+    # held to the FFN bar against the oracle; out of place and in place (y = x) agree.
+    print(f"[case] ffn block types={types} {d_model}x{d_ff}", flush=True)
+    oracle.set_threads(min(16, oracle.max_threads()))
+    lay, (wg, wu, wd), pack = make_pack(engine, types, d_model, d_ff, 22)
+    desc = engine.ffn_desc(types, d_model, d_ff, lay)
+    rng = np.random.default_rng(d_model + d_ff)
+    x = (3.0 * rng.standard_normal(d_model)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, d_model).astype(np.float32)
+    eps = 1e-5
+    ref = oracle.ffn_block(types, d_model, d_ff, wg, wu, wd, nw, eps, x)
+    xb, nb, yb = engine.upload(x), engine.upload(nw), engine.alloc(4 * d_model)
+    engine.ffn_block_dev(desc, pack, 0, nb, 0, eps, xb, 0, yb, 0)
+    y = yb.read(np.float32, d_model)
+    assert np.isfinite(y).all()
+    err = rel_err(y - x, ref - x)
+    print(f"  rel_err of the FFN part {err:.3e}", flush=True)
+    assert err <= REL_TOL, err
+    engine.ffn_block_dev(desc, pack, 0, nb, 0, eps, xb, 0, xb, 0)  # in place
+    np.testing.assert_array_equal(xb.read(np.float32, d_model), y)
+    # the host-activation form
+    np.testing.assert_array_equal(engine.ffn_block(desc, pack, 0, nw, eps, x), y)
+
+
+def test_ffn_block_unaligned_norm_takes_the_three_step_path(engine):
+    # A norm weight that is not 16-byte aligned keeps the ring kernels out (their prologue
+    # reads it as float4s): the three-step path gives the same block within tolerance.
+    types, d_model, d_ff = (12, 12, 12), 4096, 14336
+    print(f"[case] ffn block, norm at offset 4, {d_model}x{d_ff}", flush=True)
+    lay, (wg, wu, wd), pack = make_pack(engine, types, d_model, d_ff, 23)
+    desc = engine.ffn_desc(types, d_model, d_ff, lay)
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(d_model).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, d_model).astype(np.float32)
+    nb = engine.alloc(4 * d_model + 16)
+    nb.write(nw, 4)
+    xb, yb = engine.upload(x), engine.alloc(4 * d_model)
+    engine.ffn_block_dev(desc, pack, 0, nb, 4, 1e-5, xb, 0, yb, 0)
+    y = yb.read(np.float32, d_model)
+    ref = oracle.ffn_block(types, d_model, d_ff, wg, wu, wd, nw, 1e-5, x)
+    assert rel_err(y - x, ref - x) <= REL_TOL
+    with pytest.raises(hayai_amd.HipError):
+        engine.ffn_block_dev(desc, pack, 0, nb, 2, 1e-5, xb, 0, yb, 0)  # misaligned float offset
+    with pytest.raises(hayai_amd.HipError):
+        engine.ffn_block_dev(desc, pack, 0, nb, 0, -1.0, xb, 0, yb, 0)  # negative eps
+
+
+def test_ffn_block_chain_of_layers(engine):
+    # Four layers applied in place on one residual stream, as a decode step runs them
+    # (x_{l+1} = x_l + FFN_l(rms_norm(x_l, norm_l))), no host sync in between, against the
+    # oracle applying the same four blocks.
+    types, d_model, d_ff, L = (12, 12, 12), 4096, 14336, 4
+    print(f"[case] ffn block chain, {L} layers {d_model}x{d_ff}", flush=True)
+    oracle.set_threads(min(16, oracle.max_threads()))
+    packs = [make_pack(engine, types, d_model, d_ff, 24, layer=l) for l in range(L)]
+    rng = np.random.default_rng(3)
+    norms = [rng.uniform(0.5, 1.5, d_model).astype(np.float32) for _ in range(L)]
+    x = rng.standard_normal(d_model).astype(np.float32)
+    xb = engine.upload(x)
+    nbs = [engine.upload(n) for n in norms]
+    for l, (lay, _, pack) in enumerate(packs):
+        engine.ffn_block_dev(engine.ffn_desc(types, d_model, d_ff, lay), pack, 0, nbs[l], 0, 1e-5, xb, 0, xb, 0)
+    y = xb.read(np.float32, d_model)
+    r = x
+    for l, (lay, (wg, wu, wd), _) in enumerate(packs):
+        r = oracle.ffn_block(types, d_model, d_ff, wg, wu, wd, norms[l], 1e-5, r)
+    err = rel_err(y - x, r - x)
+    print(f"  rel_err of the 4-layer update {err:.3e}", flush=True)
+    assert err <= REL_TOL, err

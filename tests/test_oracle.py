@@ -453,3 +453,52 @@ def test_validation_rules():
     assert not oracle.validate_weights(oracle.Q4_K, 4, 256, 4 * 144 - 1)
     with pytest.raises(oracle.OracleError):
         oracle.gemv(oracle.Q4_K, 4, 256, np.zeros(100, np.uint8), np.zeros(256, np.float32))
+
+
+# ------------------------------------------------------------------ RMSNorm / FFN block
+@pytest.mark.parametrize("n", [8, 11, 576, 4096, 4099])
+def test_rms_norm_matches_fp64(n):
+    # rms_norm (attention.rs:142-147) against the formula in float64; n = 11 and 4099 take
+    # the scalar tail after the f32x8 body.  A divisor of n-1, eps outside the root or a
+    # missing weight moves the result far beyond this bound.
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    for eps in (1e-5, 1e-6, 0.5):
+        y = oracle.rms_norm(x, w, eps)
+        ref = x.astype(np.float64) * w / np.sqrt(np.mean(x.astype(np.float64) ** 2) + eps)
+        assert np.max(np.abs(y - ref) / np.abs(ref).max()) < 2e-6
+
+
+def test_rms_norm_scale_invariant_and_constant():
+    # eps = 0: scaling x by 4 scales every intermediate by an exact power of two, so the
+    # output is identical bit for bit; a constant vector normalizes to +-1 (times the weight).
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(1003).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 1003).astype(np.float32)
+    np.testing.assert_array_equal(oracle.rms_norm(x, w, 0.0), oracle.rms_norm(4 * x, w, 0.0))
+    c = np.full(1003, -3.0, np.float32)
+    np.testing.assert_allclose(oracle.rms_norm(c, w, 0.0), -w, rtol=2e-7)
+    # large eps dominates: x / sqrt(eps) for tiny x
+    t = np.full(64, 1e-4, np.float32)
+    np.testing.assert_allclose(oracle.rms_norm(t, np.ones(64, np.float32), 1.0), t, rtol=1e-6)
+
+
+def test_ffn_block_zero_norm_weight_is_identity_and_composes():
+    # ffn_apply = x + FFN(rms_norm(x)): with a zero norm weight the FFN input is 0, SiLU(0) * 0
+    # = 0, and y == x exactly; otherwise y - x equals the FFN of the normalized x.
+    d_model, d_ff = 256, 512
+    rng = np.random.default_rng(9)
+    wg, wu, wd = (rng.integers(0, 256, (r * c) // 32 * 18, dtype=np.uint8) for r, c in
+                  ((d_ff, d_model), (d_ff, d_model), (d_model, d_ff)))
+    for a in (wg, wu, wd):  # finite f16 scales (0x2E66) in every Q4_0 block
+        a.reshape(-1, 18)[:, 0] = 0x66
+        a.reshape(-1, 18)[:, 1] = 0x2E
+    x = rng.standard_normal(d_model).astype(np.float32)
+    t = (oracle.Q4_0,) * 3
+    y0 = oracle.ffn_block(t, d_model, d_ff, wg, wu, wd, np.zeros(d_model, np.float32), 1e-5, x)
+    np.testing.assert_array_equal(y0, x)
+    nw = rng.uniform(0.5, 1.5, d_model).astype(np.float32)
+    y = oracle.ffn_block(t, d_model, d_ff, wg, wu, wd, nw, 1e-5, x)
+    f = oracle.ffn(t, d_model, d_ff, wg, wu, wd, oracle.rms_norm(x, nw, 1e-5))
+    np.testing.assert_array_equal(y, x + f)
