@@ -21,7 +21,47 @@ STATUS_NAMES = {
     4: "HH_ERR_RUNTIME",
     5: "HH_ERR_OUT_OF_MEMORY",
     6: "HH_ERR_UNSUPPORTED_DEVICE",
+    7: "HH_ERR_IO",
+    8: "HH_ERR_NOT_FOUND",
 }
+
+class GgufInfo(C.Structure):
+    _fields_ = [
+        ("version", C.c_uint32),
+        ("io_uring", C.c_uint32),
+        ("alignment", C.c_uint64),
+        ("data_offset", C.c_uint64),
+        ("header_bytes", C.c_uint64),
+        ("n_tensors", C.c_uint64),
+        ("n_metadata", C.c_uint64),
+        ("file_size", C.c_uint64),
+    ]
+
+
+class GgufTensor(C.Structure):
+    _fields_ = [
+        ("name", C.c_char_p),
+        ("n_dims", C.c_uint32),
+        ("type", C.c_uint32),
+        ("dims", C.c_uint64 * 4),
+        ("offset", C.c_uint64),
+        ("abs_offset", C.c_uint64),
+        ("nbytes", C.c_uint64),
+    ]
+
+
+class LayerPack(C.Structure):
+    _fields_ = [
+        ("off", C.c_size_t * 8),
+        ("len", C.c_size_t * 8),
+        ("type", C.c_uint32 * 8),
+        ("cols", C.c_uint64 * 8),
+        ("rows", C.c_uint64 * 8),
+        ("total", C.c_size_t),
+        ("fused_gate_up", C.c_int32),
+        ("pad", C.c_int32),
+    ]
+
 
 # Every symbol include/hayai_hip.h declares, with (restype, argtypes).
 P = C.c_void_p
@@ -82,6 +122,19 @@ class MoeDesc(C.Structure):
 
 
 SIGNATURES = {
+    "hh_gguf_open": (ST, [C.c_char_p, PP]),
+    "hh_gguf_close": (None, [P]),
+    "hh_gguf_header": (ST, [P, C.POINTER(GgufInfo)]),
+    "hh_gguf_tensor_at": (ST, [P, C.c_uint64, C.POINTER(GgufTensor)]),
+    "hh_gguf_find": (ST, [P, C.c_char_p, C.POINTER(GgufTensor)]),
+    "hh_gguf_meta_u32": (ST, [P, C.c_char_p, C.POINTER(C.c_uint32)]),
+    "hh_gguf_meta_u64": (ST, [P, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "hh_gguf_meta_f32": (ST, [P, C.c_char_p, C.POINTER(C.c_float)]),
+    "hh_gguf_meta_str": (ST, [P, C.c_char_p, C.POINTER(C.c_char_p), C.POINTER(SZ)]),
+    "hh_tensor_nbytes": (ST, [C.c_uint32, C.POINTER(C.c_uint64), C.c_uint32, C.POINTER(C.c_uint64)]),
+    "hh_gguf_layer_pack": (ST, [P, SZ, C.POINTER(LayerPack)]),
+    "hh_gguf_load_layer_pack": (ST, [P, SZ, P, SZ, C.POINTER(LayerPack)]),
+    "hh_gguf_read_tensor": (ST, [P, C.c_char_p, P, SZ]),
     "hh_abi_version": (C.c_int, []),
     "hh_last_error": (C.c_char_p, []),
     "hh_status_name": (C.c_char_p, [ST]),

@@ -69,7 +69,7 @@ def build_runtime(verbose: bool = False) -> list[str]:
     os.makedirs(BUILD, exist_ok=True)
     cxx = os.environ.get("CXX", "g++")
     objs = []
-    for name in ("engine.cpp", "capi.cpp", "streamer.cpp"):
+    for name in ("engine.cpp", "capi.cpp", "streamer.cpp", "gguf.cpp"):
         src = os.path.join(CSRC, "runtime", name)
         obj = os.path.join(BUILD, name.replace(".cpp", ".o"))
         _run([cxx, "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",

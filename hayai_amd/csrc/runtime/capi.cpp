@@ -55,6 +55,8 @@ const char* hh_status_name(hh_status st) {
     case HH_ERR_RUNTIME: return "HH_ERR_RUNTIME";
     case HH_ERR_OUT_OF_MEMORY: return "HH_ERR_OUT_OF_MEMORY";
     case HH_ERR_UNSUPPORTED_DEVICE: return "HH_ERR_UNSUPPORTED_DEVICE";
+    case HH_ERR_IO: return "HH_ERR_IO";
+    case HH_ERR_NOT_FOUND: return "HH_ERR_NOT_FOUND";
     }
     return "HH_ERR_UNKNOWN";
 }

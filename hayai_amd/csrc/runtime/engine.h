@@ -25,6 +25,7 @@ namespace hh {
 
 // Thread-local last error.
 hh_status fail(hh_status st, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+const std::string& last_error();
 hh_status hip_fail(hipError_t err, const char* what);
 
 #define HH_TRY_HIP(call, what)                        \

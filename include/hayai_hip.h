@@ -48,7 +48,9 @@ typedef enum hh_status {
     HH_ERR_KERNEL_MISSING = 3,
     HH_ERR_RUNTIME = 4,
     HH_ERR_OUT_OF_MEMORY = 5,
-    HH_ERR_UNSUPPORTED_DEVICE = 6
+    HH_ERR_UNSUPPORTED_DEVICE = 6,
+    HH_ERR_IO = 7,        /* file could not be opened or read (GgufError::Io / short file) */
+    HH_ERR_NOT_FOUND = 8  /* no such tensor or metadata key (GgufError::MissingTensor) */
 } hh_status;
 
 /* GGML type ids (crates/hayai-model/src/gguf_types.rs:6-78) with a kernel here. */
@@ -388,6 +390,73 @@ void hh_graph_destroy(hh_graph* g);
  * reference's bench_* helpers (async_gemv.rs:309-428). */
 hh_status hh_synth_weights_dev(hh_engine* e, int ggml_type, hh_buf* dst, size_t off, size_t n_blocks,
                                uint64_t seed, float lo, float hi);
+
+/* ------------------------------------------------------------------ GGUF catalog ------
+ * The model file side of the path: GgufCatalog's header parse (crates/hayai-model/src/
+ * gguf.rs:25-127, gguf_stream.rs:34-192) and load_layer_pack_into (gguf_stream.rs:451-638),
+ * reading through io_uring in one batch per layer (weight_io.rs:14-105,351-470; positioned
+ * reads when io_uring is refused or HAYAI_FORCE_FILE_IO=1).  Host memory only: the
+ * destination is typically a pinned streaming slot (hh_streamer_host_slot).  Malformed
+ * files are HH_ERR_INVALID (bad magic or version, more than 4 dims, a zero dim, duplicate
+ * names, unknown types, alignment not a power of two, size overflow), unreadable or short
+ * ones HH_ERR_IO, missing tensors and keys HH_ERR_NOT_FOUND. */
+typedef struct hh_gguf hh_gguf;
+
+typedef struct hh_gguf_info {
+    uint32_t version;      /* 1..4 */
+    uint32_t io_uring;     /* 1: reads go through io_uring */
+    uint64_t alignment;    /* general.alignment (default 32) */
+    uint64_t data_offset;  /* absolute offset of the tensor data section */
+    uint64_t header_bytes; /* bytes of header + directory */
+    uint64_t n_tensors;
+    uint64_t n_metadata;
+    uint64_t file_size;
+} hh_gguf_info;
+
+typedef struct hh_gguf_tensor {
+    const char* name;     /* owned by the catalog until hh_gguf_close */
+    uint32_t n_dims;
+    uint32_t type;        /* GGML type id */
+    uint64_t dims[4];     /* ne0 (columns) first; unused dims are 1 */
+    uint64_t offset;      /* relative to the data section */
+    uint64_t abs_offset;  /* data_offset + offset */
+    uint64_t nbytes;      /* tensor_nbytes (gguf.rs:240-284) */
+} hh_gguf_tensor;
+
+/* LayerPackLayout (gguf_stream.rs:1416-1432) plus each region's matrix shape and type.
+ * Slots: 0 attn_q, 1 attn_k, 2 attn_v, 3 attn_output, 4 ffn_gate, 5 ffn_up, 6 ffn_down,
+ * 7 attn_gate.  Regions are back to back in slot order (no padding); an absent optional
+ * tensor (attn_v, ffn_gate, attn_gate) has length 0. */
+typedef struct hh_layer_pack {
+    size_t off[8];
+    size_t len[8];
+    uint32_t type[8];
+    uint64_t cols[8];
+    uint64_t rows[8];
+    size_t total;
+    int32_t fused_gate_up; /* gate and up are the two row halves of one fused tensor */
+    int32_t pad;
+} hh_layer_pack;
+
+hh_status hh_gguf_open(const char* path, hh_gguf** out);
+void hh_gguf_close(hh_gguf* g);
+hh_status hh_gguf_header(const hh_gguf* g, hh_gguf_info* out);
+hh_status hh_gguf_tensor_at(const hh_gguf* g, uint64_t index, hh_gguf_tensor* out);
+/* GgufCatalog::tensor (gguf.rs:176-182) */
+hh_status hh_gguf_find(const hh_gguf* g, const char* name, hh_gguf_tensor* out);
+/* meta_u32 / as_u64 / meta_f32 / meta_str (gguf.rs:160-174, gguf_types.rs:100-135) */
+hh_status hh_gguf_meta_u32(const hh_gguf* g, const char* key, uint32_t* out);
+hh_status hh_gguf_meta_u64(const hh_gguf* g, const char* key, uint64_t* out);
+hh_status hh_gguf_meta_f32(const hh_gguf* g, const char* key, float* out);
+hh_status hh_gguf_meta_str(const hh_gguf* g, const char* key, const char** out, size_t* len);
+/* tensor_nbytes (gguf.rs:240-284) for a type and shape */
+hh_status hh_tensor_nbytes(uint32_t type, const uint64_t* dims, uint32_t n_dims, uint64_t* out);
+/* The layout load_layer_pack_into would produce for `layer`, without reading. */
+hh_status hh_gguf_layer_pack(const hh_gguf* g, size_t layer, hh_layer_pack* out);
+/* load_layer_pack_into: the layer's tensors into dst[0, total), one batch of reads. */
+hh_status hh_gguf_load_layer_pack(hh_gguf* g, size_t layer, void* dst, size_t dst_len, hh_layer_pack* out);
+/* read_tensor_into (gguf_stream.rs:266-290): one whole tensor into dst. */
+hh_status hh_gguf_read_tensor(hh_gguf* g, const char* name, void* dst, size_t dst_len);
 
 #ifdef __cplusplus
 }
