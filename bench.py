@@ -388,6 +388,116 @@ def bench_stream(eng, args) -> int:
     return 0
 
 
+def bench_disk(eng, args) -> int:
+    """BASELINE.json configs[4] with the reference's real I/O step: the 70B-shaped IQ2_XXS
+    FFN layers are read from a GGUF file through the catalog (io_uring, one batch of reads
+    per layer, load_layer_pack_into) into the 2 pinned ping-pong slots, then DMAed and run
+    as in the stream workload.  The file (written first, under $TMPDIR) holds --disk-layers
+    distinct layers (each with small F16 attention tensors ahead of its FFN, as a layer pack
+    has them); the 80 layers of a token cycle through them, so after the first pass the
+    reads come from the host page cache.  value = streamed bytes per token / token time."""
+    import tempfile
+
+    import hayai_amd
+    from hayai_amd import synth
+    from hayai_amd.gguf import GgufCatalog, write_gguf
+
+    T = hayai_amd.IQ2_XXS
+    DM, DF, L, NF = 8192, 28672, 80, max(2, args.disk_layers)
+    lo, hi = synth.SCALE_RANGE[T]
+    path = os.path.join(os.environ.get("TMPDIR", tempfile.gettempdir()), f"hayai_bench_{os.getpid()}.gguf")
+
+    def tensors():
+        for l in range(NF):
+            for name in ("attn_q", "attn_k", "attn_v", "attn_output"):
+                yield f"blk.{l}.{name}.weight", (64, 64), 1, np.zeros(64 * 64 * 2, np.uint8)
+            for name, mat, rows, cols in (("ffn_gate", synth.GATE, DF, DM), ("ffn_up", synth.UP, DF, DM),
+                                          ("ffn_down", synth.DOWN, DM, DF)):
+                yield f"blk.{l}.{name}.weight", (cols, rows), T, synth.matrix(T, rows, cols,
+                                                                               synth.seed_for(5, l, mat), lo, hi)
+
+    t0 = time.perf_counter()
+    write_gguf(path, [("general.architecture", "llama")], list(tensors()))
+    log(f"[bench] wrote {os.path.getsize(path) / 2**30:.2f} GiB GGUF ({NF} layers) in {time.perf_counter() - t0:.1f} s")
+    try:
+        cat = GgufCatalog(path)
+        lp = cat.layer_pack(0)
+        lay = lp.ffn_layout()
+        desc = eng.ffn_desc((T, T, T), DM, DF, lay)
+        st = hayai_amd.StreamingScratch(eng, lp.total, k_chunk=1, n_slots=2)
+        xs = synth.normal(synth.seed_for(5, 0, synth.ACT), L * DM).reshape(L, DM)
+        xbuf = eng.upload(xs)
+        ybuf = eng.alloc(4 * DM * L)
+        ffn_bytes = lay.gate_len + lay.up_len + lay.down_len
+        read_s = [0.0]
+
+        def load(l):
+            view = st.host_slot(l)  # waits for the DMA still reading this slot
+            r0 = time.perf_counter()
+            cat.load_layer_pack(l % NF, view)
+            read_s[0] += time.perf_counter() - r0
+            st.dma(l, lay.gate_off, lay.down_off + lay.down_len - lay.gate_off)
+
+        def token():
+            load(0)
+            for l in range(L):
+                if l + 1 < L:
+                    load(l + 1)
+                mirror, off = st.weight_bind(l)
+                eng.ffn_dev(desc, mirror, off, xbuf, 4 * DM * l, ybuf, 4 * DM * l)
+
+        for _ in range(args.warmup):
+            token()
+        eng.sync()
+        steps = max(1, min(args.steps, 20))
+        read_s[0] = 0.0
+        a, b = eng.event(), eng.event()
+        w0 = time.perf_counter()
+        a.record()
+        for _ in range(steps):
+            token()
+        b.record()
+        eng.sync()
+        wall = (time.perf_counter() - w0) / steps
+        ms_tok = a.elapsed_ms(b) / steps
+        read_gbs = L * lp.total / (read_s[0] / steps) / 1e9
+        tok_bytes = L * (lp.total + 2 * 4 * DM)
+        gbs = tok_bytes / (ms_tok / 1e3) / 1e9
+        log(f"[bench] disk: {ms_tok:.2f} ms/token ({ms_tok / L * 1e3:.0f} us/layer), {gbs:.2f} GB/s; file reads alone "
+            f"{read_s[0] / steps * 1e3:.2f} ms/token ({read_gbs:.2f} GB/s, io_uring={int(cat.io_uring)}); "
+            f"wall {wall * 1e3:.2f} ms/token")
+        out = {
+            "metric": "FFN tok/s and streamed GB/s, 70B-shape IQ2_XXS FFN read from a GGUF file (io_uring) into "
+                      "2 pinned slots",
+            "value": round(gbs, 3),
+            "unit": "GB/s",
+            "n_gpus": 1,
+            "steps": steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(ms_tok, 4),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "f32",
+            "data": f"synthetic GGUF file of {NF} distinct IQ2_XXS layers (page-cache resident after the first "
+                    "pass), N(0,1) f32 activations",
+            "config": {"workload": "llama3-70b-ffn-iq2_xxs-bs1-80layers-gguf-io_uring", "d_model": DM, "d_ff": DF,
+                       "layers": L, "file_layers": NF, "batch": 1, "weights": "IQ2_XXS", "slots": 2,
+                       "layer_pack_bytes": lp.total, "ffn_bytes": ffn_bytes},
+            "ffn_tok_s": round(1e3 / ms_tok, 3),
+            "file_read_gbs": round(read_gbs, 3),
+            "io_uring": bool(cat.io_uring),
+            "cpu_baseline": None,
+        }
+        print(json.dumps(out), flush=True)
+        st.free()
+        cat.close()
+    finally:
+        os.unlink(path)
+    eng.close()
+    return 0
+
+
 def bench_smollm(eng, args) -> int:
     """SmolLM2-135M-shaped SwiGLU FFN (d_model 576, d_ff 1536) in
     Q4_0, 30 layers, batch 1.  The 30-layer stack is 45 MB; 8 copies (360 MB, beyond the
@@ -603,12 +713,14 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 256 MiB device copy before timing (reference point for HBM counters)")
-    ap.add_argument("--workload", default="bs1", choices=["bs1", "batched", "moe", "stream", "smollm", "q4km", "block"],
+    ap.add_argument("--workload", default="bs1", choices=["bs1", "batched", "moe", "stream", "smollm", "q4km", "block", "disk"],
                     help="bs1: BASELINE.json configs[1] (the headline); batched: configs[2], --batch tokens per "
                          "step; moe: configs[3], --batch tokens per step; stream: configs[4] (70B IQ2_XXS "
                          "streamed from pinned host); smollm: configs[0]; q4km: the 8B FFN with a Q6_K down "
                          "projection (Q4_K_M layout); block: the 8B FFN residual block (RMSNorm + FFN + "
-                         "residual) chained over 32 layers")
+                         "residual) chained over 32 layers; disk: configs[4] read from a GGUF file through "
+                         "io_uring into the pinned slots")
+    ap.add_argument("--disk-layers", type=int, default=8, help="distinct layers in the --workload disk file")
     ap.add_argument("--batch", type=int, default=16, help="tokens per step for --workload batched")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -629,6 +741,8 @@ def main() -> int:
         return bench_smollm(eng, args)
     if args.workload == "q4km":
         return bench_q4km(eng, args)
+    if args.workload == "disk":
+        return bench_disk(eng, args)
     gate = hayai_amd.QuantMatrix("ffn_gate", D_MODEL, D_FF, Q4_K)
     up = hayai_amd.QuantMatrix("ffn_up", D_MODEL, D_FF, Q4_K)
     down = hayai_amd.QuantMatrix("ffn_down", D_FF, D_MODEL, Q4_K)

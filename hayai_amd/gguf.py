@@ -76,6 +76,12 @@ class LayerPack:
     def down_off(self) -> int:
         return self.off[6]
 
+    def ffn_layout(self):
+        """The FFN part as the engine's LayerPackLayout (offsets inside this pack)."""
+        from .engine import LayerPackLayout
+        return LayerPackLayout(self.off[4], self.off[5], self.off[6], self.len[4], self.len[5], self.len[6],
+                               self.total)
+
 
 def _pack(lp: _abi.LayerPack) -> LayerPack:
     return LayerPack(tuple(lp.off), tuple(lp.len), tuple(lp.type), tuple(lp.cols), tuple(lp.rows), lp.total,
