@@ -498,6 +498,74 @@ def bench_disk(eng, args) -> int:
     return 0
 
 
+def bench_lmhead(eng, args) -> int:
+    """The LM head of a Q4_K_M 8B model (stream_infer.rs:2003-2019: execute_quant_gemv of
+    output.weight after the final norm): Q6_K, vocab 128256 x d_model 4096, batch 1, as x
+    digits + the Q6_K ring kernel.  Reported beside the f32 team kernel (ring off)."""
+    import hayai_amd
+    from hayai_amd import synth
+
+    T, M, N = hayai_amd.Q6_K, 128256, 4096
+    w = eng.alloc(M * (N // 256) * 210)
+    lo, hi = synth.SCALE_RANGE[T]
+    eng.synth_weights_dev(T, w, 0, M * N // 256, synth.seed_for(6, 0, synth.DOWN), lo, hi)
+    x = eng.upload(synth.normal(synth.seed_for(6, 0, synth.ACT), N))
+    y = eng.alloc(4 * M)
+
+    def timed(e, reps):
+        for _ in range(args.warmup):
+            e.gemv_dev(T, M, N, w, 0, x, 0, y, 0)
+        e.sync()
+        a, b = e.event(), e.event()
+        a.record()
+        for _ in range(reps):
+            e.gemv_dev(T, M, N, w, 0, x, 0, y, 0)
+        b.record()
+        e.sync()
+        return a.elapsed_ms(b) / reps
+
+    ms = timed(eng, args.steps)
+    nbytes = M * (N // 256) * 210 + 4 * N + 4 * M
+    gbs = nbytes / (ms / 1e3) / 1e9
+    os.environ["HAYAI_HIP_RING"] = "0"
+    plain = hayai_amd.HipEngine(0)
+    del os.environ["HAYAI_HIP_RING"]
+    wp, xp, yp = plain.alloc(w.nbytes), plain.upload(synth.normal(synth.seed_for(6, 0, synth.ACT), N)), plain.alloc(4 * M)
+    plain.synth_weights_dev(T, wp, 0, M * N // 256, synth.seed_for(6, 0, synth.DOWN), lo, hi)
+    for _ in range(args.warmup):
+        plain.gemv_dev(T, M, N, wp, 0, xp, 0, yp, 0)
+    plain.sync()
+    a, b = plain.event(), plain.event()
+    a.record()
+    for _ in range(args.steps):
+        plain.gemv_dev(T, M, N, wp, 0, xp, 0, yp, 0)
+    b.record()
+    plain.sync()
+    ms_plain = a.elapsed_ms(b) / args.steps
+    plain.close()
+    log(f"[bench] lm head q6_k {M}x{N}: {ms * 1e3:.1f} us ({gbs:.1f} GB/s); f32 team kernel {ms_plain * 1e3:.1f} us "
+        f"({nbytes / (ms_plain / 1e3) / 1e9:.1f} GB/s)")
+    out = {
+        "metric": "LM-head GEMV achieved HBM GB/s, Q6_K 128256x4096 (Llama-3 8B Q4_K_M output.weight) bs=1",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Q6_K blocks, N(0,1) f32 activations)",
+        "config": {"workload": "llama3-8b-lm-head-q6_k-bs1", "vocab": M, "d_model": N, "weights": "Q6_K"},
+        "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "team_kernel_us": round(ms_plain * 1e3, 2),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def bench_smollm(eng, args) -> int:
     """SmolLM2-135M-shaped SwiGLU FFN (d_model 576, d_ff 1536) in
     Q4_0, 30 layers, batch 1.  The 30-layer stack is 45 MB; 8 copies (360 MB, beyond the
@@ -713,13 +781,13 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 256 MiB device copy before timing (reference point for HBM counters)")
-    ap.add_argument("--workload", default="bs1", choices=["bs1", "batched", "moe", "stream", "smollm", "q4km", "block", "disk"],
+    ap.add_argument("--workload", default="bs1", choices=["bs1", "batched", "moe", "stream", "smollm", "q4km", "block", "disk", "lmhead"],
                     help="bs1: BASELINE.json configs[1] (the headline); batched: configs[2], --batch tokens per "
                          "step; moe: configs[3], --batch tokens per step; stream: configs[4] (70B IQ2_XXS "
                          "streamed from pinned host); smollm: configs[0]; q4km: the 8B FFN with a Q6_K down "
                          "projection (Q4_K_M layout); block: the 8B FFN residual block (RMSNorm + FFN + "
                          "residual) chained over 32 layers; disk: configs[4] read from a GGUF file through "
-                         "io_uring into the pinned slots")
+                         "io_uring into the pinned slots; lmhead: the 8B Q4_K_M LM head (Q6_K 128256x4096)")
     ap.add_argument("--disk-layers", type=int, default=8, help="distinct layers in the --workload disk file")
     ap.add_argument("--batch", type=int, default=16, help="tokens per step for --workload batched")
     args = ap.parse_args()
@@ -743,6 +811,8 @@ def main() -> int:
         return bench_q4km(eng, args)
     if args.workload == "disk":
         return bench_disk(eng, args)
+    if args.workload == "lmhead":
+        return bench_lmhead(eng, args)
     gate = hayai_amd.QuantMatrix("ffn_gate", D_MODEL, D_FF, Q4_K)
     up = hayai_amd.QuantMatrix("ffn_up", D_MODEL, D_FF, Q4_K)
     down = hayai_amd.QuantMatrix("ffn_down", D_FF, D_MODEL, Q4_K)

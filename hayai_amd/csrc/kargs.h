@@ -60,6 +60,14 @@ struct hh_norm_args {
     float eps;
 };
 
+// x (n f32) -> q1[n] | q2[n] int8 | scale[n/8] f32, the ring down kernels' digit form
+struct hh_xd_args {
+    const float* x;
+    uint8_t* hx;
+    uint32_t n;
+    uint32_t pad;
+};
+
 // y = a + b over n elements (the residual add)
 struct hh_add_args {
     const float* a;

@@ -228,3 +228,35 @@ HH_Q6K_DN_RING(1)
 HH_Q6K_DN_RING(2)
 HH_Q6K_DN_RING(4)
 HH_Q6K_DN_RING(8)
+
+// x -> digits for the ring GEMV (the same two-digit form the gate/up ring kernel writes for
+// h): per granule of 8, scale = max|x| / 127, d1 = rint(x / scale), d2 = rint((x - d1 scale)
+// * 256 / scale), both clamped to +-127.  One thread per granule.
+extern "C" __global__ void __launch_bounds__(256) hh_x_digits(const hh_xd_args a) {
+    const uint32_t g = blockIdx.x * 256 + threadIdx.x;
+    if (g >= a.n / 8) return;
+    float v[8];
+    float amax = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        v[k] = a.x[8 * g + k];
+        amax = fmaxf(amax, fabsf(v[k]));
+    }
+    const float scale = amax * (1.0f / 127.0f);
+    const float inv = amax > 0.f ? 127.0f / amax : 0.f;
+    uint32_t q1[2] = {0u, 0u}, q2[2] = {0u, 0u};
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float d1 = fminf(fmaxf(rintf(v[k] * inv), -127.f), 127.f);
+        const float r = v[k] - d1 * scale;
+        const float d2 = fminf(fmaxf(rintf(r * inv * 256.0f), -127.f), 127.f);
+        q1[k / 4] |= ((uint32_t)(int32_t)d1 & 0xFFu) << (8 * (k % 4));
+        q2[k / 4] |= ((uint32_t)(int32_t)d2 & 0xFFu) << (8 * (k % 4));
+    }
+    int8_t* hq1 = reinterpret_cast<int8_t*>(a.hx);
+    int8_t* hq2 = hq1 + a.n;
+    float* hsc = reinterpret_cast<float*>(hq2 + a.n);
+    *reinterpret_cast<uint2*>(hq1 + 8 * g) = make_uint2(q1[0], q1[1]);
+    *reinterpret_cast<uint2*>(hq2 + 8 * g) = make_uint2(q2[0], q2[1]);
+    hsc[g] = scale;
+}

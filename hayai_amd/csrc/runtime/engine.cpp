@@ -282,6 +282,10 @@ hh_status hh_engine::enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w
         hh_status st = enqueue_q4k(m, n, w, nullptr, x, y, 0, false, nullptr, nullptr);
         if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
     }
+    if (type == HH_TYPE_Q6_K) {
+        hh_status st = enqueue_q6k_ring_gemv(m, n, w, x, y);
+        if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
+    }
     std::string name;
     int team = 0, upl = 1;
     if ((type == HH_TYPE_F32 || type == HH_TYPE_F16) && (n % 32 != 0 || !aligned16)) {
@@ -554,33 +558,54 @@ hh_status hh_engine::enqueue_q4k_ring_gu(const hh_ffn_desc* d, const uint8_t* wg
 }
 
 hh_status hh_engine::enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd, float* y, const float* res) {
-    const size_t dm = d->d_model, df = d->d_ff;
+    return launch_dn_ring(d->type_down == HH_TYPE_Q6_K, d->d_model, d->d_ff, wd, (const uint8_t*)ws_hq, y, res);
+}
+
+// The ring down kernel over m rows of n columns (Q4_K or Q6_K) from digits `hx`.  Each
+// workgroup keeps the digits and its rows' lane partials in LDS: the grid is at least one
+// workgroup per CU and large enough that every workgroup's rows fit.
+hh_status hh_engine::launch_dn_ring(bool q6, size_t m, size_t n, const uint8_t* w, const uint8_t* hx, float* y,
+                                    const float* res) {
     int w2 = 1;
-    while ((size_t)w2 * 64 < df / 64) w2 *= 2;
-    const bool q6 = d->type_down == HH_TYPE_Q6_K;
+    while ((size_t)w2 * 64 < n / 64) w2 *= 2;
     const std::string name = std::string(q6 ? "hh_q6k_dn_ring_d" : "hh_q4k_dn_ring_d") + std::to_string(w2);
     hipFunction_t fn;
     HH_TRY(kernel(name, &fn));
     const int block = 9 * 64;  // 8 compute waves + the wave that copies the intermediate
-    int occ = 0;
     const size_t cus = (size_t)props.multiProcessorCount;
-    // LDS: the intermediate + lane partials (rows x 64*w2), sized for the smallest grid
-    const size_t rows_max = (dm + cus - 1) / cus;
-    const size_t smem = (((2 * df + (df / 8) * 4) + 15) & ~size_t(15)) + rows_max * (size_t)w2 * 64 * 4;
-    if (smem > props.sharedMemPerBlock) return HH_ERR_UNSUPPORTED_DEVICE;
+    const size_t lds = (size_t)props.sharedMemPerBlock;
+    const size_t hb = ((2 * n + (n / 8) * 4) + 15) & ~size_t(15), per_row = (size_t)w2 * 64 * 4;
+    if (hb + per_row > lds) return HH_ERR_UNSUPPORTED_DEVICE;
+    const size_t rows_fit = (lds - hb) / per_row;
+    int occ = 0;
     auto it = blocks_per_cu.find(name);
     if (it != blocks_per_cu.end()) {
         occ = it->second;
     } else {
-        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, block, smem) != hipSuccess) occ = 1;
+        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, block, hb + per_row) != hipSuccess) occ = 1;
         blocks_per_cu[name] = occ;
     }
-    const size_t grid = ring_grid(occ, ring_dn_per_cu, cus);
-    DnrArgs a{wd, (const uint8_t*)ws_hq, y, res, (uint64_t)((df / 256) * (q6 ? 210 : 144)), (uint32_t)dm, (uint32_t)df};
+    const size_t grid = std::max(ring_grid(occ, ring_dn_per_cu, cus), (m + rows_fit - 1) / rows_fit);
+    const size_t rows_max = (m + grid - 1) / grid;
+    const size_t smem = hb + rows_max * per_row;
+    DnrArgs a{w, hx, y, res, (uint64_t)((n / 256) * (q6 ? 210 : 144)), (uint32_t)m, (uint32_t)n};
     void* params[] = {&a};
     hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
-    if (err != hipSuccess) return hip_fail(err, "launch(ring q4k down)");
+    if (err != hipSuccess) return hip_fail(err, "launch(ring down)");
     return HH_OK;
+}
+
+// x -> the ring down kernels' digit form (q1 | q2 | one scale per 8), then the Q6_K ring
+// kernel as a GEMV: the LM head of Q4_K_M files (output.weight in Q6_K).
+hh_status hh_engine::enqueue_q6k_ring_gemv(size_t m, size_t n, const uint8_t* w, const float* x, float* y) {
+    if (!ring || n % 512 || n > 32768 || m > UINT32_MAX / 2 || (((uintptr_t)w | (uintptr_t)x) & 15u))
+        return HH_ERR_UNSUPPORTED_DEVICE;
+    HH_TRY(grow(&ws_xq, &ws_xq_cap, 2 * n + (n / 8) * 4 + 16));
+    hipFunction_t fn;
+    HH_TRY(kernel("hh_x_digits", &fn));
+    hh_xd_args xa{x, (uint8_t*)ws_xq, (uint32_t)n, 0u};
+    HH_TRY(launch(fn, (uint32_t)((n / 8 + 255) / 256), 256, xa));
+    return launch_dn_ring(true, m, n, w, (const uint8_t*)ws_xq, y, nullptr);
 }
 
 hh_status hh_engine::check_device_error() {
@@ -1128,6 +1153,7 @@ static std::vector<std::string> required_kernels() {
         k.push_back(std::string("hh_moe_") + f);
     k.push_back("hh_moe_route");
     k.push_back("hh_rmsnorm_kernel");
+    k.push_back("hh_x_digits");
     k.push_back("hh_add_kernel");
     for (int t : {16, 32, 64})
         for (const char* kind : {"hh_moe_gateup_t", "hh_moe_down_t"}) k.push_back(std::string(kind) + std::to_string(t));
@@ -1193,7 +1219,7 @@ void engine_destroy(hh_engine* e) {
     if (e->stream) (void)hipStreamSynchronize(e->stream);
     if (e->copy_stream) (void)hipStreamSynchronize(e->copy_stream);
     for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq, e->ws_xop, e->ws_hop, e->ws_part,
-                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->ws_xn, e->ws_f, e->grid_sync})
+                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->ws_xn, e->ws_f, e->ws_xq, e->grid_sync})
         if (p) (void)hipFree(p);
     if (e->stream) (void)hipStreamDestroy(e->stream);
     if (e->copy_stream) (void)hipStreamDestroy(e->copy_stream);

@@ -106,6 +106,8 @@ struct hh_engine {
     size_t ws_xn_cap = 0;
     void* ws_f = nullptr;
     size_t ws_f_cap = 0;
+    void* ws_xq = nullptr;  // GEMV activations as ring digits (Q6_K ring GEMV)
+    size_t ws_xq_cap = 0;
     // Batched (MFMA) path: tokens as MFMA operand stages (f16 hi/lo pairs + 16-element
     // sums), the FFN intermediate in the same form, split-K partials and their per-row-group
     // arrival counters.
@@ -186,6 +188,9 @@ struct hh_engine {
     hh_status enqueue_q4k_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const float* x,
                                   const float* norm = nullptr, float eps = 0.f);
     hh_status enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd, float* y, const float* res = nullptr);
+    hh_status launch_dn_ring(bool q6, size_t m, size_t n, const uint8_t* w, const uint8_t* hx, float* y,
+                             const float* res);
+    hh_status enqueue_q6k_ring_gemv(size_t m, size_t n, const uint8_t* w, const float* x, float* y);
     hh_status enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                                const float* x, float* y);
     // Batched GEMV Y[b][m] = W . X[b] (x, y device pointers, row-major by token).  Q4_K with

@@ -272,3 +272,33 @@ def test_gemv_full_size_properties(engine):
     y2 = engine.ggml_gemv_dispatch_bound(t, m, n, wb, 0, x2)
     y12 = engine.ggml_gemv_dispatch_bound(t, m, n, wb, 0, (a * x1 + b * x2).astype(np.float32))
     assert rel_err(y12, a * y1.astype(np.float64) + b * y2.astype(np.float64)) <= 2e-4
+
+
+@pytest.mark.parametrize("m,n", [(128256, 4096), (32000, 4096), (1000, 8192)])
+def test_q6_k_lm_head_ring_gemv(engine, m, n):
+    # The LM head of Q4_K_M files (output.weight, vocab x d_model in Q6_K) runs as x digits +
+    # the Q6_K ring kernel; against the oracle and against the f32 team kernel (ring off).
+    import os
+    say(f"q6_k lm head m={m} n={n}")
+    oracle.set_threads(min(16, oracle.max_threads()))
+    t = hayai_amd.Q6_K
+    w = synth.matrix(t, m, n, seed=synth.seed_for(t, m, n))
+    x = synth.normal(m + n, n)
+    got = engine.ggml_gemv_dispatch(t, m, n, w, x)
+    ref = oracle.gemv(t, m, n, w, x)
+    assert rel_err(got, ref) <= REL_TOL, rel_err(got, ref)
+    old = os.environ.get("HAYAI_HIP_RING")
+    os.environ["HAYAI_HIP_RING"] = "0"
+    try:
+        plain = hayai_amd.HipEngine(0)
+    finally:
+        if old is None:
+            del os.environ["HAYAI_HIP_RING"]
+        else:
+            os.environ["HAYAI_HIP_RING"] = old
+    try:
+        got2 = plain.ggml_gemv_dispatch(t, m, n, w, x)
+    finally:
+        plain.close()
+    assert rel_err(got2, ref) <= REL_TOL
+    say(f"  rel_err ring {rel_err(got, ref):.2e}, team kernel {rel_err(got2, ref):.2e}")
