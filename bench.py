@@ -505,8 +505,9 @@ def bench_lmhead(eng, args) -> int:
     import hayai_amd
     from hayai_amd import synth
 
-    T, M, N = hayai_amd.Q6_K, 128256, 4096
-    w = eng.alloc(M * (N // 256) * 210)
+    T, M, N = (hayai_amd.Q4_K if args.lm_type == "q4_k" else hayai_amd.Q6_K), 128256, 4096
+    bb = 144 if T == hayai_amd.Q4_K else 210
+    w = eng.alloc(M * (N // 256) * bb)
     lo, hi = synth.SCALE_RANGE[T]
     eng.synth_weights_dev(T, w, 0, M * N // 256, synth.seed_for(6, 0, synth.DOWN), lo, hi)
     x = eng.upload(synth.normal(synth.seed_for(6, 0, synth.ACT), N))
@@ -525,7 +526,7 @@ def bench_lmhead(eng, args) -> int:
         return a.elapsed_ms(b) / reps
 
     ms = timed(eng, args.steps)
-    nbytes = M * (N // 256) * 210 + 4 * N + 4 * M
+    nbytes = M * (N // 256) * bb + 4 * N + 4 * M
     gbs = nbytes / (ms / 1e3) / 1e9
     os.environ["HAYAI_HIP_RING"] = "0"
     plain = hayai_amd.HipEngine(0)
@@ -543,7 +544,7 @@ def bench_lmhead(eng, args) -> int:
     plain.sync()
     ms_plain = a.elapsed_ms(b) / args.steps
     plain.close()
-    log(f"[bench] lm head q6_k {M}x{N}: {ms * 1e3:.1f} us ({gbs:.1f} GB/s); f32 team kernel {ms_plain * 1e3:.1f} us "
+    log(f"[bench] lm head {args.lm_type} {M}x{N}: {ms * 1e3:.1f} us ({gbs:.1f} GB/s); ring off {ms_plain * 1e3:.1f} us "
         f"({nbytes / (ms_plain / 1e3) / 1e9:.1f} GB/s)")
     out = {
         "metric": "LM-head GEMV achieved HBM GB/s, Q6_K 128256x4096 (Llama-3 8B Q4_K_M output.weight) bs=1",
@@ -789,6 +790,7 @@ def main() -> int:
                          "residual) chained over 32 layers; disk: configs[4] read from a GGUF file through "
                          "io_uring into the pinned slots; lmhead: the 8B Q4_K_M LM head (Q6_K 128256x4096)")
     ap.add_argument("--disk-layers", type=int, default=8, help="distinct layers in the --workload disk file")
+    ap.add_argument("--lm-type", default="q6_k", choices=["q6_k", "q4_k"], help="--workload lmhead weight format")
     ap.add_argument("--batch", type=int, default=16, help="tokens per step for --workload batched")
     args = ap.parse_args()
     if args.gpus != 1:

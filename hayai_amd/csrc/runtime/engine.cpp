@@ -283,7 +283,7 @@ hh_status hh_engine::enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w
         if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
     }
     if (type == HH_TYPE_Q6_K) {
-        hh_status st = enqueue_q6k_ring_gemv(m, n, w, x, y);
+        hh_status st = enqueue_ring_gemv(true, m, n, w, x, y);
         if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
     }
     std::string name;
@@ -597,15 +597,15 @@ hh_status hh_engine::launch_dn_ring(bool q6, size_t m, size_t n, const uint8_t* 
 
 // x -> the ring down kernels' digit form (q1 | q2 | one scale per 8), then the Q6_K ring
 // kernel as a GEMV: the LM head of Q4_K_M files (output.weight in Q6_K).
-hh_status hh_engine::enqueue_q6k_ring_gemv(size_t m, size_t n, const uint8_t* w, const float* x, float* y) {
-    if (!ring || n % 512 || n > 32768 || m > UINT32_MAX / 2 || (((uintptr_t)w | (uintptr_t)x) & 15u))
+hh_status hh_engine::enqueue_ring_gemv(bool q6, size_t m, size_t n, const uint8_t* w, const float* x, float* y) {
+    if (!ring || n % (q6 ? 512 : 256) || n > 32768 || m > UINT32_MAX / 2 || (((uintptr_t)w | (uintptr_t)x) & 15u))
         return HH_ERR_UNSUPPORTED_DEVICE;
     HH_TRY(grow(&ws_xq, &ws_xq_cap, 2 * n + (n / 8) * 4 + 16));
     hipFunction_t fn;
     HH_TRY(kernel("hh_x_digits", &fn));
     hh_xd_args xa{x, (uint8_t*)ws_xq, (uint32_t)n, 0u};
     HH_TRY(launch(fn, (uint32_t)((n / 8 + 255) / 256), 256, xa));
-    return launch_dn_ring(true, m, n, w, (const uint8_t*)ws_xq, y, nullptr);
+    return launch_dn_ring(q6, m, n, w, (const uint8_t*)ws_xq, y, nullptr);
 }
 
 hh_status hh_engine::check_device_error() {

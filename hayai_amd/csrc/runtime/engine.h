@@ -190,7 +190,7 @@ struct hh_engine {
     hh_status enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd, float* y, const float* res = nullptr);
     hh_status launch_dn_ring(bool q6, size_t m, size_t n, const uint8_t* w, const uint8_t* hx, float* y,
                              const float* res);
-    hh_status enqueue_q6k_ring_gemv(size_t m, size_t n, const uint8_t* w, const float* x, float* y);
+    hh_status enqueue_ring_gemv(bool q6, size_t m, size_t n, const uint8_t* w, const float* x, float* y);
     hh_status enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                                const float* x, float* y);
     // Batched GEMV Y[b][m] = W . X[b] (x, y device pointers, row-major by token).  Q4_K with
