@@ -1,0 +1,205 @@
+// The MoE expert FFN for several tokens as a grouped gather-GEMV (gfx950): every selected
+// expert's weights are read once per call for all the tokens routed to it, instead of once
+// per (token, expert) pair.  Same results as the expert loop + combine of
+// crates/hayai-core/src/moe_infer.rs:342-455 (y[t] = sum over slots s of
+// w[t][s] * down_e(act(gate_e x_t) * up_e x_t), e = ids[t][s]):
+//   hh_moe_prep:         (token, slot) pairs p = t * k + s grouped by expert, in p order
+//                        within an expert, the active experts in ascending order; and every
+//                        token's x as int8 digits
+//   hh_moe_gu_grp_t<TM>: grid.y = active expert; every row of gate and up is read once and
+//                        dotted with each of the expert's tokens: h[p][row] = act(g) * u
+//   hh_moe_hdigits:      h as digits, by pair
+//   hh_moe_dn_grp_t<TM>: grid.y = active expert; every down row read once: yp[p][row]
+//   hh_moe_combine:      y[t][row] = sum over valid slots, in slot order, of w[t][s] * yp[t*k+s][row]
+// (Compiled after moe.hip in the same translation unit: hh_moe_digits and the Q4_K digit dot
+// products of q4k.hip.)
+
+struct hh_moeg_args {
+    const uint8_t* experts;  // expert packs, expert e at e * expert_stride
+    uint64_t expert_stride;
+    uint64_t gate_off, up_off, down_off;
+    uint64_t rb_in, rb_ff;   // row bytes of gate/up (d_model columns) and down (d_ff columns)
+    const int32_t* ids;      // [T][k]
+    const float* wts;        // [T][k]
+    const float* x;          // [T][d_model]
+    float* h;                // [T * k][d_ff], by pair
+    float* yp;               // [T * k][d_model], by pair
+    float* y;                // [T][d_model]
+    int32_t* order;          // [T * k] pairs grouped by expert
+    int32_t* estart;         // [E + 1] first position of each expert in order
+    int32_t* elist;          // [E + 1] active experts ascending; elist[E] = their count
+    uint8_t* xq;             // [T] digit forms of x (hh_moe_digits layout, d_model elements)
+    uint8_t* hq;             // [T * k] digit forms of h (d_ff elements)
+    uint32_t T, k, d_model, d_ff, n_experts;
+    int32_t act;
+};
+
+#define HH_MOEG_MAX_E 512     // experts the grouping kernel handles
+#define HH_MOEG_MAX_P 4096    // (token, slot) pairs
+#define HH_MOEG_GU_RPT 2      // rows per team, loads issued together (gate/up: 2 matrices)
+#define HH_MOEG_DN_RPT 4
+
+// bytes of the digit form of n elements (q1, q2, scale and sum per 32), as hh_moe_digits lays
+// it out; a multiple of 16 for n % 64 == 0
+HH_DEV size_t hh_digits_bytes_dev(uint32_t n) { return 2u * (size_t)n + (size_t)(n / 32u) * 8u; }
+
+// Sum over a team of TEAM (16, 32, 64) lanes by DPP row operations; the total is valid in
+// the team's last lane (TEAM - 1).
+template <int TEAM>
+HH_DEV float hh_moeg_team_sum(float v) {
+    v += hh_dpp<0xB1>(v);  // quad_perm [1,0,3,2]
+    v += hh_dpp<0x4E>(v);  // quad_perm [2,3,0,1]
+    v += hh_dpp<0x124>(v);  // row_ror:4
+    v += hh_dpp<0x128>(v);  // row_ror:8 -> every lane of a row of 16 holds its sum
+    if constexpr (TEAM >= 32) v += hh_dpp<0x142, 0xA>(v);  // row_bcast:15 -> rows 1, 3 hold 32-lane sums
+    if constexpr (TEAM >= 64) v += hh_dpp<0x143, 0xC>(v);  // row_bcast:31 -> lane 63 holds the total
+    return v;
+}
+
+HH_DEV int hh_moeg_valid(const hh_moeg_args& a, int e) { return (e < 0 || (uint32_t)e >= a.n_experts) ? -1 : e; }
+
+// Workgroup 0 groups the pairs; workgroup 1 + t turns token t's x into digits (global, read
+// by every expert's gate/up workgroups from L2).  Grouping: pair p's position is its expert's
+// start plus the number of earlier pairs with the same expert; an expert's start is the sum
+// of the counts of the experts before it; all sums are over LDS copies, one thread per pair or
+// expert, so the order is deterministic.
+extern "C" __global__ void __launch_bounds__(256) hh_moe_prep(const hh_moeg_args a) {
+    __shared__ int cnt[HH_MOEG_MAX_E];
+    __shared__ int first[HH_MOEG_MAX_E];
+    __shared__ int pid[HH_MOEG_MAX_P];
+    const uint32_t tid = threadIdx.x;
+    if (blockIdx.x > 0) {
+        const uint32_t t = blockIdx.x - 1;
+        hh_quantize_digits(a.x + (size_t)t * a.d_model, a.d_model,
+                           hh_moe_digits((char*)a.xq + t * hh_digits_bytes_dev(a.d_model), a.d_model));
+        return;
+    }
+    const uint32_t E = a.n_experts, P = a.T * a.k;
+    for (uint32_t e = tid; e < E; e += 256) cnt[e] = 0;
+    for (uint32_t p = tid; p < P; p += 256) pid[p] = hh_moeg_valid(a, a.ids[p]);
+    __syncthreads();
+    for (uint32_t p = tid; p < P; p += 256)
+        if (pid[p] >= 0) atomicAdd(&cnt[pid[p]], 1);  // counts only: order-free
+    __syncthreads();
+    for (uint32_t e = tid; e < E; e += 256) {
+        int s = 0, na = 0;
+        for (uint32_t f = 0; f < e; f++) {
+            s += cnt[f];
+            na += cnt[f] > 0;
+        }
+        first[e] = s;
+        a.estart[e] = s;
+        if (cnt[e]) a.elist[na] = (int)e;
+        if (e == E - 1) {
+            a.estart[E] = s + cnt[e];
+            a.elist[E] = na + (cnt[e] > 0);
+        }
+    }
+    __syncthreads();
+    for (uint32_t p = tid; p < P; p += 256) {
+        const int e = pid[p];
+        if (e < 0) continue;
+        int r = 0;
+        for (uint32_t q = 0; q < p; q++) r += pid[q] == e;
+        a.order[first[e] + r] = (int)p;
+    }
+}
+
+// h (f32, by pair) -> digits, one workgroup per pair.
+extern "C" __global__ void __launch_bounds__(256) hh_moe_hdigits(const hh_moeg_args a) {
+    const uint32_t p = blockIdx.x;
+    if (hh_moeg_valid(a, a.ids[p]) < 0) return;
+    hh_quantize_digits(a.h + (size_t)p * a.d_ff, a.d_ff,
+                       hh_moe_digits((char*)a.hq + p * hh_digits_bytes_dev(a.d_ff), a.d_ff));
+}
+
+// Gate/up: a team of TEAM lanes per row (lane = 64-column unit, d_model <= 64 * TEAM); each
+// team takes HH_MOEG_GU_RPT rows with all their loads in flight, then dots them with every token
+// of the expert (the lane's slice of the token's digits, from L2).
+template <int TEAM>
+HH_DEV void hh_moe_gu_grp_body(const hh_moeg_args& a) {
+    const int na = a.elist[a.n_experts];
+    if ((int)blockIdx.y >= na) return;  // grid.y covers the most experts a call can select
+    const int e = a.elist[blockIdx.y];
+    const int p0 = a.estart[e], np = a.estart[e + 1] - p0;
+    const uint32_t dm = a.d_model, df = a.d_ff, P = dm / 64;
+    const size_t xbytes = hh_digits_bytes_dev(dm);
+    constexpr uint32_t TPB = 256 / TEAM;
+    const uint32_t l = threadIdx.x % TEAM, team = threadIdx.x / TEAM;
+    const uint32_t rows_per_block = TPB * HH_MOEG_GU_RPT;
+    const uint32_t j0 = blockIdx.x * rows_per_block + team * HH_MOEG_GU_RPT;
+    const uint8_t* pack = a.experts + (size_t)e * a.expert_stride;
+    const bool act = l < P;
+    const uint32_t u = act ? l : 0u;
+    hh_q4k_data g[HH_MOEG_GU_RPT], up[HH_MOEG_GU_RPT];
+#pragma unroll
+    for (int r = 0; r < HH_MOEG_GU_RPT; r++) {
+        const uint32_t j = min(j0 + r, df - 1);
+        hh_q4k_load(pack + a.gate_off + (size_t)j * a.rb_in, u, g[r]);
+        hh_q4k_load(pack + a.up_off + (size_t)j * a.rb_in, u, up[r]);
+    }
+    for (int i = 0; i < np; i++) {
+        const uint32_t p = (uint32_t)a.order[p0 + i], t = p / a.k;
+        hh_q4k_x xr;
+        hh_q4k_load_lane_x(hh_moe_digits((char*)a.xq + t * xbytes, dm), u, xr);
+#pragma unroll
+        for (int r = 0; r < HH_MOEG_GU_RPT; r++) {
+            const float gv = hh_moeg_team_sum<TEAM>(act ? hh_q4k_unit(g[r], xr) : 0.f);
+            const float uv = hh_moeg_team_sum<TEAM>(act ? hh_q4k_unit(up[r], xr) : 0.f);
+            if (l == TEAM - 1 && j0 + r < df) a.h[(size_t)p * df + j0 + r] = hh_act_mul(gv, uv, a.act);
+        }
+    }
+}
+
+// Down: the same with the expert's pairs' h (d_ff columns) and d_model rows -> yp[p][row].
+template <int TEAM>
+HH_DEV void hh_moe_dn_grp_body(const hh_moeg_args& a) {
+    const int na = a.elist[a.n_experts];
+    if ((int)blockIdx.y >= na) return;
+    const int e = a.elist[blockIdx.y];
+    const int p0 = a.estart[e], np = a.estart[e + 1] - p0;
+    const uint32_t dm = a.d_model, df = a.d_ff, P = df / 64;
+    const size_t hbytes = hh_digits_bytes_dev(df);
+    constexpr uint32_t TPB = 256 / TEAM;
+    const uint32_t l = threadIdx.x % TEAM, team = threadIdx.x / TEAM;
+    const uint32_t rows_per_block = TPB * HH_MOEG_DN_RPT;
+    const uint32_t j0 = blockIdx.x * rows_per_block + team * HH_MOEG_DN_RPT;
+    const uint8_t* pack = a.experts + (size_t)e * a.expert_stride;
+    const bool act = l < P;
+    const uint32_t u = act ? l : 0u;
+    hh_q4k_data w[HH_MOEG_DN_RPT];
+#pragma unroll
+    for (int r = 0; r < HH_MOEG_DN_RPT; r++) hh_q4k_load(pack + a.down_off + (size_t)min(j0 + r, dm - 1) * a.rb_ff, u, w[r]);
+    for (int i = 0; i < np; i++) {
+        const uint32_t p = (uint32_t)a.order[p0 + i];
+        hh_q4k_x hr;
+        hh_q4k_load_lane_x(hh_moe_digits((char*)a.hq + p * hbytes, df), u, hr);
+#pragma unroll
+        for (int r = 0; r < HH_MOEG_DN_RPT; r++) {
+            const float d = hh_moeg_team_sum<TEAM>(act ? hh_q4k_unit(w[r], hr) : 0.f);
+            if (l == TEAM - 1 && j0 + r < dm) a.yp[(size_t)p * dm + j0 + r] = d;
+        }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) hh_moe_combine(const hh_moeg_args a) {
+    const uint32_t j = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
+    if (j >= a.d_model) return;
+    float acc = 0.f;
+    for (uint32_t s = 0; s < a.k; s++) {
+        const uint32_t p = t * a.k + s;
+        if (hh_moeg_valid(a, a.ids[p]) >= 0) acc += a.wts[p] * a.yp[(size_t)p * a.d_model + j];
+    }
+    a.y[(size_t)t * a.d_model + j] = acc;
+}
+
+#define HH_MOEG_KERNELS(TEAM)                                                                          \
+    extern "C" __global__ void __launch_bounds__(256) hh_moe_gu_grp_t##TEAM(const hh_moeg_args a) {     \
+        hh_moe_gu_grp_body<TEAM>(a);                                                                   \
+    }                                                                                                  \
+    extern "C" __global__ void __launch_bounds__(256) hh_moe_dn_grp_t##TEAM(const hh_moeg_args a) {     \
+        hh_moe_dn_grp_body<TEAM>(a);                                                                   \
+    }
+HH_MOEG_KERNELS(16)
+HH_MOEG_KERNELS(32)
+HH_MOEG_KERNELS(64)

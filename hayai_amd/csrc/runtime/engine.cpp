@@ -1009,6 +1009,7 @@ struct hh_moe_args {
 };
 constexpr int kMoeBlock = 256;
 constexpr size_t kMoeDownRows = 4;  // output rows per down workgroup (moe.hip)
+constexpr size_t kMoegGuRows = 2, kMoegDnRows = 4;  // grouped MoE rows per team (HH_MOEG_*_RPT, moe_group.hip)
 
 static int moe_team(size_t units) { return units <= 16 ? 16 : (units <= 32 ? 32 : 64); }
 
@@ -1090,6 +1091,64 @@ hh_status hh_engine::enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* expert
         ffn_calls += 3;
         return HH_OK;
     }
+    // Several tokens: the grouped gather-GEMV (moe_group.hip), every selected expert read once.
+    const size_t P = T * k, E = d->n_experts;
+    if (moe_grouped && P <= 4096 && E <= 512 && dm / 64 <= 64 && df / 64 <= 64 &&
+        ((d->expert_stride | d->gate_off | d->up_off | d->down_off | (uintptr_t)experts | (uintptr_t)x) & 15u) == 0) {
+        if (logits) HH_TRY(enqueue_moe_route(d, logits, bias, T, ids, wts));
+        HH_TRY(grow(&ws_moe_yp, &ws_moe_yp_cap, P * dm * sizeof(float)));
+        HH_TRY(grow(&ws_moe_grp, &ws_moe_grp_cap, (P + 2 * (E + 1)) * sizeof(int32_t)));
+        const size_t xqb = hh_digits_bytes(dm), hqb = hh_digits_bytes(df);
+        HH_TRY(grow(&ws_moe_q, &ws_moe_q_cap, T * xqb + P * hqb));
+        struct {
+            const uint8_t* experts;
+            uint64_t expert_stride, gate_off, up_off, down_off, rb_in, rb_ff;
+            const int32_t* ids;
+            const float* wts;
+            const float* x;
+            float *h, *yp, *y;
+            int32_t *order, *estart, *elist;
+            uint8_t *xq, *hq;
+            uint32_t T, k, d_model, d_ff, n_experts;
+            int32_t act;
+        } g{experts, d->expert_stride, d->gate_off, d->up_off, d->down_off, a.rb_in, a.rb_ff, ids, wts, x,
+            (float*)ws_moe_h, (float*)ws_moe_yp, y, (int32_t*)ws_moe_grp, (int32_t*)ws_moe_grp + P,
+            (int32_t*)ws_moe_grp + P + E + 1, (uint8_t*)ws_moe_q, (uint8_t*)ws_moe_q + T * xqb, (uint32_t)T,
+            (uint32_t)k, (uint32_t)dm, (uint32_t)df, (uint32_t)E, d->act};
+        hipFunction_t fn;
+        HH_TRY(kernel("hh_moe_prep", &fn));
+        HH_TRY(launch(fn, (uint32_t)(1 + T), 256, g));
+        const uint32_t gy = (uint32_t)std::min(E, P);
+        {
+            const int team = moe_team(dm / 64);
+            const size_t rows = (size_t)(kMoeBlock / team) * kMoegGuRows;
+            HH_TRY(kernel("hh_moe_gu_grp_t" + std::to_string(team), &fn));
+            void* gp[] = {&g};
+            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)((df + rows - 1) / rows), gy, 1, kMoeBlock, 1, 1, 0, stream,
+                                             gp, nullptr),
+                       "launch(moe grouped gate/up)");
+        }
+        HH_TRY(kernel("hh_moe_hdigits", &fn));
+        HH_TRY(launch(fn, (uint32_t)P, 256, g));
+        {
+            const int team = moe_team(df / 64);
+            const size_t rows = (size_t)(kMoeBlock / team) * kMoegDnRows;
+            HH_TRY(kernel("hh_moe_dn_grp_t" + std::to_string(team), &fn));
+            void* gp[] = {&g};
+            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)((dm + rows - 1) / rows), gy, 1, kMoeBlock, 1, 1, 0, stream,
+                                             gp, nullptr),
+                       "launch(moe grouped down)");
+        }
+        HH_TRY(kernel("hh_moe_combine", &fn));
+        {
+            void* gp[] = {&g};
+            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)((dm + 255) / 256), (uint32_t)T, 1, 256, 1, 1, 0, stream, gp,
+                                             nullptr),
+                       "launch(moe combine)");
+        }
+        ffn_calls += 3 * T;
+        return HH_OK;
+    }
     const size_t cap = std::max<size_t>(1, ((size_t)props.multiProcessorCount * 2 + T - 1) / T);
     void* params[] = {&a};
     {
@@ -1152,6 +1211,9 @@ static std::vector<std::string> required_kernels() {
                           "dn_ring_d8"})
         k.push_back(std::string("hh_moe_") + f);
     k.push_back("hh_moe_route");
+    for (const char* f : {"hh_moe_prep", "hh_moe_hdigits", "hh_moe_combine", "hh_moe_gu_grp_t16", "hh_moe_gu_grp_t32", "hh_moe_gu_grp_t64",
+                          "hh_moe_dn_grp_t16", "hh_moe_dn_grp_t32", "hh_moe_dn_grp_t64"})
+        k.push_back(f);
     k.push_back("hh_rmsnorm_kernel");
     k.push_back("hh_x_digits");
     k.push_back("hh_add_kernel");
@@ -1201,6 +1263,7 @@ hh_status engine_create(int device, hh_engine** out) {
     if (const char* f = getenv("HAYAI_HIP_FFN_FUSED")) e->ffn_fused = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_FFNP")) e->ffnp = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_RING")) e->ring = atoi(f) != 0;
+    if (const char* f = getenv("HAYAI_HIP_MOE_GROUPED")) e->moe_grouped = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_RING_GU_PER_CU")) e->ring_gu_per_cu = std::max(1, atoi(f));
     if (const char* f = getenv("HAYAI_HIP_RING_DN_PER_CU")) e->ring_dn_per_cu = std::max(1, atoi(f));
     if (const char* f = getenv("HAYAI_HIP_MMR")) e->mmr = atoi(f) != 0;
@@ -1219,7 +1282,7 @@ void engine_destroy(hh_engine* e) {
     if (e->stream) (void)hipStreamSynchronize(e->stream);
     if (e->copy_stream) (void)hipStreamSynchronize(e->copy_stream);
     for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq, e->ws_xop, e->ws_hop, e->ws_part,
-                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->ws_xn, e->ws_f, e->ws_xq, e->grid_sync})
+                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->ws_xn, e->ws_f, e->ws_xq, e->ws_moe_yp, e->ws_moe_grp, e->ws_moe_q, e->grid_sync})
         if (p) (void)hipFree(p);
     if (e->stream) (void)hipStreamDestroy(e->stream);
     if (e->copy_stream) (void)hipStreamDestroy(e->copy_stream);

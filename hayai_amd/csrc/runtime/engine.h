@@ -128,6 +128,12 @@ struct hh_engine {
     size_t ws_moe_ids_cap = 0;
     void* ws_moe_w = nullptr;
     size_t ws_moe_w_cap = 0;
+    void* ws_moe_yp = nullptr;   // grouped MoE: per-pair down outputs [T*k][d_model]
+    size_t ws_moe_yp_cap = 0;
+    void* ws_moe_grp = nullptr;  // grouped MoE: pair order, expert starts, active experts
+    size_t ws_moe_grp_cap = 0;
+    void* ws_moe_q = nullptr;    // grouped MoE: x digits per token, h digits per pair
+    size_t ws_moe_q_cap = 0;
     void* grid_sync = nullptr;  // fused FFN grid-barrier state (counters, flags, error word)
     uint32_t ffn_gen = 0;       // generation of the last fused FFN launch
     hh_ffn_desc ffn_stage{};    // FFN whose gate/up output is pending in ws_h (/ws_hq)
@@ -137,6 +143,7 @@ struct hh_engine {
     bool ffn_fused = false;     // HAYAI_HIP_FFN_FUSED=1: one-launch Q4_K FFN (grid barrier)
     bool ffnp = true;           // HAYAI_HIP_FFNP=0: skip the persistent pipelined Q4_K FFN
     bool ring = true;           // HAYAI_HIP_RING=0: skip the two-launch ring Q4_K FFN
+    bool moe_grouped = true;    // HAYAI_HIP_MOE_GROUPED=0: several-token MoE per (token, expert)
     int ring_gu_per_cu = 1;     // HAYAI_HIP_RING_GU_PER_CU: ring gate/up workgroups per CU
     int ring_dn_per_cu = 1;     // HAYAI_HIP_RING_DN_PER_CU: ring down workgroups per CU
     bool mmr = true;            // HAYAI_HIP_MMR=0: batched Q4_K (<= 16 tokens) on the q4k_mm kernels

@@ -101,6 +101,8 @@ def make_experts(engine, E, d_model, d_ff, seed):
     (16, 4, 1024, 512, 1),     # one token, 4 gate/up rows per wave item
     (8, 2, 4096, 1024, 3),     # wider rows: 64-lane teams, several units per lane on down
     (16, 4, 1024, 512, 2),
+    (128, 8, 2048, 768, 32),   # config 4 at 32 tokens: the grouped gather-GEMV
+    (4, 2, 1024, 512, 40),     # ~20 tokens per expert: several LDS passes per expert
 ])
 def test_moe_ffn_matches_oracle(engine, E, k, d_model, d_ff, T):
     oracle.set_threads(min(16, oracle.max_threads()))
@@ -159,3 +161,47 @@ def test_moe_rejects_bad_descriptors(engine):
     for d in bad:
         with pytest.raises(hayai_amd.HipError):
             engine.moe_dev(d, buf, 0, lb, 0, None, 0, xb, 0, 1, y, 0)
+
+
+def test_moe_grouped_matches_per_token_path_and_skips_empty_slots(engine):
+    # Several tokens with some empty slots (id -1, or out of range): the grouped kernels give
+    # the per-(token, expert) kernels' result within tolerance and ignore the empty slots.
+    import os
+    E, k, d_model, d_ff, T = 16, 4, 2048, 768, 6
+    print(f"[case] moe grouped vs per-token E={E} k={k} T={T}", flush=True)
+    buf, host, stride, offs = make_experts(engine, E, d_model, d_ff, 91)
+    d = engine.moe_desc(d_model, d_ff, E, k, stride, offs)
+    rng = np.random.default_rng(11)
+    ids = rng.integers(0, E, (T, k)).astype(np.int32)
+    for t in range(T):  # distinct experts per token, as routing gives
+        ids[t] = rng.permutation(E)[:k]
+    ids[1, 2] = -1
+    ids[4, 0] = E + 3
+    w = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
+    x = synth.normal(17, T * d_model).reshape(T, d_model)
+    xb, ib, wb, y1 = engine.upload(x), engine.upload(ids), engine.upload(w), engine.alloc(4 * T * d_model)
+    engine.moe_ffn_dev(d, buf, 0, xb, 0, T, ib, 0, wb, 0, y1, 0)
+    Y = y1.read(np.float32, T * d_model).reshape(T, d_model)
+    old = os.environ.get("HAYAI_HIP_MOE_GROUPED")
+    os.environ["HAYAI_HIP_MOE_GROUPED"] = "0"
+    try:
+        plain = hayai_amd.HipEngine(0)
+    finally:
+        if old is None:
+            del os.environ["HAYAI_HIP_MOE_GROUPED"]
+        else:
+            os.environ["HAYAI_HIP_MOE_GROUPED"] = old
+    try:
+        pb = plain.alloc(buf.nbytes)
+        pb.write(host)
+        d2 = plain.moe_desc(d_model, d_ff, E, k, stride, offs)
+        y2 = plain.alloc(4 * T * d_model)
+        plain.moe_ffn_dev(d2, pb, 0, plain.upload(x), 0, T, plain.upload(ids), 0, plain.upload(w), 0, y2, 0)
+        Y2 = y2.read(np.float32, T * d_model).reshape(T, d_model)
+    finally:
+        plain.close()
+    for t in range(T):
+        keep = [(int(e), float(v)) for e, v in zip(ids[t], w[t]) if 0 <= e < E]
+        ref = oracle.moe_token(Q4_K, d_model, d_ff, host, stride, offs, [e for e, _ in keep], [v for _, v in keep], x[t])
+        for got in (Y[t], Y2[t]):
+            assert float(np.max(np.abs(got - ref)) / np.max(np.abs(ref))) <= REL_TOL
