@@ -117,6 +117,43 @@ def cpu_baseline(engine, pack, lay, stride, xs, budget_s: float) -> dict:
     }
 
 
+def cpu_time(fn, budget_s: float):
+    """Median seconds per fn(i) call of the oracle on the host cores (calls repeat for about
+    budget_s seconds, at least 3; the first is a warm-up).  Returns (seconds, threads, calls,
+    total seconds)."""
+    import oracle
+
+    oracle.build()
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    threads = max(1, min(16, cores))
+    oracle.set_threads(threads)
+    times, i, t_end = [], 0, time.time() + budget_s
+    while time.time() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        fn(i)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    return statistics.median(times[1:]), threads, len(times), sum(times)
+
+
+def cpu_entry(fn, budget_s: float, bytes_per_call: float, what: str) -> dict:
+    """cpu_baseline of a workload: the oracle's restatement of the reference's CPU path,
+    GB/s over the same algorithmic bytes as the GPU value."""
+    t, threads, n, total = cpu_time(fn, budget_s)
+    return {"value": round(bytes_per_call / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{what}: {n} calls in {total:.1f}s, median {t * 1e3:.2f} ms per call; {threads} OpenMP threads"}
+
+
+def roofline_step(gbs: float, what: str) -> dict:
+    """Roofline of a secondary workload over its whole step (all its launches): achieved =
+    the step's algorithmic bytes / step time."""
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": what}
+
+
 def bench_batched(eng, pack, lay, stride, desc, args) -> int:
     """the 8B Q4_K FFN for B tokens per step (all 32 layers
     resident), gate/up(+SiLU) and down on the matrix cores.  value = algorithmic bytes per
@@ -189,6 +226,8 @@ def bench_batched(eng, pack, lay, stride, desc, args) -> int:
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "ffn_tok_s": round(B * 1e3 / ms, 2),
         "tflops": round(tflops, 2),
+        "roofline": roofline_step(gbs, "whole step: token prep + weight-stream MFMA gate/up and down (B <= 16) or the "
+                                       "tiled MFMA kernels (B > 16); MFMA rate in tflops"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
@@ -228,8 +267,9 @@ def bench_moe(eng, args) -> int:
     lbuf, xbuf = eng.upload(logits), eng.upload(x)
     ybuf = eng.alloc(4 * L * T * DM)
     # distinct experts per (set, layer) from the routing itself
-    ids, _ = eng.route_experts(desc, logits.reshape(-1, E))
+    ids, rw = eng.route_experts(desc, logits.reshape(-1, E))
     ids = ids.reshape(SETS, L, T, K)
+    rw = np.asarray(rw).reshape(SETS, L, T, K)
     distinct = [[len(set(ids[s, l].reshape(-1).tolist()) - {-1}) for l in range(L)] for s in range(SETS)]
     eng.sync()
     log(f"[bench] moe T={T}: mean distinct experts per layer {np.mean(distinct):.1f}")
@@ -253,6 +293,19 @@ def bench_moe(eng, args) -> int:
     bytes_step = np.mean([sum(distinct[i % SETS]) for i in range(args.steps)]) * stride + L * T * (2 * 4 * DM + 4 * E)
     gbs = bytes_step / (ms / 1e3) / 1e9
     log(f"[bench] moe T={T}: {ms * 1e3:.1f} us/step ({ms * 1e3 / L:.1f} us/layer), {gbs:.1f} GB/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        host = experts.read(np.uint8, E * stride, 0)  # layer 0's experts
+
+        def moe_layer(i):
+            for t in range(T):
+                keep = [(int(e), float(v)) for e, v in zip(ids[0, 0, t], rw[0, 0, t]) if e >= 0]
+                oracle.moe_token(Q4_K, DM, DF, host, stride, offs, [e for e, _ in keep], [v for _, v in keep], x[0, t])
+
+        import oracle
+        cpu = cpu_entry(moe_layer, args.cpu_budget, distinct[0][0] * stride + T * (2 * 4 * DM + 4 * E),
+                        f"oracle MoE layer (the {T} tokens' routed experts, expert loop + combine, moe_infer.rs:342-455) "
+                        f"over layer 0's {distinct[0][0]} distinct experts")
     out = {
         "metric": "FFN GEMV achieved HBM GB/s (% of peak), Qwen3-30B-A3B-shaped MoE layer",
         "value": round(gbs, 2),
@@ -271,7 +324,9 @@ def bench_moe(eng, args) -> int:
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "us_per_layer": round(ms * 1e3 / L, 3),
         "mean_distinct_experts_per_layer": round(float(np.mean(distinct)), 2),
-        "cpu_baseline": None,
+        "roofline": roofline_step(gbs, "whole MoE step: routing + grouped expert gate/up and down (T > 1) or the ring "
+                                       "kernels (T = 1)"),
+        "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
     eng.close()
@@ -354,6 +409,13 @@ def bench_stream(eng, args) -> int:
 
     ffn_only()
     ms_ffn = timed(ffn_only, max(1, args.steps))
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+        v = np.array(st.host_slot(0))  # layer 0's image, copied out of the pinned slot
+        wl = [v[o:o + n] for o, n in (lay.ffn_region(r) for r in range(3))]
+        cpu = cpu_entry(lambda i: oracle.ffn((T, T, T), DM, DF, wl[0], wl[1], wl[2], xs[i % L]), args.cpu_budget,
+                        wbytes + 2 * 4 * DM, "oracle fp32 IQ2_XXS FFN of one 70B layer from host memory")
     tok_bytes = L * (wbytes + 2 * 4 * DM)
     gbs = tok_bytes / (ms_tok / 1e3) / 1e9
     h2d = L * wbytes / (ms_copy / 1e3) / 1e9
@@ -380,7 +442,11 @@ def bench_stream(eng, args) -> int:
         "overlap_efficiency": round(ms_copy / ms_tok, 4),
         "ffn_resident_hbm_gbs": round(ffn_gbs, 1),
         "ffn_resident_pct_of_peak": round(100.0 * ffn_gbs / PEAK_HBM_GBS, 2),
-        "cpu_baseline": None,
+        "roofline": {"bound": "hbm", "achieved": round(ffn_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(ffn_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "the IQ2_XXS FFN kernels on a staged (device-resident) layer; the token itself is "
+                               "host-link bound"},
+        "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
     st.free()
@@ -461,6 +527,17 @@ def bench_disk(eng, args) -> int:
         wall = (time.perf_counter() - w0) / steps
         ms_tok = a.elapsed_ms(b) / steps
         read_gbs = L * lp.total / (read_s[0] / steps) / 1e9
+        cpu = None
+        if not args.no_cpu_baseline:
+            import oracle
+            v = np.zeros(lp.total, np.uint8)
+            cat.load_layer_pack(0, v)
+            wl = [v[lay.gate_off:lay.gate_off + lay.gate_len], v[lay.up_off:lay.up_off + lay.up_len],
+                  v[lay.down_off:lay.down_off + lay.down_len]]
+            cpu = cpu_entry(lambda i: (cat.load_layer_pack(i % NF, v),
+                                       oracle.ffn((T, T, T), DM, DF, wl[0], wl[1], wl[2], xs[i % L])), args.cpu_budget,
+                            lp.total + 2 * 4 * DM, "one layer read from the GGUF file (io_uring) + the oracle's fp32 "
+                                                   "IQ2_XXS FFN on host cores")
         tok_bytes = L * (lp.total + 2 * 4 * DM)
         gbs = tok_bytes / (ms_tok / 1e3) / 1e9
         log(f"[bench] disk: {ms_tok:.2f} ms/token ({ms_tok / L * 1e3:.0f} us/layer), {gbs:.2f} GB/s; file reads alone "
@@ -487,7 +564,10 @@ def bench_disk(eng, args) -> int:
             "ffn_tok_s": round(1e3 / ms_tok, 3),
             "file_read_gbs": round(read_gbs, 3),
             "io_uring": bool(cat.io_uring),
-            "cpu_baseline": None,
+            "roofline": {"bound": "host link", "achieved": round(gbs, 2), "peak": None, "unit": "GB/s", "frac": None,
+                         "traffic": None, "kernel": "file -> pinned slot -> HBM per layer pack; PCIe-bound, see the "
+                                                    "stream workload for the H2D copy rate"},
+            "cpu_baseline": cpu,
         }
         print(json.dumps(out), flush=True)
         st.free()
@@ -546,6 +626,12 @@ def bench_lmhead(eng, args) -> int:
     plain.close()
     log(f"[bench] lm head {args.lm_type} {M}x{N}: {ms * 1e3:.1f} us ({gbs:.1f} GB/s); ring off {ms_plain * 1e3:.1f} us "
         f"({nbytes / (ms_plain / 1e3) / 1e9:.1f} GB/s)")
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+        wh, xh = w.read(np.uint8, w.nbytes), x.read(np.float32, N)
+        cpu = cpu_entry(lambda i: oracle.gemv(T, M, N, wh, xh), args.cpu_budget, nbytes,
+                        f"oracle fp32 gemv of the {M}x{N} matrix")
     out = {
         "metric": "LM-head GEMV achieved HBM GB/s, Q6_K 128256x4096 (Llama-3 8B Q4_K_M output.weight) bs=1",
         "value": round(gbs, 2),
@@ -562,6 +648,8 @@ def bench_lmhead(eng, args) -> int:
         "config": {"workload": "llama3-8b-lm-head-q6_k-bs1", "vocab": M, "d_model": N, "weights": "Q6_K"},
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "team_kernel_us": round(ms_plain * 1e3, 2),
+        "roofline": roofline_step(gbs, "x digits + the Q6_K ring kernel" if T != hayai_amd.Q4_K else "Q4_K GEMV kernel"),
+        "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
     return 0
@@ -614,6 +702,13 @@ def bench_smollm(eng, args) -> int:
     bytes_step = L * (wb + 2 * 4 * DM)
     gbs = bytes_step / (ms / 1e3) / 1e9
     log(f"[bench] smollm: {ms * 1e3:.1f} us/step ({ms * 1e3 / L:.2f} us/layer), {gbs:.1f} GB/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+        mats = [[pack.read(np.uint8, m.nbytes, l * stride + o) for m, o in ((gate, lay.gate_off), (up, lay.up_off),
+                                                                            (down, lay.down_off))] for l in range(4)]
+        cpu = cpu_entry(lambda i: oracle.ffn((T, T, T), DM, DF, *mats[i % 4], xs[i % L]), args.cpu_budget,
+                        wb + 2 * 4 * DM, "oracle fp32 Q4_0 FFN over 4 of the 30 layers in rotation")
     out = {
         "metric": "FFN GEMV achieved HBM GB/s (% of peak) + FFN tok/s, SmolLM2-135M-shape Q4_0 bs=1",
         "value": round(gbs, 2),
@@ -632,7 +727,8 @@ def bench_smollm(eng, args) -> int:
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "ffn_tok_s": round(1e3 / ms, 2),
         "us_per_layer": round(ms * 1e3 / L, 3),
-        "cpu_baseline": None,
+        "roofline": roofline_step(gbs, "whole step: Q4_0 gate/up + down team kernels (launch-latency bound)"),
+        "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
     eng.close()
@@ -682,6 +778,13 @@ def bench_q4km(eng, args) -> int:
     bytes_step = LAYERS * (wb + 2 * 4 * D_MODEL + 2 * 4 * D_FF)
     gbs = bytes_step / (ms / 1e3) / 1e9
     log(f"[bench] q4_k_m: {ms * 1e3:.1f} us/step ({ms * 1e3 / LAYERS:.2f} us/layer), {gbs:.1f} GB/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+        mats = [[pack.read(np.uint8, m.nbytes, l * stride + o) for m, o in ((gate, lay.gate_off), (up, lay.up_off),
+                                                                            (down, lay.down_off))] for l in range(4)]
+        cpu = cpu_entry(lambda i: oracle.ffn((Q4_K, Q4_K, Q6_K), D_MODEL, D_FF, *mats[i % 4], xs[i % 4]),
+                        args.cpu_budget, bytes_step / LAYERS, "oracle fp32 Q4_K_M FFN over 4 of the 32 layers")
     out = {
         "metric": "FFN GEMV achieved HBM GB/s (% of peak) + FFN tok/s, 8B-shape Q4_K_M (Q6_K down) bs=1",
         "value": round(gbs, 2),
@@ -700,7 +803,8 @@ def bench_q4km(eng, args) -> int:
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "ffn_tok_s": round(1e3 / ms, 2),
         "us_per_layer": round(ms * 1e3 / LAYERS, 3),
-        "cpu_baseline": None,
+        "roofline": roofline_step(gbs, "ring gate/up (Q4_K) + Q6_K ring down, per layer"),
+        "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
     eng.close()
@@ -712,6 +816,7 @@ def bench_block(eng, pack, lay, stride, desc, args) -> int:
     on one residual stream, x_{l+1} = x_l + FFN_l(rms_norm(x_l, norm_l)) (ffn_apply,
     hybrid_infer.rs:883-936), the RMSNorm and the residual add fused into the ring kernels.
     Reported beside the plain FFN op on the same weights (independent per-layer x)."""
+    import hayai_amd
     from hayai_amd import synth
 
     norms = eng.upload(np.concatenate([synth.normal(synth.seed_for(CONFIG_ID, l, 7), D_MODEL) * 0.1 + 1.0
@@ -750,6 +855,16 @@ def bench_block(eng, pack, lay, stride, desc, args) -> int:
     gbs = bytes_step / (ms_block / 1e3) / 1e9
     log(f"[bench] block: {ms_block * 1e3:.1f} us/step ({ms_block * 1e3 / LAYERS:.2f} us/layer), {gbs:.1f} GB/s; "
         f"plain FFN op {ms_ffn * 1e3 / LAYERS:.2f} us/layer")
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+        rg, rd = hayai_amd.row_bytes(Q4_K, D_MODEL), hayai_amd.row_bytes(Q4_K, D_FF)
+        mats = [(pack.read(np.uint8, D_FF * rg, l * stride + lay.gate_off), pack.read(np.uint8, D_FF * rg, l * stride + lay.up_off),
+                 pack.read(np.uint8, D_MODEL * rd, l * stride + lay.down_off)) for l in range(4)]
+        nw = norms.read(np.float32, D_MODEL * 4).reshape(4, D_MODEL)
+        cpu = cpu_entry(lambda i: oracle.ffn_block((Q4_K,) * 3, D_MODEL, D_FF, *mats[i % 4], nw[i % 4], 1e-5, x0),
+                        args.cpu_budget, layer_bytes() + 4 * D_MODEL,
+                        "oracle ffn_apply (rms_norm + fp32 Q4_K FFN + residual) over 4 of the 32 layers")
     out = {
         "metric": "FFN residual block (RMSNorm + FFN + residual) achieved HBM GB/s, 8B-shape Q4_K bs=1",
         "value": round(gbs, 2),
@@ -768,6 +883,8 @@ def bench_block(eng, pack, lay, stride, desc, args) -> int:
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "us_per_layer": round(ms_block * 1e3 / LAYERS, 3),
         "plain_ffn_us_per_layer": round(ms_ffn * 1e3 / LAYERS, 3),
+        "roofline": roofline_step(gbs, "ring gate/up with the RMSNorm prologue + ring down with the residual epilogue"),
+        "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
     return 0
