@@ -691,8 +691,61 @@ hh_status hh_engine::enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, cons
         }
         if (fst != HH_ERR_UNSUPPORTED_DEVICE) return fst;
     }
+    if (d->type_gate == d->type_up && d->type_up == d->type_down &&
+        (d->type_gate == HH_TYPE_Q4_0 || d->type_gate == HH_TYPE_Q8_0)) {
+        const hh_status sst = enqueue_small_ffn(d, pack + d->gate_off, pack + d->up_off, pack + d->down_off, x, y);
+        if (sst == HH_OK) {
+            ffn_stage_valid = false;
+            ffn_calls += 3;
+            return HH_OK;
+        }
+        if (sst != HH_ERR_UNSUPPORTED_DEVICE) return sst;
+    }
     HH_TRY(enqueue_ffn_begin(d, pack, x));
     return enqueue_ffn_finish(d, pack, y);
+}
+
+// Must match struct hh_sffn_args in kernels/small_ffn.hip.
+struct SffnArgs {
+    const uint8_t *wg, *wu, *wd;
+    const float* x;
+    float* y;
+    float* h;
+    unsigned* bar;
+    uint64_t rb_in, rb_ff;
+    uint32_t d_model, d_ff;
+    unsigned gen;
+    int32_t act;
+};
+
+// A small Q4_0 / Q8_0 FFN in one launch (small_ffn.hip): every workgroup's rows fit its teams
+// (at most two rows per team and phase), one workgroup per CU, a grid barrier between gate/up
+// and down.
+hh_status hh_engine::enqueue_small_ffn(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
+                                       const float* x, float* y) {
+    const size_t dm = d->d_model, df = d->d_ff, G = (size_t)props.multiProcessorCount;
+    auto team_of = [](size_t units) { return units <= 16 ? 16 : (units <= 32 ? 32 : 64); };
+    const int t1 = team_of(dm / 32), t2 = team_of(df / 32);
+    if (capturing || !small_ffn || dm % 32 || df % 32 || dm / 32 > 64 || df / 32 > 64 ||
+        (df + G - 1) / G > 2 * (256 / (size_t)t1) || (dm + G - 1) / G > 2 * (256 / (size_t)t2) ||
+        (((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd) & 1u) || ((uintptr_t)x & 3u) || ((uintptr_t)y & 3u))
+        return HH_ERR_UNSUPPORTED_DEVICE;
+    const std::string name = std::string("hh_sffn_") + (d->type_gate == HH_TYPE_Q4_0 ? "q4_0" : "q8_0") + "_t" +
+                             std::to_string(t1) + "_" + std::to_string(t2);
+    hipFunction_t fn;
+    HH_TRY(kernel(name, &fn));
+    HH_TRY(grow(&ws_h, &ws_h_cap, df * sizeof(float)));
+    size_t rin, rff;
+    HH_TRY(row_bytes(d->type_gate, dm, &rin));
+    HH_TRY(row_bytes(d->type_down, df, &rff));
+    SffnArgs a{wg, wu, wd, x, y, (float*)ws_h, (unsigned*)grid_sync, (uint64_t)rin, (uint64_t)rff, (uint32_t)dm,
+               (uint32_t)df, 0u, d->act};
+    if (++ffn_gen == 0) ffn_gen = 1;
+    a.gen = ffn_gen;
+    void* params[] = {&a};
+    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)G, 1, 1, 256, 1, 1, 0, stream, params, nullptr);
+    if (err != hipSuccess) return hip_fail(err, "launch(small ffn)");
+    return HH_OK;
 }
 
 // The FFN residual block of one token: y = x + FFN(RMSNorm(x)) (ffn_apply,
@@ -1211,6 +1264,10 @@ static std::vector<std::string> required_kernels() {
                           "dn_ring_d8"})
         k.push_back(std::string("hh_moe_") + f);
     k.push_back("hh_moe_route");
+    for (const char* fmt : {"q4_0", "q8_0"})
+        for (int t1 : {16, 32, 64})
+            for (int t2 : {16, 32, 64})
+                k.push_back(std::string("hh_sffn_") + fmt + "_t" + std::to_string(t1) + "_" + std::to_string(t2));
     for (const char* f : {"hh_moe_prep", "hh_moe_hdigits", "hh_moe_combine", "hh_moe_gu_grp_t16", "hh_moe_gu_grp_t32", "hh_moe_gu_grp_t64",
                           "hh_moe_dn_grp_t16", "hh_moe_dn_grp_t32", "hh_moe_dn_grp_t64"})
         k.push_back(f);
@@ -1264,6 +1321,7 @@ hh_status engine_create(int device, hh_engine** out) {
     if (const char* f = getenv("HAYAI_HIP_FFNP")) e->ffnp = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_RING")) e->ring = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_MOE_GROUPED")) e->moe_grouped = atoi(f) != 0;
+    if (const char* f = getenv("HAYAI_HIP_SMALL_FFN")) e->small_ffn = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_RING_GU_PER_CU")) e->ring_gu_per_cu = std::max(1, atoi(f));
     if (const char* f = getenv("HAYAI_HIP_RING_DN_PER_CU")) e->ring_dn_per_cu = std::max(1, atoi(f));
     if (const char* f = getenv("HAYAI_HIP_MMR")) e->mmr = atoi(f) != 0;

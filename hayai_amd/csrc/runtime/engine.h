@@ -144,6 +144,7 @@ struct hh_engine {
     bool ffnp = true;           // HAYAI_HIP_FFNP=0: skip the persistent pipelined Q4_K FFN
     bool ring = true;           // HAYAI_HIP_RING=0: skip the two-launch ring Q4_K FFN
     bool moe_grouped = true;    // HAYAI_HIP_MOE_GROUPED=0: several-token MoE per (token, expert)
+    bool small_ffn = true;      // HAYAI_HIP_SMALL_FFN=0: small Q4_0/Q8_0 FFNs as two launches
     int ring_gu_per_cu = 1;     // HAYAI_HIP_RING_GU_PER_CU: ring gate/up workgroups per CU
     int ring_dn_per_cu = 1;     // HAYAI_HIP_RING_DN_PER_CU: ring down workgroups per CU
     bool mmr = true;            // HAYAI_HIP_MMR=0: batched Q4_K (<= 16 tokens) on the q4k_mm kernels
@@ -173,6 +174,8 @@ struct hh_engine {
     hh_status enqueue_gateup(int type_g, int type_u, size_t d_ff, size_t d_model, const uint8_t* wg,
                              const uint8_t* wu, const float* x, float* h, int act);
     hh_status enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y);
+    hh_status enqueue_small_ffn(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
+                                const float* x, float* y);
     hh_status enqueue_ffn_block(const hh_ffn_desc* d, const uint8_t* pack, const float* x, const float* norm,
                                 float eps, float* y);
     // The two halves of enqueue_ffn's two-launch path: gate/up(+act) into the engine's FFN

@@ -344,3 +344,38 @@ def test_ffn_block_chain_of_layers(engine):
     err = rel_err(y - x, r - x)
     print(f"  rel_err of the 4-layer update {err:.3e}", flush=True)
     assert err <= REL_TOL, err
+
+
+@pytest.mark.parametrize("types,d_model,d_ff", [((2, 2, 2), 576, 1536), ((8, 8, 8), 1024, 2048),
+                                                ((2, 2, 2), 2048, 4096), ((2, 2, 2), 2048, 8192)])
+def test_small_ffn_one_launch_equals_two_launches(engine, types, d_model, d_ff):
+    # The one-launch small FFN (gate/up, grid barrier, down; Q4_0 / Q8_0 shapes whose rows fit
+    # two per team) gives the two-launch kernels' bits: the same unit dots and team sums.
+    # 2048 x 8192 exceeds it (4 down rows per team) and runs the two launches in both engines.
+    import os
+    print(f"[case] small ffn types={types} {d_model}x{d_ff}", flush=True)
+    old = os.environ.get("HAYAI_HIP_SMALL_FFN")
+    os.environ["HAYAI_HIP_SMALL_FFN"] = "0"
+    try:
+        two = hayai_amd.HipEngine(0)
+    finally:
+        if old is None:
+            del os.environ["HAYAI_HIP_SMALL_FFN"]
+        else:
+            os.environ["HAYAI_HIP_SMALL_FFN"] = old
+    try:
+        lay, (wg, wu, wd), pack = make_pack(engine, types, d_model, d_ff, 25)
+        lay2, _, pack2 = make_pack(two, types, d_model, d_ff, 25)
+        desc = engine.ffn_desc(types, d_model, d_ff, lay)
+        xb = engine.upload(synth.normal(88, d_model))
+        yb = engine.alloc(4 * d_model)
+        for k in range(3):  # repeated launches: a new barrier generation each time
+            x = synth.normal(100 + k, d_model)
+            y1 = engine.ffn(desc, pack, 0, x)
+            y2 = two.ffn(two.ffn_desc(types, d_model, d_ff, lay2), pack2, 0, x)
+            np.testing.assert_array_equal(y1, y2)
+            assert rel_err(y1, oracle.ffn(types, d_model, d_ff, wg, wu, wd, x)) <= REL_TOL
+        engine.ffn_dev(desc, pack, 0, xb, 0, yb, 0)
+        engine.sync()  # reports a timed-out barrier if one was recorded
+    finally:
+        two.close()
