@@ -287,6 +287,59 @@ struct TensorRec {
 
 enum class Parse { ok, truncated, bad };
 
+// Strings of the file as String::from_utf8_lossy makes them (gguf.rs:620-626): every maximal
+// prefix of an invalid UTF-8 sequence becomes one U+FFFD, so names and keys compare as the
+// reference's do.
+static std::string utf8_lossy(const uint8_t* p, size_t n) {
+    std::string out;
+    out.reserve(n);
+    size_t i = 0;
+    while (i < n) {
+        const uint8_t c = p[i];
+        if (c < 0x80) {
+            out.push_back((char)c);
+            i++;
+            continue;
+        }
+        size_t need = 0;
+        uint8_t lo = 0x80, hi = 0xBF;  // range of the second byte
+        if (c >= 0xC2 && c <= 0xDF) {
+            need = 1;
+        } else if (c >= 0xE0 && c <= 0xEF) {
+            need = 2;
+            if (c == 0xE0) lo = 0xA0;
+            if (c == 0xED) hi = 0x9F;
+        } else if (c >= 0xF0 && c <= 0xF4) {
+            need = 3;
+            if (c == 0xF0) lo = 0x90;
+            if (c == 0xF4) hi = 0x8F;
+        }
+        size_t k = 1;  // bytes of the sequence seen to be valid so far
+        bool ok = need > 0;
+        for (size_t j = 1; ok && j <= need; j++) {
+            if (i + j >= n) {
+                ok = false;
+                break;
+            }
+            const uint8_t b = p[i + j];
+            const uint8_t l = j == 1 ? lo : 0x80, h = j == 1 ? hi : 0xBF;
+            if (b < l || b > h) {
+                ok = false;
+                break;
+            }
+            k++;
+        }
+        if (ok) {
+            out.append((const char*)p + i, need + 1);
+            i += need + 1;
+        } else {
+            out.append("\xEF\xBF\xBD");
+            i += k;
+        }
+    }
+    return out;
+}
+
 struct Reader {
     const uint8_t* p;
     size_t len, pos = 0;
@@ -310,7 +363,7 @@ struct Reader {
         uint64_t n;
         if (!get(&n, what)) return false;
         if (!need((size_t)n, what)) return false;
-        s->assign((const char*)p + pos, (size_t)n);
+        *s = utf8_lossy(p + pos, (size_t)n);
         pos += (size_t)n;
         return true;
     }

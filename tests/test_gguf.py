@@ -291,3 +291,59 @@ def test_catalog_reads_are_identical_through_io_uring_and_pread(tmp_path):
         out.append(r.stdout.split())
     assert out[1][0] == "0"
     assert out[0][1:] == out[1][1:]
+
+
+def test_mutated_headers_never_crash(tmp_path):
+    # 300 files, each a valid header with a few random bytes changed (or cut short): opening
+    # either succeeds with a self-consistent directory or fails with a status; a successful
+    # open's tensors all lie inside 64-bit ranges and reading them either works or reports
+    # HH_ERR_IO / HH_ERR_INVALID.
+    rng = np.random.default_rng(123)
+    p = str(tmp_path / "base.gguf")
+    write_gguf(p, [("general.architecture", "llama"), ("n", (gguf.U32, 7)),
+                   ("arr", (gguf.ARRAY, (gguf.I32, [1, -2, 3]))), ("s", "abc")],
+               [("a.weight", (256, 2), 12, np.arange(288, dtype=np.uint8)),
+                ("b.weight", (32, 3), 8, np.arange(102, dtype=np.uint8))])
+    blob = bytearray(open(p, "rb").read())
+    with GgufCatalog(p) as g:
+        hdr = g.header_bytes
+    opened = 0
+    for i in range(300):
+        b = bytearray(blob)
+        for _ in range(int(rng.integers(1, 4))):
+            pos = int(rng.integers(0, hdr))
+            b[pos] = int(rng.integers(0, 256))
+        if i % 10 == 0:
+            b = b[: int(rng.integers(0, len(b)))]
+        q = str(tmp_path / f"m{i}.gguf")
+        with open(q, "wb") as f:
+            f.write(b)
+        try:
+            g = GgufCatalog(q)
+        except hayai_amd.HipError as e:
+            assert e.status in (2, 3, 7), e  # invalid / unknown type / io
+            continue
+        opened += 1
+        with g:
+            for t in g.tensors():
+                assert t.abs_offset == g.data_offset + t.offset
+                if t.nbytes <= 1 << 20:
+                    try:
+                        g.read_tensor(t.name)
+                    except hayai_amd.HipError as e:
+                        assert e.status in (2, 7), e
+    assert opened > 0
+
+
+def test_names_are_decoded_like_from_utf8_lossy(tmp_path):
+    # String::from_utf8_lossy (gguf.rs:620-626): each maximal prefix of an invalid sequence ->
+    # one U+FFFD; Python's "replace" handler follows the same rule, so it is the reference here.
+    raws = [b"ok.weight", b"t\xff.weight", b"e\xe2\x82A", b"s\xed\xa0\x80x", b"f\xf0\x9f\x98\x80y", b"c\xc0\xafz",
+            b"tail\xe2\x82"]
+    p = str(tmp_path / "names.gguf")
+    write_gguf(p, [], [(r, (32,), 8, np.zeros(34, np.uint8)) for r in raws])
+    with GgufCatalog(p) as g:
+        names = [t.name for t in g.tensors()]
+        assert names == [r.decode("utf-8", "replace") for r in raws]
+        for n in names:
+            assert g.tensor(n).nbytes == 34
