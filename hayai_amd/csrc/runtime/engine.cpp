@@ -1291,6 +1291,7 @@ hh_status engine_create(int device, hh_engine** out) {
         if (e->grid_sync) (void)hipFree(e->grid_sync);
         if (e->stream) (void)hipStreamDestroy(e->stream);
         if (e->copy_stream) (void)hipStreamDestroy(e->copy_stream);
+    if (e->copy_stream2) (void)hipStreamDestroy(e->copy_stream2);
         if (e->module) (void)hipModuleUnload(e->module);
         delete e;
         return st;
@@ -1311,6 +1312,8 @@ hh_status engine_create(int device, hh_engine** out) {
     if (err != hipSuccess) return bail(hip_fail(err, "hipStreamCreate(compute)"));
     err = hipStreamCreateWithFlags(&e->copy_stream, hipStreamNonBlocking);
     if (err != hipSuccess) return bail(hip_fail(err, "hipStreamCreate(copy)"));
+    err = hipStreamCreateWithFlags(&e->copy_stream2, hipStreamNonBlocking);
+    if (err != hipSuccess) return bail(hip_fail(err, "hipStreamCreate(copy 2)"));
     for (const std::string& k : required_kernels()) {
         hipFunction_t f;
         if (hh_status st = e->kernel(k, &f); st != HH_OK) return bail(st);
@@ -1322,6 +1325,7 @@ hh_status engine_create(int device, hh_engine** out) {
     if (const char* f = getenv("HAYAI_HIP_RING")) e->ring = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_MOE_GROUPED")) e->moe_grouped = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_SMALL_FFN")) e->small_ffn = atoi(f) != 0;
+    if (const char* f = getenv("HAYAI_HIP_DMA_SPLIT")) e->dma_split = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_RING_GU_PER_CU")) e->ring_gu_per_cu = std::max(1, atoi(f));
     if (const char* f = getenv("HAYAI_HIP_RING_DN_PER_CU")) e->ring_dn_per_cu = std::max(1, atoi(f));
     if (const char* f = getenv("HAYAI_HIP_MMR")) e->mmr = atoi(f) != 0;
@@ -1339,11 +1343,13 @@ void engine_destroy(hh_engine* e) {
     (void)hipSetDevice(e->device);
     if (e->stream) (void)hipStreamSynchronize(e->stream);
     if (e->copy_stream) (void)hipStreamSynchronize(e->copy_stream);
+    if (e->copy_stream2) (void)hipStreamSynchronize(e->copy_stream2);
     for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq, e->ws_xop, e->ws_hop, e->ws_part,
                     e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->ws_xn, e->ws_f, e->ws_xq, e->ws_moe_yp, e->ws_moe_grp, e->ws_moe_q, e->grid_sync})
         if (p) (void)hipFree(p);
     if (e->stream) (void)hipStreamDestroy(e->stream);
     if (e->copy_stream) (void)hipStreamDestroy(e->copy_stream);
+    if (e->copy_stream2) (void)hipStreamDestroy(e->copy_stream2);
     if (e->module) (void)hipModuleUnload(e->module);
     delete e;
 }

@@ -82,6 +82,8 @@ struct hh_engine {
     hipModule_t module = nullptr;
     hipStream_t stream = nullptr;       // compute stream (default priority)
     hipStream_t copy_stream = nullptr;  // side stream for host<->device DMA
+    hipStream_t copy_stream2 = nullptr; // second DMA stream: large streamer copies split in two
+    bool dma_split = true;              // HAYAI_HIP_DMA_SPLIT=0: one copy stream per DMA
     std::unordered_map<std::string, hipFunction_t> fns;
     std::unordered_map<std::string, int> blocks_per_cu;  // occupancy per kernel
     std::atomic<uint64_t> ffn_calls{0};

@@ -34,6 +34,7 @@ struct hh_streamer {
     std::vector<bool> dma_pending;      // per slot: dma_done was recorded and not yet waited on the host
     std::vector<long long> staged;      // per slot: block id whose DMA was issued last (-1 none)
     hipEvent_t tail = nullptr;          // re-recorded on the compute stream before each DMA
+    hipEvent_t half = nullptr;          // re-recorded on the second copy stream after its half
 };
 
 static void streamer_free(hh_streamer* s) {
@@ -41,11 +42,13 @@ static void streamer_free(hh_streamer* s) {
     if (s->engine) {
         (void)hipSetDevice(s->engine->device);
         (void)hipStreamSynchronize(s->engine->copy_stream);
+        (void)hipStreamSynchronize(s->engine->copy_stream2);
         (void)hipStreamSynchronize(s->engine->stream);
     }
     for (hipEvent_t ev : s->dma_done)
         if (ev) (void)hipEventDestroy(ev);
     if (s->tail) (void)hipEventDestroy(s->tail);
+    if (s->half) (void)hipEventDestroy(s->half);
     for (void* p : s->host)
         if (p) (void)hipHostFree(p);
     for (hh_buf* b : s->mirror)
@@ -86,6 +89,10 @@ hh_status hh_streamer_create(hh_engine* e, size_t layer_bytes, size_t block_k, s
     s->dma_done.assign(n_slots, nullptr);
     s->dma_pending.assign(n_slots, false);
     s->staged.assign(n_slots, -1);
+    if (hipError_t err = hipEventCreateWithFlags(&s->half, hipEventDisableTiming); err != hipSuccess) {
+        streamer_free(s);
+        return hip_fail(err, "hipEventCreate(streamer)");
+    }
     if (hipError_t err = hipEventCreateWithFlags(&s->tail, hipEventDisableTiming); err != hipSuccess) {
         streamer_free(s);
         return hip_fail(err, "hipEventCreate(streamer)");
@@ -165,9 +172,21 @@ hh_status hh_streamer_dma(hh_streamer* s, size_t layer, size_t off, size_t len) 
         HH_TRY_HIP(hipEventRecord(s->tail, e->stream), "hipEventRecord(streamer tail)");
         HH_TRY_HIP(hipStreamWaitEvent(e->copy_stream, s->tail, 0), "hipStreamWaitEvent(streamer dma)");
         const size_t at = in_slot + off;
-        HH_TRY_HIP(hipMemcpyAsync((char*)s->mirror[slot]->ptr + at, (const char*)s->host[slot] + at, len,
+        // copies of 32 MB and more go out as two halves on two copy streams (two DMA engines
+        // pulling over the host link); the first stream waits for the second's half before
+        // the slot's completion event, so dma_done covers both
+        const size_t first = (e->dma_split && len >= ((size_t)32 << 20)) ? (len / 2) & ~(size_t)4095 : len;
+        HH_TRY_HIP(hipMemcpyAsync((char*)s->mirror[slot]->ptr + at, (const char*)s->host[slot] + at, first,
                                   hipMemcpyHostToDevice, e->copy_stream),
                    "hipMemcpyAsync(streamer dma)");
+        if (first < len) {
+            HH_TRY_HIP(hipStreamWaitEvent(e->copy_stream2, s->tail, 0), "hipStreamWaitEvent(streamer dma 2)");
+            HH_TRY_HIP(hipMemcpyAsync((char*)s->mirror[slot]->ptr + at + first, (const char*)s->host[slot] + at + first,
+                                      len - first, hipMemcpyHostToDevice, e->copy_stream2),
+                       "hipMemcpyAsync(streamer dma 2)");
+            HH_TRY_HIP(hipEventRecord(s->half, e->copy_stream2), "hipEventRecord(streamer half)");
+            HH_TRY_HIP(hipStreamWaitEvent(e->copy_stream, s->half, 0), "hipStreamWaitEvent(streamer half)");
+        }
     }
     HH_TRY_HIP(hipEventRecord(s->dma_done[slot], e->copy_stream), "hipEventRecord(streamer dma)");
     s->dma_pending[slot] = true;
