@@ -1005,6 +1005,33 @@ hh_status hh_engine::enqueue_ffn_batched(const hh_ffn_desc* d, const uint8_t* pa
     const uint8_t* wd = pack + d->down_off;
     const bool mfma = d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K && d->type_down == HH_TYPE_Q4_K &&
                       batch >= 2 && !q4k_generic && (((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd | (uintptr_t)x) & 15u) == 0;
+    // Q4_K_M layers (Q4_K gate/up, Q6_K down): gate and up for all tokens as weight-stream MFMA
+    // GEMMs, the activation over [batch][d_ff], then the Q6_K ring GEMV per token.
+    const bool q4km = d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K && d->type_down == HH_TYPE_Q6_K &&
+                      batch >= 4 && batch <= kMmrMaxTokens && df % 512 == 0 && !capturing &&
+                      mmr_ok(df, dm, batch, wg, wg, x) && mmr_ok(df, dm, batch, wu, wu, x) &&
+                      (((uintptr_t)wd | (uintptr_t)x) & 15u) == 0;
+    if (q4km) {
+        HH_TRY(grow(&ws_g, &ws_g_cap, batch * df * sizeof(float)));
+        HH_TRY(grow(&ws_u, &ws_u_cap, batch * df * sizeof(float)));
+        HH_TRY(grow(&ws_h, &ws_h_cap, batch * df * sizeof(float)));
+        HH_TRY(enqueue_q4k_mmr(MMR_GEMM, df, dm, wg, nullptr, x, batch, (float*)ws_g, 0));
+        HH_TRY(enqueue_q4k_mmr(MMR_GEMM, df, dm, wu, nullptr, x, batch, (float*)ws_u, 0));
+        hipFunction_t fn;
+        HH_TRY(kernel("hh_act_mul_kernel", &fn));
+        hh_act_args aa{(const float*)ws_g, (const float*)ws_u, (float*)ws_h, (uint32_t)(batch * df), d->act};
+        HH_TRY(launch(fn, (uint32_t)((batch * df + 255) / 256), 256, aa));
+        for (size_t b = 0; b < batch; b++) {
+            const hh_status st = enqueue_ring_gemv(true, dm, df, wd, (const float*)ws_h + b * df, y + b * dm);
+            if (st == HH_ERR_UNSUPPORTED_DEVICE)
+                HH_TRY(enqueue_gemv(HH_TYPE_Q6_K, dm, df, wd, (const float*)ws_h + b * df, y + b * dm));
+            else if (st != HH_OK)
+                return st;
+        }
+        ffn_stage_valid = false;
+        ffn_calls += 3 * batch;
+        return HH_OK;
+    }
     if (!mfma) {
         for (size_t b = 0; b < batch; b++) HH_TRY(enqueue_ffn(d, pack, x + b * dm, y + b * dm));
         return HH_OK;

@@ -379,3 +379,23 @@ def test_small_ffn_one_launch_equals_two_launches(engine, types, d_model, d_ff):
         engine.sync()  # reports a timed-out barrier if one was recorded
     finally:
         two.close()
+
+
+@pytest.mark.parametrize("batch", [2, 4, 16])
+def test_q4k_m_batched_ffn_matches_oracle(engine, batch):
+    # Batched tokens through a Q4_K_M layer: gate/up as weight-stream MFMA GEMMs, the
+    # activation, the Q6_K ring GEMV per token (batch >= 4; batch 2 runs the one-token op per
+    # token); each token against the oracle.
+    types, d_model, d_ff = (12, 12, 14), 4096, 14336
+    print(f"[case] q4_k_m batched B={batch}", flush=True)
+    oracle.set_threads(min(16, oracle.max_threads()))
+    lay, (wg, wu, wd), pack = make_pack(engine, types, d_model, d_ff, 26)
+    desc = engine.ffn_desc(types, d_model, d_ff, lay)
+    X = synth.normal(synth.seed_for(26, batch, synth.ACT), batch * d_model).reshape(batch, d_model)
+    Y = engine.ffn_batched(desc, pack, 0, X)
+    worst = 0.0
+    for b in range(batch):
+        ref = oracle.ffn(types, d_model, d_ff, wg, wu, wd, X[b])
+        worst = max(worst, rel_err(Y[b], ref))
+    print(f"  worst per-token rel_err {worst:.3e}", flush=True)
+    assert worst <= REL_TOL, worst
