@@ -70,6 +70,7 @@ def lib():
         L.or_iq3xxs_grid.argtypes = [P]
         L.or_ksigns.argtypes = [P]
         L.or_set_threads.argtypes = [C.c_int]
+        L.or_set_mutation.argtypes = [C.c_int]
         L.or_max_threads.restype = C.c_int
         _lib = L
     return _lib
@@ -90,6 +91,12 @@ def _check(rc: int, what: str):
 
 def set_threads(n: int) -> None:
     lib().or_set_threads(int(n))
+
+
+def set_mutation(m: int) -> None:
+    """Plant a known mistake in the oracle (0 = none, 1 = FFN gate/up swapped, 2 = MoE expert
+    id + 1); only the tests that show the oracle's pins catch such mistakes use this."""
+    lib().or_set_mutation(int(m))
 
 
 def max_threads() -> int:

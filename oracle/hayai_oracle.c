@@ -27,6 +27,9 @@
  *                        invariants, golden fixtures in tests/golden/
  *   gemv (all types)     fp64 brute force bound, linearity in x, reference fixtures
  *   route_experts        the reference's own known-answer tests (moe_infer.rs:1039-1121)
+ *   or_ffn, or_moe_token float64 compositions of the pinned dequant with numpy's exp,
+ *                        under a propagated fp32 rounding bound; planted mistakes
+ *                        (or_set_mutation) must fail the same checks
  */
 #include <math.h>
 #include <stdint.h>
@@ -55,6 +58,13 @@ int or_max_threads(void) {
     return 1;
 #endif
 }
+
+/* Planted mistakes for the tests that pin this oracle: a pin check must fail when one of
+ * these is switched on (0 = none, 1 = or_ffn swaps gate and up, 2 = or_moe_token reads
+ * expert ids[t] + 1 instead of ids[t]). */
+static int g_mutation = 0;
+
+void or_set_mutation(int m) { g_mutation = m; }
 
 /* ---------------------------------------------------------------- f16 ---------- */
 
@@ -623,6 +633,11 @@ int or_ffn(int tg, int tu, int td, size_t d_model, size_t d_ff, const uint8_t* w
     if (!g || !u || !h) goto out;
     if ((rc = or_gemv(tg, d_ff, d_model, wg, lg, x, g)) != OR_OK) goto out;
     if ((rc = or_gemv(tu, d_ff, d_model, wu, lu, x, u)) != OR_OK) goto out;
+    if (g_mutation == 1) {
+        float* t = g;
+        g = u;
+        u = t;
+    }
     if (act == 0)
         or_swiglu(g, u, h, d_ff);
     else
@@ -755,7 +770,9 @@ int or_moe_token(int type, size_t d_model, size_t d_ff, const uint8_t* w, size_t
     float* d = (float*)malloc(d_model * sizeof(float));
     int rc = OR_OK;
     for (int t = 0; t < k && rc == OR_OK; t++) {
-        const uint8_t* base = w + (size_t)ids[t] * expert_stride;
+        size_t e = (size_t)ids[t];
+        if (g_mutation == 2) e = e + 1; /* the pinning test keeps every id below the last expert */
+        const uint8_t* base = w + e * expert_stride;
         rc = or_gemv(type, d_ff, d_model, base + g_off, d_ff * rg, x, g);
         if (rc == OR_OK) rc = or_gemv(type, d_ff, d_model, base + u_off, d_ff * rg, x, u);
         if (rc == OR_OK) {

@@ -502,3 +502,170 @@ def test_ffn_block_zero_norm_weight_is_identity_and_composes():
     y = oracle.ffn_block(t, d_model, d_ff, wg, wu, wd, nw, 1e-5, x)
     f = oracle.ffn(t, d_model, d_ff, wg, wu, wd, oracle.rms_norm(x, nw, 1e-5))
     np.testing.assert_array_equal(y, x + f)
+
+
+# ---------------------------------------------------------------------------------------
+# or_ffn and or_moe_token pinned by float64 compositions of the pinned pieces.
+#
+# The reference's FFN (stream_infer.rs:3752-3864: gate and up GEMV, act(g) * u, down GEMV)
+# and its MoE token (moe_infer.rs:342-380: per selected expert the same FFN at its own
+# weights, acc += w_e * down_e in top order) are composed here from the dequant (pinned
+# above), numpy float64 products and numpy's exp/tanh, and the oracle's fp32 result must
+# sit inside the rounding bound propagated through the chain.  Planted mistakes in the
+# oracle (gate/up swapped, expert id off by one) must fall outside it.
+
+U32 = 2.0 ** -23  # twice the fp32 unit roundoff: the per-term factor of the GEMV bound above
+
+
+def _mat(t, rows, cols, w):
+    return oracle.dequant(t, w, rows * cols).reshape(rows, cols).astype(np.float64)
+
+
+def _act64(g, act):
+    if act == 0:
+        return g / (1.0 + np.exp(-g))
+    return 0.5 * g * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (g + 0.044715 * g ** 3)))
+
+
+def _ffn64_with_bound(types, d_model, d_ff, wg, wu, wd, x, act):
+    """FFN in float64 and a bound on |fp32 oracle - float64| for y and for h."""
+    tg, tu, td = types
+    Wg, Wu, Wd = _mat(tg, d_ff, d_model, wg), _mat(tu, d_ff, d_model, wu), _mat(td, d_model, d_ff, wd)
+    x64 = x.astype(np.float64)
+    g, u = Wg @ x64, Wu @ x64
+    bg = d_model * U32 * (np.abs(Wg) @ np.abs(x64))
+    bu = d_model * U32 * (np.abs(Wu) @ np.abs(x64))
+    s = _act64(g, act)
+    h = s * u
+    # |act'| <= 1.2 for SiLU (max 1.0998) and tanh-GELU (max 1.129); 16 units for the
+    # activation's own roundings (exp/tanh, the divide, the products)
+    bh = 1.2 * bg * (np.abs(u) + bu) + (np.abs(s) + 1.2 * bg) * bu + 16 * U32 * np.abs(h)
+    y = Wd @ h
+    by = np.abs(Wd) @ bh + d_ff * U32 * (np.abs(Wd) @ (np.abs(h) + bh))
+    return y, by, h, bh
+
+
+def _ffn_weights(types, d_model, d_ff, seed):
+    import hayai_amd.synth as synth
+
+    tg, tu, td = types
+    return (synth.matrix(tg, d_ff, d_model, seed), synth.matrix(tu, d_ff, d_model, seed + 1),
+            synth.matrix(td, d_model, d_ff, seed + 2))
+
+
+FFN_PIN_CASES = [
+    ((oracle.Q4_0,) * 3, 256, 512, 0),
+    ((oracle.Q4_K,) * 3, 256, 512, 0),
+    ((oracle.Q4_K, oracle.Q4_K, oracle.Q6_K), 512, 256, 0),
+    ((oracle.IQ2_XXS,) * 3, 256, 512, 0),
+    ((oracle.IQ3_XXS, oracle.Q8_0, oracle.Q4_K), 256, 256, 1),
+    ((oracle.F16, oracle.Q4_0, oracle.Q8_0), 64, 96, 1),
+]
+
+
+def _f16_weights(rng, rows, cols):
+    return (rng.normal(size=rows * cols) * 0.05).astype(np.float16).view(np.uint8)
+
+
+@pytest.mark.parametrize("types,d_model,d_ff,act", FFN_PIN_CASES)
+def test_ffn_pinned_by_fp64_composition(types, d_model, d_ff, act):
+    rng = np.random.default_rng(31 + d_model + act)
+    if types[0] == oracle.F16:
+        wg = _f16_weights(rng, d_ff, d_model)
+        _, wu, wd = _ffn_weights(types, d_model, d_ff, 501)
+    else:
+        wg, wu, wd = _ffn_weights(types, d_model, d_ff, 500 + sum(types))
+    x = rng.normal(size=d_model).astype(np.float32)
+    y, h = oracle.ffn(types, d_model, d_ff, wg, wu, wd, x, act=act, return_h=True)
+    y64, by, h64, bh = _ffn64_with_bound(types, d_model, d_ff, wg, wu, wd, x, act)
+    assert np.all(np.abs(h - h64) <= bh)
+    assert np.all(np.abs(y - y64) <= by)
+    # the worst-case bound (no cancellation assumed) stays well under the outputs, and the
+    # error actually seen is far tighter (measured <= 6e-7 of max|y| on these cases), so a
+    # mistake that moves any output by 1e-5 of the largest one fails as well
+    assert np.max(by) < 1e-2 * np.max(np.abs(y64))
+    assert np.max(np.abs(y - y64)) <= 1e-5 * np.max(np.abs(y64))
+
+
+def test_ffn_pin_catches_gate_up_swap():
+    types, d_model, d_ff = (oracle.Q4_K,) * 3, 256, 512
+    wg, wu, wd = _ffn_weights(types, d_model, d_ff, 700)
+    x = np.random.default_rng(5).normal(size=d_model).astype(np.float32)
+    y64, by, _, _ = _ffn64_with_bound(types, d_model, d_ff, wg, wu, wd, x, 0)
+    assert np.all(np.abs(oracle.ffn(types, d_model, d_ff, wg, wu, wd, x) - y64) <= by)
+    oracle.set_mutation(1)
+    try:
+        ym = oracle.ffn(types, d_model, d_ff, wg, wu, wd, x)
+    finally:
+        oracle.set_mutation(0)
+    assert not np.all(np.abs(ym - y64) <= by)
+
+
+def _moe_setup(t, n_exp, d_model, d_ff, seed):
+    """n_exp experts in one buffer; per expert the regions are stored down, up, gate (not
+    the offsets' natural order) so a swapped offset reads the wrong matrix."""
+    import hayai_amd.synth as synth
+
+    rg, rd = oracle.row_bytes(t, d_model), oracle.row_bytes(t, d_ff)
+    d_off, u_off, g_off = 0, d_model * rd, d_model * rd + d_ff * rg
+    stride = g_off + d_ff * rg + 64  # padding between experts
+    buf = np.zeros(n_exp * stride, np.uint8)
+    for e in range(n_exp):
+        b = e * stride
+        buf[b + g_off:b + g_off + d_ff * rg] = synth.matrix(t, d_ff, d_model, seed + 3 * e)
+        buf[b + u_off:b + u_off + d_ff * rg] = synth.matrix(t, d_ff, d_model, seed + 3 * e + 1)
+        buf[b + d_off:b + d_off + d_model * rd] = synth.matrix(t, d_model, d_ff, seed + 3 * e + 2)
+    return buf, stride, (g_off, u_off, d_off)
+
+
+def _moe64_with_bound(t, d_model, d_ff, buf, stride, offs, ids, wts, x, acc0):
+    g_off, u_off, d_off = offs
+    rg, rd = oracle.row_bytes(t, d_model), oracle.row_bytes(t, d_ff)
+    acc = acc0.astype(np.float64)
+    bound = np.zeros(d_model)
+    mag = np.abs(acc)
+    for e, w in zip(ids, wts):  # explicit loop over the selected experts, in top order
+        b = int(e) * stride
+        y, by, _, _ = _ffn64_with_bound((t, t, t), d_model, d_ff, buf[b + g_off:b + g_off + d_ff * rg],
+                                        buf[b + u_off:b + u_off + d_ff * rg],
+                                        buf[b + d_off:b + d_off + d_model * rd], x, 0)
+        acc = acc + float(w) * y
+        bound += abs(float(w)) * by
+        mag += np.abs(float(w) * y)
+    # each acc += w * d rounds twice per selected expert
+    return acc, bound + 2 * len(ids) * U32 * (mag + bound)
+
+
+@pytest.mark.parametrize("t,d_model,d_ff", [(oracle.Q4_K, 256, 256), (oracle.Q4_0, 128, 96)])
+def test_moe_token_pinned_by_fp64_loop(t, d_model, d_ff):
+    n_exp = 7
+    buf, stride, offs = _moe_setup(t, n_exp, d_model, d_ff, 900 + t)
+    rng = np.random.default_rng(17)
+    x = rng.normal(size=d_model).astype(np.float32)
+    ids, wts = oracle.route_experts(rng.normal(size=n_exp - 1).astype(np.float32), 4, norm_topk_prob=True)
+    acc0 = rng.normal(size=d_model).astype(np.float32)
+    got = oracle.moe_token(t, d_model, d_ff, buf, stride, offs, ids, wts, x, acc=acc0)
+    ref, bound = _moe64_with_bound(t, d_model, d_ff, buf, stride, offs, ids, wts, x, acc0)
+    assert np.all(np.abs(got - ref) <= bound)
+    assert np.max(bound) < 2e-2 * np.max(np.abs(ref - acc0))
+    assert np.max(np.abs(got - ref)) <= 1e-5 * np.max(np.abs(ref))
+    # accumulated into acc, not overwritten
+    zero = oracle.moe_token(t, d_model, d_ff, buf, stride, offs, ids, wts, x)
+    assert np.max(np.abs((got - acc0) - zero)) <= 4 * U32 * np.max(np.abs(got))
+
+
+def test_moe_pin_catches_expert_index_slip():
+    t, d_model, d_ff, n_exp = oracle.Q4_K, 256, 256, 6
+    buf, stride, offs = _moe_setup(t, n_exp, d_model, d_ff, 1300)
+    rng = np.random.default_rng(23)
+    x = rng.normal(size=d_model).astype(np.float32)
+    ids, wts = [3, 0, 4, 1], np.array([0.4, 0.3, 0.2, 0.1], np.float32)  # every id + 1 exists
+    zero = np.zeros(d_model, np.float32)
+    ref, bound = _moe64_with_bound(t, d_model, d_ff, buf, stride, offs, ids, wts, x, zero)
+    assert np.all(np.abs(oracle.moe_token(t, d_model, d_ff, buf, stride, offs, ids, wts, x) - ref) <= bound)
+    oracle.set_mutation(2)
+    try:
+        bad = oracle.moe_token(t, d_model, d_ff, buf, stride, offs, ids, wts, x)
+    finally:
+        oracle.set_mutation(0)
+    assert not np.all(np.abs(bad - ref) <= bound)
