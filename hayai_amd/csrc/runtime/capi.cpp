@@ -169,6 +169,7 @@ void* hh_buf_host_ptr(hh_buf* b) { return (b && b->kind == HH_BUF_PINNED_HOST) ?
 
 hh_status hh_buf_write(hh_engine* e, hh_buf* dst, size_t off, const void* src, size_t bytes) {
     HH_NOT_NULL(e, "engine");
+    HH_TRY(e->no_capture("buf_write"));
     HH_TRY(check_engine(e, dst, "hh_buf_write"));
     HH_TRY(check_range(dst, off, bytes, "hh_buf_write"));
     if (bytes == 0) return HH_OK;
@@ -181,6 +182,7 @@ hh_status hh_buf_write(hh_engine* e, hh_buf* dst, size_t off, const void* src, s
 
 hh_status hh_buf_read(hh_engine* e, const hh_buf* src, size_t off, void* dst, size_t bytes) {
     HH_NOT_NULL(e, "engine");
+    HH_TRY(e->no_capture("buf_read"));
     HH_TRY(check_engine(e, src, "hh_buf_read"));
     HH_TRY(check_range(src, off, bytes, "hh_buf_read"));
     if (bytes == 0) return HH_OK;
@@ -193,6 +195,7 @@ hh_status hh_buf_read(hh_engine* e, const hh_buf* src, size_t off, void* dst, si
 
 hh_status hh_buf_copy(hh_engine* e, hh_buf* dst, size_t dst_off, const hh_buf* src, size_t src_off, size_t bytes) {
     HH_NOT_NULL(e, "engine");
+    HH_TRY(e->no_capture("buf_copy"));
     HH_TRY(check_engine(e, dst, "hh_buf_copy"));
     HH_TRY(check_engine(e, src, "hh_buf_copy"));
     HH_TRY(check_range(dst, dst_off, bytes, "hh_buf_copy dst"));
@@ -207,6 +210,7 @@ hh_status hh_buf_copy(hh_engine* e, hh_buf* dst, size_t dst_off, const hh_buf* s
 
 hh_status hh_buf_fill(hh_engine* e, hh_buf* dst, size_t off, uint8_t value, size_t bytes) {
     HH_NOT_NULL(e, "engine");
+    HH_TRY(e->no_capture("buf_fill"));
     HH_TRY(check_engine(e, dst, "hh_buf_fill"));
     HH_TRY(check_range(dst, off, bytes, "hh_buf_fill"));
     if (bytes == 0) return HH_OK;
@@ -862,6 +866,7 @@ hh_status hh_graph_end(hh_engine* e, hh_graph** out) {
         (void)hipGraphDestroy(g);
         return fail(HH_ERR_OUT_OF_MEMORY, "host allocation failed");
     }
+    e->live_graphs++;
     *out = h;
     return HH_OK;
 }
@@ -877,10 +882,15 @@ hh_status hh_graph_launch(hh_graph* g) {
 
 void hh_graph_destroy(hh_graph* g) {
     if (!g) return;
-    g->engine->select();
+    hh_engine* e = g->engine;
+    (void)e->select();
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    // a replay may still be running on the stream
+    (void)hipStreamSynchronize(e->stream);
     (void)hipGraphExecDestroy(g->exec);
     (void)hipGraphDestroy(g->graph);
     delete g;
+    if (--e->live_graphs == 0) e->free_retired();
 }
 
 // ---------------------------------------------------------------- synthetic data -----

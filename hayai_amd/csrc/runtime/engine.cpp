@@ -133,6 +133,13 @@ int hh_engine::resident_blocks(const std::string& name, int block) {
     return nb;
 }
 
+void hh_engine::free_retired() {
+    if (ws_retired.empty()) return;
+    (void)hipStreamSynchronize(stream);
+    for (void* p : ws_retired) (void)hipFree(p);
+    ws_retired.clear();
+}
+
 hh_status hh_engine::no_capture(const char* what) const {
     if (capturing) return fail(HH_ERR_INVALID, "%s cannot be captured into a graph", what);
     return HH_OK;
@@ -144,9 +151,14 @@ hh_status hh_engine::grow(void** p, size_t* cap, size_t need) {
         return fail(HH_ERR_INVALID,
                     "a workspace would grow during graph capture: run the sequence once before capturing it");
     if (*p) {
-        hipError_t e1 = hipStreamSynchronize(stream);
-        if (e1 != hipSuccess) return hip_fail(e1, "hipStreamSynchronize");
-        (void)hipFree(*p);
+        if (live_graphs > 0) {
+            // a graph may name this allocation in its kernels' arguments: keep it alive
+            ws_retired.push_back(*p);
+        } else {
+            hipError_t e1 = hipStreamSynchronize(stream);
+            if (e1 != hipSuccess) return hip_fail(e1, "hipStreamSynchronize");
+            (void)hipFree(*p);
+        }
         *p = nullptr;
         *cap = 0;
     }
@@ -1374,6 +1386,7 @@ void engine_destroy(hh_engine* e) {
     for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq, e->ws_xop, e->ws_hop, e->ws_part,
                     e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->ws_xn, e->ws_f, e->ws_xq, e->ws_moe_yp, e->ws_moe_grp, e->ws_moe_q, e->grid_sync})
         if (p) (void)hipFree(p);
+    for (void* p : e->ws_retired) (void)hipFree(p);
     if (e->stream) (void)hipStreamDestroy(e->stream);
     if (e->copy_stream) (void)hipStreamDestroy(e->copy_stream);
     if (e->copy_stream2) (void)hipStreamDestroy(e->copy_stream2);

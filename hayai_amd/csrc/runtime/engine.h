@@ -158,6 +158,12 @@ struct hh_engine {
     // Between hh_graph_begin and hh_graph_end the compute stream is being captured into a
     // HIP graph: nothing may allocate, synchronize, or bake per-launch state into a kernel.
     bool capturing = false;
+    // Instantiated graphs of this engine still alive.  Their kernels hold workspace
+    // addresses, so while any exists a workspace that grows keeps its old allocation here
+    // (freed when the last graph is destroyed, or with the engine) instead of freeing it.
+    int live_graphs = 0;
+    std::vector<void*> ws_retired;
+    void free_retired();
     hh_status no_capture(const char* what) const;
     hh_status kernel(const std::string& name, hipFunction_t* out);
     int resident_blocks(const std::string& name, int block);

@@ -52,6 +52,10 @@ struct Uring {
     io_uring_cqe* cqes = nullptr;
     unsigned entries = 0;
     bool broken = false;
+    // IORING_ASYNC_CANCEL_ANY (Linux 5.19 uapi; older kernels reject the request, which is
+    // harmless here) and the user_data tag of that cancel request's own completion.
+    static constexpr uint32_t kCancelAny = 1u << 2;
+    static constexpr uint64_t kCancelTag = ~(uint64_t)0;
 
     bool setup(unsigned n) {
         io_uring_params p;
@@ -92,7 +96,49 @@ struct Uring {
         if (fd >= 0) close(fd);
     }
 
-    // Reads `n` requests (each at most 1 GiB) into dst; 0 or -errno.  Every queued entry
+    // Waits for `outstanding` submitted requests to complete, dropping their results.  When
+    // waiting itself fails, asks the kernel to cancel everything in flight on the ring
+    // (IORING_ASYNC_CANCEL_ANY) and waits again; false if that fails too.
+    bool drain(unsigned outstanding) {
+        int failures = 0;
+        bool cancel_queued = false;
+        while (outstanding > 0) {
+            const unsigned submit = cancel_queued ? 1u : 0u;
+            const int rc = (int)syscall(__NR_io_uring_enter, fd, submit, 1u, IORING_ENTER_GETEVENTS, nullptr, 0);
+            if (rc < 0) {
+                if (errno == EINTR || errno == EAGAIN || errno == EBUSY) continue;
+                if (++failures > 4) return false;
+                if (!cancel_queued) {
+                    // entries queued but never submitted are dropped from the ring (no
+                    // SQPOLL here: the kernel reads the tail only inside io_uring_enter), so
+                    // the cancel request is the next entry the kernel sees
+                    unsigned tail = __atomic_load_n(sq_head, __ATOMIC_ACQUIRE);
+                    const unsigned idx = tail & *sq_mask;
+                    io_uring_sqe* e = &sqes[idx];
+                    memset(e, 0, sizeof *e);
+                    e->opcode = IORING_OP_ASYNC_CANCEL;
+                    e->fd = -1;
+                    e->cancel_flags = kCancelAny;
+                    e->user_data = kCancelTag;
+                    sq_array[idx] = idx;
+                    __atomic_store_n(sq_tail, tail + 1, __ATOMIC_RELEASE);
+                    cancel_queued = true;
+                }
+                continue;
+            }
+            if (cancel_queued && rc > 0) cancel_queued = false;  // the cancel request went in
+            unsigned head = __atomic_load_n(cq_head, __ATOMIC_RELAXED);
+            const unsigned ctail = __atomic_load_n(cq_tail, __ATOMIC_ACQUIRE);
+            while (head != ctail) {
+                if (cqes[head & *cq_mask].user_data != kCancelTag && outstanding > 0) outstanding--;
+                head++;
+            }
+            __atomic_store_n(cq_head, head, __ATOMIC_RELEASE);
+        }
+        return true;
+    }
+
+    // Reads `n` requests (each at most 1 GiB) into dst; 0 or -errno.  Every submitted entry
     // is completed and reaped before returning, also on error, so no request outlives the
     // call.
     int read_batch(int file, char* dst, const IoReq* reqs, size_t n, bool async, std::string* why) {
@@ -125,11 +171,15 @@ struct Uring {
                                             IORING_ENTER_GETEVENTS, nullptr, 0);
                 if (rc < 0) {
                     if (errno == EINTR || errno == EAGAIN || errno == EBUSY) continue;
-                    // the ring cannot be trusted with what it still holds: the caller drops
-                    // it (closing its descriptor) and reads with pread from then on
+                    const int e = errno;
+                    // Requests already submitted may still be copying into dst on the
+                    // kernel's worker threads: wait for every one of them before returning,
+                    // so none outlives the call.  The ring is then dropped by the caller
+                    // (pread from then on).  Entries never submitted never run.
                     broken = true;
                     *why = "io_uring_enter failed";
-                    return -errno;
+                    if (!drain(submitted - reaped)) *why = "io_uring_enter failed; in-flight reads not confirmed";
+                    return -e;
                 }
                 submitted += (unsigned)rc;
                 unsigned head = __atomic_load_n(cq_head, __ATOMIC_RELAXED);

@@ -124,3 +124,75 @@ def test_graph_refuses_workspace_growth():
         g.free()
     finally:
         eng.close()
+
+
+def test_graph_refuses_buffer_operations(engine):
+    # fills, copies, writes and reads would record memset/memcpy nodes (or synchronise)
+    # inside the capture; they are refused and the engine stays usable
+    print("[case] graph buffer operations", flush=True)
+    a = engine.alloc(1024)
+    b = engine.alloc(1024)
+    host = np.arange(256, dtype=np.float32)
+    for name, fn in (("fill", lambda: a.fill(0)), ("copy", lambda: a.copy_from(b, 1024)),
+                     ("write", lambda: a.write(host)), ("read", lambda: a.read(np.float32, 256))):
+        with pytest.raises(hayai_amd.HipError) as e:
+            engine.capture(fn)
+        assert e.value.status_name == "HH_ERR_INVALID", name
+    a.write(host)
+    b.copy_from(a, 1024)
+    engine.sync()
+    assert np.array_equal(b.read(np.float32, 256), host)
+
+
+def test_graph_replay_after_workspace_growth():
+    # A graph holds workspace addresses in its kernels' arguments.  Capture a Q6_K GEMV
+    # (its x digits live in a workspace sized for n = 1024), then let a Q4_K_M batched FFN
+    # grow that workspace (its per-token Q6_K GEMVs run at n = d_ff = 2048): replays must
+    # still equal the eager GEMV, since the old allocation stays alive while the graph does.
+    print("[case] graph replay after workspace growth", flush=True)
+    eng = hayai_amd.HipEngine(0)
+    try:
+        m, n = 512, 1024
+        w6 = synth.matrix(hayai_amd.Q6_K, m, n, 41)
+        wbuf = eng.upload(w6)
+        x = synth.normal(42, n)
+        xbuf = eng.upload(x)
+        y_eager = eng.alloc(4 * m)
+        eng.gemv_dev(hayai_amd.Q6_K, m, n, wbuf, 0, xbuf, 0, y_eager, 0)
+        eng.sync()
+        ref = y_eager.read(np.float32, m)
+        assert np.max(np.abs(ref - oracle.gemv(oracle.Q6_K, m, n, w6, x))) <= 1e-3 * np.max(np.abs(ref))
+        y = eng.alloc(4 * m)
+        g = eng.capture(lambda: eng.gemv_dev(hayai_amd.Q6_K, m, n, wbuf, 0, xbuf, 0, y, 0))
+        g.launch()
+        eng.sync()
+        assert np.array_equal(y.read(np.float32, m).view(np.uint32), ref.view(np.uint32))
+
+        d_model, d_ff, B = 1024, 2048, 8
+        Q4, Q6 = hayai_amd.Q4_K, hayai_amd.Q6_K
+        gate = hayai_amd.QuantMatrix("ffn_gate", d_model, d_ff, Q4)
+        up = hayai_amd.QuantMatrix("ffn_up", d_model, d_ff, Q4)
+        down = hayai_amd.QuantMatrix("ffn_down", d_ff, d_model, Q6)
+        lay = hayai_amd.LayerPackLayout.ffn_only(gate, up, down)
+        pack = eng.alloc(lay.total)
+        pack.write(synth.matrix(Q4, d_ff, d_model, 43), lay.gate_off)
+        pack.write(synth.matrix(Q4, d_ff, d_model, 44), lay.up_off)
+        pack.write(synth.matrix(Q6, d_model, d_ff, 45), lay.down_off)
+        desc = eng.ffn_desc((Q4, Q4, Q6), d_model, d_ff, lay)
+        xb = np.stack([synth.normal(46 + b, d_model) for b in range(B)])
+        yb = eng.ffn_batched(desc, pack, 0, xb)  # grows the GEMV digit workspace
+        assert np.all(np.isfinite(yb))
+
+        for rep in range(3):
+            y.fill(0)
+            g.launch()
+            eng.sync()
+            assert np.array_equal(y.read(np.float32, m).view(np.uint32), ref.view(np.uint32)), f"replay {rep}"
+            eng.ffn_batched(desc, pack, 0, xb)  # eager work between replays
+        g.free()
+        # with no graph left, the engine still runs the GEMV eagerly
+        eng.gemv_dev(hayai_amd.Q6_K, m, n, wbuf, 0, xbuf, 0, y, 0)
+        eng.sync()
+        assert np.array_equal(y.read(np.float32, m).view(np.uint32), ref.view(np.uint32))
+    finally:
+        eng.close()

@@ -146,3 +146,54 @@ def test_bind_and_dma_validation(engine):
     engine.sync()
     assert (mirror.read(np.uint8, 4096, off) == 7).all()
     st.free()
+
+
+def test_stream_70b_full_layer(engine):
+    # configs[4] at its real shape: 70B IQ2_XXS FFN layers (d_model 8192, d_ff 28672,
+    # 181.7 MB per layer) through two pinned slots.  Every region is >= 32 MB, so each DMA
+    # goes out as two halves on two copy streams.  Streamed == resident bit for bit, and
+    # every layer against the oracle.
+    n_layers, d_model, d_ff = 2, 8192, 28672
+    print(f"[case] stream iq2_xxs 70B layer {d_model}x{d_ff} layers={n_layers}", flush=True)
+    lay, packs, mats = make_layers(n_layers, d_model=d_model, d_ff=d_ff, cfg=5)
+    desc = engine.ffn_desc((T, T, T), d_model, d_ff, lay)
+    xs = np.stack([synth.normal(synth.seed_for(5, l, synth.ACT), d_model) for l in range(n_layers)])
+    xbuf = engine.upload(xs)
+    got = streamed_outputs(engine, desc, lay, packs, xbuf, d_model)
+    ref = resident_outputs(engine, desc, lay, packs, xbuf, d_model)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    oracle.set_threads(min(16, oracle.max_threads()))
+    try:
+        for l in range(n_layers):
+            r = oracle.ffn((T, T, T), d_model, d_ff, *mats[l], xs[l])
+            err = np.max(np.abs(got[l] - r)) / np.max(np.abs(r))
+            print(f"[case] layer {l} rel_err={err:.3e}", flush=True)
+            assert err <= 1e-3
+    finally:
+        oracle.set_threads(1)
+
+
+@pytest.mark.parametrize("split", [1, 0])
+def test_large_dma_bytes(split, monkeypatch):
+    # A DMA of 32 MB or more is split over two copy streams (HAYAI_HIP_DMA_SPLIT=1, the
+    # default): an odd length at an odd offset, into the second layer of a two-layer slot,
+    # must land byte for byte, with the switch on and off.
+    monkeypatch.setenv("HAYAI_HIP_DMA_SPLIT", str(split))
+    print(f"[case] large dma split={split}", flush=True)
+    eng = hayai_amd.HipEngine(0)
+    try:
+        layer_bytes = 80 << 20
+        st = hayai_amd.StreamingScratch(eng, layer_bytes, k_chunk=2, n_slots=2)
+        off, length = 12345, (70 << 20) + 77
+        for layer in (1, 2):  # slot 0 at in-slot offset layer_bytes, then slot 1 at 0
+            pat = ((np.arange(layer_bytes, dtype=np.uint64) * (7 + layer)) % 251).astype(np.uint8)
+            st.host_slot(layer)[:] = pat
+            st.dma(layer, off, length)
+            mirror, moff = st.weight_bind(layer)
+            assert moff == (layer % 2) * layer_bytes
+            eng.sync()
+            back = mirror.read(np.uint8, length, moff + off)
+            assert np.array_equal(back, pat[off:off + length]), f"layer {layer}"
+        st.free()
+    finally:
+        eng.close()
