@@ -79,6 +79,19 @@ def build_runtime(verbose: bool = False) -> list[str]:
     return objs
 
 
+def build_noalloc(verbose: bool = False) -> str:
+    """The one host+device translation unit (runtime/noalloc.hip: the no-allocation entry
+    point's file-scope scratch array and its address lookup), compiled by hipcc for gfx950."""
+    os.makedirs(BUILD, exist_ok=True)
+    hipcc = os.path.join(rocm_path(), "bin", "hipcc")
+    src = os.path.join(CSRC, "runtime", "noalloc.hip")
+    obj = os.path.join(BUILD, "noalloc.o")
+    _run([hipcc, f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-fPIC", "-Wall",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          f"-I{ROOT}/include", "-c", src, "-o", obj], verbose)
+    return obj
+
+
 def link(objs: list[str], verbose: bool = False) -> str:
     blob_s = os.path.join(BUILD, "blob.S")
     with open(blob_s, "w") as f:
@@ -101,11 +114,12 @@ def link(objs: list[str], verbose: bool = False) -> str:
 def build(verbose: bool = False) -> str:
     """Compile everything; always rebuilds (this is the "does it build" check)."""
     t0 = time.time()
-    with ThreadPoolExecutor(max_workers=2) as ex:
+    with ThreadPoolExecutor(max_workers=3) as ex:
         fk = ex.submit(build_kernels, verbose)
         fr = ex.submit(build_runtime, verbose)
+        fn = ex.submit(build_noalloc, verbose)
         fk.result()
-        objs = fr.result()
+        objs = fr.result() + [fn.result()]
     lib = link(objs, verbose)
     if verbose:
         print(f"built {lib} in {time.time() - t0:.1f}s", flush=True)

@@ -511,6 +511,20 @@ hh_status hh_ffn_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, siz
                           (float*)((char*)y->ptr + y_off));
 }
 
+hh_status hh_ffn_dev_noalloc(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                             const hh_buf* x, size_t x_off, hh_buf* y, size_t y_off) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_ffn(e, d, pack, pack_off));
+    HH_TRY(check_engine(e, x, "x"));
+    HH_TRY(check_engine(e, y, "y"));
+    HH_TRY(check_range(x, x_off, d->d_model * sizeof(float), "x"));
+    HH_TRY(check_range(y, y_off, d->d_model * sizeof(float), "y"));
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    return e->enqueue_ffn_noalloc(d, (const uint8_t*)pack->ptr + pack_off,
+                                  (const float*)((const char*)x->ptr + x_off), (float*)((char*)y->ptr + y_off));
+}
+
 hh_status hh_ffn_block_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
                            const hh_buf* norm, size_t norm_off, float eps, const hh_buf* x, size_t x_off, hh_buf* y,
                            size_t y_off) {

@@ -276,7 +276,8 @@ hh_status hh_engine::enqueue_lut(size_t m, size_t n, const uint8_t* w, const flo
     return launch(f, (uint32_t)grid, 256, a);
 }
 
-hh_status hh_engine::enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w, const float* x, float* y) {
+hh_status hh_engine::enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w, const float* x, float* y,
+                                  void* xq_ws) {
     const Format* f = format_of(type);
     if (!f) return fail(HH_ERR_KERNEL_MISSING, "no GEMV kernel for GGML type %d", type);
     size_t rb;
@@ -295,7 +296,7 @@ hh_status hh_engine::enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w
         if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
     }
     if (type == HH_TYPE_Q6_K) {
-        hh_status st = enqueue_ring_gemv(true, m, n, w, x, y);
+        hh_status st = enqueue_ring_gemv(true, m, n, w, x, y, xq_ws);
         if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
     }
     std::string name;
@@ -328,7 +329,7 @@ hh_status hh_engine::enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w
 }
 
 hh_status hh_engine::enqueue_gateup(int tg, int tu, size_t d_ff, size_t d_model, const uint8_t* wg,
-                                    const uint8_t* wu, const float* x, float* h, int act) {
+                                    const uint8_t* wu, const float* x, float* h, int act, float* gu_ws) {
     const Format* f = format_of(tg);
     if (!f || !format_of(tu)) return fail(HH_ERR_KERNEL_MISSING, "no GEMV kernel for GGML type %d/%d", tg, tu);
     size_t rb;
@@ -358,13 +359,19 @@ hh_status hh_engine::enqueue_gateup(int tg, int tu, size_t d_ff, size_t d_model,
         return launch(fn, (uint32_t)std::max<size_t>(1, std::min(need, cap)), (uint32_t)block, a);
     }
     // Unfused: gate and up in their own formats, then act(g) * u.
-    HH_TRY(grow(&ws_g, &ws_g_cap, d_ff * sizeof(float)));
-    HH_TRY(grow(&ws_u, &ws_u_cap, d_ff * sizeof(float)));
-    HH_TRY(enqueue_gemv(tg, d_ff, d_model, wg, x, (float*)ws_g));
-    HH_TRY(enqueue_gemv(tu, d_ff, d_model, wu, x, (float*)ws_u));
+    float *g = gu_ws, *u = gu_ws ? gu_ws + d_ff : nullptr;
+    void* xq = gu_ws ? (void*)(gu_ws + 2 * d_ff) : nullptr;
+    if (!gu_ws) {
+        HH_TRY(grow(&ws_g, &ws_g_cap, d_ff * sizeof(float)));
+        HH_TRY(grow(&ws_u, &ws_u_cap, d_ff * sizeof(float)));
+        g = (float*)ws_g;
+        u = (float*)ws_u;
+    }
+    HH_TRY(enqueue_gemv(tg, d_ff, d_model, wg, x, g, xq));
+    HH_TRY(enqueue_gemv(tu, d_ff, d_model, wu, x, u, xq));
     hipFunction_t fn;
     HH_TRY(kernel("hh_act_mul_kernel", &fn));
-    hh_act_args a{(const float*)ws_g, (const float*)ws_u, h, (uint32_t)d_ff, act};
+    hh_act_args a{(const float*)g, (const float*)u, h, (uint32_t)d_ff, act};
     return launch(fn, (uint32_t)((d_ff + 255) / 256), 256, a);
 }
 
@@ -540,7 +547,7 @@ bool hh_engine::ring_ok(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* 
 }
 
 hh_status hh_engine::enqueue_q4k_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu,
-                                         const float* x, const float* norm, float eps) {
+                                         const float* x, const float* norm, float eps, uint8_t* hx) {
     const size_t dm = d->d_model, df = d->d_ff;
     const int w1 = dm <= 4096 ? 1 : 2;
     const std::string name = "hh_q4k_gu_ring_g" + std::to_string(w1) + (norm ? "_n" : "");
@@ -561,8 +568,11 @@ hh_status hh_engine::enqueue_q4k_ring_gu(const hh_ffn_desc* d, const uint8_t* wg
         blocks_per_cu[name] = occ;
     }
     const size_t grid = ring_grid(occ, ring_gu_per_cu, cus);
-    HH_TRY(grow(&ws_hq, &ws_hq_cap, 2 * df + (df / 8) * 4 + 16));
-    GurArgs a{wg, wu, x, (uint8_t*)ws_hq, norm, (uint64_t)((dm / 256) * 144), (uint32_t)dm, (uint32_t)df, d->act, eps};
+    if (!hx) {
+        HH_TRY(grow(&ws_hq, &ws_hq_cap, hh::ring_digits_bytes(df)));
+        hx = (uint8_t*)ws_hq;
+    }
+    GurArgs a{wg, wu, x, hx, norm, (uint64_t)((dm / 256) * 144), (uint32_t)dm, (uint32_t)df, d->act, eps};
     void* params[] = {&a};
     hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
     if (err != hipSuccess) return hip_fail(err, "launch(ring q4k gate/up)");
@@ -609,15 +619,19 @@ hh_status hh_engine::launch_dn_ring(bool q6, size_t m, size_t n, const uint8_t* 
 
 // x -> the ring down kernels' digit form (q1 | q2 | one scale per 8), then the Q6_K ring
 // kernel as a GEMV: the LM head of Q4_K_M files (output.weight in Q6_K).
-hh_status hh_engine::enqueue_ring_gemv(bool q6, size_t m, size_t n, const uint8_t* w, const float* x, float* y) {
+hh_status hh_engine::enqueue_ring_gemv(bool q6, size_t m, size_t n, const uint8_t* w, const float* x, float* y,
+                                       void* xq_ws) {
     if (!ring || n % (q6 ? 512 : 256) || n > 32768 || m > UINT32_MAX / 2 || (((uintptr_t)w | (uintptr_t)x) & 15u))
         return HH_ERR_UNSUPPORTED_DEVICE;
-    HH_TRY(grow(&ws_xq, &ws_xq_cap, 2 * n + (n / 8) * 4 + 16));
+    if (!xq_ws) {
+        HH_TRY(grow(&ws_xq, &ws_xq_cap, hh::ring_digits_bytes(n)));
+        xq_ws = ws_xq;
+    }
     hipFunction_t fn;
     HH_TRY(kernel("hh_x_digits", &fn));
-    hh_xd_args xa{x, (uint8_t*)ws_xq, (uint32_t)n, 0u};
+    hh_xd_args xa{x, (uint8_t*)xq_ws, (uint32_t)n, 0u};
     HH_TRY(launch(fn, (uint32_t)((n / 8 + 255) / 256), 256, xa));
-    return launch_dn_ring(q6, m, n, w, (const uint8_t*)ws_xq, y, nullptr);
+    return launch_dn_ring(q6, m, n, w, (const uint8_t*)xq_ws, y, nullptr);
 }
 
 hh_status hh_engine::check_device_error() {
@@ -715,6 +729,44 @@ hh_status hh_engine::enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, cons
     }
     HH_TRY(enqueue_ffn_begin(d, pack, x));
     return enqueue_ffn_finish(d, pack, y);
+}
+
+// The FFN op with every intermediate in the device's fixed scratch array instead of the
+// engine's workspaces (hh_ffn_dev_noalloc): nothing here allocates.  The ring layouts keep
+// h's digits in the scratch; the others run the two-step form (gate/up + activation into an
+// f32 h, then the down GEMV) with h, the unfused form's gate and up outputs and a Q6_K
+// GEMV's x digits in the scratch.  The one-launch forms (persistent Q4_K, small Q4_0/Q8_0),
+// whose grid barriers keep per-launch state, are not used.
+hh_status hh_engine::enqueue_ffn_noalloc(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y) {
+    if (!noalloc_ws)
+        return fail(HH_ERR_RUNTIME, "ffn_dev_noalloc: no scratch array on device %d (%s)", device,
+                    noalloc_error.c_str());
+    const size_t dm = d->d_model, df = d->d_ff;
+    if (df > HH_NOALLOC_MAX_D_FF)
+        return fail(HH_ERR_INVALID, "ffn_dev_noalloc: d_ff=%zu exceeds the scratch limit of %u", df,
+                    (unsigned)HH_NOALLOC_MAX_D_FF);
+    uint8_t* ws = (uint8_t*)noalloc_ws;
+    const uint8_t* wg = pack + d->gate_off;
+    const uint8_t* wu = pack + d->up_off;
+    const uint8_t* wd = pack + d->down_off;
+    if (ring_ok(d, wg, wu, wd, x)) {
+        HH_TRY(enqueue_q4k_ring_gu(d, wg, wu, x, nullptr, 0.f, ws));
+        HH_TRY(launch_dn_ring(d->type_down == HH_TYPE_Q6_K, dm, df, wd, ws, y, nullptr));
+        ffn_calls += 3;
+        return HH_OK;
+    }
+    // [h: df f32][g: df f32][u: df f32][x digits of the widest ring GEMV]
+    const size_t widest = std::min<size_t>(std::max(dm, df), 32768);
+    const size_t need = 3 * df * sizeof(float) + hh::ring_digits_bytes(widest);
+    if (need > HH_NOALLOC_SCRATCH_BYTES)
+        return fail(HH_ERR_INVALID, "ffn_dev_noalloc: d_model=%zu, d_ff=%zu need %zu bytes of scratch, more than %u",
+                    dm, df, need, (unsigned)HH_NOALLOC_SCRATCH_BYTES);
+    float* h = (float*)ws;
+    float* gu = h + df;
+    HH_TRY(enqueue_gateup(d->type_gate, d->type_up, df, dm, wg, wu, x, h, d->act, gu));
+    HH_TRY(enqueue_gemv(d->type_down, dm, df, wd, h, y, (void*)(gu + 2 * df)));
+    ffn_calls += 3;
+    return HH_OK;
 }
 
 // Must match struct hh_sffn_args in kernels/small_ffn.hip.
@@ -1356,6 +1408,14 @@ hh_status engine_create(int device, hh_engine** out) {
     for (const std::string& k : required_kernels()) {
         hipFunction_t f;
         if (hh_status st = e->kernel(k, &f); st != HH_OK) return bail(st);
+    }
+    {
+        // the no-allocation entry point's scratch array: its address on this device, once
+        void* p = nullptr;
+        if (noalloc_scratch(device, &p) == HH_OK)
+            e->noalloc_ws = p;
+        else
+            e->noalloc_error = last_error();
     }
     if (const char* b = getenv("HAYAI_HIP_BLOCKS_PER_CU")) e->blocks_per_cu_override = atoi(b);
     if (const char* g = getenv("HAYAI_HIP_Q4K_GENERIC")) e->q4k_generic = atoi(g) != 0;

@@ -54,6 +54,14 @@ hh_status row_bytes(int ggml_type, size_t n, size_t* out);
 hh_status validate_shape(int ggml_type, size_t m, size_t n);
 hh_status validate_weights(int ggml_type, size_t m, size_t n, size_t len);
 
+// Bytes of the ring kernels' digit form of an n-element activation (q1[n] | q2[n] | one
+// f32 scale per 8 elements, + 16 bytes of slack for the kernels' vector tail).
+inline size_t ring_digits_bytes(size_t n) { return 2 * n + (n / 8) * 4 + 16; }
+
+// The device address of noalloc.hip's fixed scratch array on `device` (which must be the
+// current device): looked up once per device and kept.
+hh_status noalloc_scratch(int device, void** out);
+
 // Team configurations instantiated in gemv.hip, in selection order.
 struct TeamCfg {
     int team;
@@ -165,6 +173,11 @@ struct hh_engine {
     std::vector<void*> ws_retired;
     void free_retired();
     hh_status no_capture(const char* what) const;
+    // hh_ffn_dev_noalloc: this device's fixed scratch array (noalloc.hip), resolved when the
+    // engine is created; null when that failed (the reason in noalloc_error).
+    void* noalloc_ws = nullptr;
+    std::string noalloc_error;
+    hh_status enqueue_ffn_noalloc(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y);
     hh_status kernel(const std::string& name, hipFunction_t* out);
     int resident_blocks(const std::string& name, int block);
     template <class A>
@@ -177,10 +190,14 @@ struct hh_engine {
     hh_status grow(void** p, size_t* cap, size_t need);
 
     // Enqueue one GEMV y = W . x on the compute stream (all pointers device-visible).
-    hh_status enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w, const float* x, float* y);
+    // xq_ws: room for a Q6_K GEMV's x digits (hh_ring_digits_bytes(n)); null: ws_xq.
+    hh_status enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w, const float* x, float* y,
+                           void* xq_ws = nullptr);
     // Enqueue the fused or unfused gate/up + activation into h.
+    // gu_ws: room for the unfused form's gate and up outputs (2 * d_ff floats, then the
+    // GEMVs' x digits); null: ws_g / ws_u (/ ws_xq).
     hh_status enqueue_gateup(int type_g, int type_u, size_t d_ff, size_t d_model, const uint8_t* wg,
-                             const uint8_t* wu, const float* x, float* h, int act);
+                             const uint8_t* wu, const float* x, float* h, int act, float* gu_ws = nullptr);
     hh_status enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y);
     hh_status enqueue_small_ffn(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                                 const float* x, float* y);
@@ -203,12 +220,14 @@ struct hh_engine {
     // barrier (q4k_ffn.hip); HH_ERR_UNSUPPORTED_DEVICE when the shape, alignment or
     // occupancy does not allow it.
     bool ring_ok(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd, const float* x) const;
+    // hx: where h's digits go (hh_ring_digits_bytes(d_ff)); null: ws_hq.
     hh_status enqueue_q4k_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const float* x,
-                                  const float* norm = nullptr, float eps = 0.f);
+                                  const float* norm = nullptr, float eps = 0.f, uint8_t* hx = nullptr);
     hh_status enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd, float* y, const float* res = nullptr);
     hh_status launch_dn_ring(bool q6, size_t m, size_t n, const uint8_t* w, const uint8_t* hx, float* y,
                              const float* res);
-    hh_status enqueue_ring_gemv(bool q6, size_t m, size_t n, const uint8_t* w, const float* x, float* y);
+    hh_status enqueue_ring_gemv(bool q6, size_t m, size_t n, const uint8_t* w, const float* x, float* y,
+                                void* xq_ws = nullptr);
     hh_status enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                                const float* x, float* y);
     // Batched GEMV Y[b][m] = W . X[b] (x, y device pointers, row-major by token).  Q4_K with

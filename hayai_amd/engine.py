@@ -563,6 +563,13 @@ class HipEngine:
         _check(self.lib.hh_ffn_dev(self.handle, C.byref(desc), pack.handle, pack_off, x.handle, x_off, y.handle,
                                    y_off))
 
+    def ffn_dev_noalloc(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, x: DeviceBuffer, x_off: int,
+                        y: DeviceBuffer, y_off: int) -> None:
+        """ffn_dev with its intermediate in the GPU's fixed scratch array (no allocation at
+        call time; calls that overlap on one GPU race on that array).  Enqueue only."""
+        _check(self.lib.hh_ffn_dev_noalloc(self.handle, C.byref(desc), pack.handle, pack_off, x.handle, x_off,
+                                           y.handle, y_off))
+
     def ffn_block_dev(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, norm: DeviceBuffer,
                       norm_off: int, eps: float, x: DeviceBuffer, x_off: int, y: DeviceBuffer, y_off: int) -> None:
         """The FFN residual block (ffn_apply, hybrid_infer.rs:883-936): y = x + FFN(rms_norm(x,

@@ -232,6 +232,21 @@ hh_status hh_ffn(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t 
 hh_status hh_ffn_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
                      const hh_buf* x, size_t x_off, hh_buf* y, size_t y_off);
 
+/* No counterpart in the reference.  For callers that cannot allocate device memory at call
+ * time (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * hh_ffn_dev with the d_ff intermediate in a fixed per-GPU scratch array of
+ * HH_NOALLOC_SCRATCH_BYTES (held by each GPU the library runs on until the process ends)
+ * instead of the engine's growable workspaces; it calls no hipMalloc/hipFree.  Same kernels
+ * and results as hh_ffn_dev's two-launch forms (the ring kernels for Q4_K and Q4_K_M layers,
+ * gate/up + down otherwise).  Limits: d_ff <= HH_NOALLOC_MAX_D_FF, and for layouts other
+ * than Q4_K / Q4_K_M 12 * d_ff + 2.5 * min(max(d_model, d_ff), 32768) bytes must fit the
+ * array; HH_ERR_INVALID otherwise.  All calls on one GPU share the array: calls that overlap
+ * on one GPU (two engines, or two threads) race.  Enqueue only. */
+#define HH_NOALLOC_SCRATCH_BYTES (512u * 1024u)
+#define HH_NOALLOC_MAX_D_FF 32768u
+hh_status hh_ffn_dev_noalloc(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                             const hh_buf* x, size_t x_off, hh_buf* y, size_t y_off);
+
 /* The FFN residual block of one token (ffn_apply, crates/hayai-core/src/hybrid_infer.rs:
  * 883-936): y = x + FFN(RMSNorm(x)), RMSNorm as rms_norm (crates/hayai-cpu/src/attention.rs:
  * 142-147): x * (1 / sqrt(mean(x^2) + eps)) * norm.  norm: d_model floats; y may be x (the
