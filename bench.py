@@ -62,19 +62,89 @@ def gateup_bytes() -> int:
     return 2 * D_FF * hayai_amd.row_bytes(Q4_K, D_MODEL) + 4 * D_MODEL + 4 * D_FF
 
 
+def gateup_bytes_n() -> int:
+    """The gate/up kernel of the residual block: W_gate + W_up + x + the norm weight + h (f32)."""
+    return gateup_bytes() + 4 * D_MODEL
+
+
+def host_cores() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def cpu_time(fn, budget_s: float, threads: int):
+    """Median seconds per fn(i) call of the oracle on `threads` host threads (calls repeat
+    for about budget_s seconds, at least 4; the first is a warm-up).  Returns (seconds,
+    calls, total seconds)."""
+    import oracle
+
+    oracle.build()
+    oracle.set_threads(threads)
+    times, i, t_end = [], 0, time.time() + budget_s
+    while time.time() < t_end or len(times) < 4:
+        t0 = time.perf_counter()
+        fn(i)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    oracle.set_threads(1)
+    return statistics.median(times[1:]), len(times), sum(times)
+
+
+def cpu_entry(fn, budget_s: float, work_per_call: float, what: str, unit: str = "GB/s") -> dict:
+    """cpu_baseline of a workload: the oracle's restatement of the reference's CPU path (rayon
+    over rows there, OpenMP over rows here), timed on all host cores (up to 16) for 2/3 of the
+    budget and on one core for the rest.  value = work_per_call (bytes, or flops for GFLOPS)
+    / median seconds per call / 1e9, in the workload's own unit."""
+    cores = host_cores()
+    threads = max(1, min(16, cores))
+    t_all, n_all, tot_all = cpu_time(fn, budget_s * 2 / 3, threads)
+    t_one, n_one, tot_one = cpu_time(fn, budget_s / 3, 1)
+    model = cpu_model()
+    return {"value": round(work_per_call / t_all / 1e9, 3), "unit": unit, "cores": threads, "kind": "port",
+            "sample": (f"{what}: {n_all} calls in {tot_all:.1f}s, median {t_all * 1e3:.3f} ms per call; "
+                       f"{threads} OpenMP threads of {cores} host cores ({model})"),
+            "cpu_model": model, "host_cores": cores,
+            "one_core": {"value": round(work_per_call / t_one / 1e9, 3), "unit": unit, "cores": 1,
+                         "sample": f"{n_one} calls in {tot_one:.1f}s, median {t_one * 1e3:.3f} ms per call"}}
+
+
+LUT_M, LUT_N = 1536, 576  # hayai bench: SmolLM2-135M's FFN layer (crates/hayai-cli/src/main.rs:601-646)
+LUT_TABLE = np.array([-0.5, -0.4, -0.3, -0.2, -0.1, 0.0, 0.1, 0.2, 0.3, 0.4, 0.5, 0.6, 0.7, 0.8, 0.9, 1.0],
+                     np.float32)
+
+
+def lut_cpu_baseline(budget_s: float) -> dict:
+    """The reference's named CPU baseline: hayai-cpu's cpu_lut_matmul_q4 (matmul.rs:48-82) at
+    `hayai bench`'s shape and inputs (1536x576, every weight byte 0xAB, x = 1.0), GFLOPS =
+    2*m*n / time per call, as main.rs:601-646 counts them."""
+    import oracle
+
+    w = np.full(LUT_M * LUT_N // 2, 0xAB, np.uint8)
+    x = np.ones(LUT_N, np.float32)
+    e = cpu_entry(lambda i: oracle.lut_matmul_q4(LUT_M, LUT_N, w, LUT_TABLE, x), budget_s,
+                  2.0 * LUT_M * LUT_N, f"oracle cpu_lut_matmul_q4 {LUT_M}x{LUT_N} (0xAB weights, x = 1)", "GFLOPS")
+    return e
+
+
 def cpu_baseline(engine, pack, lay, stride, xs, budget_s: float) -> dict:
     """Time the oracle FFN (fp32 restatement of gemv_q4_k, q4k.rs:206-256) on host cores
-    over a bounded sample of the benchmark's own layers (copied back from HBM)."""
+    over a bounded sample of the benchmark's own layers (copied back from HBM); the
+    reference's LUT MatMul baseline is reported beside it."""
     import oracle
     import hayai_amd
 
-    oracle.build()
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count() or 1
-    threads = max(1, min(16, cores))
-    oracle.set_threads(threads)
     n_layers = 4  # 4 x 99 MB rotating weight sets: far beyond any host LLC
     rg = hayai_amd.row_bytes(Q4_K, D_MODEL)
     rd = hayai_amd.row_bytes(Q4_K, D_FF)
@@ -85,66 +155,13 @@ def cpu_baseline(engine, pack, lay, stride, xs, budget_s: float) -> dict:
         wu = pack.read(np.uint8, D_FF * rg, base + lay.up_off)
         wd = pack.read(np.uint8, D_MODEL * rd, base + lay.down_off)
         mats.append((wg, wu, wd))
-    times = []
-    t_end = time.time() + budget_s
-    i = 0
-    while time.time() < t_end or len(times) < 3:
-        wg, wu, wd = mats[i % n_layers]
-        t0 = time.perf_counter()
-        oracle.ffn((Q4_K, Q4_K, Q4_K), D_MODEL, D_FF, wg, wu, wd, xs[i % n_layers])
-        times.append(time.perf_counter() - t0)
-        i += 1
-    warm = times[min(3, len(times) - 1):] or times
-    t_layer = statistics.median(warm)
-    gbs = layer_bytes() / t_layer / 1e9
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {
-        "value": round(gbs, 3),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"oracle fp32 FFN (gate/up/down gemv_q4_k + SiLU) over {n_layers} of the 32 benchmark layers "
-                   f"in rotation, {len(times)} layer-FFNs in {sum(times):.1f}s, median {t_layer * 1e3:.1f} ms/layer "
-                   f"after 3 warm-ups; {threads} OpenMP threads of {cores} host cores ({cpu_model})"),
-        "ffn_tok_s": round(1.0 / (t_layer * LAYERS), 4),
-    }
-
-
-def cpu_time(fn, budget_s: float):
-    """Median seconds per fn(i) call of the oracle on the host cores (calls repeat for about
-    budget_s seconds, at least 3; the first is a warm-up).  Returns (seconds, threads, calls,
-    total seconds)."""
-    import oracle
-
-    oracle.build()
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count() or 1
-    threads = max(1, min(16, cores))
-    oracle.set_threads(threads)
-    times, i, t_end = [], 0, time.time() + budget_s
-    while time.time() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        fn(i)
-        times.append(time.perf_counter() - t0)
-        i += 1
-    return statistics.median(times[1:]), threads, len(times), sum(times)
-
-
-def cpu_entry(fn, budget_s: float, bytes_per_call: float, what: str) -> dict:
-    """cpu_baseline of a workload: the oracle's restatement of the reference's CPU path,
-    GB/s over the same algorithmic bytes as the GPU value."""
-    t, threads, n, total = cpu_time(fn, budget_s)
-    return {"value": round(bytes_per_call / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{what}: {n} calls in {total:.1f}s, median {t * 1e3:.2f} ms per call; {threads} OpenMP threads"}
+    e = cpu_entry(lambda i: oracle.ffn((Q4_K, Q4_K, Q4_K), D_MODEL, D_FF, *mats[i % n_layers], xs[i % n_layers]),
+                  budget_s, layer_bytes(),
+                  f"oracle fp32 FFN (gate/up/down gemv_q4_k + SiLU) over {n_layers} of the 32 benchmark layers")
+    t_layer = layer_bytes() / (e["value"] * 1e9)
+    e["ffn_tok_s"] = round(1.0 / (t_layer * LAYERS), 4)
+    e["lut_matmul_q4"] = lut_cpu_baseline(max(3.0, budget_s / 3))
+    return e
 
 
 def roofline_step(gbs: float, what: str) -> dict:
@@ -890,6 +907,252 @@ def bench_block(eng, pack, lay, stride, desc, args) -> int:
     return 0
 
 
+def bench_lut(eng, args) -> int:
+    """`hayai bench` (crates/hayai-cli/src/main.rs:601-646) on the GPU: the Q4 LUT MatMul
+    (Hayai's 4-bit dictionary format) at SmolLM2-135M's FFN layer shape, 1536x576, every
+    weight byte 0xAB, x = 1.0, GFLOPS = 2*m*n / time per call.  value: device-resident
+    operands, kernel launches back to back (events on the compute stream); host_io: the
+    reference's execute_lut_matmul form (host arrays in and out, blocking, PCIe included).
+    The 442 KB weight matrix stays in cache, so the HBM roofline is taken on the same kernel
+    at the 8B gate shape (14336x4096, 29 MB) over 10 rotating copies (294 MB, beyond the
+    256 MB last-level cache).  cpu_baseline: the oracle's cpu_lut_matmul_q4 at the bench
+    shape (the reference's named CPU baseline), all host cores and one core."""
+    M, N = LUT_M, LUT_N
+    w = np.full(M * N // 2, 0xAB, np.uint8)
+    x = np.ones(N, np.float32)
+    wb, tb, xb, yb = eng.upload(w), eng.upload(LUT_TABLE), eng.upload(x), eng.alloc(4 * M)
+    inner = 100
+
+    def run():
+        for _ in range(inner):
+            eng.lut_gemv_dev(M, N, wb, 0, tb, 0, xb, 0, yb, 0)
+
+    for _ in range(args.warmup):
+        run()
+    eng.sync()
+    e0, e1 = eng.event(), eng.event()
+    e0.record()
+    for _ in range(args.steps):
+        run()
+    e1.record()
+    eng.sync()
+    ms = e0.elapsed_ms(e1) / (args.steps * inner)
+    y = yb.read(np.float32, M)
+    flops = 2.0 * M * N
+    gflops = flops / (ms / 1e3) / 1e9
+    # host-array form (compute.rs:45-128 uploads W, LUT and x and reads y back per call)
+    reps = max(20, args.steps)
+    for _ in range(5):
+        eng.lut_matmul_q4(M, N, w, LUT_TABLE, x)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        yh = eng.lut_matmul_q4(M, N, w, LUT_TABLE, x)
+    host_s = (time.perf_counter() - t0) / reps
+    assert np.array_equal(yh, y)
+    # the kernel streaming from HBM
+    BM, BN, COPIES = 14336, 4096, 10
+    wbig = eng.alloc(BM * BN // 2 * COPIES)
+    for c in range(COPIES):
+        eng.synth_weights_dev(0, wbig, c * BM * BN // 2, BM * BN // 8, 77 + c, 0.0, 0.0)
+    xbig = eng.upload(np.ones(BN, np.float32))
+    ybig = eng.alloc(4 * BM)
+    for c in range(COPIES):
+        eng.lut_gemv_dev(BM, BN, wbig, c * BM * BN // 2, tb, 0, xbig, 0, ybig, 0)
+    eng.sync()
+    n_big = max(COPIES, (args.steps // COPIES) * COPIES)
+    e0.record()
+    for i in range(n_big):
+        eng.lut_gemv_dev(BM, BN, wbig, (i % COPIES) * BM * BN // 2, tb, 0, xbig, 0, ybig, 0)
+    e1.record()
+    eng.sync()
+    big_us = e0.elapsed_ms(e1) / n_big * 1e3
+    big_bytes = BM * BN // 2 + 4 * BN + 4 * BM + 64
+    big_gbs = big_bytes / (big_us / 1e6) / 1e9
+    log(f"[bench] lut {M}x{N}: {ms * 1e3:.2f} us per call, {gflops:.1f} GFLOPS (device), "
+        f"{flops / host_s / 1e9:.2f} GFLOPS host-io; {BM}x{BN}: {big_us:.2f} us, {big_gbs:.0f} GB/s")
+    cpu = None if args.no_cpu_baseline else lut_cpu_baseline(args.cpu_budget)
+    out = {
+        "metric": "Q4 LUT MatMul GFLOPS (hayai bench: SmolLM2-135M FFN layer 1536x576)",
+        "value": round(gflops, 2),
+        "unit": "GFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms * inner, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "hayai bench inputs (weights 0xAB, x = 1.0, the reference's 16-entry LUT)",
+        "config": {"workload": "hayai-bench-lut-matmul-q4-1536x576", "m": M, "n": N, "calls_per_step": inner},
+        "us_per_call": round(ms * 1e3, 3),
+        "host_io": {"gflops": round(flops / host_s / 1e9, 3), "us_per_call": round(host_s * 1e6, 2),
+                    "note": "host arrays in/out per call, blocking (PCIe included)"},
+        "roofline": {"bound": "hbm", "achieved": round(big_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(big_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": f"hh_lut_gemv at {BM}x{BN} over {COPIES} rotating weight copies",
+                     "mean_us": round(big_us, 3), "algorithmic_bytes": big_bytes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    eng.close()
+    return 0
+
+
+SHAPES = {"8b": (4096, 14336, 32), "70b": (8192, 28672, 80), "smollm": (576, 1536, 30)}
+
+
+def bench_ffn_resident(eng, args) -> int:
+    """One format through the FFN op, every layer resident in HBM, batch 1: --fmt (q4_0,
+    q8_0, q4_k, q6_k, iq2_xxs, iq3_xxs) at --shape (8b: 4096x14336 x 32 layers; 70b:
+    8192x28672 x 80 layers; smollm: 576x1536 x 30).  Shows each format's own kernel where it is
+    the whole cost (a resident 70B IQ2_XXS model is 14.5 GB, well inside 288 GB of HBM).
+    value = algorithmic bytes per step (weights once + x in + y out per layer) / step time."""
+    import hayai_amd
+    from hayai_amd import synth
+
+    T = FMTS[args.fmt]
+    DM, DF, L = SHAPES[args.shape]
+    if args.layers:
+        L = args.layers
+    gate = hayai_amd.QuantMatrix("ffn_gate", DM, DF, T)
+    up = hayai_amd.QuantMatrix("ffn_up", DM, DF, T)
+    down = hayai_amd.QuantMatrix("ffn_down", DF, DM, T)
+    lay = hayai_amd.LayerPackLayout.ffn_only(gate, up, down)
+    stride = (lay.total + 255) // 256 * 256
+    pack = eng.alloc(stride * L)
+    blk = synth.BLOCK[T][0]
+    lo, hi = synth.SCALE_RANGE[T]
+    for l in range(L):
+        for mat, off, rows, cols in ((synth.GATE, lay.gate_off, DF, DM), (synth.UP, lay.up_off, DF, DM),
+                                     (synth.DOWN, lay.down_off, DM, DF)):
+            eng.synth_weights_dev(T, pack, l * stride + off, rows * cols // blk, synth.seed_for(20 + T, l, mat), lo, hi)
+    xs = synth.normal(synth.seed_for(20 + T, 0, synth.ACT), L * DM).reshape(L, DM)
+    xbuf = eng.upload(xs)
+    ybuf = eng.alloc(4 * DM * L)
+    desc = eng.ffn_desc((T, T, T), DM, DF, lay)
+
+    def step():
+        for l in range(L):
+            eng.ffn_dev(desc, pack, l * stride, xbuf, 4 * DM * l, ybuf, 4 * DM * l)
+
+    for _ in range(args.warmup):
+        step()
+    eng.sync()
+    a, b = eng.event(), eng.event()
+    a.record()
+    for _ in range(args.steps):
+        step()
+    b.record()
+    eng.sync()
+    ms = a.elapsed_ms(b) / args.steps
+    wb = gate.nbytes + up.nbytes + down.nbytes
+    bytes_layer = wb + 2 * 4 * DM
+    gbs = bytes_layer * L / (ms / 1e3) / 1e9
+    log(f"[bench] ffn {args.fmt} {args.shape}: {ms * 1e3:.1f} us/step ({ms * 1e3 / L:.2f} us/layer), {gbs:.1f} GB/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+        nl = min(2, L)
+        mats = [[pack.read(np.uint8, m.nbytes, l * stride + o) for m, o in ((gate, lay.gate_off), (up, lay.up_off),
+                                                                            (down, lay.down_off))] for l in range(nl)]
+        cpu = cpu_entry(lambda i: oracle.ffn((T, T, T), DM, DF, *mats[i % nl], xs[i % nl]), args.cpu_budget,
+                        bytes_layer, f"oracle fp32 {args.fmt} FFN over {nl} of the {L} layers")
+    out = {
+        "metric": f"FFN GEMV achieved HBM GB/s (% of peak) + FFN tok/s, {args.shape}-shape {args.fmt} bs=1, resident",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": FMT_DTYPE.get(args.fmt, "f32"),
+        "data": f"synthetic (seeded {args.fmt} blocks, N(0,1) f32 activations)",
+        "config": {"workload": f"{args.shape}-ffn-{args.fmt}-bs1-{L}layers-resident", "d_model": DM, "d_ff": DF,
+                   "layers": L, "batch": 1, "weights": args.fmt, "act": "silu"},
+        "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "ffn_tok_s": round(1e3 / ms, 2),
+        "us_per_layer": round(ms * 1e3 / L, 3),
+        "roofline": roofline_step(gbs, f"{args.fmt} gate/up + down, per layer"),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    eng.close()
+    return 0
+
+
+def bench_gemv(eng, args) -> int:
+    """One GEMV, --fmt at --m x --n (default: hayai's calibration probe, Q4_K 4096x4096,
+    crates/hayai-core/src/calibration.rs:175-196), over rotating weight copies that exceed the
+    256 MB last-level cache.  value = (weights + x + y) bytes / time per GEMV."""
+    import hayai_amd
+    from hayai_amd import synth
+
+    T = FMTS[args.fmt]
+    M, N = args.m, args.n
+    rb = hayai_amd.row_bytes(T, N)
+    wbytes = M * rb
+    copies = max(2, -(-(300 << 20) // wbytes))
+    stride = (wbytes + 255) // 256 * 256
+    wbuf = eng.alloc(stride * copies)
+    blk = synth.BLOCK[T][0]
+    lo, hi = synth.SCALE_RANGE.get(T, (0.0, 0.0))
+    for c in range(copies):
+        eng.synth_weights_dev(T, wbuf, c * stride, M * N // blk, 300 + c, lo, hi)
+    x = synth.normal(301, N)
+    xb, yb = eng.upload(x), eng.alloc(4 * M)
+    for c in range(copies):
+        eng.gemv_dev(T, M, N, wbuf, c * stride, xb, 0, yb, 0)
+    eng.sync()
+    n = max(copies, args.steps // copies * copies)
+    a, b = eng.event(), eng.event()
+    a.record()
+    for i in range(n):
+        eng.gemv_dev(T, M, N, wbuf, (i % copies) * stride, xb, 0, yb, 0)
+    b.record()
+    eng.sync()
+    us = a.elapsed_ms(b) / n * 1e3
+    nbytes = wbytes + 4 * N + 4 * M
+    gbs = nbytes / (us / 1e6) / 1e9
+    log(f"[bench] gemv {args.fmt} {M}x{N}: {us:.2f} us, {gbs:.0f} GB/s over {copies} copies")
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+        wh = wbuf.read(np.uint8, wbytes, 0)
+        wh2 = wbuf.read(np.uint8, wbytes, stride)
+        cpu = cpu_entry(lambda i: oracle.gemv(T, M, N, wh if i % 2 == 0 else wh2, x), args.cpu_budget, nbytes,
+                        f"oracle fp32 {args.fmt} GEMV {M}x{N}, two weight copies in rotation")
+    out = {
+        "metric": f"GEMV achieved HBM GB/s, {args.fmt} {M}x{N}",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": n,
+        "warmup": copies,
+        "ms_per_step": round(us / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": FMT_DTYPE.get(args.fmt, "f32"),
+        "data": f"synthetic (seeded {args.fmt} blocks, N(0,1) f32 x), {copies} rotating weight copies",
+        "config": {"workload": f"gemv-{args.fmt}-{M}x{N}", "m": M, "n": N},
+        "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "roofline": roofline_step(gbs, f"{args.fmt} GEMV kernel"),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    eng.close()
+    return 0
+
+
+FMTS = {"q4_0": 2, "q8_0": 8, "q4_k": 12, "q6_k": 14, "iq2_xxs": 16, "iq3_xxs": 18}
+FMT_DTYPE = {"q4_k": "q4_k x int8-digit activations (v_dot4 i32 sums, f32 scales)",
+             "q6_k": "q6_k x int8-digit activations (v_dot4 i32 sums, f32 scales)"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -899,16 +1162,26 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 256 MiB device copy before timing (reference point for HBM counters)")
-    ap.add_argument("--workload", default="bs1", choices=["bs1", "batched", "moe", "stream", "smollm", "q4km", "block", "disk", "lmhead"],
+    ap.add_argument("--workload", default="bs1", choices=["bs1", "batched", "moe", "stream", "smollm", "q4km", "block", "disk",
+                                                          "lmhead", "lut", "ffn", "gemv"],
                     help="bs1: BASELINE.json configs[1] (the headline); batched: configs[2], --batch tokens per "
                          "step; moe: configs[3], --batch tokens per step; stream: configs[4] (70B IQ2_XXS "
                          "streamed from pinned host); smollm: configs[0]; q4km: the 8B FFN with a Q6_K down "
                          "projection (Q4_K_M layout); block: the 8B FFN residual block (RMSNorm + FFN + "
                          "residual) chained over 32 layers; disk: configs[4] read from a GGUF file through "
-                         "io_uring into the pinned slots; lmhead: the 8B Q4_K_M LM head (Q6_K 128256x4096)")
+                         "io_uring into the pinned slots; lmhead: the 8B Q4_K_M LM head (Q6_K 128256x4096); "
+                         "lut: hayai bench's Q4 LUT MatMul (1536x576, GFLOPS); ffn: --fmt at --shape, every "
+                         "layer resident; gemv: one --fmt GEMV at --m x --n (default: the calibration probe, "
+                         "Q4_K 4096x4096)")
     ap.add_argument("--disk-layers", type=int, default=8, help="distinct layers in the --workload disk file")
     ap.add_argument("--lm-type", default="q6_k", choices=["q6_k", "q4_k"], help="--workload lmhead weight format")
     ap.add_argument("--batch", type=int, default=16, help="tokens per step for --workload batched")
+    ap.add_argument("--fmt", default="q4_k", choices=["q4_0", "q8_0", "q4_k", "q6_k", "iq2_xxs", "iq3_xxs"],
+                    help="--workload ffn / gemv weight format")
+    ap.add_argument("--shape", default="8b", choices=["8b", "70b", "smollm"], help="--workload ffn shape")
+    ap.add_argument("--layers", type=int, default=0, help="--workload ffn: layers (0: the shape's own count)")
+    ap.add_argument("--m", type=int, default=4096, help="--workload gemv rows")
+    ap.add_argument("--n", type=int, default=4096, help="--workload gemv columns")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the FFN path would shard "
@@ -932,6 +1205,12 @@ def main() -> int:
         return bench_disk(eng, args)
     if args.workload == "lmhead":
         return bench_lmhead(eng, args)
+    if args.workload == "lut":
+        return bench_lut(eng, args)
+    if args.workload == "ffn":
+        return bench_ffn_resident(eng, args)
+    if args.workload == "gemv":
+        return bench_gemv(eng, args)
     gate = hayai_amd.QuantMatrix("ffn_gate", D_MODEL, D_FF, Q4_K)
     up = hayai_amd.QuantMatrix("ffn_up", D_MODEL, D_FF, Q4_K)
     down = hayai_amd.QuantMatrix("ffn_down", D_FF, D_MODEL, Q4_K)
@@ -955,7 +1234,20 @@ def main() -> int:
     if args.workload == "block":
         return bench_block(eng, pack, lay, stride, desc, args)
 
+    # One decode step's FFN half: the 32 layers chained on one residual stream, as ffn_apply
+    # runs them (hybrid_infer.rs:883-938): x_{l+1} = x_l + FFN_l(rms_norm(x_l, norm_l)).  A
+    # chain of bare FFNs diverges (the FFN is about quadratic in x), so the decode's RMSNorm
+    # and residual, fused into the two ring kernels, carry the chain.
+    norms = eng.upload(np.concatenate([synth.normal(synth.seed_for(CONFIG_ID, l, 7), D_MODEL) * 0.1 + 1.0
+                                       for l in range(LAYERS)]).astype(np.float32))
+    xres = eng.upload(xs[0])
+    EPS = 1e-5
+
     def step():
+        for l in range(LAYERS):
+            eng.ffn_block_dev(desc, pack, l * stride, norms, 4 * D_MODEL * l, EPS, xres, 0, xres, 0)
+
+    def ffn_unchained():  # the plain FFN op per layer on independent inputs (no norm/residual)
         for l in range(LAYERS):
             eng.ffn_dev(desc, pack, l * stride, xbuf, 4 * D_MODEL * l, ybuf, 4 * D_MODEL * l)
 
@@ -964,6 +1256,7 @@ def main() -> int:
         cal.copy_from(pack, 256 << 20)
         eng.sync()
         cal.free()
+
     def timed(run, n) -> float:  # ms per call of run(), events on the compute stream
         e0, e1 = eng.event(), eng.event()
         e0.record()
@@ -975,25 +1268,36 @@ def main() -> int:
 
     for _ in range(args.warmup):
         step()
+        ffn_unchained()
     eng.sync()
+    xres.write(xs[0])
     t0 = time.perf_counter()
     ms_eager = timed(step, args.steps)
     wall = time.perf_counter() - t0
+    y_end = xres.read(np.float32, D_MODEL)
+    finite = bool(np.isfinite(y_end).all())
+    log(f"[bench] chained residual stream after {args.steps} steps: finite={finite}, "
+        f"max|x|={float(np.max(np.abs(y_end))):.3e}")
+    xres.write(xs[0])
     graph = eng.capture(step)
     for _ in range(3):
         graph.launch()
     eng.sync()
     ms_graph = timed(graph.launch, args.steps)
     graph.free()
+    ms_plain = timed(ffn_unchained, args.steps)
     ms = ms_eager
-    bytes_step = layer_bytes() * LAYERS
+    bytes_layer = layer_bytes() + 4 * D_MODEL  # + the norm weight
+    bytes_step = bytes_layer * LAYERS
     gbs = bytes_step / (ms / 1e3) / 1e9
     gbs_graph = bytes_step / (ms_graph / 1e3) / 1e9
+    gbs_plain = layer_bytes() * LAYERS / (ms_plain / 1e3) / 1e9
     log(f"[bench] {ms * 1e3:.1f} us/step (event), wall {wall / args.steps * 1e6:.1f} us/step, {gbs:.1f} GB/s; "
-        f"graph replay {ms_graph * 1e3:.1f} us/step, {gbs_graph:.1f} GB/s")
+        f"graph replay {ms_graph * 1e3:.1f} us/step, {gbs_graph:.1f} GB/s; plain FFN op (unchained) "
+        f"{ms_plain * 1e3:.1f} us/step, {gbs_plain:.1f} GB/s")
 
-    # Each kernel of the step on its own, through the FFN's two-call form (it issues exactly
-    # the kernels of the one-call op): a region of gate/up launches alone over all layers,
+    # Each kernel of the step on its own, through ffn_apply's two-call form (it issues exactly
+    # the kernels of the one-call block): a region of gate/up launches alone over all layers,
     # then one of gate/up + down, each bracketed by events on the compute stream;
     # down = (gate/up + down) - gate/up.  Back-to-back launches of one kernel: the time per
     # launch includes the dispatch gap between launches.
@@ -1003,15 +1307,15 @@ def main() -> int:
         def run():
             for l in range(LAYERS):
                 base = l * stride
-                eng.ffn_begin_dev(desc, pack, base, xbuf, 4 * D_MODEL * l)
+                eng.ffn_block_begin_dev(desc, pack, base, norms, 4 * D_MODEL * l, EPS, xbuf, 4 * D_MODEL * l)
                 if with_down:
-                    eng.ffn_finish_dev(desc, pack, base, ybuf, 4 * D_MODEL * l)
+                    eng.ffn_block_finish_dev(desc, pack, base, xbuf, 4 * D_MODEL * l, ybuf, 4 * D_MODEL * l)
         return timed(run, n_prof) / LAYERS
 
     gu = region(False)
     dn = region(True) - gu
-    gu_gbs = gateup_bytes() / (gu / 1e3) / 1e9
-    dn_gbs = (D_MODEL * hayai_amd.row_bytes(Q4_K, D_FF) + 4 * D_FF + 4 * D_MODEL) / (dn / 1e3) / 1e9
+    gu_gbs = gateup_bytes_n() / (gu / 1e3) / 1e9
+    dn_gbs = (D_MODEL * hayai_amd.row_bytes(Q4_K, D_FF) + 4 * D_FF + 2 * 4 * D_MODEL) / (dn / 1e3) / 1e9
     log(f"[bench] per kernel: gate/up {gu * 1e3:.2f} us ({gu_gbs:.0f} GB/s), down {dn * 1e3:.2f} us "
         f"({dn_gbs:.0f} GB/s)")
     layer_us = ms * 1e3 / LAYERS
@@ -1019,7 +1323,8 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(eng, pack, lay, stride, xs, args.cpu_budget)
-        log(f"[bench] cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+        log(f"[bench] cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads, {cpu['one_core']['value']} GB/s "
+            f"on one core; LUT MatMul {cpu['lut_matmul_q4']['value']} GFLOPS")
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
@@ -1037,22 +1342,27 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (seeded Q4_K blocks, N(0,1) f32 activations)",
+        "dtype": "q4_k x int8-digit activations (v_dot4 i32 sums, f32 scales)",
+        "data": "synthetic (seeded Q4_K blocks, N(0,1) f32 activations, norm weights 1 + 0.1 N(0,1))",
         "config": {"workload": "llama3-8b-ffn-q4_k-bs1-32layers-resident", "d_model": D_MODEL, "d_ff": D_FF,
                    "layers": LAYERS, "batch": 1, "weights": "Q4_K", "act": "silu",
+                   "step": "32 layers chained on one residual stream (RMSNorm + FFN + residual, ffn_apply)",
                    "launch": "eager, 2 kernels per layer"},
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "ffn_tok_s": round(1e3 / ms, 2),
         "us_per_layer": round(layer_us, 3),
+        "output_finite": finite,
         "graph_replay": {"ms_per_step": round(ms_graph, 5), "value": round(gbs_graph, 2),
                          "ffn_tok_s": round(1e3 / ms_graph, 2)},
+        "ffn_op_unchained": {"ms_per_step": round(ms_plain, 5), "value": round(gbs_plain, 2),
+                             "us_per_layer": round(ms_plain * 1e3 / LAYERS, 3)},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes": gateup_bytes(),
-                     "kernel": "hh_q4k_gu_ring_g1: ring gate/up + SwiGLU, h as int8 digits",
+                     "algorithmic_bytes": gateup_bytes_n(),
+                     "kernel": "hh_q4k_gu_ring_g1_n: ring gate/up with the RMSNorm + SwiGLU, h as int8 digits",
                      "mean_us": round(gu * 1e3, 3)},
-        "down_kernel": {"kernel": "hh_q4k_dn_ring_d4", "us": round(dn * 1e3, 3), "gbs": round(dn_gbs, 1)},
+        "down_kernel": {"kernel": "hh_q4k_dn_ring_d4 (residual epilogue)", "us": round(dn * 1e3, 3),
+                        "gbs": round(dn_gbs, 1)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

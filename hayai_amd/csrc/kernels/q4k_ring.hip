@@ -119,27 +119,23 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < P; s++) issue((uint32_t)s, ring[s]);
-    float inv = 1.f;
     if constexpr (NORM) {
         // RMSNorm (rms_norm, crates/hayai-cpu/src/attention.rs:142-147, applied before the
         // FFN by ffn_apply, crates/hayai-core/src/hybrid_infer.rs:895-896): every workgroup
-        // forms sum(x^2) itself (d_model floats from L2), then x * inv * weight
+        // forms sum(x^2) itself (d_model floats from L2).  The GEMVs are linear in x, so x *
+        // weight is quantized right away and the common factor inv = 1 / sqrt(mean + eps)
+        // scales the gate and up row sums in the epilogue: no barrier on the prologue's path.
         float ss = has ? hh_sq8(t0, t1) : 0.f;
         for (uint32_t c2 = c + HH_RING_BLOCK; c2 < dm / 8; c2 += HH_RING_BLOCK) ss += hh_sq8(x4[2 * c2], x4[2 * c2 + 1]);
         ss = hh_wave_sum(ss);
         float* red = reinterpret_cast<float*>(stage);  // free until the epilogue
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        float tot = 0.f;
-#pragma unroll
-        for (int k = 0; k < HH_FFNP_CW; k++) tot += red[k];
-        inv = 1.0f / sqrtf(tot / (float)dm + a.eps);
-        hh_norm8(t0, t1, m0, m1, inv);
+        if (lane == 0) red[wave] = ss;                   // read after the main loop's barrier
+        hh_norm8(t0, t1, m0, m1, 1.f);
     }
     hh_ffnp_digits_chunk(t0, t1, c, has, xd);
     for (uint32_t c2 = c + HH_RING_BLOCK; c2 < dm / 8; c2 += HH_RING_BLOCK) {
         float4 v0 = x4[2 * c2], v1 = x4[2 * c2 + 1];  // d_model > 4096: later passes
-        if constexpr (NORM) hh_norm8(v0, v1, n4[2 * c2], n4[2 * c2 + 1], inv);
+        if constexpr (NORM) hh_norm8(v0, v1, n4[2 * c2], n4[2 * c2 + 1], 1.f);
         hh_ffnp_digits_chunk(v0, v1, c2, true, xd);
     }
 #pragma unroll
@@ -166,6 +162,14 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
     __syncthreads();  // row sums are in LDS
 
     if (wave == 0) {
+        float inv = 1.f;
+        if constexpr (NORM) {
+            const float* red = reinterpret_cast<const float*>(stage);
+            float tot = 0.f;
+#pragma unroll
+            for (int k = 0; k < HH_FFNP_CW; k++) tot += red[k];
+            inv = 1.0f / sqrtf(tot / (float)dm + a.eps);
+        }
         // h = act(g) * u, two int8 digits per element, one scale per granule of 8 rows
         int8_t* gq1 = reinterpret_cast<int8_t*>(a.hx);
         int8_t* gq2 = gq1 + dff;
@@ -180,6 +184,10 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
                 for (int k = 0; k < WPT1; k++) {
                     g += gu[(2 * rho) * WPT1 + k];
                     u += gu[(2 * rho + 1) * WPT1 + k];
+                }
+                if constexpr (NORM) {
+                    g *= inv;
+                    u *= inv;
                 }
                 hv = hh_act_mul(g, u, a.act);
             }

@@ -608,6 +608,37 @@ hh_status hh_ffn_finish_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pa
     return e->enqueue_ffn_finish(d, (const uint8_t*)pack->ptr + pack_off, (float*)((char*)y->ptr + y_off));
 }
 
+hh_status hh_ffn_block_begin_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                                 const hh_buf* norm, size_t norm_off, float eps, const hh_buf* x, size_t x_off) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_ffn(e, d, pack, pack_off));
+    HH_TRY(check_engine(e, norm, "norm"));
+    HH_TRY(check_engine(e, x, "x"));
+    HH_TRY(check_range(norm, norm_off, d->d_model * sizeof(float), "norm"));
+    HH_TRY(check_range(x, x_off, d->d_model * sizeof(float), "x"));
+    if (((norm_off | x_off) & 3u) != 0) return fail(HH_ERR_INVALID, "ffn_block_begin: norm/x offsets must be 4-byte aligned");
+    if (!(eps >= 0.f) || eps > 1.f) return fail(HH_ERR_INVALID, "ffn_block_begin: eps=%g outside [0, 1]", (double)eps);
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    return e->enqueue_ffn_begin(d, (const uint8_t*)pack->ptr + pack_off, (const float*)((const char*)x->ptr + x_off),
+                                (const float*)((const char*)norm->ptr + norm_off), eps);
+}
+
+hh_status hh_ffn_block_finish_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                                  const hh_buf* res, size_t res_off, hh_buf* y, size_t y_off) {
+    HH_NOT_NULL(e, "engine");
+    HH_TRY(validate_ffn(e, d, pack, pack_off));
+    HH_TRY(check_engine(e, res, "res"));
+    HH_TRY(check_engine(e, y, "y"));
+    HH_TRY(check_range(res, res_off, d->d_model * sizeof(float), "res"));
+    HH_TRY(check_range(y, y_off, d->d_model * sizeof(float), "y"));
+    if (((res_off | y_off) & 3u) != 0) return fail(HH_ERR_INVALID, "ffn_block_finish: res/y offsets must be 4-byte aligned");
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    return e->enqueue_ffn_finish(d, (const uint8_t*)pack->ptr + pack_off, (float*)((char*)y->ptr + y_off),
+                                 (const float*)((const char*)res->ptr + res_off));
+}
+
 hh_status hh_ffn(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off, const float* x, float* y) {
     HH_NOT_NULL(e, "engine");
     HH_TRY(validate_ffn(e, d, pack, pack_off));

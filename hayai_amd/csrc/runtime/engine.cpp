@@ -651,22 +651,33 @@ static bool same_ffn(const hh_ffn_desc* a, const hh_ffn_desc* b) {
            a->act == b->act && a->d_model == b->d_model && a->d_ff == b->d_ff;
 }
 
-hh_status hh_engine::enqueue_ffn_begin(const hh_ffn_desc* d, const uint8_t* pack, const float* x) {
+hh_status hh_engine::enqueue_ffn_begin(const hh_ffn_desc* d, const uint8_t* pack, const float* x,
+                                       const float* norm, float eps) {
     ffn_stage_valid = false;
     HH_TRY(grow(&ws_h, &ws_h_cap, d->d_ff * sizeof(float)));
     const uint8_t* wg = pack + d->gate_off;
     const uint8_t* wu = pack + d->up_off;
     bool digits = false;
     hh_status st = HH_ERR_UNSUPPORTED_DEVICE;
-    if (ring_ok(d, wg, wu, pack + d->down_off, x)) {
+    if (ring_ok(d, wg, wu, pack + d->down_off, x) && ((uintptr_t)norm & 15u) == 0) {
         // the ring kernels: gate/up writes h's granule digits, the finish step reads them
-        HH_TRY(enqueue_q4k_ring_gu(d, wg, wu, x));
+        // (with norm: the RMSNorm rides in gate/up's prologue and epilogue)
+        HH_TRY(enqueue_q4k_ring_gu(d, wg, wu, x, norm, eps));
         ffn_stage = *d;
         ffn_stage_digits = false;
         ffn_stage_ring = true;
         ffn_stage_valid = true;
         ffn_calls += 2;
         return HH_OK;
+    }
+    if (norm) {
+        // other layouts: RMSNorm as its own kernel, then the plain begin step on its output
+        HH_TRY(grow(&ws_xn, &ws_xn_cap, d->d_model * sizeof(float)));
+        hipFunction_t fn;
+        HH_TRY(kernel("hh_rmsnorm_kernel", &fn));
+        hh_norm_args na{x, norm, (float*)ws_xn, (uint32_t)d->d_model, eps};
+        HH_TRY(launch(fn, 1, 1024, na));
+        x = (const float*)ws_xn;
     }
     if (d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K && d->type_down == HH_TYPE_Q4_K) {
         // Gate/up writes h and its int8 digits; the down projection consumes the digits.
@@ -685,17 +696,31 @@ hh_status hh_engine::enqueue_ffn_begin(const hh_ffn_desc* d, const uint8_t* pack
     return HH_OK;
 }
 
-hh_status hh_engine::enqueue_ffn_finish(const hh_ffn_desc* d, const uint8_t* pack, float* y) {
+hh_status hh_engine::enqueue_ffn_finish(const hh_ffn_desc* d, const uint8_t* pack, float* y, const float* res) {
     if (!ffn_stage_valid || !same_ffn(d, &ffn_stage))
         return fail(HH_ERR_INVALID, "ffn finish: no gate/up of this FFN shape is pending (call the begin step first)");
     ffn_stage_valid = false;
     const uint8_t* wd = pack + d->down_off;
+    if (ffn_stage_ring) {  // the ring down kernel adds the residual as it stores y
+        const hh_status st = enqueue_q4k_ring_dn(d, wd, y, res);
+        if (st == HH_OK) ffn_calls += 1;
+        return st;
+    }
+    float* out = y;
+    if (res) {
+        HH_TRY(grow(&ws_f, &ws_f_cap, d->d_model * sizeof(float)));
+        out = (float*)ws_f;
+    }
     hh_status st = HH_ERR_UNSUPPORTED_DEVICE;
-    if (ffn_stage_ring) st = enqueue_q4k_ring_dn(d, wd, y);
-    else if (ffn_stage_digits) st = enqueue_q4k(d->d_model, d->d_ff, wd, nullptr, nullptr, y, 0, false, ws_hq, nullptr);
-    if (st == HH_ERR_UNSUPPORTED_DEVICE) st = enqueue_gemv(d->type_down, d->d_model, d->d_ff, wd, (const float*)ws_h, y);
-    if (st == HH_OK) ffn_calls += 1;
-    return st;
+    if (ffn_stage_digits) st = enqueue_q4k(d->d_model, d->d_ff, wd, nullptr, nullptr, out, 0, false, ws_hq, nullptr);
+    if (st == HH_ERR_UNSUPPORTED_DEVICE) st = enqueue_gemv(d->type_down, d->d_model, d->d_ff, wd, (const float*)ws_h, out);
+    if (st != HH_OK) return st;
+    ffn_calls += 1;
+    if (!res) return HH_OK;
+    hipFunction_t fn;
+    HH_TRY(kernel("hh_add_kernel", &fn));
+    hh_add_args aa{res, (const float*)ws_f, y, (uint32_t)d->d_model, 0u};
+    return launch(fn, (uint32_t)((d->d_model + 255) / 256), 256, aa);
 }
 
 hh_status hh_engine::enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y) {

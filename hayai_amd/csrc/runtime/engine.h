@@ -205,8 +205,11 @@ struct hh_engine {
                                 float eps, float* y);
     // The two halves of enqueue_ffn's two-launch path: gate/up(+act) into the engine's FFN
     // intermediate, then the down projection of that intermediate.
-    hh_status enqueue_ffn_begin(const hh_ffn_desc* d, const uint8_t* pack, const float* x);
-    hh_status enqueue_ffn_finish(const hh_ffn_desc* d, const uint8_t* pack, float* y);
+    // With norm: the begin step of the FFN residual block (x is RMSNorm'ed first); with res:
+    // the finish step adds the residual (y = res + down; y may be res).
+    hh_status enqueue_ffn_begin(const hh_ffn_desc* d, const uint8_t* pack, const float* x,
+                                const float* norm = nullptr, float eps = 0.f);
+    hh_status enqueue_ffn_finish(const hh_ffn_desc* d, const uint8_t* pack, float* y, const float* res = nullptr);
     // Q4_K batch-1 kernels (q4k.hip); returns HH_ERR_UNSUPPORTED_DEVICE when the shape or
     // alignment needs the generic kernels instead (the caller then falls back).  xdigits:
     // x given as int8 digits (then x is unused); hdigits: gate/up also writes h's digits.

@@ -563,6 +563,20 @@ class HipEngine:
         _check(self.lib.hh_ffn_dev(self.handle, C.byref(desc), pack.handle, pack_off, x.handle, x_off, y.handle,
                                    y_off))
 
+    def ffn_block_begin_dev(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, norm: DeviceBuffer,
+                            norm_off: int, eps: float, x: DeviceBuffer, x_off: int) -> None:
+        """ffn_apply's first half (hybrid_infer.rs:895-918): rms_norm(x) then gate/up(+act)
+        into the engine's FFN intermediate.  Enqueue only."""
+        _check(self.lib.hh_ffn_block_begin_dev(self.handle, C.byref(desc), pack.handle, pack_off, norm.handle, norm_off,
+                                               eps, x.handle, x_off))
+
+    def ffn_block_finish_dev(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, res: DeviceBuffer,
+                             res_off: int, y: DeviceBuffer, y_off: int) -> None:
+        """ffn_apply's second half (:919-935): the down projection plus the residual, y = res +
+        down (y may be res).  Enqueue only."""
+        _check(self.lib.hh_ffn_block_finish_dev(self.handle, C.byref(desc), pack.handle, pack_off, res.handle, res_off,
+                                                y.handle, y_off))
+
     def ffn_dev_noalloc(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, x: DeviceBuffer, x_off: int,
                         y: DeviceBuffer, y_off: int) -> None:
         """ffn_dev with its intermediate in the GPU's fixed scratch array (no allocation at

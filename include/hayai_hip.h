@@ -278,6 +278,17 @@ hh_status hh_ffn_begin_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pac
 hh_status hh_ffn_finish_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off, hh_buf* y,
                             size_t y_off);
 
+/* hh_ffn_block_dev as the reference's ffn_apply runs it (crates/hayai-core/src/
+ * hybrid_infer.rs:883-938): hh_ffn_block_begin_dev = rms_norm(x, norm, eps) (:895-896)
+ * followed by ffn_begin_gate_up_scratch (:906-918); hh_ffn_block_finish_dev =
+ * ffn_finish_scratch (:919-930) followed by the residual add x[i] += ws_down[i] (:933-935),
+ * here y = res + down (y may be res).  Same kernels as hh_ffn_block_dev; the same pending
+ * rule as hh_ffn_begin_dev / hh_ffn_finish_dev.  Enqueue only. */
+hh_status hh_ffn_block_begin_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                                 const hh_buf* norm, size_t norm_off, float eps, const hh_buf* x, size_t x_off);
+hh_status hh_ffn_block_finish_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                                  const hh_buf* res, size_t res_off, hh_buf* y, size_t y_off);
+
 /* The first half of the FFN op: ffn_begin_gate_up_scratch (stream_infer.rs:3752-3806)
  * fused with the activation of ffn_finish_scratch (:3836-3840):
  * h[d_ff] = act(W_gate . x) * (W_up . x), one kernel when gate and up share a format.

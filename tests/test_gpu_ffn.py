@@ -299,6 +299,31 @@ def test_ffn_block_matches_oracle(engine, types, d_model, d_ff):
     np.testing.assert_array_equal(engine.ffn_block(desc, pack, 0, nw, eps, x), y)
 
 
+@pytest.mark.parametrize("types,d_model,d_ff", [((12, 12, 12), 4096, 14336), ((12, 12, 14), 4096, 14336),
+                                                ((2, 2, 2), 576, 1536), ((16, 16, 16), 1024, 2048)])
+def test_ffn_block_begin_finish_equals_block(engine, types, d_model, d_ff):
+    # ffn_apply's own two calls (rms_norm + begin, finish + residual) run the block's kernels:
+    # bit-identical to the one-call block, out of place and in place.
+    print(f"[case] ffn block begin/finish types={types} {d_model}x{d_ff}", flush=True)
+    lay, _, pack = make_pack(engine, types, d_model, d_ff, 25)
+    desc = engine.ffn_desc(types, d_model, d_ff, lay)
+    rng = np.random.default_rng(d_model)
+    x = rng.standard_normal(d_model).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, d_model).astype(np.float32)
+    xb, nb, y1, y2 = engine.upload(x), engine.upload(nw), engine.alloc(4 * d_model), engine.alloc(4 * d_model)
+    engine.ffn_block_dev(desc, pack, 0, nb, 0, 1e-5, xb, 0, y1, 0)
+    engine.ffn_block_begin_dev(desc, pack, 0, nb, 0, 1e-5, xb, 0)
+    engine.ffn_block_finish_dev(desc, pack, 0, xb, 0, y2, 0)
+    ref = y1.read(np.float32, d_model)
+    np.testing.assert_array_equal(y2.read(np.float32, d_model).view(np.uint32), ref.view(np.uint32))
+    engine.ffn_block_begin_dev(desc, pack, 0, nb, 0, 1e-5, xb, 0)
+    engine.ffn_block_finish_dev(desc, pack, 0, xb, 0, xb, 0)  # in place, as ffn_apply updates x
+    np.testing.assert_array_equal(xb.read(np.float32, d_model).view(np.uint32), ref.view(np.uint32))
+    with pytest.raises(hayai_amd.HipError) as e:  # the finish consumed the pending intermediate
+        engine.ffn_block_finish_dev(desc, pack, 0, xb, 0, y2, 0)
+    assert e.value.status_name == "HH_ERR_INVALID"
+
+
 def test_ffn_block_unaligned_norm_takes_the_three_step_path(engine):
     # A norm weight that is not 16-byte aligned keeps the ring kernels out (their prologue
     # reads it as float4s): the three-step path gives the same block within tolerance.
