@@ -499,6 +499,8 @@ def bench_disk(eng, args) -> int:
                 yield f"blk.{l}.{name}.weight", (cols, rows), T, synth.matrix(T, rows, cols,
                                                                                synth.seed_for(5, l, mat), lo, hi)
 
+    if args.o_direct:  # the reference's HAYAI_O_DIRECT: reads bypass the page cache
+        os.environ["HAYAI_O_DIRECT"] = "1"
     t0 = time.perf_counter()
     write_gguf(path, [("general.architecture", "llama")], list(tensors()))
     log(f"[bench] wrote {os.path.getsize(path) / 2**30:.2f} GiB GGUF ({NF} layers) in {time.perf_counter() - t0:.1f} s")
@@ -558,7 +560,8 @@ def bench_disk(eng, args) -> int:
         tok_bytes = L * (lp.total + 2 * 4 * DM)
         gbs = tok_bytes / (ms_tok / 1e3) / 1e9
         log(f"[bench] disk: {ms_tok:.2f} ms/token ({ms_tok / L * 1e3:.0f} us/layer), {gbs:.2f} GB/s; file reads alone "
-            f"{read_s[0] / steps * 1e3:.2f} ms/token ({read_gbs:.2f} GB/s, io_uring={int(cat.io_uring)}); "
+            f"{read_s[0] / steps * 1e3:.2f} ms/token ({read_gbs:.2f} GB/s, io_uring={int(cat.io_uring)}, "
+            f"o_direct={int(cat.o_direct)}); "
             f"wall {wall * 1e3:.2f} ms/token")
         out = {
             "metric": "FFN tok/s and streamed GB/s, 70B-shape IQ2_XXS FFN read from a GGUF file (io_uring) into "
@@ -573,14 +576,16 @@ def bench_disk(eng, args) -> int:
             "scaling": "weak",
             "vs_baseline": None,
             "dtype": "f32",
-            "data": f"synthetic GGUF file of {NF} distinct IQ2_XXS layers (page-cache resident after the first "
-                    "pass), N(0,1) f32 activations",
+            "data": (f"synthetic GGUF file of {NF} distinct IQ2_XXS layers ("
+                     + ("read from the device with O_DIRECT" if cat.o_direct else
+                        "page-cache resident after the first pass") + "), N(0,1) f32 activations"),
             "config": {"workload": "llama3-70b-ffn-iq2_xxs-bs1-80layers-gguf-io_uring", "d_model": DM, "d_ff": DF,
                        "layers": L, "file_layers": NF, "batch": 1, "weights": "IQ2_XXS", "slots": 2,
                        "layer_pack_bytes": lp.total, "ffn_bytes": ffn_bytes},
             "ffn_tok_s": round(1e3 / ms_tok, 3),
             "file_read_gbs": round(read_gbs, 3),
             "io_uring": bool(cat.io_uring),
+            "o_direct": bool(cat.o_direct),
             "roofline": {"bound": "host link", "achieved": round(gbs, 2), "peak": None, "unit": "GB/s", "frac": None,
                          "traffic": None, "kernel": "file -> pinned slot -> HBM per layer pack; PCIe-bound, see the "
                                                     "stream workload for the H2D copy rate"},
@@ -1174,6 +1179,8 @@ def main() -> int:
                          "layer resident; gemv: one --fmt GEMV at --m x --n (default: the calibration probe, "
                          "Q4_K 4096x4096)")
     ap.add_argument("--disk-layers", type=int, default=8, help="distinct layers in the --workload disk file")
+    ap.add_argument("--o-direct", action="store_true",
+                    help="--workload disk: read the file with O_DIRECT (HAYAI_O_DIRECT), bypassing the page cache")
     ap.add_argument("--lm-type", default="q6_k", choices=["q6_k", "q4_k"], help="--workload lmhead weight format")
     ap.add_argument("--batch", type=int, default=16, help="tokens per step for --workload batched")
     ap.add_argument("--fmt", default="q4_k", choices=["q4_0", "q8_0", "q4_k", "q6_k", "iq2_xxs", "iq3_xxs"],

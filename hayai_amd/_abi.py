@@ -29,6 +29,8 @@ class GgufInfo(C.Structure):
     _fields_ = [
         ("version", C.c_uint32),
         ("io_uring", C.c_uint32),
+        ("o_direct", C.c_uint32),
+        ("pad", C.c_uint32),
         ("alignment", C.c_uint64),
         ("data_offset", C.c_uint64),
         ("header_bytes", C.c_uint64),

@@ -220,10 +220,72 @@ struct WeightIo {
     // 55 GB/s, 256 KiB pieces 63 GB/s.
     size_t chunk = (size_t)256 << 10;
     std::string path;
+    // HAYAI_O_DIRECT (iouring_reader.rs:36-50, weight_io.rs:243-263,329-405): a second
+    // descriptor opened with O_DIRECT, so reads bypass the page cache (cold reads from the
+    // device itself).  Direct reads need offsets, lengths and buffers aligned to the logical
+    // block size: each run is read as its 4096-aligned cover into an aligned bounce buffer
+    // and copied out.  A run whose cover crosses an unaligned end of file, or a failed
+    // direct read, switches the catalog to page-cache reads for good, as the reference does.
+    static constexpr uint64_t kDirectAlign = 4096;
+    int dfd = -1;
+    void* bounce = nullptr;
+    size_t bounce_cap = 0;
 
     ~WeightIo() {
         delete ring;
         if (fd >= 0) close(fd);
+        drop_direct();
+    }
+
+    void drop_direct() {
+        if (dfd >= 0) close(dfd);
+        dfd = -1;
+        free(bounce);
+        bounce = nullptr;
+        bounce_cap = 0;
+    }
+
+    // One run [off, off + len) -> dst through O_DIRECT; false (nothing written to dst) when
+    // the run cannot be served that way.
+    bool read_direct(uint64_t off, char* dst, size_t len) {
+        const uint64_t a0 = off & ~(kDirectAlign - 1);
+        const uint64_t a1 = (off + len + kDirectAlign - 1) & ~(kDirectAlign - 1);
+        if (a1 > size) return false;  // the cover would cross an unaligned end of file
+        const size_t n = (size_t)(a1 - a0);
+        if (n > bounce_cap) {
+            free(bounce);
+            bounce = nullptr;
+            bounce_cap = 0;
+            if (posix_memalign(&bounce, kDirectAlign, n) != 0) {
+                bounce = nullptr;
+                return false;
+            }
+            bounce_cap = n;
+        }
+        char* b = (char*)bounce;
+        const size_t piece = ring && chunk ? chunk : ((size_t)1 << 30);  // chunk is a multiple of 4096
+        if (ring && piece % kDirectAlign == 0) {
+            std::vector<IoReq> pieces;
+            for (size_t s = 0; s < n; s += piece) pieces.push_back({a0 + s, s, std::min(n, s + piece)});
+            std::string why;
+            if (ring->read_batch(dfd, b, pieces.data(), pieces.size(), pieces.size() > 1, &why) != 0) {
+                if (ring->broken) {
+                    delete ring;
+                    ring = nullptr;
+                }
+                return false;
+            }
+        } else {
+            size_t done = 0;
+            while (done < n) {
+                const ssize_t r = pread(dfd, b + done, std::min<size_t>(n - done, (size_t)1 << 30), (off_t)(a0 + done));
+                if (r < 0 && errno == EINTR) continue;
+                if (r <= 0 || ((size_t)r % kDirectAlign != 0 && done + (size_t)r < n)) return false;
+                done += (size_t)r;
+            }
+        }
+        memcpy(dst, b + (off - a0), len);
+        return true;
     }
 
     hh_status open_file(const char* p) {
@@ -234,6 +296,10 @@ struct WeightIo {
         if (fstat(fd, &st) != 0) return fail(HH_ERR_IO, "gguf: fstat %s: %s", p, strerror(errno));
         size = (uint64_t)st.st_size;
         if (const char* c = getenv("HAYAI_IO_CHUNK_KB")) chunk = (size_t)std::max(0, atoi(c)) << 10;
+        if (getenv("HAYAI_O_DIRECT")) {
+            dfd = ::open(p, O_RDONLY | O_CLOEXEC | O_DIRECT);  // refused (tmpfs...): page cache
+            if (dfd < 0) dfd = -1;
+        }
         const char* force = getenv("HAYAI_FORCE_FILE_IO");
         if (!(force && *force && strcmp(force, "0") != 0)) {
             ring = new (std::nothrow) Uring;
@@ -274,25 +340,37 @@ struct WeightIo {
         std::sort(order.begin(), order.end(), [](const IoReq& a, const IoReq& b) { return a.start < b.start; });
         for (size_t i = 1; i < order.size(); i++)
             if (order[i - 1].end > order[i].start) return fail(HH_ERR_INVALID, "overlapping io ranges");
-        std::vector<IoReq> runs;
-        const size_t piece = ring && chunk ? chunk : (size_t)1 << 30;
+        std::vector<IoReq> whole;  // runs contiguous in the file and in dst, coalesced
         for (size_t i = 0; i < reqs.size();) {
             size_t j = i;
             while (j + 1 < reqs.size() && reqs[j].offset + (reqs[j].end - reqs[j].start) == reqs[j + 1].offset &&
                    reqs[j].end == reqs[j + 1].start)
                 j++;
-            // split into pieces of at most `piece` bytes (one read returns at most ~2 GiB;
-            // io_uring reads large runs as parallel pieces)
-            for (size_t s = reqs[i].start; s < reqs[j].end; s += piece) {
-                const size_t e = std::min(reqs[j].end, s + piece);
-                runs.push_back({reqs[i].offset + (s - reqs[i].start), s, e});
-            }
+            whole.push_back({reqs[i].offset, reqs[i].start, reqs[j].end});
             i = j + 1;
         }
-        for (const IoReq& r : runs)
+        for (const IoReq& r : whole)
             if (r.offset > size || r.end - r.start > size - r.offset)
                 return fail(HH_ERR_IO, "gguf: read of %zu bytes at %llu past the end of %s (%llu bytes)",
                             r.end - r.start, (unsigned long long)r.offset, path.c_str(), (unsigned long long)size);
+        size_t first = 0;  // runs before this one were read directly
+        while (dfd >= 0 && first < whole.size()) {
+            const IoReq& r = whole[first];
+            if (r.end > r.start && !read_direct(r.offset, (char*)dst + r.start, r.end - r.start)) {
+                drop_direct();  // page-cache reads from now on (weight_io.rs:388-400)
+                break;
+            }
+            first++;
+        }
+        std::vector<IoReq> runs;
+        const size_t piece = ring && chunk ? chunk : (size_t)1 << 30;
+        for (size_t i = first; i < whole.size(); i++) {
+            // split into pieces of at most `piece` bytes (one read returns at most ~2 GiB;
+            // io_uring reads large runs as parallel pieces)
+            for (size_t s = whole[i].start; s < whole[i].end; s += piece)
+                runs.push_back({whole[i].offset + (s - whole[i].start), s, std::min(whole[i].end, s + piece)});
+        }
+        if (runs.empty()) return HH_OK;
         if (ring) {
             std::string why;
             const int rc = ring->read_batch(fd, (char*)dst, runs.data(), runs.size(), chunk != 0 && runs.size() > 1, &why);
@@ -658,6 +736,7 @@ hh_status hh_gguf_header(const hh_gguf* g, hh_gguf_info* out) {
     if (!g || !out) return fail(HH_ERR_INVALID, "hh_gguf_header: null argument");
     out->version = g->version;
     out->io_uring = g->io.ring != nullptr;
+    out->o_direct = g->io.dfd >= 0;
     out->alignment = g->alignment;
     out->data_offset = g->data_offset;
     out->header_bytes = g->header_bytes;

@@ -110,6 +110,7 @@ class GgufCatalog:
         _check(self.lib.hh_gguf_header(self.handle, C.byref(info)))
         self.version = info.version
         self.io_uring = bool(info.io_uring)
+        self.o_direct = bool(info.o_direct)
         self.alignment = info.alignment
         self.data_offset = info.data_offset
         self.header_bytes = info.header_bytes

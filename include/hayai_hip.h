@@ -431,6 +431,9 @@ typedef struct hh_gguf hh_gguf;
 typedef struct hh_gguf_info {
     uint32_t version;      /* 1..4 */
     uint32_t io_uring;     /* 1: reads go through io_uring */
+    uint32_t o_direct;     /* 1: reads bypass the page cache (HAYAI_O_DIRECT set, O_DIRECT open
+                            * accepted, no fallback to page-cache reads yet) */
+    uint32_t pad;
     uint64_t alignment;    /* general.alignment (default 32) */
     uint64_t data_offset;  /* absolute offset of the tensor data section */
     uint64_t header_bytes; /* bytes of header + directory */

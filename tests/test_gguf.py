@@ -293,6 +293,35 @@ def test_catalog_reads_are_identical_through_io_uring_and_pread(tmp_path):
     assert out[0][1:] == out[1][1:]
 
 
+@pytest.mark.parametrize("tail", [0, 123])
+def test_o_direct_reads_are_identical(tmp_path, tail):
+    # HAYAI_O_DIRECT (weight_io.rs:243-263,329-405): runs read as their 4096-aligned cover
+    # through O_DIRECT and copied out; identical bytes to page-cache reads.  A file whose
+    # size is not a multiple of 4096 (tail > 0) sends the run that reaches its end back to
+    # page-cache reads, for good; a filesystem that refuses O_DIRECT (tmpfs) does the same
+    # from the start.
+    rng = np.random.default_rng(4)
+    p, _ = _model(tmp_path, rng, layers=2)
+    with open(p, "ab") as f:  # pad to a 4096 multiple, then `tail` more bytes
+        f.write(b"\0" * ((-os.path.getsize(p)) % 4096 + tail))
+    out = []
+    for env_extra in ({}, {"HAYAI_O_DIRECT": "1"}, {"HAYAI_O_DIRECT": "1", "HAYAI_FORCE_FILE_IO": "1"}):
+        code = ("import numpy as np, sys; from hayai_amd.gguf import GgufCatalog; g = GgufCatalog(sys.argv[1]); "
+                "d0 = int(g.o_direct); r = []\n"
+                "for l in (1, 0, 1):\n"
+                "    lp = g.layer_pack(l); d = np.zeros(lp.total, np.uint8); g.load_layer_pack(l, d)\n"
+                "    r.append(d.sum(dtype=np.uint64)); r.append(d[::991].tobytes().hex())\n"
+                "print(d0, *r)")
+        env = dict(os.environ, **env_extra)
+        env.pop("HAYAI_O_DIRECT", None) if not env_extra else None
+        r = subprocess.run([sys.executable, "-c", code, p], env=env, capture_output=True, text=True,
+                           cwd=os.path.dirname(HERE), timeout=120)
+        assert r.returncode == 0, r.stderr
+        out.append(r.stdout.split())
+    assert out[0][0] == "0"
+    assert out[0][1:] == out[1][1:] == out[2][1:]
+
+
 def test_mutated_headers_never_crash(tmp_path):
     # 300 files, each a valid header with a few random bytes changed (or cut short): opening
     # either succeeds with a self-consistent directory or fails with a status; a successful
