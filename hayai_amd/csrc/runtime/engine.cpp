@@ -1059,6 +1059,107 @@ hh_status hh_engine::enqueue_q4k_mmr(int kind, size_t m, size_t n, const uint8_t
     return HH_OK;
 }
 
+// ---- int8 MFMA batched Q4_K (q4k_mmq.hip) ----
+
+// Must match struct hh_mmq_prep_args / hh_mmq_args in kernels/q4k_mmq.hip.
+struct MmqPrepArgs {
+    const float* x;
+    uint8_t* xs;
+    uint32_t n, b, tp, pad;
+};
+struct MmqArgs {
+    const uint8_t* w0;
+    const uint8_t* w1;
+    const uint8_t* xs;
+    float* y;
+    float* part;
+    unsigned* cnt;
+    uint64_t row_bytes;
+    uint32_t m, n, b, nw, kc;
+    int32_t act;
+};
+constexpr size_t kMmqMinTokens = 16, kMmqMaxTokens = 64;
+static size_t mmq_stage_bytes(size_t tp) { return 320 * tp; }
+
+bool hh_engine::mmq_ok(size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const {
+    return mmq && !q4k_generic && b >= kMmqMinTokens && b <= kMmqMaxTokens && m >= 1 && m <= 0xFFFFFFFFu &&
+           n >= 256 && n % 256 == 0 && n <= 0xFFFFFFFFu &&
+           ((((uintptr_t)w0 | (uintptr_t)w1 | (uintptr_t)x) & 15u) == 0);
+}
+
+hh_status hh_engine::enqueue_mmq_prep(const float* x, size_t b, size_t n, size_t tp, void* xs) {
+    hipFunction_t fn;
+    HH_TRY(kernel("hh_mmq_prep", &fn));
+    MmqPrepArgs a{x, (uint8_t*)xs, (uint32_t)n, (uint32_t)b, (uint32_t)tp, 0u};
+    const size_t blocks = tp * (n / 32);  // one 32-lane team per (token, block), 8 per workgroup
+    return launch(fn, (uint32_t)((blocks + 7) / 8), 256, a);
+}
+
+hh_status hh_engine::enqueue_q4k_mmq(bool ffn, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1,
+                                     const void* xs, size_t b, float* y, int act) {
+    const size_t tt = (b + 15) / 16, tp = 16 * tt, nsb = n / 256, nu = (m + 15) / 16;
+    // Superblocks per chunk and units per workgroup, as measured on the MI355X (8B shapes, 16
+    // and 64 tokens): up to 32 tokens, long chunks (whole rows where they fit: no split-K
+    // partials) on 4-wave workgroups; 48..64 tokens, whose stages leave room for few
+    // superblocks, 8-wave workgroups over chunks of 7 (or 4) superblocks.
+    static const int kS[5][6] = {{0}, {2, 4, 7, 8, 14, 16}, {2, 4, 7, 8, 14, 0}, {2, 4, 7, 8, 0, 0}, {2, 4, 6, 7, 0, 0}};
+    const size_t lds = (size_t)props.sharedMemPerBlock;
+    auto fits = [&](int cand) { return cand > 0 && (size_t)cand * mmq_stage_bytes(tp) + 64 <= lds; };
+    int S = 0;
+    for (int i = 0; i < 6; i++) {
+        const int cand = kS[tt][i];
+        if (!fits(cand)) continue;
+        if (mmq_s > 0) {  // HAYAI_HIP_MMQ_S: a fixed chunk size where instantiated
+            if (cand == mmq_s) S = cand;
+            continue;
+        }
+        if (tt <= 2) {
+            // the longest chunk that divides the row (else the longest it holds)
+            if ((size_t)cand <= nsb && (nsb % (size_t)cand == 0 || S == 0 || nsb % (size_t)S != 0)) S = cand;
+        } else if (nsb % 7 == 0 ? cand == 7 : cand == 4) {
+            S = cand;
+        }
+    }
+    if (S == 0)
+        for (int i = 0; i < 6 && S == 0; i++)
+            if (fits(kS[tt][i])) S = kS[tt][i];
+    if (S == 0) return HH_ERR_UNSUPPORTED_DEVICE;
+    const uint32_t kc = (uint32_t)((nsb + S - 1) / S);
+    const size_t nw_want = mmq_nw > 0 ? (size_t)mmq_nw : (tt <= 2 ? 4 : 8);
+    const uint32_t nw = (uint32_t)std::min<size_t>(nw_want, nu);
+    const uint32_t groups = (uint32_t)((nu + nw - 1) / nw);
+    const size_t nt = ffn ? 2 : 1;
+    if (kc > 1) {
+        HH_TRY(grow(&ws_part, &ws_part_cap, (size_t)groups * kc * nw * nt * tt * 4 * 64 * sizeof(float)));
+        if (ws_cnt_cap < groups * sizeof(unsigned)) {
+            HH_TRY(grow(&ws_cnt, &ws_cnt_cap, groups * sizeof(unsigned)));
+            HH_TRY_HIP(hipMemsetAsync(ws_cnt, 0, ws_cnt_cap, stream), "hipMemsetAsync(counters)");
+        }
+    }
+    hipFunction_t fn;
+    HH_TRY(kernel(std::string(ffn ? "hh_q4k_mmq_gu_s" : "hh_q4k_mmq_s") + std::to_string(S) + "_t" + std::to_string(tt),
+                  &fn));
+    MmqArgs a{};
+    a.w0 = w0;
+    a.w1 = ffn ? w1 : w0;
+    a.xs = (const uint8_t*)xs;
+    a.y = y;
+    a.part = (float*)ws_part;
+    a.cnt = (unsigned*)ws_cnt;
+    a.row_bytes = (uint64_t)(nsb * 144);
+    a.m = (uint32_t)m;
+    a.n = (uint32_t)n;
+    a.b = (uint32_t)b;
+    a.nw = nw;
+    a.kc = kc;
+    a.act = act;
+    void* params[] = {&a};
+    const size_t smem = (size_t)S * mmq_stage_bytes(tp);
+    hipError_t err = hipModuleLaunchKernel(fn, groups * kc, 1, 1, nw * 64, 1, 1, (unsigned)smem, stream, params, nullptr);
+    if (err != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel(q4k_mmq)");
+    return HH_OK;
+}
+
 hh_status hh_engine::enqueue_gemv_batched(int type, size_t m, size_t n, const uint8_t* w, const float* x, size_t batch,
                                           float* y) {
     if (batch == 0) return HH_OK;
@@ -1072,6 +1173,13 @@ hh_status hh_engine::enqueue_gemv_batched(int type, size_t m, size_t n, const ui
         const size_t nb = std::min(kMmMaxTokens, batch - b0);
         if (nb == 1) {
             HH_TRY(enqueue_gemv(type, m, n, w, x + b0 * n, y + b0 * m));
+            continue;
+        }
+        if (mmq_ok(m, n, nb, w, w, x + b0 * n)) {  // 16..64 tokens: int8 MFMA
+            const size_t tp = 16 * ((nb + 15) / 16);
+            HH_TRY(grow(&ws_xop, &ws_xop_cap, (n / 256) * mmq_stage_bytes(tp)));
+            HH_TRY(enqueue_mmq_prep(x + b0 * n, nb, n, tp, ws_xop));
+            HH_TRY(enqueue_q4k_mmq(false, m, n, w, nullptr, ws_xop, nb, y + b0 * m, 0));
             continue;
         }
         if (nb <= kMmrMaxTokens && mmr_ok(m, n, nb, w, w, x + b0 * n)) {
@@ -1129,6 +1237,21 @@ hh_status hh_engine::enqueue_ffn_batched(const hh_ffn_desc* d, const uint8_t* pa
         const size_t nb = std::min(kMmMaxTokens, batch - b0);
         if (nb == 1) {
             HH_TRY(enqueue_ffn(d, pack, x + b0 * dm, y + b0 * dm));
+            continue;
+        }
+        if (df % 256 == 0 && mmq_ok(df, dm, nb, wg, wu, x + b0 * dm) && mmq_ok(dm, df, nb, wd, wd, wd)) {
+            // 16..64 tokens on the int8 matrix cores: x -> int8 stages, gate/up + act -> h (f32),
+            // h -> int8 stages, down
+            const size_t tp = 16 * ((nb + 15) / 16);
+            HH_TRY(grow(&ws_xop, &ws_xop_cap, (dm / 256) * mmq_stage_bytes(tp)));
+            HH_TRY(grow(&ws_hop, &ws_hop_cap, (df / 256) * mmq_stage_bytes(tp)));
+            HH_TRY(grow(&ws_h, &ws_h_cap, nb * df * sizeof(float)));
+            HH_TRY(enqueue_mmq_prep(x + b0 * dm, nb, dm, tp, ws_xop));
+            HH_TRY(enqueue_q4k_mmq(true, df, dm, wg, wu, ws_xop, nb, (float*)ws_h, d->act));
+            HH_TRY(enqueue_mmq_prep((const float*)ws_h, nb, df, tp, ws_hop));
+            HH_TRY(enqueue_q4k_mmq(false, dm, df, wd, nullptr, ws_hop, nb, y + b0 * dm, 0));
+            ffn_stage_valid = false;
+            ffn_calls += 3 * nb;
             continue;
         }
         if (nb <= kMmrMaxTokens && df % 256 == 0 && mmr_ok(df, dm, nb, wg, wu, x + b0 * dm) &&
@@ -1370,6 +1493,10 @@ static std::vector<std::string> required_kernels() {
     for (int S : {2, 4, 7, 8})
         for (const char* kind : {"hh_q4k_mmr_s", "hh_q4k_mmr_gu_s"}) k.push_back(std::string(kind) + std::to_string(S));
     for (int S : {2, 4, 7, 8, 14, 16}) k.push_back("hh_q4k_mmr_dn_s" + std::to_string(S));
+    k.push_back("hh_mmq_prep");
+    for (const char* st : {"s2_t1", "s4_t1", "s7_t1", "s8_t1", "s14_t1", "s16_t1", "s2_t2", "s4_t2", "s7_t2", "s8_t2",
+                           "s14_t2", "s2_t3", "s4_t3", "s7_t3", "s8_t3", "s2_t4", "s4_t4", "s6_t4", "s7_t4"})
+        for (const char* kind : {"hh_q4k_mmq_", "hh_q4k_mmq_gu_"}) k.push_back(std::string(kind) + st);
     k.push_back("hh_lut_gemv");
     for (const char* f : {"g1_d1", "g1_d2", "g1_d4", "g1_d8", "g2_d2", "g2_d4", "g2_d8"})
         k.push_back(std::string("hh_q4k_ffnp_") + f);
@@ -1449,6 +1576,9 @@ hh_status engine_create(int device, hh_engine** out) {
     if (const char* f = getenv("HAYAI_HIP_RING")) e->ring = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_MOE_GROUPED")) e->moe_grouped = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_SMALL_FFN")) e->small_ffn = atoi(f) != 0;
+    if (const char* f = getenv("HAYAI_HIP_MMQ")) e->mmq = atoi(f) != 0;
+    if (const char* f = getenv("HAYAI_HIP_MMQ_S")) e->mmq_s = atoi(f);
+    if (const char* f = getenv("HAYAI_HIP_MMQ_NW")) e->mmq_nw = std::min(8, std::max(0, atoi(f)));
     if (const char* f = getenv("HAYAI_HIP_DMA_SPLIT")) e->dma_split = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_RING_GU_PER_CU")) e->ring_gu_per_cu = std::max(1, atoi(f));
     if (const char* f = getenv("HAYAI_HIP_RING_DN_PER_CU")) e->ring_dn_per_cu = std::max(1, atoi(f));

@@ -65,6 +65,7 @@ def lib():
         L.or_moe_token.argtypes = [C.c_int, sz, sz, P, sz, sz, sz, sz, C.c_int, P, P, P, P]
         L.or_quantize_q4_k.argtypes = [P, sz, P]
         L.or_quantize_act_q8.argtypes = [P, sz, P, P]
+        L.or_ffn_q8.argtypes = [C.c_int, C.c_int, C.c_int, sz, sz, P, sz, P, sz, P, sz, C.c_int, P, P]
         L.or_get_scale_min_k4.argtypes = [C.c_int, P, P, P]
         L.or_iq2xxs_grid.argtypes = [P]
         L.or_iq3xxs_grid.argtypes = [P]
@@ -195,6 +196,24 @@ def ffn(types, d_model: int, d_ff: int, wg, wu, wd, x, act: int = 0, return_h: b
     _check(lib().or_ffn(tg, tu, td, d_model, d_ff, _p(wg), wg.size, _p(wu), wu.size, _p(wd), wd.size,
                         act, _p(x), _p(y), _p(h)), "ffn")
     return (y, h) if return_h else y
+
+
+def dequant_act_q8(x: np.ndarray) -> np.ndarray:
+    """q * s of quantize_act_q8: the activation the batched int8 path computes with."""
+    q, s = quantize_act_q8(x)
+    return (q.astype(np.float32) * np.repeat(s, 32)).astype(np.float32)
+
+
+def ffn_q8(types, d_model: int, d_ff: int, wg, wu, wd, x, act: int = 0) -> np.ndarray:
+    """The batched int8 path's FFN: both GEMV inputs (x, and h before down) dequantized from
+    their int8 per-32-block quantization."""
+    tg, tu, td = types
+    wg, wu, wd = (np.ascontiguousarray(a, dtype=np.uint8) for a in (wg, wu, wd))
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(d_model, np.float32)
+    _check(lib().or_ffn_q8(tg, tu, td, d_model, d_ff, _p(wg), wg.size, _p(wu), wu.size, _p(wd), wd.size, act,
+                           _p(x), _p(y)), "ffn_q8")
+    return y
 
 
 def rms_norm(x, w, eps: float) -> np.ndarray:

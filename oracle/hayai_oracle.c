@@ -880,6 +880,42 @@ int or_quantize_act_q8(const float* x, size_t n, int8_t* q, float* s) {
     return OR_OK;
 }
 
+/* x -> q * s, the activation the batched int8 path computes with (q, s of
+ * or_quantize_act_q8; one f32 product per element). */
+static int dequant_act_q8(const float* x, size_t n, float* out) {
+    int8_t* q = (int8_t*)malloc(n);
+    float* s = (float*)malloc(sizeof(float) * (n / 32 + 1));
+    int rc = OR_EINVAL;
+    if (q && s && or_quantize_act_q8(x, n, q, s) == OR_OK) {
+        for (size_t i = 0; i < n; i++) out[i] = (float)q[i] * s[i / 32];
+        rc = OR_OK;
+    }
+    free(q);
+    free(s);
+    return rc;
+}
+
+/* The FFN of the batched int8 path (activations quantized to int8
+ * per 32-element block): both GEMV inputs are the dequantized int8 activations, x -> q * s
+ * before gate and up, h -> q * s before down; otherwise or_ffn. */
+int or_ffn_q8(int tg, int tu, int td, size_t d_model, size_t d_ff, const uint8_t* wg, size_t lg,
+              const uint8_t* wu, size_t lu, const uint8_t* wd, size_t ld, int act, const float* x, float* y) {
+    float* xq = (float*)malloc(d_model * sizeof(float));
+    float* h = (float*)malloc(d_ff * sizeof(float));
+    float* hq = (float*)malloc(d_ff * sizeof(float));
+    float* tmp = (float*)malloc(d_model * sizeof(float));
+    int rc = OR_EINVAL;
+    if (xq && h && hq && tmp && dequant_act_q8(x, d_model, xq) == OR_OK &&
+        or_ffn(tg, tu, td, d_model, d_ff, wg, lg, wu, lu, wd, ld, act, xq, tmp, h) == OR_OK &&
+        dequant_act_q8(h, d_ff, hq) == OR_OK)
+        rc = or_gemv(td, d_model, d_ff, wd, ld, hq, y);
+    free(xq);
+    free(h);
+    free(hq);
+    free(tmp);
+    return rc;
+}
+
 /* Table accessors for the tests. */
 void or_iq2xxs_grid(uint64_t* out) { memcpy(out, OR_IQ2XXS_GRID, sizeof(OR_IQ2XXS_GRID)); }
 void or_iq3xxs_grid(uint32_t* out) { memcpy(out, OR_IQ3XXS_GRID, sizeof(OR_IQ3XXS_GRID)); }

@@ -2,9 +2,12 @@
 
 ggml_gemv_batched_q4_k (crates/hayai-opencl/src/compute.rs:179-257) computes B GEMVs that
 share W; execute_quant_gemv_batched (crates/hayai-core/src/orchestrator.rs:240-269) runs
-other types token by token.  The MFMA path rounds x (and the FFN intermediate) to f16, so
-parity is held to the FFN tolerance (max |y - ref| / max |ref| <= 1e-3 per token) against
-the oracle's f32 restatement fed the original f32 inputs.
+other types token by token.  Two matrix-core paths:
+- 16..64 tokens per pass: activations quantized to int8 per
+  32-element block, int8 MFMA; parity against the oracle fed the same quantized activations
+  (oracle.dequant_act_q8 / oracle.ffn_q8), the quantization's own error printed beside it;
+- 2..15 tokens: f16 operands with f32-level accuracy, against the oracle's f32 restatement.
+Both are held to the FFN tolerance (max |y - ref| / max |ref| <= 1e-3 per token).
 """
 import numpy as np
 import pytest
@@ -26,6 +29,22 @@ def rel_err(y, ref):
 
 def per_token_err(Y, R):
     return max(rel_err(Y[b], R[b]) for b in range(Y.shape[0]))
+
+
+def int8_tokens(batch):
+    """Which tokens go through the int8 path: passes of up to 64 tokens, those of 16 or more."""
+    on = np.zeros(batch, bool)
+    for b0 in range(0, batch, 64):
+        nb = min(64, batch - b0)
+        on[b0:b0 + nb] = nb >= 16
+    return on
+
+
+def batched_ref(t, m, n, w, X):
+    """Per token: the oracle GEMV of the activation the path computes with."""
+    on = int8_tokens(X.shape[0])
+    Xq = np.stack([oracle.dequant_act_q8(X[b]) if on[b] else X[b] for b in range(X.shape[0])])
+    return oracle.gemv_batched(t, m, n, w, Xq)
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -54,9 +73,11 @@ def test_q4_k_batched_matches_oracle(engine, m, n, batch):
     w = synth.matrix(Q4_K, m, n, synth.seed_for(3, batch, m))
     X = synth.normal(synth.seed_for(3, batch, n), batch * n).reshape(batch, n)
     Y = engine.ggml_gemv_batched_q4_k(m, n, w, X, batch).reshape(batch, m)
-    R = oracle.gemv_batched(Q4_K, m, n, w, X)
+    R = batched_ref(Q4_K, m, n, w, X)
     err = per_token_err(Y, R)
-    print(f"  per-token max rel err {err:.3e}", flush=True)
+    qerr = per_token_err(Y, oracle.gemv_batched(Q4_K, m, n, w, X))
+    print(f"  per-token max rel err {err:.3e} (vs f32 activations: {qerr:.3e}, "
+          f"int8 tokens {int(int8_tokens(batch).sum())})", flush=True)
     assert np.isfinite(Y).all()
     assert err <= REL_TOL
 
@@ -94,7 +115,7 @@ def test_batched_dev_offsets(engine):
     ybuf = engine.alloc(128 + 4 * batch * m)
     engine.gemv_batched_dev(Q4_K, m, n, wbuf, 256, xbuf, 64, batch, ybuf, 128)
     Y = ybuf.read(np.float32, batch * m, 128).reshape(batch, m)
-    assert per_token_err(Y, oracle.gemv_batched(Q4_K, m, n, w, X)) <= REL_TOL
+    assert per_token_err(Y, batched_ref(Q4_K, m, n, w, X)) <= REL_TOL
     with pytest.raises(hayai_amd.HipError):
         engine.gemv_batched_dev(Q4_K, m, n, wbuf, 256, xbuf, 64, batch + 1, ybuf, 128)  # x too short
 
@@ -125,10 +146,31 @@ def test_ffn_batched_matches_oracle(engine, types, d_model, d_ff, batch, act):
     desc = engine.ffn_desc(types, d_model, d_ff, lay, act)
     X = synth.normal(synth.seed_for(3, batch, synth.ACT), batch * d_model).reshape(batch, d_model)
     Y = engine.ffn_batched(desc, pack, 0, X)
-    R = np.stack([oracle.ffn(types, d_model, d_ff, wg, wu, wd, X[b], act=act) for b in range(batch)])
+    on = int8_tokens(batch) if types == (12, 12, 12) else np.zeros(batch, bool)
+    R = np.stack([(oracle.ffn_q8 if on[b] else oracle.ffn)(types, d_model, d_ff, wg, wu, wd, X[b], act=act)
+                  for b in range(batch)])
     err = per_token_err(Y, R)
-    print(f"  per-token max rel err {err:.3e}", flush=True)
+    R32 = np.stack([oracle.ffn(types, d_model, d_ff, wg, wu, wd, X[b], act=act) for b in range(batch)])
+    print(f"  per-token max rel err {err:.3e} (vs f32 activations: {per_token_err(Y, R32):.3e})", flush=True)
     assert err <= REL_TOL
     if types == (2, 2, 2):
         for b in range(batch):  # non-Q4_K formats: the single-token op per token
             np.testing.assert_array_equal(Y[b], engine.ffn(desc, pack, 0, X[b]))
+
+
+@pytest.mark.parametrize("batch", [16, 40, 64])
+def test_int8_path_off_keeps_f16_kernels(monkeypatch, batch):
+    # HAYAI_HIP_MMQ=0: 16..64 tokens run the f16 kernels (f32-level accuracy) instead, held to
+    # the oracle fed the original f32 activations; the int8 engine's output differs from them
+    # by the activation quantization only
+    print(f"[case] batched f16 kernels batch={batch}", flush=True)
+    monkeypatch.setenv("HAYAI_HIP_MMQ", "0")
+    eng = hayai_amd.HipEngine(0)
+    try:
+        m, n = 4096, 14336
+        w = synth.matrix(Q4_K, m, n, 71)
+        X = synth.normal(72 + batch, batch * n).reshape(batch, n)
+        Y = eng.ggml_gemv_batched_q4_k(m, n, w, X, batch).reshape(batch, m)
+        assert per_token_err(Y, oracle.gemv_batched(Q4_K, m, n, w, X)) <= REL_TOL
+    finally:
+        eng.close()

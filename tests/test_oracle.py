@@ -669,3 +669,20 @@ def test_moe_pin_catches_expert_index_slip():
     finally:
         oracle.set_mutation(0)
     assert not np.all(np.abs(bad - ref) <= bound)
+
+
+def test_ffn_q8_composes_the_pinned_pieces():
+    # or_ffn_q8 (the batched int8 path's FFN) = or_ffn on x -> q*s, then the down GEMV of
+    # h -> q*s, with or_quantize_act_q8, or_ffn and or_gemv each pinned above: bit-exact
+    types, d_model, d_ff = (oracle.Q4_K,) * 3, 256, 512
+    wg, wu, wd = _ffn_weights(types, d_model, d_ff, 800)
+    x = np.random.default_rng(8).normal(size=d_model).astype(np.float32)
+    xq = oracle.dequant_act_q8(x)
+    q, s = oracle.quantize_act_q8(x)
+    assert np.array_equal(xq, q.astype(np.float32) * np.repeat(s, 32))
+    _, h = oracle.ffn(types, d_model, d_ff, wg, wu, wd, xq, return_h=True)
+    y = oracle.gemv(oracle.Q4_K, d_model, d_ff, wd, oracle.dequant_act_q8(h))
+    np.testing.assert_array_equal(oracle.ffn_q8(types, d_model, d_ff, wg, wu, wd, x), y)
+    # and the quantization moves the FFN by about the int8 step, not more
+    yf = oracle.ffn(types, d_model, d_ff, wg, wu, wd, x)
+    assert 1e-4 < np.max(np.abs(y - yf)) / np.max(np.abs(yf)) < 3e-2
