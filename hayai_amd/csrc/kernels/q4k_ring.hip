@@ -14,6 +14,16 @@
 //
 // Intermediate: q1[d_ff] | q2[d_ff] int8 | scale[d_ff/8] f32, h ~ scale * (q1 + q2/256) per
 // granule of 8 rows (granules never straddle workgroups).
+//
+// The two bodies are generic over the weight format F (Q4_K here; Q6_K in q6k_ring.hip,
+// IQ2_XXS / IQ3_XXS in iq_ring.hip).  F supplies:
+//   UNIT             columns per lane unit (64 for every format)
+//   TAB_BYTES        lookup tables the format keeps in static LDS (multiple of 16; 0: none),
+//                    copied from tables() by the kernel
+//   lane_t, lane(u)  the lane's fixed byte offsets within a row for unit u
+//   data, issue()    one ring item: the lane's loads of one row
+//   xr_t, load_x()   x as per-32 digits (gate/up); unit_x(): the (row, unit) contribution
+//   hr_t, load_h()   h as per-8 digits (down);     unit_h(): the (row, unit) contribution
 
 #define HH_RING_BLOCK (HH_FFNP_CW * HH_WAVE)
 
@@ -56,11 +66,50 @@ struct hh_dnr_args {
     uint32_t d_ff;
 };
 
+// The format's LDS tables: a static LDS array (its address is a compile-time constant, so
+// table reads take an immediate offset), or none.
+template <uint32_t N>
+HH_DEV char* hh_ring_tables_lds() {
+    __shared__ __attribute__((aligned(16))) char t[N];
+    return t;
+}
+template <>
+HH_DEV char* hh_ring_tables_lds<0>() {
+    return nullptr;
+}
+
+struct hh_ring_q4k {
+    static constexpr uint32_t UNIT = 64;
+    static constexpr uint32_t TAB_BYTES = 0;
+    struct lane_t {
+        uint32_t oh, oq;  // block header, this unit's 32 qs bytes
+    };
+    typedef hh_q4k_data data;
+    typedef hh_q4k_x xr_t;
+    typedef hh_ffnp_h hr_t;
+    static HH_DEV lane_t lane(uint32_t u) {
+        const uint32_t oh = (u >> 2) * 144u;
+        return lane_t{oh, oh + 16u + (u & 3u) * 32u};
+    }
+    static HH_DEV void issue(const uint8_t* row, const lane_t& l, data& s) {
+        s.h = hh_ld16(row + l.oh);
+        s.q0 = hh_ld16(row + l.oq);
+        s.q1 = hh_ld16(row + l.oq + 16);
+    }
+    static HH_DEV const uint4* tables() { return nullptr; }
+    static HH_DEV void load_x(const hh_digits_ptr& xd, uint32_t u, xr_t& xr) { hh_q4k_load_lane_x(xd, u, xr); }
+    static HH_DEV void load_h(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hr_t& h) {
+        hh_ffnp_load_h(q1, q2, sc, u, h);
+    }
+    static HH_DEV float unit_x(const data& s, const lane_t&, const xr_t& xr, const char*) { return hh_q4k_unit(s, xr); }
+    static HH_DEV float unit_h(const data& s, const lane_t&, const hr_t& h, const char*) { return hh_ffnp_unit_g8(s, h); }
+};
+
 // Gate/up: workgroup w owns the 8-row granules [w*NG/G, (w+1)*NG/G) of W_gate and W_up; a
 // team of WPT1 waves reads one row (lane = unit, x as per-32 digits in registers).  After
 // the last row, wave 0 applies the activation to the workgroup's rows and writes their
 // digits.
-template <int WPT1, int D, int P, bool NORM>
+template <class F, int WPT1, int D, int P, bool NORM>
 HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
     extern __shared__ __attribute__((aligned(16))) char hh_smem[];
     constexpr uint32_t TEAM1 = WPT1 * HH_WAVE, TPW1 = HH_FFNP_CW / WPT1;
@@ -76,35 +125,43 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
     const uint32_t n1 = (RR + TPW1 - 1) / TPW1;
     const uint32_t n1p = (n1 + D - 1) / D * D;
 
-    // LDS: [x digits][gate/up row sums][staging 128 B]
+    // LDS: static: the format's tables; dynamic: [x digits][gate/up row sums][staging 128 B]
+    char* const tabs = hh_ring_tables_lds<F::TAB_BYTES>();
+    char* const lds = hh_smem;
     const uint32_t xbytes = 2u * dm + (dm / 32u) * 8u;
     hh_digits_ptr xd;
-    xd.q1 = reinterpret_cast<int8_t*>(hh_smem);
+    xd.q1 = reinterpret_cast<int8_t*>(lds);
     xd.q2 = xd.q1 + dm;
     xd.sc = reinterpret_cast<float*>(xd.q2 + dm);
     xd.sum = xd.sc + dm / 32;
-    float* gu = reinterpret_cast<float*>(hh_smem + ((xbytes + 15u) & ~15u));  // [RR][WPT1]
+    float* gu = reinterpret_cast<float*>(lds + ((xbytes + 15u) & ~15u));  // [RR][WPT1]
     uint8_t* stage = reinterpret_cast<uint8_t*>(gu + ((RR * WPT1 + 3u) & ~3u));
 
     const uint32_t lane1 = tid % TEAM1, team1 = (wave / WPT1) % TPW1;
-    const bool act1 = lane1 < dm / 64;
+    const bool act1 = lane1 < dm / F::UNIT;
     const uint32_t u1 = act1 ? lane1 : 0u;
     const uint8_t* const wgp = a.wg;
     const uint8_t* const wup = a.wu;
-    const uint32_t oh = (u1 >> 2) * 144u, oq = oh + 16u + (u1 & 3u) * 32u;
+    const typename F::lane_t lo = F::lane(u1);
     // item j of this team: row read i = team1 + j*TPW1 (gate and up rows interleaved); reads
     // past the workgroup's rows (ring padding) re-read the start of W_gate
-    auto issue = [&](uint32_t j, hh_q4k_data& s) {
+    auto issue = [&](uint32_t j, typename F::data& s) {
         const uint32_t i = team1 + j * TPW1;
         const uint8_t* row = i < RR ? ((i & 1u) ? wup : wgp) + (size_t)(r0 + (i >> 1)) * a.rb1 : wgp;
-        s.h = hh_ld16(row + oh);
-        s.q0 = hh_ld16(row + oq);
-        s.q1 = hh_ld16(row + oq + 16);
+        F::issue(row, lo, s);
     };
+
+    // the format's tables (if any) are requested first and stored to LDS with x's digits
+    constexpr uint32_t TAB16 = F::TAB_BYTES / 16u;
+    uint4 tab = make_uint4(0u, 0u, 0u, 0u);
+    if constexpr (TAB16 > 0) {
+        static_assert(TAB16 <= HH_RING_BLOCK, "one 16-byte table chunk per thread");
+        if (tid < TAB16) tab = F::tables()[tid];
+    }
 
     // prologue: x loads first, then P ring items, x -> per-32 digits in LDS, the rest of the
     // ring (x is not queued behind a burst of weight requests)
-    hh_q4k_data ring[D];
+    typename F::data ring[D];
     const uint32_t c = tid;  // chunk of 8 elements (d_model <= 8 * 512 per pass)
     const bool has = c < dm / 8;
     const float4* x4 = reinterpret_cast<const float4*>(a.x);
@@ -132,6 +189,9 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
         if (lane == 0) red[wave] = ss;                   // read after the main loop's barrier
         hh_norm8(t0, t1, m0, m1, 1.f);
     }
+    if constexpr (TAB16 > 0) {
+        if (tid < TAB16) reinterpret_cast<uint4*>(tabs)[tid] = tab;
+    }
     hh_ffnp_digits_chunk(t0, t1, c, has, xd);
     for (uint32_t c2 = c + HH_RING_BLOCK; c2 < dm / 8; c2 += HH_RING_BLOCK) {
         float4 v0 = x4[2 * c2], v1 = x4[2 * c2 + 1];  // d_model > 4096: later passes
@@ -143,15 +203,15 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
     __syncthreads();
 
     {
-        hh_q4k_x xr;
-        hh_q4k_load_lane_x(xd, u1, xr);
+        typename F::xr_t xr;
+        F::load_x(xd, u1, xr);
         for (uint32_t j0 = 0; j0 < n1p; j0 += D) {
 #pragma unroll
             for (int s = 0; s < D; s++) {
                 const uint32_t j = j0 + (uint32_t)s;
                 const uint32_t i = team1 + j * TPW1;
                 if (i < RR) {  // wave-uniform
-                    float v = hh_q4k_unit(ring[s], xr);
+                    float v = F::unit_x(ring[s], lo, xr, tabs);
                     v = hh_wave_sum(act1 ? v : 0.f);
                     if (lane == 0) gu[i * WPT1 + wave % WPT1] = v;
                 }
@@ -220,7 +280,7 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
 // lane partials meet in LDS and a 32-lane DPP reduction per row writes y (fixed order:
 // deterministic).
 #define HH_DN_BLOCK ((HH_FFNP_CW + 1) * HH_WAVE)
-template <int WPT2, int D>
+template <class F, int WPT2, int D>
 HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
     extern __shared__ __attribute__((aligned(16))) char hh_smem[];
     constexpr uint32_t TEAM2 = WPT2 * HH_WAVE, TPW2 = HH_FFNP_CW / WPT2;
@@ -238,53 +298,61 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
     float res0 = 0.f;
     if (a.res && tid % 32 == 31 && tid / 32 < q1 - q0) res0 = a.res[q0 + tid / 32];
 
-    // LDS: [intermediate][lane partials: rows x TEAM2]
+    // LDS: static: the format's tables; dynamic: [intermediate][lane partials: rows x TEAM2]
+    char* const tabs = hh_ring_tables_lds<F::TAB_BYTES>();
+    char* const lds = hh_smem;
     const uint32_t hbytes = 2u * dff + (dff / 8u) * 4u;
-    int8_t* hq1 = reinterpret_cast<int8_t*>(hh_smem);
+    int8_t* hq1 = reinterpret_cast<int8_t*>(lds);
     int8_t* hq2 = hq1 + dff;
     float* hsc = reinterpret_cast<float*>(hq2 + dff);
-    float* part = reinterpret_cast<float*>(hh_smem + ((hbytes + 15u) & ~15u));
+    float* part = reinterpret_cast<float*>(lds + ((hbytes + 15u) & ~15u));
 
     const uint32_t lane2 = tid % TEAM2, team2 = (wave / WPT2) % TPW2;
-    const bool act2 = lane2 < dff / 64;
+    const bool act2 = lane2 < dff / F::UNIT;
     const uint32_t u2 = act2 ? lane2 : 0u;
     const uint8_t* const wdp = a.wd;
-    const uint32_t oh = (u2 >> 2) * 144u, oq = oh + 16u + (u2 & 3u) * 32u;
-    auto issue = [&](uint32_t k, hh_q4k_data& s) {  // item k: row team2 + k*TPW2
+    const typename F::lane_t lo = F::lane(u2);
+    auto issue = [&](uint32_t k, typename F::data& s) {  // item k: row team2 + k*TPW2
         const uint32_t r = q0 + team2 + k * TPW2;
-        const uint8_t* row = r < q1 ? wdp + (size_t)r * a.rb2 : wdp;
-        s.h = hh_ld16(row + oh);
-        s.q0 = hh_ld16(row + oq);
-        s.q1 = hh_ld16(row + oq + 16);
+        F::issue(wdp + (size_t)(r < q1 ? r : q0) * a.rb2, lo, s);  // padding re-reads row q0
     };
 
-    hh_q4k_data ring[D];
+    typename F::data ring[D];
     if (wave < HH_FFNP_CW) {
 #pragma unroll
         for (int s = 0; s < D; s++) issue((uint32_t)s, ring[s]);
     } else {
-        // the intermediate -> LDS, every 16-byte chunk in flight at once
+        // the format's tables and the intermediate -> LDS, every 16-byte chunk in flight at once
+        constexpr uint32_t TAB16 = F::TAB_BYTES / 16u;
+        if constexpr (TAB16 > 0) {
+            for (uint32_t c0 = 0; c0 < TAB16; c0 += HH_WAVE) {
+                if (c0 + lane < TAB16)
+                    __builtin_amdgcn_global_load_lds(
+                        (const __attribute__((address_space(1))) void*)(F::tables() + c0 + lane),
+                        (__attribute__((address_space(3))) void*)(tabs + (size_t)c0 * 16), 16, 0, 0);
+            }
+        }
         const uint32_t chunks = hbytes / 16u;
         for (uint32_t c0 = 0; c0 < chunks; c0 += HH_WAVE) {
             if (c0 + lane < chunks)
                 __builtin_amdgcn_global_load_lds(
                     (const __attribute__((address_space(1))) void*)(a.hx + (size_t)(c0 + lane) * 16),
-                    (__attribute__((address_space(3))) void*)(hh_smem + (size_t)c0 * 16), 16, 0, 0);
+                    (__attribute__((address_space(3))) void*)(lds + (size_t)c0 * 16), 16, 0, 0);
         }
         __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();  // the intermediate is in LDS (the rings stay in flight)
 
     if (wave < HH_FFNP_CW) {
-        hh_ffnp_h hr;
-        hh_ffnp_load_h(hq1, hq2, hsc, u2, hr);
+        typename F::hr_t hr;
+        F::load_h(hq1, hq2, hsc, u2, hr);
         for (uint32_t j0 = 0; j0 < n2p; j0 += D) {
 #pragma unroll
             for (int s = 0; s < D; s++) {
                 const uint32_t k = j0 + (uint32_t)s;
                 const uint32_t rl = team2 + k * TPW2;  // local row
                 if (q0 + rl < q1) {                    // wave-uniform
-                    const float v = hh_ffnp_unit_g8(ring[s], hr);
+                    const float v = F::unit_h(ring[s], lo, hr, tabs);
                     part[rl * TEAM2 + lane2] = act2 ? v : 0.f;  // reduced after the loop
                 }
                 issue(k + D, ring[s]);
@@ -319,14 +387,14 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
 // _n: with the RMSNorm prologue (the FFN residual block)
 #define HH_GU_RING(G1)                                                                          \
     extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_q4k_gu_ring_g##G1(const hh_gur_args a) { \
-        hh_gu_ring_body<G1, 3, 1, false>(a);                                                    \
+        hh_gu_ring_body<hh_ring_q4k, G1, 3, 1, false>(a);                                       \
     }                                                                                           \
     extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_q4k_gu_ring_g##G1##_n(const hh_gur_args a) { \
-        hh_gu_ring_body<G1, 3, 1, true>(a);                                                     \
+        hh_gu_ring_body<hh_ring_q4k, G1, 3, 1, true>(a);                                        \
     }
 #define HH_DN_RING(G2)                                                                          \
     extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) hh_q4k_dn_ring_d##G2(const hh_dnr_args a) { \
-        hh_dn_ring_body<G2, 3>(a);                                                              \
+        hh_dn_ring_body<hh_ring_q4k, G2, 3>(a);                                                 \
     }
 HH_GU_RING(1)
 HH_GU_RING(2)

@@ -113,116 +113,55 @@ HH_DEV float hh_q6k_unit(const hh_q6k_raw& raw, uint32_t sh, uint32_t is, const 
     return d * acc;
 }
 
-template <int WPT2, int D>
-HH_DEV void hh_q6k_dn_ring_body(const hh_dnr_args& a) {
-    extern __shared__ __attribute__((aligned(16))) char hh_smem[];
-    constexpr uint32_t TEAM2 = WPT2 * HH_WAVE, TPW2 = HH_FFNP_CW / WPT2;
-    const uint32_t tid = threadIdx.x;
-    const uint32_t lane = tid % HH_WAVE;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / HH_WAVE);
-    const uint32_t G = gridDim.x, w = blockIdx.x;
-    const uint32_t dm = a.d_model, dff = a.d_ff;
-    const uint32_t q0 = (uint32_t)(((uint64_t)w * dm) / G);
-    const uint32_t q1 = (uint32_t)(((uint64_t)(w + 1) * dm) / G);
-    const uint32_t n2 = (q1 - q0 + TPW2 - 1) / TPW2;
-    const uint32_t n2p = (n2 + D - 1) / D * D;
-
-    // the residual of the first row this thread stores, fetched now rather than on the tail
-    float res0 = 0.f;
-    if (a.res && tid % 32 == 31 && tid / 32 < q1 - q0) res0 = a.res[q0 + tid / 32];
-
-    // LDS: [intermediate][lane partials: rows x TEAM2]
-    const uint32_t hbytes = 2u * dff + (dff / 8u) * 4u;
-    int8_t* hq1 = reinterpret_cast<int8_t*>(hh_smem);
-    int8_t* hq2 = hq1 + dff;
-    float* hsc = reinterpret_cast<float*>(hq2 + dff);
-    float* part = reinterpret_cast<float*>(hh_smem + ((hbytes + 15u) & ~15u));
-
-    const uint32_t lane2 = tid % TEAM2, team2 = (wave / WPT2) % TPW2;
-    const bool act2 = lane2 < dff / 64;
-    const uint32_t u2 = act2 ? lane2 : 0u;
-    // this lane's superblock within a row and its pieces (row-relative byte offsets); rows
-    // start 4-byte aligned (the host checks: an even number of superblocks per row), so the
-    // block's alignment is 210*b mod 4 and the last block of a row (odd b) ends its row's
-    // reads exactly
-    const uint32_t blk = (u2 >> 2) * 210u, hh = (u2 >> 1) & 1u, is = u2 & 1u;
-    const uint32_t sh = (blk & 2u) * 8u;  // 0 or 16 bits
-    const uint32_t base = blk & ~3u;
-    const uint32_t oa = base + 64u * hh + 16u * is, ob = oa + 32u, oh = base + 128u + 32u * hh + 16u * is;
-    const uint32_t os = base + 192u + 8u * hh, od = base + 208u;
-    const uint8_t* const wdp = a.wd;
-    auto issue = [&](uint32_t k, hh_q6k_raw& s) {  // item k: row team2 + k*TPW2
-        const uint32_t r = q0 + team2 + k * TPW2;
-        const uint8_t* row = wdp + (size_t)(r < q1 ? r : q0) * a.rb2;
-        hh_q6k_ld5(row + oa, s.a);
-        hh_q6k_ld5(row + ob, s.b);
-        hh_q6k_ld5(row + oh, s.h);
-        s.s[0] = *reinterpret_cast<const uint32_t*>(row + os);
-        s.s[1] = *reinterpret_cast<const uint32_t*>(row + os + 4);
-        s.s[2] = *reinterpret_cast<const uint32_t*>(row + os + 8);
-        s.d = *reinterpret_cast<const uint32_t*>(row + od);
+// The Q6_K down format of the generic ring body (hh_dn_ring_body, q4k_ring.hip).  Rows start
+// 4-byte aligned (the host checks: an even number of superblocks per row), so the lane's
+// block is 4-byte aligned or 2 bytes off (210*b mod 4) and the last block of a row (odd b)
+// ends its row's reads exactly.
+struct hh_ring_q6k {
+    static constexpr uint32_t UNIT = 64;
+    static constexpr uint32_t TAB_BYTES = 0;
+    struct lane_t {
+        uint32_t oa, ob, oh, os, od;  // dword-aligned offsets of the lane's pieces
+        uint32_t sh, is;              // realignment (0 or 16 bits), quarter within the half
     };
-
-    hh_q6k_raw ring[D];
-    if (wave < HH_FFNP_CW) {
-#pragma unroll
-        for (int s = 0; s < D; s++) issue((uint32_t)s, ring[s]);
-    } else {
-        // the intermediate -> LDS, every 16-byte chunk in flight at once
-        const uint32_t chunks = hbytes / 16u;
-        for (uint32_t c0 = 0; c0 < chunks; c0 += HH_WAVE) {
-            if (c0 + lane < chunks)
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void*)(a.hx + (size_t)(c0 + lane) * 16),
-                    (__attribute__((address_space(3))) void*)(hh_smem + (size_t)c0 * 16), 16, 0, 0);
-        }
-        __builtin_amdgcn_s_waitcnt(0);
+    typedef hh_q6k_raw data;
+    typedef hh_q6k_h hr_t;
+    static HH_DEV lane_t lane(uint32_t u) {
+        const uint32_t blk = (u >> 2) * 210u, hh = (u >> 1) & 1u, is = u & 1u;
+        const uint32_t base = blk & ~3u;
+        lane_t l;
+        l.oa = base + 64u * hh + 16u * is;
+        l.ob = l.oa + 32u;
+        l.oh = base + 128u + 32u * hh + 16u * is;
+        l.os = base + 192u + 8u * hh;
+        l.od = base + 208u;
+        l.sh = (blk & 2u) * 8u;
+        l.is = is;
+        return l;
     }
-    __syncthreads();  // the intermediate is in LDS (the rings stay in flight)
-
-    if (wave < HH_FFNP_CW) {
-        hh_q6k_h hr;
-        hh_q6k_load_h(hq1, hq2, hsc, u2, hr);
-        for (uint32_t j0 = 0; j0 < n2p; j0 += D) {
-#pragma unroll
-            for (int s = 0; s < D; s++) {
-                const uint32_t k = j0 + (uint32_t)s;
-                const uint32_t rl = team2 + k * TPW2;  // local row
-                if (q0 + rl < q1) {                    // wave-uniform
-                    const float v = hh_q6k_unit(ring[s], sh, is, hr);
-                    part[rl * TEAM2 + lane2] = act2 ? v : 0.f;  // reduced after the loop
-                }
-                issue(k + D, ring[s]);
-            }
-        }
+    static HH_DEV void issue(const uint8_t* row, const lane_t& l, data& s) {
+        hh_q6k_ld5(row + l.oa, s.a);
+        hh_q6k_ld5(row + l.ob, s.b);
+        hh_q6k_ld5(row + l.oh, s.h);
+        s.s[0] = *reinterpret_cast<const uint32_t*>(row + l.os);
+        s.s[1] = *reinterpret_cast<const uint32_t*>(row + l.os + 4);
+        s.s[2] = *reinterpret_cast<const uint32_t*>(row + l.os + 8);
+        s.d = *reinterpret_cast<const uint32_t*>(row + l.od);
     }
-    __syncthreads();  // lane partials are in LDS
-    {
-        constexpr uint32_t PER = TEAM2 / 32;
-        const uint32_t nrows = q1 - q0;
-        for (uint32_t rl0 = 0; rl0 < nrows; rl0 += HH_DN_BLOCK / 32) {
-            const uint32_t rl = rl0 + tid / 32, seg = tid % 32;
-            float s = 0.f;
-            if (rl < nrows) {
-                const float* p = part + rl * TEAM2 + seg * PER;
-#pragma unroll
-                for (uint32_t i = 0; i < PER; i++) s += p[i];
-            }
-            s += hh_dpp<0xB1>(s);        // quad_perm [1,0,3,2]
-            s += hh_dpp<0x4E>(s);        // quad_perm [2,3,0,1]
-            s += hh_dpp<0x124>(s);       // row_ror:4
-            s += hh_dpp<0x128>(s);       // row_ror:8 -> each row of 16 holds its sum
-            s += hh_dpp<0x142, 0xA>(s);  // row_bcast:15 -> lanes 31 and 63 hold their half's sum
-            if (rl < nrows && seg == 31) a.y[q0 + rl] = a.res ? (rl0 == 0 ? res0 : a.res[q0 + rl]) + s : s;
-        }
+    static HH_DEV const uint4* tables() { return nullptr; }
+    static HH_DEV void load_h(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hr_t& h) {
+        hh_q6k_load_h(q1, q2, sc, u, h);
     }
-}
+    static HH_DEV float unit_h(const data& s, const lane_t& l, const hr_t& h, const char*) {
+        return hh_q6k_unit(s, l.sh, l.is, h);
+    }
+};
 
 // Two rows in flight per wave: deeper rings measured slower here (8B down, 4096 x 14336:
 // 14.2 us at D = 2, 14.8 at 3, 15.8 at 4, 17.3 at 5).
 #define HH_Q6K_DN_RING(W2)                                                                              \
     extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) hh_q6k_dn_ring_d##W2(const hh_dnr_args a) { \
-        hh_q6k_dn_ring_body<W2, 2>(a);                                                                  \
+        hh_dn_ring_body<hh_ring_q6k, W2, 2>(a);                                                         \
     }
 HH_Q6K_DN_RING(1)
 HH_Q6K_DN_RING(2)

@@ -295,8 +295,8 @@ hh_status hh_engine::enqueue_gemv(int type, size_t m, size_t n, const uint8_t* w
         hh_status st = enqueue_q4k(m, n, w, nullptr, x, y, 0, false, nullptr, nullptr);
         if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
     }
-    if (type == HH_TYPE_Q6_K) {
-        hh_status st = enqueue_ring_gemv(true, m, n, w, x, y, xq_ws);
+    if (type == HH_TYPE_Q6_K || type == HH_TYPE_IQ2_XXS || type == HH_TYPE_IQ3_XXS) {
+        hh_status st = enqueue_ring_gemv(type, m, n, w, x, y, xq_ws);
         if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
     }
     std::string name;
@@ -535,22 +535,53 @@ struct DnrArgs {
 // The ring kernels' grid: `per_cu` workgroups per CU when the occupancy allows it.
 static size_t ring_grid(int occ, int per_cu, size_t cus) { return cus * (size_t)std::max(1, std::min(occ, per_cu)); }
 
+// Weight formats of the ring kernels (kernels/q4k_ring.hip, q6k_ring.hip, iq_ring.hip):
+// kernel stem, block bytes, the static LDS tables the kernels keep, whether a gate/up
+// kernel exists.  Formats whose blocks are not a multiple of 4 bytes need an even number of
+// blocks per row, so that rows start 4-byte aligned.
+struct RingFmt {
+    int type;
+    const char* stem;
+    uint32_t block_bytes;
+    uint32_t tab_bytes;
+    bool gate_up;
+};
+static const RingFmt kRingFmts[] = {
+    {HH_TYPE_Q4_K, "q4k", 144, 0, true},
+    {HH_TYPE_Q6_K, "q6k", 210, 0, false},
+    {HH_TYPE_IQ2_XXS, "iq2", 66, 4096, true},
+    {HH_TYPE_IQ3_XXS, "iq3", 98, 3072, true},
+};
+static const RingFmt* ring_fmt(int type) {
+    for (const RingFmt& f : kRingFmts)
+        if (f.type == type) return &f;
+    return nullptr;
+}
+// Columns per row the ring kernels accept for a format: whole 256-column blocks, 4-byte
+// aligned rows, at most 32768 (digits in LDS).
+static bool ring_cols_ok(const RingFmt* f, size_t n) {
+    return f && n % 256 == 0 && (f->block_bytes % 4 == 0 || n % 512 == 0) && n <= 32768;
+}
+
 bool hh_engine::ring_ok(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                         const float* x) const {
     const size_t dm = d->d_model, df = d->d_ff;
-    // a Q6_K W_down (Q4_K_M files) needs an even number of 210-byte superblocks per row, so
-    // that its rows start 4-byte aligned
-    const bool down_ok = d->type_down == HH_TYPE_Q4_K || (d->type_down == HH_TYPE_Q6_K && df % 512 == 0);
-    return ring && !q4k_generic && d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K && down_ok &&
-           dm % 256 == 0 && df % 256 == 0 && dm <= 8192 && df <= 32768 &&
+    const RingFmt* fg = ring_fmt(d->type_gate);
+    const RingFmt* fd = ring_fmt(d->type_down);
+    // gate and up share the gate/up kernel's format; any ring format for down (h's digits
+    // are the same for all of them)
+    return ring && !q4k_generic && fg && fg->gate_up && d->type_up == d->type_gate && ring_cols_ok(fg, dm) &&
+           dm <= 8192 && ring_cols_ok(fd, df) &&
            ((((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd | (uintptr_t)x) & 15u) == 0);
 }
 
-hh_status hh_engine::enqueue_q4k_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu,
-                                         const float* x, const float* norm, float eps, uint8_t* hx) {
+hh_status hh_engine::enqueue_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu,
+                                     const float* x, const float* norm, float eps, uint8_t* hx) {
     const size_t dm = d->d_model, df = d->d_ff;
+    const RingFmt* f = ring_fmt(d->type_gate);
+    if (!f || !f->gate_up) return fail(HH_ERR_INVALID, "ring gate/up: no kernel for GGML type %d", d->type_gate);
     const int w1 = dm <= 4096 ? 1 : 2;
-    const std::string name = "hh_q4k_gu_ring_g" + std::to_string(w1) + (norm ? "_n" : "");
+    const std::string name = std::string("hh_") + f->stem + "_gu_ring_g" + std::to_string(w1) + (norm ? "_n" : "");
     hipFunction_t fn;
     HH_TRY(kernel(name, &fn));
     const int block = 8 * 64;
@@ -572,30 +603,32 @@ hh_status hh_engine::enqueue_q4k_ring_gu(const hh_ffn_desc* d, const uint8_t* wg
         HH_TRY(grow(&ws_hq, &ws_hq_cap, hh::ring_digits_bytes(df)));
         hx = (uint8_t*)ws_hq;
     }
-    GurArgs a{wg, wu, x, hx, norm, (uint64_t)((dm / 256) * 144), (uint32_t)dm, (uint32_t)df, d->act, eps};
+    GurArgs a{wg, wu, x, hx, norm, (uint64_t)((dm / 256) * f->block_bytes), (uint32_t)dm, (uint32_t)df, d->act, eps};
     void* params[] = {&a};
     hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
     if (err != hipSuccess) return hip_fail(err, "launch(ring q4k gate/up)");
     return HH_OK;
 }
 
-hh_status hh_engine::enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd, float* y, const float* res) {
-    return launch_dn_ring(d->type_down == HH_TYPE_Q6_K, d->d_model, d->d_ff, wd, (const uint8_t*)ws_hq, y, res);
+hh_status hh_engine::enqueue_ring_dn(const hh_ffn_desc* d, const uint8_t* wd, float* y, const float* res) {
+    return launch_dn_ring(d->type_down, d->d_model, d->d_ff, wd, (const uint8_t*)ws_hq, y, res);
 }
 
-// The ring down kernel over m rows of n columns (Q4_K or Q6_K) from digits `hx`.  Each
+// The ring down kernel over m rows of n columns (any ring format) from digits `hx`.  Each
 // workgroup keeps the digits and its rows' lane partials in LDS: the grid is at least one
 // workgroup per CU and large enough that every workgroup's rows fit.
-hh_status hh_engine::launch_dn_ring(bool q6, size_t m, size_t n, const uint8_t* w, const uint8_t* hx, float* y,
+hh_status hh_engine::launch_dn_ring(int type, size_t m, size_t n, const uint8_t* w, const uint8_t* hx, float* y,
                                     const float* res) {
+    const RingFmt* f = ring_fmt(type);
+    if (!f) return fail(HH_ERR_INVALID, "ring down: no kernel for GGML type %d", type);
     int w2 = 1;
     while ((size_t)w2 * 64 < n / 64) w2 *= 2;
-    const std::string name = std::string(q6 ? "hh_q6k_dn_ring_d" : "hh_q4k_dn_ring_d") + std::to_string(w2);
+    const std::string name = std::string("hh_") + f->stem + "_dn_ring_d" + std::to_string(w2);
     hipFunction_t fn;
     HH_TRY(kernel(name, &fn));
     const int block = 9 * 64;  // 8 compute waves + the wave that copies the intermediate
     const size_t cus = (size_t)props.multiProcessorCount;
-    const size_t lds = (size_t)props.sharedMemPerBlock;
+    const size_t lds = (size_t)props.sharedMemPerBlock - f->tab_bytes;  // the tables are static LDS
     const size_t hb = ((2 * n + (n / 8) * 4) + 15) & ~size_t(15), per_row = (size_t)w2 * 64 * 4;
     if (hb + per_row > lds) return HH_ERR_UNSUPPORTED_DEVICE;
     const size_t rows_fit = (lds - hb) / per_row;
@@ -610,18 +643,19 @@ hh_status hh_engine::launch_dn_ring(bool q6, size_t m, size_t n, const uint8_t* 
     const size_t grid = std::max(ring_grid(occ, ring_dn_per_cu, cus), (m + rows_fit - 1) / rows_fit);
     const size_t rows_max = (m + grid - 1) / grid;
     const size_t smem = hb + rows_max * per_row;
-    DnrArgs a{w, hx, y, res, (uint64_t)((n / 256) * (q6 ? 210 : 144)), (uint32_t)m, (uint32_t)n};
+    DnrArgs a{w, hx, y, res, (uint64_t)((n / 256) * f->block_bytes), (uint32_t)m, (uint32_t)n};
     void* params[] = {&a};
     hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
     if (err != hipSuccess) return hip_fail(err, "launch(ring down)");
     return HH_OK;
 }
 
-// x -> the ring down kernels' digit form (q1 | q2 | one scale per 8), then the Q6_K ring
-// kernel as a GEMV: the LM head of Q4_K_M files (output.weight in Q6_K).
-hh_status hh_engine::enqueue_ring_gemv(bool q6, size_t m, size_t n, const uint8_t* w, const float* x, float* y,
+// x -> the ring down kernels' digit form (q1 | q2 | one scale per 8), then a ring down kernel
+// as a GEMV: the LM head of Q4_K_M files (output.weight in Q6_K), and every IQ2_XXS /
+// IQ3_XXS GEMV of a shape the ring kernels take.
+hh_status hh_engine::enqueue_ring_gemv(int type, size_t m, size_t n, const uint8_t* w, const float* x, float* y,
                                        void* xq_ws) {
-    if (!ring || n % (q6 ? 512 : 256) || n > 32768 || m > UINT32_MAX / 2 || (((uintptr_t)w | (uintptr_t)x) & 15u))
+    if (!ring || !ring_cols_ok(ring_fmt(type), n) || m > UINT32_MAX / 2 || (((uintptr_t)w | (uintptr_t)x) & 15u))
         return HH_ERR_UNSUPPORTED_DEVICE;
     if (!xq_ws) {
         HH_TRY(grow(&ws_xq, &ws_xq_cap, hh::ring_digits_bytes(n)));
@@ -631,7 +665,7 @@ hh_status hh_engine::enqueue_ring_gemv(bool q6, size_t m, size_t n, const uint8_
     HH_TRY(kernel("hh_x_digits", &fn));
     hh_xd_args xa{x, (uint8_t*)xq_ws, (uint32_t)n, 0u};
     HH_TRY(launch(fn, (uint32_t)((n / 8 + 255) / 256), 256, xa));
-    return launch_dn_ring(q6, m, n, w, (const uint8_t*)xq_ws, y, nullptr);
+    return launch_dn_ring(type, m, n, w, (const uint8_t*)xq_ws, y, nullptr);
 }
 
 hh_status hh_engine::check_device_error() {
@@ -662,7 +696,7 @@ hh_status hh_engine::enqueue_ffn_begin(const hh_ffn_desc* d, const uint8_t* pack
     if (ring_ok(d, wg, wu, pack + d->down_off, x) && ((uintptr_t)norm & 15u) == 0) {
         // the ring kernels: gate/up writes h's granule digits, the finish step reads them
         // (with norm: the RMSNorm rides in gate/up's prologue and epilogue)
-        HH_TRY(enqueue_q4k_ring_gu(d, wg, wu, x, norm, eps));
+        HH_TRY(enqueue_ring_gu(d, wg, wu, x, norm, eps));
         ffn_stage = *d;
         ffn_stage_digits = false;
         ffn_stage_ring = true;
@@ -702,7 +736,7 @@ hh_status hh_engine::enqueue_ffn_finish(const hh_ffn_desc* d, const uint8_t* pac
     ffn_stage_valid = false;
     const uint8_t* wd = pack + d->down_off;
     if (ffn_stage_ring) {  // the ring down kernel adds the residual as it stores y
-        const hh_status st = enqueue_q4k_ring_dn(d, wd, y, res);
+        const hh_status st = enqueue_ring_dn(d, wd, y, res);
         if (st == HH_OK) ffn_calls += 1;
         return st;
     }
@@ -725,8 +759,8 @@ hh_status hh_engine::enqueue_ffn_finish(const hh_ffn_desc* d, const uint8_t* pac
 
 hh_status hh_engine::enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, const float* x, float* y) {
     if (ring_ok(d, pack + d->gate_off, pack + d->up_off, pack + d->down_off, x)) {
-        HH_TRY(enqueue_q4k_ring_gu(d, pack + d->gate_off, pack + d->up_off, x));
-        HH_TRY(enqueue_q4k_ring_dn(d, pack + d->down_off, y));
+        HH_TRY(enqueue_ring_gu(d, pack + d->gate_off, pack + d->up_off, x));
+        HH_TRY(enqueue_ring_dn(d, pack + d->down_off, y));
         ffn_stage_valid = false;
         ffn_calls += 3;
         return HH_OK;
@@ -775,8 +809,8 @@ hh_status hh_engine::enqueue_ffn_noalloc(const hh_ffn_desc* d, const uint8_t* pa
     const uint8_t* wu = pack + d->up_off;
     const uint8_t* wd = pack + d->down_off;
     if (ring_ok(d, wg, wu, wd, x)) {
-        HH_TRY(enqueue_q4k_ring_gu(d, wg, wu, x, nullptr, 0.f, ws));
-        HH_TRY(launch_dn_ring(d->type_down == HH_TYPE_Q6_K, dm, df, wd, ws, y, nullptr));
+        HH_TRY(enqueue_ring_gu(d, wg, wu, x, nullptr, 0.f, ws));
+        HH_TRY(launch_dn_ring(d->type_down, dm, df, wd, ws, y, nullptr));
         ffn_calls += 3;
         return HH_OK;
     }
@@ -848,8 +882,8 @@ hh_status hh_engine::enqueue_ffn_block(const hh_ffn_desc* d, const uint8_t* pack
     const uint8_t* wu = pack + d->up_off;
     const uint8_t* wd = pack + d->down_off;
     if (ring_ok(d, wg, wu, wd, x) && ((uintptr_t)norm & 15u) == 0) {
-        HH_TRY(enqueue_q4k_ring_gu(d, wg, wu, x, norm, eps));
-        HH_TRY(enqueue_q4k_ring_dn(d, wd, y, x));
+        HH_TRY(enqueue_ring_gu(d, wg, wu, x, norm, eps));
+        HH_TRY(enqueue_ring_dn(d, wd, y, x));
         ffn_stage_valid = false;
         ffn_calls += 3;
         return HH_OK;
@@ -1219,7 +1253,7 @@ hh_status hh_engine::enqueue_ffn_batched(const hh_ffn_desc* d, const uint8_t* pa
         hh_act_args aa{(const float*)ws_g, (const float*)ws_u, (float*)ws_h, (uint32_t)(batch * df), d->act};
         HH_TRY(launch(fn, (uint32_t)((batch * df + 255) / 256), 256, aa));
         for (size_t b = 0; b < batch; b++) {
-            const hh_status st = enqueue_ring_gemv(true, dm, df, wd, (const float*)ws_h + b * df, y + b * dm);
+            const hh_status st = enqueue_ring_gemv(HH_TYPE_Q6_K, dm, df, wd, (const float*)ws_h + b * df, y + b * dm);
             if (st == HH_ERR_UNSUPPORTED_DEVICE)
                 HH_TRY(enqueue_gemv(HH_TYPE_Q6_K, dm, df, wd, (const float*)ws_h + b * df, y + b * dm));
             else if (st != HH_OK)
@@ -1503,6 +1537,11 @@ static std::vector<std::string> required_kernels() {
     for (const char* f : {"gu_ring_g1", "gu_ring_g2", "gu_ring_g1_n", "gu_ring_g2_n", "dn_ring_d1", "dn_ring_d2", "dn_ring_d4", "dn_ring_d8"})
         k.push_back(std::string("hh_q4k_") + f);
     for (int w : {1, 2, 4, 8}) k.push_back("hh_q6k_dn_ring_d" + std::to_string(w));
+    for (const char* f : {"iq2", "iq3"}) {
+        for (int w : {1, 2, 4, 8}) k.push_back(std::string("hh_") + f + "_dn_ring_d" + std::to_string(w));
+        for (int w : {1, 2})
+            for (const char* n : {"", "_n"}) k.push_back(std::string("hh_") + f + "_gu_ring_g" + std::to_string(w) + n);
+    }
     for (const char* f : {"gu_ring_u16", "gu_ring_u32", "gu_ring_u64", "dn_ring_d1", "dn_ring_d2", "dn_ring_d4",
                           "dn_ring_d8"})
         k.push_back(std::string("hh_moe_") + f);

@@ -226,13 +226,15 @@ struct hh_engine {
     // barrier (q4k_ffn.hip); HH_ERR_UNSUPPORTED_DEVICE when the shape, alignment or
     // occupancy does not allow it.
     bool ring_ok(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd, const float* x) const;
-    // hx: where h's digits go (hh_ring_digits_bytes(d_ff)); null: ws_hq.
-    hh_status enqueue_q4k_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const float* x,
-                                  const float* norm = nullptr, float eps = 0.f, uint8_t* hx = nullptr);
-    hh_status enqueue_q4k_ring_dn(const hh_ffn_desc* d, const uint8_t* wd, float* y, const float* res = nullptr);
-    hh_status launch_dn_ring(bool q6, size_t m, size_t n, const uint8_t* w, const uint8_t* hx, float* y,
+    // Ring gate/up (Q4_K, IQ2_XXS, IQ3_XXS); hx: where h's digits go
+    // (hh_ring_digits_bytes(d_ff)); null: ws_hq.
+    hh_status enqueue_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const float* x,
+                              const float* norm = nullptr, float eps = 0.f, uint8_t* hx = nullptr);
+    hh_status enqueue_ring_dn(const hh_ffn_desc* d, const uint8_t* wd, float* y, const float* res = nullptr);
+    // Ring down kernel of GGML type `type` (Q4_K, Q6_K, IQ2_XXS, IQ3_XXS) over digits hx.
+    hh_status launch_dn_ring(int type, size_t m, size_t n, const uint8_t* w, const uint8_t* hx, float* y,
                              const float* res);
-    hh_status enqueue_ring_gemv(bool q6, size_t m, size_t n, const uint8_t* w, const float* x, float* y,
+    hh_status enqueue_ring_gemv(int type, size_t m, size_t n, const uint8_t* w, const float* x, float* y,
                                 void* xq_ws = nullptr);
     hh_status enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                                const float* x, float* y);

@@ -47,6 +47,14 @@ FFN_CASES = [
     ((12, 12, 14), 4096, 14336, 0, 9),   # Q4_K_M layout: gate/up Q4_K, down Q6_K
     ((14, 14, 14), 1024, 2048, 0, 10),   # all Q6_K
     ((8, 8, 8), 1024, 2048, 1, 11),      # all Q8_0, GELU
+    # IQ ring kernels with other down formats (h's digits are shared by every ring down
+    # kernel), GELU on IQ2_XXS, and widths the ring kernels refuse (odd block counts per row:
+    # the generic team kernels)
+    ((16, 16, 18), 8192, 3584, 0, 12),   # IQ2_XXS gate/up, IQ3_XXS down
+    ((18, 18, 14), 4096, 14336, 0, 13),  # IQ3_XXS gate/up, Q6_K down
+    ((16, 16, 12), 8192, 4096, 1, 14),   # IQ2_XXS gate/up, Q4_K down, GELU
+    ((18, 18, 16), 1024, 6144, 0, 15),   # IQ3_XXS gate/up, IQ2_XXS down
+    ((16, 16, 16), 4352, 1280, 0, 16),   # 17 / 5 blocks per row: no ring kernels
 ]
 
 
@@ -264,12 +272,53 @@ def test_ffn_begin_finish_equals_ffn(engine, two_launch_engine, types, d_model, 
             eng.ffn_finish_dev(other, pack, 0, y2, 0)
 
 
+IQ_RING_CASES = [
+    # (types, d_model, d_ff): config 5's 70B IQ2_XXS layer (8 waves per down row), IQ3_XXS at
+    # the 8B shape, a narrow layer (one block pair per gate/up row, fewer h granules than
+    # workgroups), and a d_model of 1536 (three lane units left idle in a 64-lane team)
+    ((16, 16, 16), 8192, 28672), ((18, 18, 18), 4096, 14336), ((16, 16, 16), 512, 1024),
+    ((18, 18, 18), 1536, 4608),
+]
+
+
+@pytest.mark.parametrize("types,d_model,d_ff", IQ_RING_CASES)
+def test_iq_ring_ffn_matches_oracle_and_generic(engine, persistent_engine, types, d_model, d_ff):
+    # The IQ2_XXS / IQ3_XXS ring kernels (int8 codebook entries, v_dot4 against the
+    # activation digits) and the generic f32 team kernels (ring form off) each meet the
+    # FFN bar against the oracle; the two-call seam runs the ring kernels bit for bit.
+    oracle.set_threads(min(16, oracle.max_threads()))
+    print(f"[case] iq ring ffn types={types} {d_model}x{d_ff}", flush=True)
+    x = synth.normal(synth.seed_for(40, d_model, synth.ACT), d_model)
+    lay, (wg, wu, wd), pack0 = make_pack(engine, types, d_model, d_ff, 40)
+    ys = {}
+    for name, eng in (("ring", engine), ("generic", persistent_engine)):
+        pack = pack0
+        if eng is not engine:
+            pack = eng.alloc(lay.total)
+            for w, off in ((wg, lay.gate_off), (wu, lay.up_off), (wd, lay.down_off)):
+                pack.write(w, off)
+        desc = eng.ffn_desc(types, d_model, d_ff, lay)
+        ys[name] = eng.ffn(desc, pack, 0, x)
+        if name == "ring":
+            xb, y2 = eng.upload(x), eng.alloc(4 * d_model)
+            eng.ffn_begin_dev(desc, pack, 0, xb, 0)
+            eng.ffn_finish_dev(desc, pack, 0, y2, 0)
+            np.testing.assert_array_equal(y2.read(np.float32, d_model), ys[name])
+    ref = oracle.ffn(types, d_model, d_ff, wg, wu, wd, x)
+    for name, y in ys.items():
+        err = rel_err(y, ref)
+        print(f"  {name}: rel_err {err:.3e}", flush=True)
+        assert np.isfinite(y).all()
+        assert err <= REL_TOL, (name, err)
+
+
 BLOCK_CASES = [
     # (types, d_model, d_ff): the ring kernels with the norm and residual fused (8B Q4_K,
-    # Q4_K_M, d_model 8192: two x passes per thread), and the generic three-step path (SmolLM
-    # Q4_0, IQ2_XXS)
+    # Q4_K_M, d_model 8192: two x passes per thread, IQ2_XXS, IQ3_XXS), and the generic
+    # three-step path (SmolLM Q4_0, IQ2_XXS with an odd block count per row)
     ((12, 12, 12), 4096, 14336), ((12, 12, 14), 4096, 14336), ((12, 12, 12), 8192, 4096),
-    ((2, 2, 2), 576, 1536), ((16, 16, 16), 1024, 2048),
+    ((2, 2, 2), 576, 1536), ((16, 16, 16), 1024, 2048), ((18, 18, 18), 4096, 14336),
+    ((16, 16, 16), 8192, 28672), ((16, 16, 16), 768, 2304),
 ]
 
 
@@ -300,7 +349,8 @@ def test_ffn_block_matches_oracle(engine, types, d_model, d_ff):
 
 
 @pytest.mark.parametrize("types,d_model,d_ff", [((12, 12, 12), 4096, 14336), ((12, 12, 14), 4096, 14336),
-                                                ((2, 2, 2), 576, 1536), ((16, 16, 16), 1024, 2048)])
+                                                ((2, 2, 2), 576, 1536), ((16, 16, 16), 1024, 2048),
+                                                ((18, 18, 18), 4096, 14336), ((16, 16, 16), 768, 2304)])
 def test_ffn_block_begin_finish_equals_block(engine, types, d_model, d_ff):
     # ffn_apply's own two calls (rms_norm + begin, finish + residual) run the block's kernels:
     # bit-identical to the one-call block, out of place and in place.

@@ -241,6 +241,10 @@ CONFIG_GEMVS = [
     (hayai_amd.Q6_K, 4096, 14336),
     (hayai_amd.Q6_K, 14336, 4096),
     (hayai_amd.Q8_0, 4096, 14336),
+    # the IQ ring GEMV at its limits: 32768 columns (digits of the widest row in LDS) and the
+    # 70B down shape with few rows per workgroup
+    (hayai_amd.IQ2_XXS, 300, 32768),
+    (hayai_amd.IQ3_XXS, 8192, 28672),
 ]
 
 
