@@ -24,9 +24,16 @@
 // it, so no load runs past its block except in even blocks, which are never a row's last.
 
 // Sign entry of ksigns(i) = i | parity(i) << 7: byte masks m (0xFF where the sign bit is set)
-// and m & 0x01010101, for elements 0-3 and 4-7.
+// for elements 0-3 and 4-7; with HH_IQ_SIGN16 also m & 0x01010101 (16-byte entries: fewer
+// VALU ops, more LDS traffic per codebook entry).
+#ifndef HH_IQ_SIGN16
+#define HH_IQ_SIGN16 0
+#endif
 struct hh_iq_sign {
-    uint32_t mlo, mhi, olo, ohi;
+    uint32_t mlo, mhi;
+#if HH_IQ_SIGN16
+    uint32_t olo, ohi;
+#endif
 };
 struct hh_iq2_tab {
     uint64_t grid[256];  // IQ2_XXS codebook
@@ -44,7 +51,11 @@ constexpr hh_iq_sign hh_sign_entry(uint32_t i) {
     uint32_t m[2] = {0u, 0u};
     for (uint32_t j = 0; j < 8; j++)
         if ((s >> j) & 1u) m[j / 4] |= 0xFFu << (8 * (j % 4));
+#if HH_IQ_SIGN16
     return hh_iq_sign{m[0], m[1], m[0] & 0x01010101u, m[1] & 0x01010101u};
+#else
+    return hh_iq_sign{m[0], m[1]};
+#endif
 }
 constexpr hh_iq2_tab hh_make_iq2_tab() {
     hh_iq2_tab t{{HH_IQ2XXS_GRID_VALUES}, {}};
@@ -70,48 +81,66 @@ HH_DEV uint32_t hh_xad(uint32_t a, uint32_t b, uint32_t c) {
     return r;
 }
 
-// A lane's x: per-32 digits of its 64 columns, the two group scales / 256.
+typedef uint32_t hh_v2u_a4i __attribute__((ext_vector_type(2), aligned(4)));
+
+// A lane's x: per-32 digits of its NG groups (32 NG columns), the group scales / 256.
+template <int NG>
 struct hh_iq_x {
-    uint32_t q1[16], q2[16];
-    float s[2];
+    uint32_t q1[8 * NG], q2[8 * NG];
+    float s[NG];
 };
-// A lane's h: per-8 digits of its 64 columns, prefix-sum weights (s_k - s_{k+1}) / 256 of
-// the four granules of each group (s_4 = 0).
+// A lane's h: per-8 digits of its columns, prefix-sum weights (s_k - s_{k+1}) / 256 of the
+// four granules of each group (s_4 = 0).
+template <int NG>
 struct hh_iq_h {
-    uint32_t q1[16], q2[16];
-    float w[8];
+    uint32_t q1[8 * NG], q2[8 * NG];
+    float w[4 * NG];
 };
 
-HH_DEV void hh_iq_load_digits(const int8_t* q1, const int8_t* q2, uint32_t u, uint32_t (&d1)[16], uint32_t (&d2)[16]) {
-    const uint4* a = reinterpret_cast<const uint4*>(q1 + (size_t)u * 64);
-    const uint4* b = reinterpret_cast<const uint4*>(q2 + (size_t)u * 64);
+template <int NG>
+HH_DEV void hh_iq_load_digits(const int8_t* q1, const int8_t* q2, uint32_t u, uint32_t (&d1)[8 * NG],
+                              uint32_t (&d2)[8 * NG]) {
+    const uint4* a = reinterpret_cast<const uint4*>(q1 + (size_t)u * 32 * NG);
+    const uint4* b = reinterpret_cast<const uint4*>(q2 + (size_t)u * 32 * NG);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < 2 * NG; i++) {
         hh_unpack4(a[i], d1 + 4 * i);
         hh_unpack4(b[i], d2 + 4 * i);
     }
 }
-HH_DEV void hh_iq_load_x(const hh_digits_ptr& xd, uint32_t u, hh_iq_x& x) {
-    hh_iq_load_digits(xd.q1, xd.q2, u, x.q1, x.q2);
-    const float2 sc = reinterpret_cast<const float2*>(xd.sc)[u];
-    x.s[0] = sc.x * (1.0f / 256.0f);
-    x.s[1] = sc.y * (1.0f / 256.0f);
-}
-HH_DEV void hh_iq_load_h(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hh_iq_h& h) {
-    hh_iq_load_digits(q1, q2, u, h.q1, h.q2);
-    const float4 s0 = reinterpret_cast<const float4*>(sc)[2 * u];
-    const float4 s1 = reinterpret_cast<const float4*>(sc)[2 * u + 1];
-    const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+template <int NG>
+HH_DEV void hh_iq_load_x(const hh_digits_ptr& xd, uint32_t u, hh_iq_x<NG>& x) {
+    hh_iq_load_digits<NG>(xd.q1, xd.q2, u, x.q1, x.q2);
 #pragma unroll
-    for (int k = 0; k < 8; k++) h.w[k] = (s[k] - ((k & 3) < 3 ? s[k + 1] : 0.f)) * (1.0f / 256.0f);
+    for (int g = 0; g < NG; g++) x.s[g] = xd.sc[NG * u + g] * (1.0f / 256.0f);
+}
+template <int NG>
+HH_DEV void hh_iq_load_h(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hh_iq_h<NG>& h) {
+    hh_iq_load_digits<NG>(q1, q2, u, h.q1, h.q2);
+    float s[4 * NG];
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const float4 v = reinterpret_cast<const float4*>(sc)[NG * u + i];
+        s[4 * i] = v.x;
+        s[4 * i + 1] = v.y;
+        s[4 * i + 2] = v.z;
+        s[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int k = 0; k < 4 * NG; k++) h.w[k] = (s[k] - ((k & 3) < 3 ? s[k + 1] : 0.f)) * (1.0f / 256.0f);
 }
 
 // One signed 8-element codebook entry against the digits of elements 8l..8l+7 of group g,
 // accumulated into the group's int32 digit sums.
 template <class X>
 HH_DEV void hh_iq_entry(uint32_t glo, uint32_t ghi, const hh_iq_sign& m, const X& x, int g, int l, int& c1, int& c2) {
-    const int vlo = (int)hh_xad(glo, m.mlo, m.olo);
-    const int vhi = (int)hh_xad(ghi, m.mhi, m.ohi);
+#if HH_IQ_SIGN16
+    const uint32_t olo = m.olo, ohi = m.ohi;
+#else
+    const uint32_t olo = m.mlo & 0x01010101u, ohi = m.mhi & 0x01010101u;
+#endif
+    const int vlo = (int)hh_xad(glo, m.mlo, olo);
+    const int vhi = (int)hh_xad(ghi, m.mhi, ohi);
     const int i = 8 * g + 2 * l;
     // |c1| <= 32 * 62 * 127 per group, so 256 * c1 + c2 fits an int32 exactly
     c1 = __builtin_amdgcn_sdot4(vlo, (int)x.q1[i], l == 0 ? 0 : c1, false);
@@ -121,14 +150,12 @@ HH_DEV void hh_iq_entry(uint32_t glo, uint32_t ghi, const hh_iq_sign& m, const X
 }
 
 // Group g's digit sums -> f32, with the per-32 x scale or the per-8 h weights.
-template <class X>
-HH_DEV float hh_iq_group_t(const X& x, int g, const int (&c1)[4], const int (&c2)[4]);
-template <>
-HH_DEV float hh_iq_group_t<hh_iq_x>(const hh_iq_x& x, int g, const int (&c1)[4], const int (&c2)[4]) {
+template <int NG>
+HH_DEV float hh_iq_group_t(const hh_iq_x<NG>& x, int g, const int (&c1)[4], const int (&c2)[4]) {
     return x.s[g] * (float)(c1[3] * 256 + c2[3]);
 }
-template <>
-HH_DEV float hh_iq_group_t<hh_iq_h>(const hh_iq_h& h, int g, const int (&c1)[4], const int (&c2)[4]) {
+template <int NG>
+HH_DEV float hh_iq_group_t(const hh_iq_h<NG>& h, int g, const int (&c1)[4], const int (&c2)[4]) {
     float t = 0.f;
 #pragma unroll
     for (int l = 0; l < 4; l++) t = fmaf(h.w[4 * g + l], (float)(c1[l] * 256 + c2[l]), t);
@@ -143,175 +170,244 @@ HH_DEV void hh_iq_piece(uint32_t p, uint32_t& off, uint32_t& sel) {
     sel = odd ? 0x05040302u : 0x07060504u;
 }
 
-typedef uint32_t hh_v2u_a4i __attribute__((ext_vector_type(2), aligned(4)));
+// Loads N dwords at p (4-byte aligned): dwordx4 pieces, then the tail.
+template <int N>
+HH_DEV void hh_iq_load_run(const uint8_t* p, uint32_t (&w)[N]) {
+#pragma unroll
+    for (int i = 0; i + 4 <= N; i += 4) {
+        const hh_v4u_a4 v = *reinterpret_cast<const hh_v4u_a4*>(p + 4 * i);
+        w[i] = v.x;
+        w[i + 1] = v.y;
+        w[i + 2] = v.z;
+        w[i + 3] = v.w;
+    }
+    if constexpr (N % 4 == 1) w[N - 1] = *reinterpret_cast<const uint32_t*>(p + 4 * (N - 1));
+    if constexpr (N % 4 == 3) {
+        const hh_v2u_a4i v = *reinterpret_cast<const hh_v2u_a4i*>(p + 4 * (N - 3));
+        w[N - 3] = v.x;
+        w[N - 2] = v.y;
+        w[N - 1] = *reinterpret_cast<const uint32_t*>(p + 4 * (N - 1));
+    }
+}
 
+// The block's d for a lane whose unit is NG groups of a block.  NG = 2: from a dword load of
+// its own.  NG = 4 (two lanes per block, the even lane first): the even lane's index run
+// starts at the block or 2 bytes before it, so its first dword holds d; the odd lane takes
+// that dword by DPP (quad_perm [0,0,2,2]).
+template <int NG>
+HH_DEV uint32_t hh_iq_block_d(uint32_t d_or_first, uint32_t dsh) {
+    if constexpr (NG == 4) d_or_first = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)d_or_first, 0xA0, 0xF, 0xF, true);
+    return (d_or_first >> dsh) & 0xFFFFu;
+}
+
+// Keeps a unit's table reads ahead of its arithmetic (the scheduler otherwise sinks each
+// read to its use and waits on it).
+#ifndef HH_IQ_PREFETCH
+#define HH_IQ_PREFETCH 0
+#endif
+#if HH_IQ_PREFETCH
+#define HH_IQ_FETCH_FENCE() __builtin_amdgcn_sched_barrier(0)
+#else
+#define HH_IQ_FETCH_FENCE() ((void)0)
+#endif
+
+// IQ2_XXS, NG groups (32 NG columns) per lane.
+template <int NG>
 struct hh_ring_iq2 {
-    static constexpr uint32_t UNIT = 64;
+    static constexpr uint32_t UNIT = 32 * NG;
     static constexpr uint32_t BB = 66;  // block bytes: d (f16) + 8 groups x (4 codebook indices, 4 sign/scale bytes)
+    static constexpr uint32_t UPB = 8 / NG;  // units per block
     static constexpr uint32_t TAB_BYTES = sizeof(hh_iq2_tab);
+    static constexpr bool LANE_PARTIALS = true;
+    static constexpr int RUN = 2 * NG + 1;  // dwords covering the lane's 8 NG index/sign bytes
     struct lane_t {
         uint32_t qo, dof, sel, dsh;
     };
     struct data {
-        uint32_t a[5];  // 20 bytes covering the lane's 16 qs bytes
-        uint32_t d;     // the dword holding the block's d
+        uint32_t a[RUN];
+        uint32_t d;  // NG = 2: the dword holding the block's d
     };
-    typedef hh_iq_x xr_t;
-    typedef hh_iq_h hr_t;
+    typedef hh_iq_x<NG> xr_t;
+    typedef hh_iq_h<NG> hr_t;
     static HH_DEV lane_t lane(uint32_t u) {
-        const uint32_t bo = (u >> 2) * BB;
+        const uint32_t bo = (u / UPB) * BB;
         lane_t l;
-        hh_iq_piece(bo + 2u + 16u * (u & 3u), l.qo, l.sel);
+        hh_iq_piece(bo + 2u + 8u * NG * (u % UPB), l.qo, l.sel);
         l.dof = bo & ~3u;
         l.dsh = (bo & 2u) * 8u;
         return l;
     }
     static HH_DEV void issue(const uint8_t* row, const lane_t& l, data& s) {
-        const hh_v4u_a4 v = *reinterpret_cast<const hh_v4u_a4*>(row + l.qo);
-        s.a[0] = v.x;
-        s.a[1] = v.y;
-        s.a[2] = v.z;
-        s.a[3] = v.w;
-        s.a[4] = *reinterpret_cast<const uint32_t*>(row + l.qo + 16);
-        s.d = *reinterpret_cast<const uint32_t*>(row + l.dof);
+        hh_iq_load_run<RUN>(row + l.qo, s.a);
+        if constexpr (NG == 2) s.d = *reinterpret_cast<const uint32_t*>(row + l.dof);
     }
     static HH_DEV const uint4* tables() { return reinterpret_cast<const uint4*>(&hh_iq2_ring_tab); }
-    static HH_DEV void load_x(const hh_digits_ptr& xd, uint32_t u, xr_t& x) { hh_iq_load_x(xd, u, x); }
+    static HH_DEV void load_x(const hh_digits_ptr& xd, uint32_t u, xr_t& x) { hh_iq_load_x<NG>(xd, u, x); }
     static HH_DEV void load_h(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hr_t& h) {
-        hh_iq_load_h(q1, q2, sc, u, h);
+        hh_iq_load_h<NG>(q1, q2, sc, u, h);
     }
     // d/8 * sum_g (2 s_g + 1) t_g  ==  sum_g d (0.5 + s_g) / 4 * t_g   (iq2.rs:513)
     template <class X>
     static HH_DEV float unit(const data& s, const lane_t& l, const X& x, const char* tab) {
         const hh_iq2_tab* t = reinterpret_cast<const hh_iq2_tab*>(tab);
-        uint32_t q[4];
+        const uint32_t d = hh_iq_block_d<NG>(NG == 2 ? s.d : s.a[0], l.dsh);
+        uint32_t q[2 * NG];
 #pragma unroll
-        for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_perm(s.a[i + 1], s.a[i], l.sel);
+        for (int i = 0; i < 2 * NG; i++) q[i] = __builtin_amdgcn_perm(s.a[i + 1], s.a[i], l.sel);
+        uint64_t gv[4 * NG];
+        hh_iq_sign m[4 * NG];
+#pragma unroll
+        for (int e = 0; e < 4 * NG; e++) {
+            gv[e] = t->grid[(q[2 * (e >> 2)] >> (8 * (e & 3))) & 0xFFu];
+            m[e] = t->sgn[(q[2 * (e >> 2) + 1] >> (7 * (e & 3))) & 0x7Fu];
+        }
+        HH_IQ_FETCH_FENCE();
         float acc = 0.f;
 #pragma unroll
-        for (int g = 0; g < 2; g++) {
-            const uint32_t a0 = q[2 * g], a1 = q[2 * g + 1];
+        for (int g = 0; g < NG; g++) {
+            const uint32_t a1 = q[2 * g + 1];
             int c1[4], c2[4];
             int r1 = 0, r2 = 0;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const uint64_t gv = t->grid[(a0 >> (8 * k)) & 0xFFu];
-                const hh_iq_sign m = t->sgn[(a1 >> (7 * k)) & 0x7Fu];
-                hh_iq_entry((uint32_t)gv, (uint32_t)(gv >> 32), m, x, g, k, r1, r2);
+                const int e = 4 * g + k;
+                hh_iq_entry((uint32_t)gv[e], (uint32_t)(gv[e] >> 32), m[e], x, g, k, r1, r2);
                 c1[k] = r1;
                 c2[k] = r2;
             }
-            acc = fmaf((float)(2u * (a1 >> 28) + 1u), hh_iq_group_t(x, g, c1, c2), acc);
+            acc = fmaf((float)(2u * (a1 >> 28) + 1u), hh_iq_group_t<NG>(x, g, c1, c2), acc);
         }
-        return hh_f16((s.d >> l.dsh) & 0xFFFFu) * 0.125f * acc;
+        return hh_f16(d) * 0.125f * acc;
     }
     static HH_DEV float unit_x(const data& s, const lane_t& l, const xr_t& x, const char* tab) { return unit(s, l, x, tab); }
     static HH_DEV float unit_h(const data& s, const lane_t& l, const hr_t& h, const char* tab) { return unit(s, l, h, tab); }
 };
 
+// IQ3_XXS, NG groups per lane.
+template <int NG>
 struct hh_ring_iq3 {
-    static constexpr uint32_t UNIT = 64;
+    static constexpr uint32_t UNIT = 32 * NG;
     static constexpr uint32_t BB = 98;  // d (f16) + 64 codebook indices + 8 x (4 sign/scale bytes)
+    static constexpr uint32_t UPB = 8 / NG;
     static constexpr uint32_t TAB_BYTES = sizeof(hh_iq3_tab);
+    static constexpr bool LANE_PARTIALS = true;
+    static constexpr int RUN = 2 * NG + 1;  // dwords covering the 8 NG index bytes
+    static constexpr int ARUN = NG + 1;     // dwords covering the NG sign/scale words
     struct lane_t {
         uint32_t qo, ao, dof, sel, dsh;
     };
     struct data {
-        uint32_t a[5];  // 20 bytes covering the lane's 16 index bytes
-        uint32_t b[3];  // 12 bytes covering its two sign/scale words
-        uint32_t d;
+        uint32_t a[RUN];
+        uint32_t b[ARUN];
+        uint32_t d;  // NG = 2
     };
-    typedef hh_iq_x xr_t;
-    typedef hh_iq_h hr_t;
+    typedef hh_iq_x<NG> xr_t;
+    typedef hh_iq_h<NG> hr_t;
     static HH_DEV lane_t lane(uint32_t u) {
-        const uint32_t bo = (u >> 2) * BB, j = u & 3u;
+        const uint32_t bo = (u / UPB) * BB, j = u % UPB;
         lane_t l;
         uint32_t sel2;
-        hh_iq_piece(bo + 2u + 16u * j, l.qo, l.sel);
-        hh_iq_piece(bo + 66u + 8u * j, l.ao, sel2);  // same parity as the indices
+        hh_iq_piece(bo + 2u + 8u * NG * j, l.qo, l.sel);
+        hh_iq_piece(bo + 66u + 4u * NG * j, l.ao, sel2);  // same parity as the indices
         l.dof = bo & ~3u;
         l.dsh = (bo & 2u) * 8u;
         return l;
     }
     static HH_DEV void issue(const uint8_t* row, const lane_t& l, data& s) {
-        const hh_v4u_a4 v = *reinterpret_cast<const hh_v4u_a4*>(row + l.qo);
-        s.a[0] = v.x;
-        s.a[1] = v.y;
-        s.a[2] = v.z;
-        s.a[3] = v.w;
-        s.a[4] = *reinterpret_cast<const uint32_t*>(row + l.qo + 16);
-        const hh_v2u_a4i w = *reinterpret_cast<const hh_v2u_a4i*>(row + l.ao);
-        s.b[0] = w.x;
-        s.b[1] = w.y;
-        s.b[2] = *reinterpret_cast<const uint32_t*>(row + l.ao + 8);
-        s.d = *reinterpret_cast<const uint32_t*>(row + l.dof);
+        hh_iq_load_run<RUN>(row + l.qo, s.a);
+        hh_iq_load_run<ARUN>(row + l.ao, s.b);
+        if constexpr (NG == 2) s.d = *reinterpret_cast<const uint32_t*>(row + l.dof);
     }
     static HH_DEV const uint4* tables() { return reinterpret_cast<const uint4*>(&hh_iq3_ring_tab); }
-    static HH_DEV void load_x(const hh_digits_ptr& xd, uint32_t u, xr_t& x) { hh_iq_load_x(xd, u, x); }
+    static HH_DEV void load_x(const hh_digits_ptr& xd, uint32_t u, xr_t& x) { hh_iq_load_x<NG>(xd, u, x); }
     static HH_DEV void load_h(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hr_t& h) {
-        hh_iq_load_h(q1, q2, sc, u, h);
+        hh_iq_load_h<NG>(q1, q2, sc, u, h);
     }
     // d/4 * sum_g (2 s_g + 1) t_g  ==  sum_g d (0.5 + s_g) / 2 * t_g   (iq3.rs:160)
     template <class X>
     static HH_DEV float unit(const data& s, const lane_t& l, const X& x, const char* tab) {
         const hh_iq3_tab* t = reinterpret_cast<const hh_iq3_tab*>(tab);
-        uint32_t q[4], aux[2];
+        const uint32_t d = hh_iq_block_d<NG>(NG == 2 ? s.d : s.a[0], l.dsh);
+        uint32_t q[2 * NG], aux[NG];
 #pragma unroll
-        for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_perm(s.a[i + 1], s.a[i], l.sel);
+        for (int i = 0; i < 2 * NG; i++) q[i] = __builtin_amdgcn_perm(s.a[i + 1], s.a[i], l.sel);
 #pragma unroll
-        for (int i = 0; i < 2; i++) aux[i] = __builtin_amdgcn_perm(s.b[i + 1], s.b[i], l.sel);
+        for (int i = 0; i < NG; i++) aux[i] = __builtin_amdgcn_perm(s.b[i + 1], s.b[i], l.sel);
+        // entry k of group g: codebook indices 2k, 2k+1 of the group (elements 8k..8k+3 and
+        // 8k+4..8k+7)
+        uint32_t g1[4 * NG], g2[4 * NG];
+        hh_iq_sign m[4 * NG];
+#pragma unroll
+        for (int e = 0; e < 4 * NG; e++) {
+            const int g = e >> 2, k = e & 3;
+            const uint32_t qq = q[2 * g + (k >> 1)] >> (16 * (k & 1));
+            g1[e] = t->grid[qq & 0xFFu];
+            g2[e] = t->grid[(qq >> 8) & 0xFFu];
+            m[e] = t->sgn[(aux[g] >> (7 * k)) & 0x7Fu];
+        }
+        HH_IQ_FETCH_FENCE();
         float acc = 0.f;
 #pragma unroll
-        for (int g = 0; g < 2; g++) {
+        for (int g = 0; g < NG; g++) {
             const uint32_t ax = aux[g];
             int c1[4], c2[4];
             int r1 = 0, r2 = 0;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                // entry k: codebook indices 2k, 2k+1 of the group (elements 8k..8k+3, 8k+4..8k+7)
-                const uint32_t qq = q[2 * g + (k >> 1)] >> (16 * (k & 1));
-                const uint32_t g1 = t->grid[qq & 0xFFu], g2 = t->grid[(qq >> 8) & 0xFFu];
-                const hh_iq_sign m = t->sgn[(ax >> (7 * k)) & 0x7Fu];
-                hh_iq_entry(g1, g2, m, x, g, k, r1, r2);
+                const int e = 4 * g + k;
+                hh_iq_entry(g1[e], g2[e], m[e], x, g, k, r1, r2);
                 c1[k] = r1;
                 c2[k] = r2;
             }
-            acc = fmaf((float)(2u * (ax >> 28) + 1u), hh_iq_group_t(x, g, c1, c2), acc);
+            acc = fmaf((float)(2u * (ax >> 28) + 1u), hh_iq_group_t<NG>(x, g, c1, c2), acc);
         }
-        return hh_f16((s.d >> l.dsh) & 0xFFFFu) * 0.25f * acc;
+        return hh_f16(d) * 0.25f * acc;
     }
     static HH_DEV float unit_x(const data& s, const lane_t& l, const xr_t& x, const char* tab) { return unit(s, l, x, tab); }
     static HH_DEV float unit_h(const data& s, const lane_t& l, const hr_t& h, const char* tab) { return unit(s, l, h, tab); }
 };
 
-// Gate/up: D rows in flight per wave (each item is 16.5 / 24.5 bytes per lane, so the ring
-// is deeper than Q4_K's 48).  Down: the same.
-#define HH_IQ_GU_DEPTH 6
-#define HH_IQ_DN_DEPTH 6
-#define HH_IQ_RING(Q, F)                                                                                      \
-    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_##Q##_gu_ring_g1(const hh_gur_args a) {    \
-        hh_gu_ring_body<F, 1, HH_IQ_GU_DEPTH, 2, false>(a);                                                  \
-    }                                                                                                         \
-    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_##Q##_gu_ring_g1_n(const hh_gur_args a) {  \
-        hh_gu_ring_body<F, 1, HH_IQ_GU_DEPTH, 2, true>(a);                                                   \
-    }                                                                                                         \
-    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_##Q##_gu_ring_g2(const hh_gur_args a) {    \
-        hh_gu_ring_body<F, 2, HH_IQ_GU_DEPTH, 2, false>(a);                                                  \
-    }                                                                                                         \
-    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_##Q##_gu_ring_g2_n(const hh_gur_args a) {  \
-        hh_gu_ring_body<F, 2, HH_IQ_GU_DEPTH, 2, true>(a);                                                   \
-    }                                                                                                         \
-    extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) hh_##Q##_dn_ring_d1(const hh_dnr_args a) {      \
-        hh_dn_ring_body<F, 1, HH_IQ_DN_DEPTH>(a);                                                            \
-    }                                                                                                         \
-    extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) hh_##Q##_dn_ring_d2(const hh_dnr_args a) {      \
-        hh_dn_ring_body<F, 2, HH_IQ_DN_DEPTH>(a);                                                            \
-    }                                                                                                         \
-    extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) hh_##Q##_dn_ring_d4(const hh_dnr_args a) {      \
-        hh_dn_ring_body<F, 4, HH_IQ_DN_DEPTH>(a);                                                            \
-    }                                                                                                         \
-    extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) hh_##Q##_dn_ring_d8(const hh_dnr_args a) {      \
-        hh_dn_ring_body<F, 8, HH_IQ_DN_DEPTH>(a);                                                            \
+// Rows in flight per wave.  Narrow lanes: 64 columns (16.5 / 24.5 bytes per row).  Wide
+// lanes: 128 columns (33 / 49 bytes per row), which stream faster; the host picks them for
+// gate/up at d_model 8192 (one wave per row) and for IQ2_XXS down projections of at least
+// 8192 columns (IQ3_XXS's wide down lane does not fit the down kernel's register budget).
+#ifndef HH_IQ_GU_DEPTH
+#define HH_IQ_GU_DEPTH 4
+#endif
+#ifndef HH_IQ_DN_DEPTH
+#define HH_IQ_DN_DEPTH 4
+#endif
+#ifndef HH_IQ_W_DEPTH
+#define HH_IQ_W_DEPTH 4
+#endif
+#ifndef HH_IQ_WDN_DEPTH
+#define HH_IQ_WDN_DEPTH 2  // the down kernels' 9-wave workgroups leave 168 VGPRs per lane
+#endif
+#define HH_IQ_GU(NAME, F, W1, D)                                                                               \
+    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) NAME##_gu_ring_g##W1(const hh_gur_args a) {   \
+        hh_gu_ring_body<F, W1, D, 2, false>(a);                                                               \
+    }                                                                                                          \
+    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) NAME##_gu_ring_g##W1##_n(const hh_gur_args a) { \
+        hh_gu_ring_body<F, W1, D, 2, true>(a);                                                                \
     }
-HH_IQ_RING(iq2, hh_ring_iq2)
-HH_IQ_RING(iq3, hh_ring_iq3)
+#define HH_IQ_DN(NAME, F, W2, D)                                                                               \
+    extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) NAME##_dn_ring_d##W2(const hh_dnr_args a) {     \
+        hh_dn_ring_body<F, W2, D>(a);                                                                         \
+    }
+HH_IQ_GU(hh_iq2, hh_ring_iq2<2>, 1, HH_IQ_GU_DEPTH)
+HH_IQ_GU(hh_iq2, hh_ring_iq2<2>, 2, HH_IQ_GU_DEPTH)
+HH_IQ_DN(hh_iq2, hh_ring_iq2<2>, 1, HH_IQ_DN_DEPTH)
+HH_IQ_DN(hh_iq2, hh_ring_iq2<2>, 2, HH_IQ_DN_DEPTH)
+HH_IQ_DN(hh_iq2, hh_ring_iq2<2>, 4, HH_IQ_DN_DEPTH)
+HH_IQ_DN(hh_iq2, hh_ring_iq2<2>, 8, HH_IQ_DN_DEPTH)
+HH_IQ_GU(hh_iq2w, hh_ring_iq2<4>, 1, HH_IQ_W_DEPTH)
+HH_IQ_DN(hh_iq2w, hh_ring_iq2<4>, 1, HH_IQ_WDN_DEPTH)
+HH_IQ_DN(hh_iq2w, hh_ring_iq2<4>, 2, HH_IQ_WDN_DEPTH)
+HH_IQ_DN(hh_iq2w, hh_ring_iq2<4>, 4, HH_IQ_WDN_DEPTH)
+HH_IQ_GU(hh_iq3, hh_ring_iq3<2>, 1, HH_IQ_GU_DEPTH)
+HH_IQ_GU(hh_iq3, hh_ring_iq3<2>, 2, HH_IQ_GU_DEPTH)
+HH_IQ_DN(hh_iq3, hh_ring_iq3<2>, 1, HH_IQ_DN_DEPTH)
+HH_IQ_DN(hh_iq3, hh_ring_iq3<2>, 2, HH_IQ_DN_DEPTH)
+HH_IQ_DN(hh_iq3, hh_ring_iq3<2>, 4, HH_IQ_DN_DEPTH)
+HH_IQ_DN(hh_iq3, hh_ring_iq3<2>, 8, HH_IQ_DN_DEPTH)
+HH_IQ_GU(hh_iq3w, hh_ring_iq3<4>, 1, HH_IQ_W_DEPTH)

@@ -24,6 +24,9 @@
 //   data, issue()    one ring item: the lane's loads of one row
 //   xr_t, load_x()   x as per-32 digits (gate/up); unit_x(): the (row, unit) contribution
 //   hr_t, load_h()   h as per-8 digits (down);     unit_h(): the (row, unit) contribution
+//   LANE_PARTIALS    gate/up: each lane's contribution goes to LDS and rows are summed once
+//                    after the loop (formats with long per-row arithmetic), instead of a
+//                    wave reduction per row
 
 #define HH_RING_BLOCK (HH_FFNP_CW * HH_WAVE)
 
@@ -81,6 +84,7 @@ HH_DEV char* hh_ring_tables_lds<0>() {
 struct hh_ring_q4k {
     static constexpr uint32_t UNIT = 64;
     static constexpr uint32_t TAB_BYTES = 0;
+    static constexpr bool LANE_PARTIALS = false;
     struct lane_t {
         uint32_t oh, oq;  // block header, this unit's 32 qs bytes
     };
@@ -125,7 +129,9 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
     const uint32_t n1 = (RR + TPW1 - 1) / TPW1;
     const uint32_t n1p = (n1 + D - 1) / D * D;
 
-    // LDS: static: the format's tables; dynamic: [x digits][gate/up row sums][staging 128 B]
+    // LDS: static: the format's tables; dynamic: [x digits][gate/up row sums][staging 128 B],
+    // with lane partials: [x digits][partials: RR x TEAM1][row sums: RR][staging 128 B]
+    constexpr bool LP = F::LANE_PARTIALS;
     char* const tabs = hh_ring_tables_lds<F::TAB_BYTES>();
     char* const lds = hh_smem;
     const uint32_t xbytes = 2u * dm + (dm / 32u) * 8u;
@@ -134,8 +140,9 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
     xd.q2 = xd.q1 + dm;
     xd.sc = reinterpret_cast<float*>(xd.q2 + dm);
     xd.sum = xd.sc + dm / 32;
-    float* gu = reinterpret_cast<float*>(lds + ((xbytes + 15u) & ~15u));  // [RR][WPT1]
-    uint8_t* stage = reinterpret_cast<uint8_t*>(gu + ((RR * WPT1 + 3u) & ~3u));
+    float* gu = reinterpret_cast<float*>(lds + ((xbytes + 15u) & ~15u));  // [RR][WPT1] or [RR][TEAM1]
+    float* rows = gu + (LP ? RR * TEAM1 : 0u);                            // [RR] (lane partials)
+    uint8_t* stage = reinterpret_cast<uint8_t*>(rows + ((RR * (LP ? 1u : WPT1) + 3u) & ~3u));
 
     const uint32_t lane1 = tid % TEAM1, team1 = (wave / WPT1) % TPW1;
     const bool act1 = lane1 < dm / F::UNIT;
@@ -212,14 +219,39 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
                 const uint32_t i = team1 + j * TPW1;
                 if (i < RR) {  // wave-uniform
                     float v = F::unit_x(ring[s], lo, xr, tabs);
-                    v = hh_wave_sum(act1 ? v : 0.f);
-                    if (lane == 0) gu[i * WPT1 + wave % WPT1] = v;
+                    if constexpr (LP) {
+                        gu[i * TEAM1 + lane1] = act1 ? v : 0.f;  // summed after the loop
+                    } else {
+                        v = hh_wave_sum(act1 ? v : 0.f);
+                        if (lane == 0) gu[i * WPT1 + wave % WPT1] = v;
+                    }
                 }
                 issue(j + D, ring[s]);
             }
         }
     }
-    __syncthreads();  // row sums are in LDS
+    __syncthreads();  // row sums (or lane partials) are in LDS
+    if constexpr (LP) {
+        // row i = the TEAM1 partials of row read i: 32 threads per row, each adding TEAM1/32
+        // consecutive partials, then a 32-lane DPP reduction (fixed order: deterministic)
+        constexpr uint32_t PER = TEAM1 / 32;
+        for (uint32_t i0 = 0; i0 < RR; i0 += HH_RING_BLOCK / 32) {
+            const uint32_t i = i0 + tid / 32, seg = tid % 32;
+            float v = 0.f;
+            if (i < RR) {
+                const float* p = gu + i * TEAM1 + seg * PER;
+#pragma unroll
+                for (uint32_t k = 0; k < PER; k++) v += p[k];
+            }
+            v += hh_dpp<0xB1>(v);        // quad_perm [1,0,3,2]
+            v += hh_dpp<0x4E>(v);        // quad_perm [2,3,0,1]
+            v += hh_dpp<0x124>(v);       // row_ror:4
+            v += hh_dpp<0x128>(v);       // row_ror:8 -> each row of 16 holds its sum
+            v += hh_dpp<0x142, 0xA>(v);  // row_bcast:15 -> lanes 31 and 63 hold their half's sum
+            if (i < RR && seg == 31) rows[i] = v;
+        }
+        __syncthreads();
+    }
 
     if (wave == 0) {
         float inv = 1.f;
@@ -240,10 +272,15 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
             float hv = 0.f;
             if (ok) {
                 float g = 0.f, u = 0.f;
+                if constexpr (LP) {
+                    g = rows[2 * rho];
+                    u = rows[2 * rho + 1];
+                } else {
 #pragma unroll
-                for (int k = 0; k < WPT1; k++) {
-                    g += gu[(2 * rho) * WPT1 + k];
-                    u += gu[(2 * rho + 1) * WPT1 + k];
+                    for (int k = 0; k < WPT1; k++) {
+                        g += gu[(2 * rho) * WPT1 + k];
+                        u += gu[(2 * rho + 1) * WPT1 + k];
+                    }
                 }
                 if constexpr (NORM) {
                     g *= inv;

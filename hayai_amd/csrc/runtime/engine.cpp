@@ -545,12 +545,15 @@ struct RingFmt {
     uint32_t block_bytes;
     uint32_t tab_bytes;
     bool gate_up;
+    bool lane_partials;  // the gate/up kernel keeps every lane's row contribution in LDS
+    bool wide_gu;        // 128-column lanes for gate/up at d_model 8192 (kernel stem + "w")
+    bool wide_dn;        // 128-column lanes for down rows of at least 8192 columns
 };
 static const RingFmt kRingFmts[] = {
-    {HH_TYPE_Q4_K, "q4k", 144, 0, true},
-    {HH_TYPE_Q6_K, "q6k", 210, 0, false},
-    {HH_TYPE_IQ2_XXS, "iq2", 66, 4096, true},
-    {HH_TYPE_IQ3_XXS, "iq3", 98, 3072, true},
+    {HH_TYPE_Q4_K, "q4k", 144, 0, true, false, false, false},
+    {HH_TYPE_Q6_K, "q6k", 210, 0, false, false, false, false},
+    {HH_TYPE_IQ2_XXS, "iq2", 66, 3072, true, true, true, true},
+    {HH_TYPE_IQ3_XXS, "iq3", 98, 2048, true, true, true, false},
 };
 static const RingFmt* ring_fmt(int type) {
     for (const RingFmt& f : kRingFmts)
@@ -580,25 +583,41 @@ hh_status hh_engine::enqueue_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, co
     const size_t dm = d->d_model, df = d->d_ff;
     const RingFmt* f = ring_fmt(d->type_gate);
     if (!f || !f->gate_up) return fail(HH_ERR_INVALID, "ring gate/up: no kernel for GGML type %d", d->type_gate);
-    const int w1 = dm <= 4096 ? 1 : 2;
-    const std::string name = std::string("hh_") + f->stem + "_gu_ring_g" + std::to_string(w1) + (norm ? "_n" : "");
+    const bool wide = f->wide_gu && dm == 8192;  // one wave of 128-column lanes per row
+    const int w1 = wide || dm <= 4096 ? 1 : 2;
+    const std::string name =
+        std::string("hh_") + f->stem + (wide ? "w" : "") + "_gu_ring_g" + std::to_string(w1) + (norm ? "_n" : "");
     hipFunction_t fn;
     HH_TRY(kernel(name, &fn));
     const int block = 8 * 64;
-    int occ = 0;
     const size_t cus = (size_t)props.multiProcessorCount;
-    // LDS: x digits + gate/up row sums + 128 B staging (the kernel's layout), sized for the
-    // smallest grid it may run with
-    const size_t rr_max = 2 * 8 * ((df / 8 + cus - 1) / cus);
-    const size_t smem = (((2 * dm + (dm / 32) * 8) + 15) & ~size_t(15)) + ((rr_max * w1 + 3) & ~size_t(3)) * 4 + 128;
-    auto it = blocks_per_cu.find(name);
-    if (it != blocks_per_cu.end()) {
-        occ = it->second;
-    } else {
+    // LDS: x digits + gate/up row sums (or lane partials and row sums) + 128 B staging (the
+    // kernel's layout), sized for a grid of g workgroups (the largest row range of any)
+    auto smem_for = [&](size_t g) {
+        const size_t rr_max = 2 * 8 * ((df / 8 + g - 1) / g);
+        const size_t sums = f->lane_partials ? rr_max * (size_t)w1 * 64 + ((rr_max + 3) & ~size_t(3))
+                                             : ((rr_max * w1 + 3) & ~size_t(3));
+        return (((2 * dm + (dm / 32) * 8) + 15) & ~size_t(15)) + sums * 4 + 128;
+    };
+    // ring_gu_per_cu workgroups per CU where that many fit with their LDS, else one
+    auto occupancy = [&](size_t smem) {
+        const std::string key = name + ":" + std::to_string(smem);
+        auto it = blocks_per_cu.find(key);
+        if (it != blocks_per_cu.end()) return it->second;
+        int occ = 0;
         if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, block, smem) != hipSuccess) occ = 1;
-        blocks_per_cu[name] = occ;
+        blocks_per_cu[key] = occ;
+        return occ;
+    };
+    size_t grid = cus, smem = smem_for(cus);
+    if (ring_gu_per_cu > 1) {
+        const size_t g2 = ring_grid(ring_gu_per_cu, ring_gu_per_cu, cus), s2 = smem_for(g2);
+        const int occ = occupancy(s2);
+        if (occ > 1) {
+            grid = ring_grid(occ, ring_gu_per_cu, cus);
+            smem = smem_for(grid);
+        }
     }
-    const size_t grid = ring_grid(occ, ring_gu_per_cu, cus);
     if (!hx) {
         HH_TRY(grow(&ws_hq, &ws_hq_cap, hh::ring_digits_bytes(df)));
         hx = (uint8_t*)ws_hq;
@@ -606,7 +625,7 @@ hh_status hh_engine::enqueue_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, co
     GurArgs a{wg, wu, x, hx, norm, (uint64_t)((dm / 256) * f->block_bytes), (uint32_t)dm, (uint32_t)df, d->act, eps};
     void* params[] = {&a};
     hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
-    if (err != hipSuccess) return hip_fail(err, "launch(ring q4k gate/up)");
+    if (err != hipSuccess) return hip_fail(err, "launch(ring gate/up)");
     return HH_OK;
 }
 
@@ -621,9 +640,11 @@ hh_status hh_engine::launch_dn_ring(int type, size_t m, size_t n, const uint8_t*
                                     const float* res) {
     const RingFmt* f = ring_fmt(type);
     if (!f) return fail(HH_ERR_INVALID, "ring down: no kernel for GGML type %d", type);
+    const bool wide = f->wide_dn && n >= 8192;
+    const size_t units = n / (wide ? 128 : 64);  // lane units per row
     int w2 = 1;
-    while ((size_t)w2 * 64 < n / 64) w2 *= 2;
-    const std::string name = std::string("hh_") + f->stem + "_dn_ring_d" + std::to_string(w2);
+    while ((size_t)w2 * 64 < units) w2 *= 2;
+    const std::string name = std::string("hh_") + f->stem + (wide ? "w" : "") + "_dn_ring_d" + std::to_string(w2);
     hipFunction_t fn;
     HH_TRY(kernel(name, &fn));
     const int block = 9 * 64;  // 8 compute waves + the wave that copies the intermediate
@@ -1541,7 +1562,9 @@ static std::vector<std::string> required_kernels() {
         for (int w : {1, 2, 4, 8}) k.push_back(std::string("hh_") + f + "_dn_ring_d" + std::to_string(w));
         for (int w : {1, 2})
             for (const char* n : {"", "_n"}) k.push_back(std::string("hh_") + f + "_gu_ring_g" + std::to_string(w) + n);
+        for (const char* n : {"", "_n"}) k.push_back(std::string("hh_") + f + "w_gu_ring_g1" + n);
     }
+    for (int w : {1, 2, 4}) k.push_back("hh_iq2w_dn_ring_d" + std::to_string(w));
     for (const char* f : {"gu_ring_u16", "gu_ring_u32", "gu_ring_u64", "dn_ring_d1", "dn_ring_d2", "dn_ring_d4",
                           "dn_ring_d8"})
         k.push_back(std::string("hh_moe_") + f);
