@@ -253,7 +253,7 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
         __syncthreads();
     }
 
-    if (wave == 0) {
+    {
         float inv = 1.f;
         if constexpr (NORM) {
             const float* red = reinterpret_cast<const float*>(stage);
@@ -262,12 +262,13 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
             for (int k = 0; k < HH_FFNP_CW; k++) tot += red[k];
             inv = 1.0f / sqrtf(tot / (float)dm + a.eps);
         }
-        // h = act(g) * u, two int8 digits per element, one scale per granule of 8 rows
+        // h = act(g) * u, two int8 digits per element, one scale per granule of 8 rows: one
+        // thread per row (every wave), the granule's max by DPP within its 8 lanes
         int8_t* gq1 = reinterpret_cast<int8_t*>(a.hx);
         int8_t* gq2 = gq1 + dff;
         float* gsc = reinterpret_cast<float*>(gq2 + dff);
-        for (uint32_t rho0 = 0; rho0 < r1 - r0; rho0 += HH_WAVE) {
-            const uint32_t rho = rho0 + lane;
+        for (uint32_t rho0 = 0; rho0 < r1 - r0; rho0 += HH_RING_BLOCK) {
+            const uint32_t rho = rho0 + tid;
             const bool ok = rho < r1 - r0;  // granule-aligned: whole 8-lane groups agree
             float hv = 0.f;
             if (ok) {
@@ -289,24 +290,20 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
                 hv = hh_act_mul(g, u, a.act);
             }
             float amax = fabsf(hv);
-#pragma unroll
-            for (int m = 1; m < 8; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, HH_WAVE));
+            amax = fmaxf(amax, hh_dpp<0xB1>(amax));   // quad_perm [1,0,3,2]
+            amax = fmaxf(amax, hh_dpp<0x4E>(amax));   // quad_perm [2,3,0,1]
+            amax = fmaxf(amax, hh_dpp<0x141>(amax));  // row_half_mirror: the other quad of the 8
             const float scale = amax * (1.0f / 127.0f);
-            const float inv = amax > 0.f ? 127.0f / amax : 0.f;
-            const float d1 = fminf(fmaxf(rintf(hv * inv), -127.f), 127.f);
+            const float rinv = amax > 0.f ? 127.0f / amax : 0.f;
+            const float d1 = fminf(fmaxf(rintf(hv * rinv), -127.f), 127.f);
             const float rr = hv - d1 * scale;
-            const float d2 = fminf(fmaxf(rintf(rr * inv * 256.0f), -127.f), 127.f);
-            stage[lane] = (uint8_t)(int8_t)(int)d1;
-            stage[64 + lane] = (uint8_t)(int8_t)(int)d2;
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): staged bytes visible to the wave
-            __builtin_amdgcn_wave_barrier();
-            if (ok && (lane & 7u) == 0) {
+            const float d2 = fminf(fmaxf(rintf(rr * rinv * 256.0f), -127.f), 127.f);
+            if (ok) {
                 const uint32_t r = r0 + rho;
-                *reinterpret_cast<uint64_t*>(gq1 + r) = *reinterpret_cast<const uint64_t*>(stage + lane);
-                *reinterpret_cast<uint64_t*>(gq2 + r) = *reinterpret_cast<const uint64_t*>(stage + 64 + lane);
-                gsc[r / 8] = scale;
+                gq1[r] = (int8_t)(int)d1;
+                gq2[r] = (int8_t)(int)d2;
+                if ((lane & 7u) == 0) gsc[r / 8] = scale;
             }
-            __builtin_amdgcn_wave_barrier();
         }
     }
 }
