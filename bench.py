@@ -42,7 +42,7 @@ D_MODEL, D_FF, LAYERS = 4096, 14336, 32
 Q4_K = 12
 PEAK_HBM_GBS = 8000.0
 CONFIG_ID = 2
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gu_ring_8b_bs1_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gu_ring_n_8b_bs1_traffic.json")
 
 
 def log(*a):

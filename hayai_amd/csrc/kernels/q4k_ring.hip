@@ -30,6 +30,26 @@
 
 #define HH_RING_BLOCK (HH_FFNP_CW * HH_WAVE)
 
+// Phase timeline of the ring kernels, compiled in only for the timeline tool
+// (csrc/trace/ring_timeline.cpp builds a separate code object with HH_RING_TRACE): one
+// timestamp of the 100 MHz realtime counter per workgroup and phase, indexed by the layer
+// that the weight pointer falls in ((w - base) / stride, set by the tool).
+#ifdef HH_RING_TRACE
+__device__ unsigned long long hh_ring_trace[2][64][512][4];  // [gate/up, down][layer][workgroup][phase]
+__device__ const uint8_t* hh_ring_trace_base;
+__device__ unsigned long long hh_ring_trace_stride;
+HH_DEV void hh_ring_mark(int kind, const uint8_t* w, int phase) {
+    const long long l = (long long)((w - hh_ring_trace_base) / (long long)hh_ring_trace_stride);
+    if (l >= 0 && l < 64 && blockIdx.x < 512) hh_ring_trace[kind][l][blockIdx.x][phase] = __builtin_amdgcn_s_memrealtime();
+}
+#define HH_RING_MARK(kind, w, phase, cond) \
+    do {                                   \
+        if (cond) hh_ring_mark(kind, w, phase); \
+    } while (0)
+#else
+#define HH_RING_MARK(kind, w, phase, cond) ((void)0)
+#endif
+
 // sum of squares of 8 elements, and x * inv * weight in the reference's order
 // (simd_scale_mul, crates/hayai-cpu/src/simd_ops.rs:28-41)
 HH_DEV float hh_sq8(const float4& a, const float4& b) {
@@ -126,6 +146,7 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
     const uint32_t r0 = 8u * (uint32_t)(((uint64_t)w * NG) / G);
     const uint32_t r1 = 8u * (uint32_t)(((uint64_t)(w + 1) * NG) / G);
     const uint32_t RR = 2u * (r1 - r0);  // row reads: (gate, up) of each row
+    HH_RING_MARK(0, a.wg, 0, tid == 0);
     const uint32_t n1 = (RR + TPW1 - 1) / TPW1;
     const uint32_t n1p = (n1 + D - 1) / D * D;
 
@@ -208,6 +229,7 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
 #pragma unroll
     for (int s = P; s < D; s++) issue((uint32_t)s, ring[s]);
     __syncthreads();
+    HH_RING_MARK(0, a.wg, 1, tid == 0);  // x's digits in LDS
 
     {
         typename F::xr_t xr;
@@ -231,6 +253,7 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
         }
     }
     __syncthreads();  // row sums (or lane partials) are in LDS
+    HH_RING_MARK(0, a.wg, 2, tid == 0);
     if constexpr (LP) {
         // row i = the TEAM1 partials of row read i: 32 threads per row, each adding TEAM1/32
         // consecutive partials, then a 32-lane DPP reduction (fixed order: deterministic)
@@ -306,6 +329,7 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
             }
         }
     }
+    HH_RING_MARK(0, a.wg, 3, lane == 0);  // the last wave to get here leaves the final stamp
 }
 
 // Down: workgroup w owns output rows [w*M/G, (w+1)*M/G); a team of WPT2 waves covers one row
@@ -327,6 +351,7 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
     const uint32_t q1 = (uint32_t)(((uint64_t)(w + 1) * dm) / G);
     const uint32_t n2 = (q1 - q0 + TPW2 - 1) / TPW2;
     const uint32_t n2p = (n2 + D - 1) / D * D;
+    HH_RING_MARK(1, a.wd, 0, tid == 0);
 
     // the residual of the first row this thread stores, fetched now rather than on the tail
     float res0 = 0.f;
@@ -376,6 +401,7 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
         __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();  // the intermediate is in LDS (the rings stay in flight)
+    HH_RING_MARK(1, a.wd, 1, tid == 0);
 
     if (wave < HH_FFNP_CW) {
         typename F::hr_t hr;
@@ -394,6 +420,7 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
         }
     }
     __syncthreads();  // lane partials are in LDS
+    HH_RING_MARK(1, a.wd, 2, tid == 0);
     // y[q0 + rl] = sum over the TEAM2 lane partials of row rl: 32 threads per row, each sums
     // TEAM2/32 consecutive partials, then a 32-lane DPP reduction (rows never straddle the
     // 32-lane halves of a wave)
@@ -416,6 +443,7 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
             if (rl < nrows && seg == 31) a.y[q0 + rl] = a.res ? (rl0 == 0 ? res0 : a.res[q0 + rl]) + s : s;
         }
     }
+    HH_RING_MARK(1, a.wd, 3, lane == 0);
 }
 
 // _n: with the RMSNorm prologue (the FFN residual block)
