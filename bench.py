@@ -243,8 +243,8 @@ def bench_batched(eng, pack, lay, stride, desc, args) -> int:
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "ffn_tok_s": round(B * 1e3 / ms, 2),
         "tflops": round(tflops, 2),
-        "roofline": roofline_step(gbs, "whole step: token prep + weight-stream MFMA gate/up and down (B <= 16) or the "
-                                       "tiled MFMA kernels (B > 16); MFMA rate in tflops"),
+        "roofline": roofline_step(gbs, "whole step: token prep + weight-stream f16 MFMA gate/up and down (B <= 16) or "
+                                       "the int8 MFMA kernels (17..64 tokens); MFMA rate in tflops"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

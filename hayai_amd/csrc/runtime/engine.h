@@ -158,7 +158,7 @@ struct hh_engine {
     int ring_gu_per_cu = 1;     // HAYAI_HIP_RING_GU_PER_CU: ring gate/up workgroups per CU
     int ring_dn_per_cu = 1;     // HAYAI_HIP_RING_DN_PER_CU: ring down workgroups per CU
     bool mmr = true;            // HAYAI_HIP_MMR=0: batched Q4_K (<= 16 tokens) on the q4k_mm kernels
-    bool mmq = true;            // HAYAI_HIP_MMQ=0: batched Q4_K (>= 16 tokens) on the f16 kernels, not int8
+    bool mmq = true;            // HAYAI_HIP_MMQ=0: batched Q4_K (>= 17 tokens) on the f16 kernels, not int8
     int mmq_s = 0;              // HAYAI_HIP_MMQ_S: superblocks per chunk of an int8 batched launch (0: chosen)
     int mmq_nw = 0;             // HAYAI_HIP_MMQ_NW: units (waves) per workgroup (0: 8)
     bool coop_launch = false;   // HAYAI_HIP_COOP=1: cooperative launch API for the fused kernel
@@ -257,7 +257,7 @@ struct hh_engine {
     // token stages, y).  HH_ERR_UNSUPPORTED_DEVICE when shape or alignment does not fit.
     enum { MMR_GEMM = 0, MMR_GU = 1, MMR_DN = 2 };
     bool mmr_ok(size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const;
-    // int8 MFMA batched Q4_K (q4k_mmq.hip) for 16..64 tokens: tokens [b][n] f32 -> int8
+    // int8 MFMA batched Q4_K (q4k_mmq.hip) for 17..64 tokens: tokens [b][n] f32 -> int8
     // stages (per 32-element block: s = amax / 127, q = round_half_away(x / s)) in `xs`,
     // then Y[b][m] = W . X (ffn == false) or H[b][m] = act(W_gate . X) * (W_up . X).
     bool mmq_ok(size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const;
