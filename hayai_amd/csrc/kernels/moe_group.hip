@@ -38,6 +38,8 @@ struct hh_moeg_args {
 #define HH_MOEG_MAX_P 4096    // (token, slot) pairs
 #define HH_MOEG_GU_RPT 2      // rows per team, loads issued together (gate/up: 2 matrices)
 #define HH_MOEG_DN_RPT 4
+#define HH_MOEG_NS 4          // tokens whose digits a workgroup stages in LDS at a time
+#define HH_MOEG_STAGE (HH_MOEG_NS * (2 * 4096 + (4096 / 32) * 8))  // d_model, d_ff <= 4096
 
 // bytes of the digit form of n elements (q1, q2, scale and sum per 32), as hh_moe_digits lays
 // it out; a multiple of 16 for n % 64 == 0
@@ -113,11 +115,26 @@ extern "C" __global__ void __launch_bounds__(256) hh_moe_hdigits(const hh_moeg_a
                        hh_moe_digits((char*)a.hq + p * hh_digits_bytes_dev(a.d_ff), a.d_ff));
 }
 
+// The digit forms of the expert's tokens (or pairs) i0 .. i0 + n - 1 -> LDS, 16 bytes per
+// thread per step (the forms are a multiple of 16 bytes); ends with a workgroup barrier.
+HH_DEV void hh_moeg_stage(uint8_t* lds, const uint8_t* src, const int32_t* order, int p0, int i0, int n,
+                          uint32_t k_div, size_t bytes) {
+    const uint32_t per = (uint32_t)(bytes / 16);
+    for (uint32_t c = threadIdx.x; c < (uint32_t)n * per; c += blockDim.x) {
+        const uint32_t i = c / per, o = c % per;
+        const uint32_t p = (uint32_t)order[p0 + i0 + (int)i], id = k_div ? p / k_div : p;
+        reinterpret_cast<uint4*>(lds + i * bytes)[o] = reinterpret_cast<const uint4*>(src + id * bytes)[o];
+    }
+    __syncthreads();
+}
+
 // Gate/up: a team of TEAM lanes per row (lane = 64-column unit, d_model <= 64 * TEAM); each
 // team takes HH_MOEG_GU_RPT rows with all their loads in flight, then dots them with every token
-// of the expert (the lane's slice of the token's digits, from L2).
+// of the expert (the lane's slice of the token's digits, staged in LDS HH_MOEG_NS tokens at a
+// time: every team reads them, so from L2 each would be read TPB times).
 template <int TEAM>
 HH_DEV void hh_moe_gu_grp_body(const hh_moeg_args& a) {
+    __shared__ __attribute__((aligned(16))) uint8_t stage[HH_MOEG_STAGE];
     const int na = a.elist[a.n_experts];
     if ((int)blockIdx.y >= na) return;  // grid.y covers the most experts a call can select
     const int e = a.elist[blockIdx.y];
@@ -138,15 +155,20 @@ HH_DEV void hh_moe_gu_grp_body(const hh_moeg_args& a) {
         hh_q4k_load(pack + a.gate_off + (size_t)j * a.rb_in, u, g[r]);
         hh_q4k_load(pack + a.up_off + (size_t)j * a.rb_in, u, up[r]);
     }
-    for (int i = 0; i < np; i++) {
-        const uint32_t p = (uint32_t)a.order[p0 + i], t = p / a.k;
-        hh_q4k_x xr;
-        hh_q4k_load_lane_x(hh_moe_digits((char*)a.xq + t * xbytes, dm), u, xr);
+    for (int i0 = 0; i0 < np; i0 += HH_MOEG_NS) {
+        const int n = min(HH_MOEG_NS, np - i0);
+        if (i0 > 0) __syncthreads();  // the previous tokens' digits are consumed
+        hh_moeg_stage(stage, a.xq, a.order, p0, i0, n, a.k, xbytes);
+        for (int i = 0; i < n; i++) {
+            const uint32_t p = (uint32_t)a.order[p0 + i0 + i];
+            hh_q4k_x xr;
+            hh_q4k_load_lane_x(hh_moe_digits((char*)stage + i * xbytes, dm), u, xr);
 #pragma unroll
-        for (int r = 0; r < HH_MOEG_GU_RPT; r++) {
-            const float gv = hh_moeg_team_sum<TEAM>(act ? hh_q4k_unit(g[r], xr) : 0.f);
-            const float uv = hh_moeg_team_sum<TEAM>(act ? hh_q4k_unit(up[r], xr) : 0.f);
-            if (l == TEAM - 1 && j0 + r < df) a.h[(size_t)p * df + j0 + r] = hh_act_mul(gv, uv, a.act);
+            for (int r = 0; r < HH_MOEG_GU_RPT; r++) {
+                const float gv = hh_moeg_team_sum<TEAM>(act ? hh_q4k_unit(g[r], xr) : 0.f);
+                const float uv = hh_moeg_team_sum<TEAM>(act ? hh_q4k_unit(up[r], xr) : 0.f);
+                if (l == TEAM - 1 && j0 + r < df) a.h[(size_t)p * df + j0 + r] = hh_act_mul(gv, uv, a.act);
+            }
         }
     }
 }
@@ -154,6 +176,7 @@ HH_DEV void hh_moe_gu_grp_body(const hh_moeg_args& a) {
 // Down: the same with the expert's pairs' h (d_ff columns) and d_model rows -> yp[p][row].
 template <int TEAM>
 HH_DEV void hh_moe_dn_grp_body(const hh_moeg_args& a) {
+    __shared__ __attribute__((aligned(16))) uint8_t stage[HH_MOEG_STAGE];
     const int na = a.elist[a.n_experts];
     if ((int)blockIdx.y >= na) return;
     const int e = a.elist[blockIdx.y];
@@ -170,14 +193,19 @@ HH_DEV void hh_moe_dn_grp_body(const hh_moeg_args& a) {
     hh_q4k_data w[HH_MOEG_DN_RPT];
 #pragma unroll
     for (int r = 0; r < HH_MOEG_DN_RPT; r++) hh_q4k_load(pack + a.down_off + (size_t)min(j0 + r, dm - 1) * a.rb_ff, u, w[r]);
-    for (int i = 0; i < np; i++) {
-        const uint32_t p = (uint32_t)a.order[p0 + i];
-        hh_q4k_x hr;
-        hh_q4k_load_lane_x(hh_moe_digits((char*)a.hq + p * hbytes, df), u, hr);
+    for (int i0 = 0; i0 < np; i0 += HH_MOEG_NS) {
+        const int n = min(HH_MOEG_NS, np - i0);
+        if (i0 > 0) __syncthreads();
+        hh_moeg_stage(stage, a.hq, a.order, p0, i0, n, 0u, hbytes);
+        for (int i = 0; i < n; i++) {
+            const uint32_t p = (uint32_t)a.order[p0 + i0 + i];
+            hh_q4k_x hr;
+            hh_q4k_load_lane_x(hh_moe_digits((char*)stage + i * hbytes, df), u, hr);
 #pragma unroll
-        for (int r = 0; r < HH_MOEG_DN_RPT; r++) {
-            const float d = hh_moeg_team_sum<TEAM>(act ? hh_q4k_unit(w[r], hr) : 0.f);
-            if (l == TEAM - 1 && j0 + r < dm) a.yp[(size_t)p * dm + j0 + r] = d;
+            for (int r = 0; r < HH_MOEG_DN_RPT; r++) {
+                const float d = hh_moeg_team_sum<TEAM>(act ? hh_q4k_unit(w[r], hr) : 0.f);
+                if (l == TEAM - 1 && j0 + r < dm) a.yp[(size_t)p * dm + j0 + r] = d;
+            }
         }
     }
 }
