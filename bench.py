@@ -724,6 +724,21 @@ def bench_smollm(eng, args) -> int:
     bytes_step = L * (wb + 2 * 4 * DM)
     gbs = bytes_step / (ms / 1e3) / 1e9
     log(f"[bench] smollm: {ms * 1e3:.1f} us/step ({ms * 1e3 / L:.2f} us/layer), {gbs:.1f} GB/s")
+    # the same steps as HIP graphs: one 30-layer graph per weight copy, captured once and
+    # replayed in rotation (the one-launch FFN's grid barrier keeps its state on the device)
+    graphs = [eng.capture(lambda c=c: step(c)) for c in range(COPIES)]
+    for i in range(args.warmup):
+        graphs[i % COPIES].launch()
+    eng.sync()
+    a.record()
+    for i in range(args.steps):
+        graphs[i % COPIES].launch()
+    b.record()
+    eng.sync()
+    ms_graph = a.elapsed_ms(b) / args.steps
+    for g in graphs:
+        g.free()
+    log(f"[bench] smollm graph replay: {ms_graph * 1e3:.1f} us/step ({ms_graph * 1e3 / L:.2f} us/layer)")
     cpu = None
     if not args.no_cpu_baseline:
         import oracle
@@ -749,7 +764,9 @@ def bench_smollm(eng, args) -> int:
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "ffn_tok_s": round(1e3 / ms, 2),
         "us_per_layer": round(ms * 1e3 / L, 3),
-        "roofline": roofline_step(gbs, "whole step: Q4_0 gate/up + down team kernels (launch-latency bound)"),
+        "graph_replay": {"ms_per_step": round(ms_graph, 5), "us_per_layer": round(ms_graph * 1e3 / L, 3),
+                         "value": round(bytes_step / (ms_graph / 1e3) / 1e9, 2)},
+        "roofline": roofline_step(gbs, "whole step: the one-launch Q4_0 FFN kernel per layer (launch-latency bound)"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

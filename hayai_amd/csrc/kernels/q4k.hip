@@ -428,21 +428,25 @@ HH_Q4K_WPT(8)
 //   line 16 + g           release flag of group g (holds the generation of the last release)
 //   line 32               arrival counter of groups
 //   line 33               error word
+//   line 34               epoch: the generation of the last release
+// A launch's generation is the epoch plus one, read by every workgroup before it arrives.
 // The last arriver of a group resets its group counter and counts the group; the last
-// group resets that counter and writes the launch's generation (a host-side counter,
-// never 0) into every release flag.  Counters therefore return to zero at every release
-// and flags need no reset.  The h digits cross workgroups (and XCDs) through device-
-// coherent stores and loads, ordered by s_waitcnt before the arrival and by the barrier.
+// group resets that counter and writes the generation into every release flag and into
+// the epoch.  Counters therefore return to zero at every release and flags need no reset.
+// The epoch changes only at a release, which needs every workgroup's arrival, so all
+// workgroups of a launch read the same value: the one the previous launch on this state
+// released (launches on one stream do not overlap).  No argument changes between
+// launches, so a captured graph replays them as they are.  The h digits cross workgroups
+// (and XCDs) through device-coherent stores and loads, ordered by s_waitcnt before the
+// arrival and by the barrier.
 #define HH_BAR_GROUPS 16
 #define HH_BAR_LINE 32  // u32 words per 128-byte line
-#define HH_BAR_WORDS (HH_BAR_LINE * (2 * HH_BAR_GROUPS + 2))
+#define HH_BAR_WORDS (HH_BAR_LINE * (2 * HH_BAR_GROUPS + 3))
 
 struct hh_q4k_ffn_args {
     hh_q4k_args gu;  // gate/up: writes h (f32) and the digits of h
     hh_q4k_args dn;  // down: reads the digits of h
     unsigned* bar;   // HH_BAR_WORDS words
-    unsigned gen;    // generation of this launch (!= 0)
-    unsigned pad;
 };
 
 HH_DEV unsigned hh_atomic_add_agent(unsigned* p, unsigned v) {
@@ -454,6 +458,15 @@ HH_DEV void hh_store_agent(unsigned* p, unsigned v) {
 HH_DEV unsigned hh_load_agent(unsigned* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+// The epoch as this launch starts; its generation is the epoch plus one.  Read at the
+// start of the kernel by every thread of a wave (one request per wave), so the wait for it
+// falls on the wait before the arrival instead of stalling the wave's first loads.
+HH_DEV unsigned hh_barrier_epoch(unsigned* bar) { return hh_load_agent(bar + (2 * HH_BAR_GROUPS + 2) * HH_BAR_LINE); }
+
+// The epoch load behind gen has returned before any later memory operation is issued: an
+// arrival that overtook it could complete a release whose epoch store the load then sees.
+HH_DEV void hh_barrier_gen_ready(unsigned gen) { asm volatile("" ::"v"(gen) : "memory"); }
 
 // The caller has completed (s_waitcnt + workgroup barrier) every store that other
 // workgroups read after this barrier.
@@ -467,12 +480,14 @@ HH_DEV bool hh_grid_barrier(unsigned* bar, unsigned gen) {
         unsigned* flag = bar + (HH_BAR_GROUPS + g) * HH_BAR_LINE;
         unsigned* top = bar + 2 * HH_BAR_GROUPS * HH_BAR_LINE;
         unsigned* err = top + HH_BAR_LINE;
+        hh_barrier_gen_ready(gen);
         if (hh_atomic_add_agent(cnt, 1u) == members - 1) {
             hh_store_agent(cnt, 0u);
             if (hh_atomic_add_agent(top, 1u) == G - 1) {
                 hh_store_agent(top, 0u);
                 __builtin_amdgcn_s_waitcnt(0);
                 for (unsigned k = 0; k < G; k++) hh_store_agent(bar + (HH_BAR_GROUPS + k) * HH_BAR_LINE, gen);
+                hh_store_agent(top + 2 * HH_BAR_LINE, gen);
             }
         }
         int good = 1;
@@ -492,6 +507,7 @@ HH_DEV bool hh_grid_barrier(unsigned* bar, unsigned gen) {
 
 template <int WPT_GU, int WPT_D>
 HH_DEV void hh_q4k_ffn_body(const hh_q4k_ffn_args& a) {
+    const unsigned epoch = hh_barrier_epoch(a.bar);
     hh_q4k_body<WPT_GU, 1, true, false, true>(a.gu);
     // Every thread's device-coherent h-digit stores are complete before the workgroup
     // arrives (vmcnt covers stores on this architecture).  No fence: a release/acquire
@@ -499,7 +515,7 @@ HH_DEV void hh_q4k_ffn_body(const hh_q4k_ffn_args& a) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     // The down phase issues its first weight loads, then waits at the grid barrier.
-    hh_q4k_body<WPT_D, 2, false, true, true>(a.dn, [&]() { return hh_grid_barrier(a.bar, a.gen); });
+    hh_q4k_body<WPT_D, 2, false, true, true>(a.dn, [&]() { return hh_grid_barrier(a.bar, epoch + 1u); });
 }
 
 // hh_q4k_ffn_g<WPT gate/up>_d<WPT down>

@@ -47,7 +47,6 @@ struct hh_ffnp_args {
     uint64_t rb2;       // row bytes of down (d_ff columns)
     uint32_t d_model;
     uint32_t d_ff;
-    uint32_t gen;       // barrier generation of this launch (!= 0)
     int32_t act;
 };
 
@@ -171,12 +170,14 @@ HH_DEV void hh_barrier_arrive(unsigned* bar, unsigned gen) {
     const unsigned members = (gridDim.x - g + HH_BAR_GROUPS - 1) / HH_BAR_GROUPS;
     unsigned* cnt = bar + g * HH_BAR_LINE;
     unsigned* top = bar + 2 * HH_BAR_GROUPS * HH_BAR_LINE;
+    hh_barrier_gen_ready(gen);
     if (hh_atomic_add_agent(cnt, 1u) == members - 1) {
         hh_store_agent(cnt, 0u);
         if (hh_atomic_add_agent(top, 1u) == G - 1) {
             hh_store_agent(top, 0u);
             __builtin_amdgcn_s_waitcnt(0);
             for (unsigned k = 0; k < G; k++) hh_store_agent(bar + (HH_BAR_GROUPS + k) * HH_BAR_LINE, gen);
+            hh_store_agent(top + 2 * HH_BAR_LINE, gen);
         }
     }
 }
@@ -207,6 +208,7 @@ HH_DEV void hh_ffnp_body(const hh_ffnp_args& a) {
     const bool xw = wave == HH_FFNP_CW;  // the exchange wave
     const uint32_t G = gridDim.x, w = blockIdx.x;
     const uint32_t dm = a.d_model, dff = a.d_ff;
+    const unsigned epoch = xw ? hh_barrier_epoch(a.bar) : 0u;  // the exchange wave's
 
     // phase-1 rows (granules of 8) and phase-2 rows of this workgroup
     const uint32_t NG = dff / 8;
@@ -364,8 +366,8 @@ HH_DEV void hh_ffnp_body(const hh_ffnp_args& a) {
         __builtin_amdgcn_s_waitcnt(0);
         int good = 1;
         if (lane == 0) {
-            hh_barrier_arrive(a.bar, a.gen);
-            good = hh_barrier_wait(a.bar, a.gen) ? 1 : 0;
+            hh_barrier_arrive(a.bar, epoch + 1u);
+            good = hh_barrier_wait(a.bar, epoch + 1u) ? 1 : 0;
         }
         good = __builtin_amdgcn_readfirstlane(good);
         if (good) {

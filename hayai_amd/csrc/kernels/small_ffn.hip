@@ -20,7 +20,6 @@ struct hh_sffn_args {
     uint64_t rb_in;  // row bytes of gate/up (d_model columns) and down (d_ff columns)
     uint64_t rb_ff;
     uint32_t d_model, d_ff;
-    unsigned gen;
     int32_t act;
 };
 
@@ -35,7 +34,8 @@ HH_DEV void hh_sffn_body(const hh_sffn_args& a) {
     const uint32_t l1 = tid % TEAM1, t1 = tid / TEAM1, l2 = tid % TEAM2, t2 = tid / TEAM2;
     const bool a1 = l1 < dm / Q::UNIT, a2 = l2 < df / Q::UNIT;
 
-    // every load of the launch first: gate/up rows, down rows, the x slice
+    // the barrier epoch, then every load of the launch: gate/up rows, down rows, the x slice
+    const unsigned epoch = hh_barrier_epoch(a.bar);
     typename Q::Data dg[2], du[2], dd[2];
 #pragma unroll
     for (int k = 0; k < 2; k++) {
@@ -61,8 +61,8 @@ HH_DEV void hh_sffn_body(const hh_sffn_args& a) {
     __builtin_amdgcn_s_waitcnt(0);  // this thread's h stores are complete
     __syncthreads();
     if (tid == 0) {
-        hh_barrier_arrive(a.bar, a.gen);
-        s_good = hh_barrier_wait(a.bar, a.gen) ? 1 : 0;
+        hh_barrier_arrive(a.bar, epoch + 1u);
+        s_good = hh_barrier_wait(a.bar, epoch + 1u) ? 1 : 0;
     }
     __syncthreads();
     if (!s_good) return;  // timed out: the error word is set, y is not written

@@ -376,23 +376,21 @@ hh_status hh_engine::enqueue_gateup(int tg, int tu, size_t d_ff, size_t d_model,
 }
 
 // Fused FFN kernel arguments and grid-barrier state (q4k.hip): 16 arrival-counter lines,
-// 16 release-flag lines, the group counter and the error word, 128 bytes each.
+// 16 release-flag lines, the group counter, the error word and the epoch, 128 bytes each.
 struct hh_q4k_ffn_args {
     hh_q4k_args gu;
     hh_q4k_args dn;
     unsigned* bar;
-    unsigned gen;
-    unsigned pad;
 };
 constexpr size_t kBarLine = 128;
-constexpr size_t kBarBytes = kBarLine * (2 * 16 + 2);
+constexpr size_t kBarBytes = kBarLine * (2 * 16 + 3);
 constexpr size_t kBarErrOffset = kBarLine * (2 * 16 + 1);
 
 hh_status hh_engine::enqueue_q4k_ffn(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                                      const float* x, float* y) {
     const size_t dm = d->d_model, df = d->d_ff;
-    // (its grid barrier carries a per-launch generation: a graph replay would reuse it)
-    if (capturing || !ffn_fused || q4k_generic || dm % 256 || df % 256 || dm / 64 > 512 || df / 64 > 512 ||
+    // (the cooperative launch API is not captured into graphs)
+    if ((capturing && coop_launch) || !ffn_fused || q4k_generic || dm % 256 || df % 256 || dm / 64 > 512 || df / 64 > 512 ||
         (((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd | (uintptr_t)x) & 15u))
         return HH_ERR_UNSUPPORTED_DEVICE;
     int wg_t = 1, wd_t = 1;
@@ -433,8 +431,6 @@ hh_status hh_engine::enqueue_q4k_ffn(const hh_ffn_desc* d, const uint8_t* wg, co
     a.dn = hh_q4k_args{wd, nullptr, nullptr, y, digits_at(ws_hq, df), hh_digits_ptr{}, (uint32_t)dm, (uint32_t)df,
                        (uint64_t)((df / 256) * 144), 0, 0};
     a.bar = (unsigned*)grid_sync;
-    if (++ffn_gen == 0) ffn_gen = 1;
-    a.gen = ffn_gen;
     void* params[] = {&a};
     hipError_t err;
     if (coop_launch)
@@ -457,15 +453,14 @@ struct FfnpArgs {
     uint8_t* hx;
     unsigned* bar;
     uint64_t rb1, rb2;
-    uint32_t d_model, d_ff, gen;
+    uint32_t d_model, d_ff;
     int32_t act;
 };
 
 hh_status hh_engine::enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu,
                                       const uint8_t* wd, const float* x, float* y) {
     const size_t dm = d->d_model, df = d->d_ff;
-    // (its grid barrier carries a per-launch generation: a graph replay would reuse it)
-    if (capturing || !ffnp || q4k_generic || dm % 256 || df % 256 || dm > 8192 || df > 32768 ||
+    if (!ffnp || q4k_generic || dm % 256 || df % 256 || dm > 8192 || df > 32768 ||
         (((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd | (uintptr_t)x) & 15u))
         return HH_ERR_UNSUPPORTED_DEVICE;
     const int w1 = dm <= 4096 ? 1 : 2;
@@ -501,9 +496,7 @@ hh_status hh_engine::enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, c
     const size_t grid = G0;
     HH_TRY(grow(&ws_hq, &ws_hq_cap, 3 * df + 16));
     FfnpArgs a{wg, wu, wd, x, y, (uint8_t*)ws_hq, (unsigned*)grid_sync, (uint64_t)((dm / 256) * 144),
-               (uint64_t)((df / 256) * 144), (uint32_t)dm, (uint32_t)df, 0u, d->act};
-    if (++ffn_gen == 0) ffn_gen = 1;
-    a.gen = ffn_gen;
+               (uint64_t)((df / 256) * 144), (uint32_t)dm, (uint32_t)df, d->act};
     void* params[] = {&a};
     hipError_t err =
         hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
@@ -858,7 +851,6 @@ struct SffnArgs {
     unsigned* bar;
     uint64_t rb_in, rb_ff;
     uint32_t d_model, d_ff;
-    unsigned gen;
     int32_t act;
 };
 
@@ -870,7 +862,7 @@ hh_status hh_engine::enqueue_small_ffn(const hh_ffn_desc* d, const uint8_t* wg, 
     const size_t dm = d->d_model, df = d->d_ff, G = (size_t)props.multiProcessorCount;
     auto team_of = [](size_t units) { return units <= 16 ? 16 : (units <= 32 ? 32 : 64); };
     const int t1 = team_of(dm / 32), t2 = team_of(df / 32);
-    if (capturing || !small_ffn || dm % 32 || df % 32 || dm / 32 > 64 || df / 32 > 64 ||
+    if (!small_ffn || dm % 32 || df % 32 || dm / 32 > 64 || df / 32 > 64 ||
         (df + G - 1) / G > 2 * (256 / (size_t)t1) || (dm + G - 1) / G > 2 * (256 / (size_t)t2) ||
         (((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd) & 1u) || ((uintptr_t)x & 3u) || ((uintptr_t)y & 3u))
         return HH_ERR_UNSUPPORTED_DEVICE;
@@ -883,9 +875,7 @@ hh_status hh_engine::enqueue_small_ffn(const hh_ffn_desc* d, const uint8_t* wg, 
     HH_TRY(row_bytes(d->type_gate, dm, &rin));
     HH_TRY(row_bytes(d->type_down, df, &rff));
     SffnArgs a{wg, wu, wd, x, y, (float*)ws_h, (unsigned*)grid_sync, (uint64_t)rin, (uint64_t)rff, (uint32_t)dm,
-               (uint32_t)df, 0u, d->act};
-    if (++ffn_gen == 0) ffn_gen = 1;
-    a.gen = ffn_gen;
+               (uint32_t)df, d->act};
     void* params[] = {&a};
     hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)G, 1, 1, 256, 1, 1, 0, stream, params, nullptr);
     if (err != hipSuccess) return hip_fail(err, "launch(small ffn)");

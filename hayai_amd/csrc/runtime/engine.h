@@ -145,7 +145,6 @@ struct hh_engine {
     void* ws_moe_q = nullptr;    // grouped MoE: x digits per token, h digits per pair
     size_t ws_moe_q_cap = 0;
     void* grid_sync = nullptr;  // fused FFN grid-barrier state (counters, flags, error word)
-    uint32_t ffn_gen = 0;       // generation of the last fused FFN launch
     hh_ffn_desc ffn_stage{};    // FFN whose gate/up output is pending in ws_h (/ws_hq)
     bool ffn_stage_valid = false;
     bool ffn_stage_digits = false;  // ws_hq holds the digits of ws_h

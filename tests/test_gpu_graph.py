@@ -85,6 +85,91 @@ def test_graph_replay_equals_eager_chain(engine):
     g.free()
 
 
+def engine_with_env(**env):
+    """A HipEngine created with the given HAYAI_HIP_* switches set (read at creation)."""
+    import os
+
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return hayai_amd.HipEngine(0)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+
+
+BARRIER_CASES = [
+    # (types, d_model, d_ff, engine switches): the one-launch FFNs with a grid barrier.  The
+    # small Q4_0 / Q8_0 FFN at SmolLM2-135M's layer; the persistent Q4_K FFN (ring form off)
+    # at the 8B layer and at a layer with fewer h granules than workgroups.
+    ((hayai_amd.Q4_0,) * 3, 576, 1536, {}),
+    ((hayai_amd.Q8_0,) * 3, 576, 1536, {}),
+    ((hayai_amd.Q4_K,) * 3, 4096, 14336, {"HAYAI_HIP_RING": "0"}),
+    ((hayai_amd.Q4_K,) * 3, 2048, 768, {"HAYAI_HIP_RING": "0"}),
+]
+
+
+@pytest.mark.parametrize("types,d_model,d_ff,env", BARRIER_CASES)
+def test_graph_replays_grid_barrier_ffns(types, d_model, d_ff, env):
+    # The barrier generation is kept on the device (an epoch the releasing workgroup
+    # advances), so a graph of one-launch FFNs replays with unchanged arguments.  Several
+    # barriers per replay (a chain of layers), eager launches between replays (the epoch
+    # keeps counting across both), and every replay equal to the eager chain bit for bit:
+    # the same kernel ran, not a fallback captured in its place.
+    n = 3
+    print(f"[case] graph grid-barrier ffn {types} {d_model}x{d_ff} {env}", flush=True)
+    eng = engine_with_env(**env)
+    try:
+        t = types[0]
+        gate = hayai_amd.QuantMatrix("ffn_gate", d_model, d_ff, t)
+        up = hayai_amd.QuantMatrix("ffn_up", d_model, d_ff, t)
+        down = hayai_amd.QuantMatrix("ffn_down", d_ff, d_model, t)
+        lay = hayai_amd.LayerPackLayout.ffn_only(gate, up, down)
+        desc = eng.ffn_desc(types, d_model, d_ff, lay)
+        packs, mats = [], []
+        for l in range(n):
+            wg = synth.matrix(t, d_ff, d_model, synth.seed_for(34, l, synth.GATE))
+            wu = synth.matrix(t, d_ff, d_model, synth.seed_for(34, l, synth.UP))
+            wd = synth.matrix(t, d_model, d_ff, synth.seed_for(34, l, synth.DOWN))
+            p = eng.alloc(lay.total)
+            p.write(wg, lay.gate_off)
+            p.write(wu, lay.up_off)
+            p.write(wd, lay.down_off)
+            packs.append(p)
+            mats.append((wg, wu, wd))
+        x = synth.normal(synth.seed_for(34, 0, synth.ACT), d_model)
+        xbuf = eng.upload(x)
+        eager = [eng.alloc(4 * d_model) for _ in range(n)]
+        chain(eng, desc, packs, xbuf, eager)
+        eng.sync()
+        y_eager = [b.read(np.float32, d_model) for b in eager]
+        r0 = oracle.ffn(types, d_model, d_ff, *mats[0], x)
+        assert np.max(np.abs(y_eager[0] - r0)) / np.max(np.abs(r0)) <= 1e-3
+
+        outs = [eng.alloc(4 * d_model) for _ in range(n)]
+        g = eng.capture(lambda: chain(eng, desc, packs, xbuf, outs))
+        other = [eng.alloc(4 * d_model) for _ in range(n)]
+        for rep in range(4):
+            for b in outs:
+                b.fill(0)
+            g.launch()
+            if rep % 2:
+                chain(eng, desc, packs, xbuf, other)  # eager barriers right behind the replay
+            eng.sync()
+            for l in range(n):
+                y = outs[l].read(np.float32, d_model)
+                assert np.array_equal(y.view(np.uint32), y_eager[l].view(np.uint32)), f"replay {rep} layer {l}"
+            if rep % 2:
+                y = other[-1].read(np.float32, d_model)
+                assert np.array_equal(y.view(np.uint32), y_eager[-1].view(np.uint32)), f"eager after replay {rep}"
+        g.free()
+    finally:
+        eng.close()
+
+
 def test_graph_refuses_unreplayable_calls(engine):
     print("[case] graph refusals", flush=True)
     lay, packs, _ = make_layers(engine, 1, d_model=256, d_ff=512, cfg=32)
