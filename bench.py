@@ -739,6 +739,36 @@ def bench_smollm(eng, args) -> int:
     for g in graphs:
         g.free()
     log(f"[bench] smollm graph replay: {ms_graph * 1e3:.1f} us/step ({ms_graph * 1e3 / L:.2f} us/layer)")
+    # The 30 layers as chained residual blocks (x_{l+1} = x_l + FFN_l(rms_norm(x_l))): one
+    # persistent launch per step (hh_ffn_block_stack_dev), and the same chain as 30 block
+    # calls for comparison.
+    norms = synth.normal(synth.seed_for(1, 0, synth.ACT) + 7, L * DM) * 0.1 + 1.0
+    nbuf = eng.upload(norms.astype(np.float32))
+    sbuf = eng.alloc(4 * DM)
+
+    def stack(s):
+        eng.ffn_block_stack_dev(desc, pack, (s % COPIES) * L * stride, stride, L, nbuf, 0, DM, 1e-5, xbuf, 0,
+                                sbuf, 0)
+
+    def blocks(s):
+        base = (s % COPIES) * L * stride
+        for l in range(L):
+            eng.ffn_block_dev(desc, pack, base + l * stride, nbuf, 4 * DM * l, 1e-5, xbuf if l == 0 else sbuf, 0,
+                              sbuf, 0)
+
+    chained = {}
+    for name, fn in (("stack", stack), ("blocks", blocks)):
+        for i in range(args.warmup):
+            fn(i)
+        eng.sync()
+        a.record()
+        for i in range(args.steps):
+            fn(i)
+        b.record()
+        eng.sync()
+        chained[name] = a.elapsed_ms(b) / args.steps
+        log(f"[bench] smollm chained {name}: {chained[name] * 1e3:.1f} us/step "
+            f"({chained[name] * 1e3 / L:.2f} us/layer)")
     cpu = None
     if not args.no_cpu_baseline:
         import oracle
@@ -766,6 +796,11 @@ def bench_smollm(eng, args) -> int:
         "us_per_layer": round(ms * 1e3 / L, 3),
         "graph_replay": {"ms_per_step": round(ms_graph, 5), "us_per_layer": round(ms_graph * 1e3 / L, 3),
                          "value": round(bytes_step / (ms_graph / 1e3) / 1e9, 2)},
+        "chained_stack": {"ms_per_step": round(chained["stack"], 5),
+                          "us_per_layer": round(chained["stack"] * 1e3 / L, 3),
+                          "value": round((bytes_step + L * 4 * DM) / (chained["stack"] / 1e3) / 1e9, 2)},
+        "chained_blocks": {"ms_per_step": round(chained["blocks"], 5),
+                           "us_per_layer": round(chained["blocks"] * 1e3 / L, 3)},
         "roofline": roofline_step(gbs, "whole step: the one-launch Q4_0 FFN kernel per layer (launch-latency bound)"),
         "cpu_baseline": cpu,
     }

@@ -173,6 +173,7 @@ SIGNATURES = {
     "hh_ffn_block_begin_dev": (ST, [P, C.POINTER(FfnDesc), P, SZ, P, SZ, C.c_float, P, SZ]),
     "hh_ffn_block_finish_dev": (ST, [P, C.POINTER(FfnDesc), P, SZ, P, SZ, P, SZ]),
     "hh_ffn_block_dev": (ST, [P, C.POINTER(FfnDesc), P, SZ, P, SZ, C.c_float, P, SZ, P, SZ]),
+    "hh_ffn_block_stack_dev": (ST, [P, C.POINTER(FfnDesc), P, SZ, SZ, SZ, P, SZ, SZ, C.c_float, P, SZ, P, SZ]),
     "hh_gemv_batched": (ST, [P, I, SZ, SZ, P, SZ, P, P, SZ]),
     "hh_gemv_batched_dev": (ST, [P, I, SZ, SZ, P, SZ, P, SZ, SZ, P, SZ]),
     "hh_ffn_batched_dev": (ST, [P, C.POINTER(FfnDesc), P, SZ, P, SZ, SZ, P, SZ]),

@@ -130,15 +130,19 @@ TRACE_DIR = os.path.join(HERE, "trace_build")
 
 
 def build_timeline(verbose: bool = False) -> str:
-    """The ring-kernel timeline tool (csrc/trace/ring_timeline.cpp) and the code object it
-    runs: the kernels again with HH_RING_TRACE (per-workgroup phase timestamps).  A
-    measurement tool, not part of the library; outputs under hayai_amd/trace_build/."""
+    """The timeline tools (csrc/trace/ring_timeline.cpp, csrc/trace/stack_timeline.cpp) and
+    the code object they run: the kernels again with HH_RING_TRACE and HH_SSTK_TRACE
+    (per-workgroup phase timestamps).  Measurement tools, not part of the library; outputs
+    under hayai_amd/trace_build/."""
     os.makedirs(TRACE_DIR, exist_ok=True)
     hipcc = os.path.join(rocm_path(), "bin", "hipcc")
     co = os.path.join(TRACE_DIR, "hayai_kernels_trace.hsaco")
-    _run([hipcc, *KERNEL_FLAGS, "-DHH_RING_TRACE", "-o", co, os.path.join(CSRC, "kernels", "all.hip")], verbose)
+    _run([hipcc, *KERNEL_FLAGS, "-DHH_RING_TRACE", "-DHH_SSTK_TRACE", "-o", co,
+          os.path.join(CSRC, "kernels", "all.hip")], verbose)
     tool = os.path.join(TRACE_DIR, "ring_timeline")
     _run([hipcc, "-O2", "-std=c++17", "-o", tool, os.path.join(CSRC, "trace", "ring_timeline.cpp")], verbose)
+    _run([hipcc, "-O2", "-std=c++17", "-o", os.path.join(TRACE_DIR, "stack_timeline"),
+          os.path.join(CSRC, "trace", "stack_timeline.cpp")], verbose)
     return tool
 
 

@@ -429,6 +429,7 @@ HH_Q4K_WPT(8)
 //   line 32               arrival counter of groups
 //   line 33               error word
 //   line 34               epoch: the generation of the last release
+//   line 35               stack epoch: the last tag of the FFN-stack exchange (small_stack.hip)
 // A launch's generation is the epoch plus one, read by every workgroup before it arrives.
 // The last arriver of a group resets its group counter and counts the group; the last
 // group resets that counter and writes the generation into every release flag and into
@@ -441,7 +442,8 @@ HH_Q4K_WPT(8)
 // arrival and by the barrier.
 #define HH_BAR_GROUPS 16
 #define HH_BAR_LINE 32  // u32 words per 128-byte line
-#define HH_BAR_WORDS (HH_BAR_LINE * (2 * HH_BAR_GROUPS + 3))
+#define HH_BAR_WORDS (HH_BAR_LINE * (2 * HH_BAR_GROUPS + 4))
+#define HH_BAR_STACK_EPOCH ((2 * HH_BAR_GROUPS + 3) * HH_BAR_LINE)
 
 struct hh_q4k_ffn_args {
     hh_q4k_args gu;  // gate/up: writes h (f32) and the digits of h

@@ -547,6 +547,39 @@ hh_status hh_ffn_block_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pac
                                 (float*)((char*)y->ptr + y_off));
 }
 
+hh_status hh_ffn_block_stack_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                                 size_t layer_stride, size_t n_layers, const hh_buf* norm, size_t norm_off,
+                                 size_t norm_stride, float eps, const hh_buf* x, size_t x_off, hh_buf* y,
+                                 size_t y_off) {
+    HH_NOT_NULL(e, "engine");
+    if (n_layers == 0) return fail(HH_ERR_INVALID, "ffn_block_stack: n_layers must be at least 1");
+    size_t last_pack, last_norm;
+    if (__builtin_mul_overflow(n_layers - 1, layer_stride, &last_pack) ||
+        __builtin_add_overflow(last_pack, pack_off, &last_pack) ||
+        __builtin_mul_overflow(n_layers - 1, norm_stride, &last_norm) ||
+        __builtin_mul_overflow(last_norm, sizeof(float), &last_norm) ||
+        __builtin_add_overflow(last_norm, norm_off, &last_norm))
+        return fail(HH_ERR_INVALID, "ffn_block_stack: layer offsets overflow");
+    HH_TRY(validate_ffn(e, d, pack, pack_off));
+    HH_TRY(validate_ffn(e, d, pack, last_pack));  // layers lie between the first and the last
+    HH_TRY(check_engine(e, norm, "norm"));
+    HH_TRY(check_engine(e, x, "x"));
+    HH_TRY(check_engine(e, y, "y"));
+    HH_TRY(check_range(norm, norm_off, d->d_model * sizeof(float), "norm"));
+    HH_TRY(check_range(norm, last_norm, d->d_model * sizeof(float), "norm"));
+    HH_TRY(check_range(x, x_off, d->d_model * sizeof(float), "x"));
+    HH_TRY(check_range(y, y_off, d->d_model * sizeof(float), "y"));
+    if (((norm_off | x_off | y_off) & 3u) != 0)
+        return fail(HH_ERR_INVALID, "ffn_block_stack: norm/x/y offsets must be 4-byte aligned");
+    if (!(eps >= 0.f) || eps > 1.f)
+        return fail(HH_ERR_INVALID, "ffn_block_stack: eps=%g outside [0, 1]", (double)eps);
+    HH_TRY(e->select());
+    std::lock_guard<std::mutex> lk(e->ws_mutex);
+    return e->enqueue_ffn_block_stack(d, (const uint8_t*)pack->ptr + pack_off, layer_stride, n_layers,
+                                      (const float*)((const char*)norm->ptr + norm_off), norm_stride, eps,
+                                      (const float*)((const char*)x->ptr + x_off), (float*)((char*)y->ptr + y_off));
+}
+
 hh_status hh_ffn_batched_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off, const hh_buf* x,
                              size_t x_off, size_t batch, hh_buf* y, size_t y_off) {
     HH_NOT_NULL(e, "engine");

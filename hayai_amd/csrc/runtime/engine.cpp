@@ -376,14 +376,16 @@ hh_status hh_engine::enqueue_gateup(int tg, int tu, size_t d_ff, size_t d_model,
 }
 
 // Fused FFN kernel arguments and grid-barrier state (q4k.hip): 16 arrival-counter lines,
-// 16 release-flag lines, the group counter, the error word and the epoch, 128 bytes each.
+// 16 release-flag lines, the group counter, the error word, the barrier epoch and the
+// FFN-stack epoch, 128 bytes each.
 struct hh_q4k_ffn_args {
     hh_q4k_args gu;
     hh_q4k_args dn;
     unsigned* bar;
 };
 constexpr size_t kBarLine = 128;
-constexpr size_t kBarBytes = kBarLine * (2 * 16 + 3);
+constexpr size_t kBarBytes = kBarLine * (2 * 16 + 4);
+constexpr size_t kBarEpochOffset = kBarLine * (2 * 16 + 2);  // the epochs survive an error reset
 constexpr size_t kBarErrOffset = kBarLine * (2 * 16 + 1);
 
 hh_status hh_engine::enqueue_q4k_ffn(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
@@ -688,8 +690,12 @@ hh_status hh_engine::check_device_error() {
     HH_TRY_HIP(hipMemcpy(&flag, (char*)grid_sync + kBarErrOffset, sizeof flag, hipMemcpyDeviceToHost),
                "hipMemcpy(err)");
     if (flag) {
-        HH_TRY_HIP(hipMemset(grid_sync, 0, kBarBytes), "hipMemset(grid_sync)");
-        return fail(HH_ERR_RUNTIME, "fused FFN grid barrier timed out (workgroups not co-resident)");
+        // Counters, flags and the error word back to zero; the epochs keep counting, so no
+        // tag or generation of the failed launch can be taken for a later one's.  The stack
+        // exchange words go back to tag 0, which no launch uses.
+        HH_TRY_HIP(hipMemset(grid_sync, 0, kBarEpochOffset), "hipMemset(grid_sync)");
+        if (ws_stk) HH_TRY_HIP(hipMemset(ws_stk, 0, ws_stk_cap), "hipMemset(stack exchange)");
+        return fail(HH_ERR_RUNTIME, "grid-wide exchange timed out (workgroups not co-resident)");
     }
     return HH_OK;
 }
@@ -879,6 +885,81 @@ hh_status hh_engine::enqueue_small_ffn(const hh_ffn_desc* d, const uint8_t* wg, 
     void* params[] = {&a};
     hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)G, 1, 1, 256, 1, 1, 0, stream, params, nullptr);
     if (err != hipSuccess) return hip_fail(err, "launch(small ffn)");
+    return HH_OK;
+}
+
+// Must match struct hh_sstk_args in kernels/small_stack.hip.
+struct SstkArgs {
+    const uint8_t* pack;
+    const float* norm;
+    const float* x;
+    float* y;
+    uint64_t* hx;
+    uint64_t* xx;
+    uint64_t* spare;
+    unsigned* bar;
+    uint64_t stride, off_g, off_u, off_d, rb_in, rb_ff;
+    uint32_t norm_stride, d_model, d_ff, n_layers;
+    float eps;
+    int32_t act;
+};
+
+// Consecutive small Q4_0 / Q8_0 FFN residual blocks in one persistent launch
+// (small_stack.hip): one workgroup per CU (every one resident: the exchange polls), 4
+// compute waves + the exchange wave, at most two rows per team and phase, every workgroup
+// with a gate/up row and a down row.
+hh_status hh_engine::enqueue_small_stack(const hh_ffn_desc* d, const uint8_t* pack, size_t stride, size_t n_layers,
+                                         const float* norm, size_t norm_stride, float eps, const float* x, float* y) {
+    const size_t dm = d->d_model, df = d->d_ff;
+    const size_t cus = (size_t)props.multiProcessorCount;
+    const size_t G = std::min({stack_grid > 0 ? std::min((size_t)stack_grid, cus) : cus, dm, df});
+    auto team_of = [](size_t units) { return units <= 16 ? 16 : (units <= 32 ? 32 : 64); };
+    const int t1 = team_of(dm / 32), t2 = team_of(df / 32);
+    // rows per team and phase (instantiated: 1..4 for Q4_0, 1..2 for Q8_0)
+    const size_t rows1 = (df + G - 1) / G, rows2 = (dm + G - 1) / G;
+    const size_t tpb1 = 256 / (size_t)t1, tpb2 = 256 / (size_t)t2;
+    const size_t R = std::max((rows1 + tpb1 - 1) / tpb1, (rows2 + tpb2 - 1) / tpb2);
+    const size_t r_max = d->type_gate == HH_TYPE_Q4_0 ? 4 : 2;
+    if (!small_stack || !(d->type_gate == d->type_up && d->type_up == d->type_down) ||
+        (d->type_gate != HH_TYPE_Q4_0 && d->type_gate != HH_TYPE_Q8_0) || dm % 32 || df % 32 || dm / 32 > 64 ||
+        df / 32 > 64 || n_layers > 0xFFFFu || norm_stride > 0xFFFFFFFFu || R > r_max ||
+        ((uintptr_t)pack | d->gate_off | d->up_off | d->down_off | stride) & 1u || ((uintptr_t)x & 3u) ||
+        ((uintptr_t)y & 3u) || ((uintptr_t)norm & 3u))
+        return HH_ERR_UNSUPPORTED_DEVICE;
+    const std::string name = std::string("hh_sstk_") + (d->type_gate == HH_TYPE_Q4_0 ? "q4_0" : "q8_0") + "_t" +
+                             std::to_string(t1) + "_" + std::to_string(t2) + "_r" + std::to_string(R);
+    hipFunction_t fn;
+    HH_TRY(kernel(name, &fn));
+    const size_t need = (df + dm + 16 * G) * sizeof(uint64_t);  // h, x, a spare line per workgroup
+    if (ws_stk_cap < need) {
+        HH_TRY(grow(&ws_stk, &ws_stk_cap, need));
+        HH_TRY_HIP(hipMemset(ws_stk, 0, ws_stk_cap), "hipMemset(stack exchange)");
+    }
+    size_t rin, rff;
+    HH_TRY(row_bytes(d->type_gate, dm, &rin));
+    HH_TRY(row_bytes(d->type_down, df, &rff));
+    SstkArgs a{pack, norm, x, y, (uint64_t*)ws_stk, (uint64_t*)ws_stk + df, (uint64_t*)ws_stk + df + dm, (unsigned*)grid_sync, (uint64_t)stride,
+               (uint64_t)d->gate_off, (uint64_t)d->up_off, (uint64_t)d->down_off, (uint64_t)rin, (uint64_t)rff,
+               (uint32_t)norm_stride, (uint32_t)dm, (uint32_t)df, (uint32_t)n_layers, eps, d->act};
+    void* params[] = {&a};
+    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)G, 1, 1, 5 * 64, 1, 1, 0, stream, params, nullptr);
+    if (err != hipSuccess) return hip_fail(err, "launch(small ffn stack)");
+    return HH_OK;
+}
+
+hh_status hh_engine::enqueue_ffn_block_stack(const hh_ffn_desc* d, const uint8_t* pack, size_t stride,
+                                             size_t n_layers, const float* norm, size_t norm_stride, float eps,
+                                             const float* x, float* y) {
+    if (n_layers == 0) return HH_OK;
+    const hh_status st = enqueue_small_stack(d, pack, stride, n_layers, norm, norm_stride, eps, x, y);
+    if (st == HH_OK) {
+        ffn_stage_valid = false;
+        ffn_calls += 3 * n_layers;
+        return HH_OK;
+    }
+    if (st != HH_ERR_UNSUPPORTED_DEVICE) return st;
+    for (size_t l = 0; l < n_layers; l++)
+        HH_TRY(enqueue_ffn_block(d, pack + l * stride, l == 0 ? x : y, norm + l * norm_stride, eps, y));
     return HH_OK;
 }
 
@@ -1630,6 +1711,8 @@ hh_status engine_create(int device, hh_engine** out) {
     if (const char* f = getenv("HAYAI_HIP_RING")) e->ring = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_MOE_GROUPED")) e->moe_grouped = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_SMALL_FFN")) e->small_ffn = atoi(f) != 0;
+    if (const char* f = getenv("HAYAI_HIP_SMALL_STACK")) e->small_stack = atoi(f) != 0;
+    if (const char* f = getenv("HAYAI_HIP_STACK_GRID")) e->stack_grid = atoi(f);
     if (const char* f = getenv("HAYAI_HIP_MMQ")) e->mmq = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_MMQ_S")) e->mmq_s = atoi(f);
     if (const char* f = getenv("HAYAI_HIP_MMQ_NW")) e->mmq_nw = std::min(8, std::max(0, atoi(f)));
@@ -1653,7 +1736,7 @@ void engine_destroy(hh_engine* e) {
     if (e->copy_stream) (void)hipStreamSynchronize(e->copy_stream);
     if (e->copy_stream2) (void)hipStreamSynchronize(e->copy_stream2);
     for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq, e->ws_xop, e->ws_hop, e->ws_part,
-                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->ws_xn, e->ws_f, e->ws_xq, e->ws_moe_yp, e->ws_moe_grp, e->ws_moe_q, e->grid_sync})
+                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->ws_xn, e->ws_f, e->ws_xq, e->ws_moe_yp, e->ws_moe_grp, e->ws_moe_q, e->ws_stk, e->grid_sync})
         if (p) (void)hipFree(p);
     for (void* p : e->ws_retired) (void)hipFree(p);
     if (e->stream) (void)hipStreamDestroy(e->stream);

@@ -144,7 +144,9 @@ struct hh_engine {
     size_t ws_moe_grp_cap = 0;
     void* ws_moe_q = nullptr;    // grouped MoE: x digits per token, h digits per pair
     size_t ws_moe_q_cap = 0;
-    void* grid_sync = nullptr;  // fused FFN grid-barrier state (counters, flags, error word)
+    void* ws_stk = nullptr;     // FFN-stack exchange: tagged words of h (d_ff) then x (d_model); zeroed
+    size_t ws_stk_cap = 0;      // when allocated and after a device error
+    void* grid_sync = nullptr;  // grid-barrier state (counters, flags, error word, epochs)
     hh_ffn_desc ffn_stage{};    // FFN whose gate/up output is pending in ws_h (/ws_hq)
     bool ffn_stage_valid = false;
     bool ffn_stage_digits = false;  // ws_hq holds the digits of ws_h
@@ -205,6 +207,15 @@ struct hh_engine {
                                 const float* x, float* y);
     hh_status enqueue_ffn_block(const hh_ffn_desc* d, const uint8_t* pack, const float* x, const float* norm,
                                 float eps, float* y);
+    // n_layers consecutive FFN residual blocks (layer l's pack at pack + l * stride, its norm
+    // at norm + l * norm_stride floats); y = x_L, y may be x.  Small Q4_0 / Q8_0 layers run
+    // in one persistent launch (small_stack.hip), others as one block per layer.
+    hh_status enqueue_ffn_block_stack(const hh_ffn_desc* d, const uint8_t* pack, size_t stride, size_t n_layers,
+                                      const float* norm, size_t norm_stride, float eps, const float* x, float* y);
+    hh_status enqueue_small_stack(const hh_ffn_desc* d, const uint8_t* pack, size_t stride, size_t n_layers,
+                                  const float* norm, size_t norm_stride, float eps, const float* x, float* y);
+    bool small_stack = true;  // HAYAI_HIP_SMALL_STACK=0: FFN stacks as one block per layer
+    int stack_grid = 0;       // HAYAI_HIP_STACK_GRID: workgroups of the persistent stack (0: one per CU)
     // The two halves of enqueue_ffn's two-launch path: gate/up(+act) into the engine's FFN
     // intermediate, then the down projection of that intermediate.
     // With norm: the begin step of the FFN residual block (x is RMSNorm'ed first); with res:

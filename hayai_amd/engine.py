@@ -591,6 +591,15 @@ class HipEngine:
         _check(self.lib.hh_ffn_block_dev(self.handle, C.byref(desc), pack.handle, pack_off, norm.handle, norm_off,
                                          eps, x.handle, x_off, y.handle, y_off))
 
+    def ffn_block_stack_dev(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, layer_stride: int,
+                            n_layers: int, norm: DeviceBuffer, norm_off: int, norm_stride: int, eps: float,
+                            x: DeviceBuffer, x_off: int, y: DeviceBuffer, y_off: int) -> None:
+        """n_layers FFN residual blocks back to back (layer l's pack at pack_off + l * layer_stride,
+        its norm at norm_off + 4 * l * norm_stride): y = x_L; y may be x.  Enqueue only."""
+        _check(self.lib.hh_ffn_block_stack_dev(self.handle, C.byref(desc), pack.handle, pack_off, layer_stride,
+                                               n_layers, norm.handle, norm_off, norm_stride, eps, x.handle, x_off,
+                                               y.handle, y_off))
+
     def ffn_block(self, desc: _abi.FfnDesc, pack: DeviceBuffer, pack_off: int, norm: np.ndarray, eps: float,
                   x: np.ndarray) -> np.ndarray:
         """ffn_apply on host activations: returns x + FFN(rms_norm(x, norm, eps)), blocking."""

@@ -257,6 +257,22 @@ hh_status hh_ffn_block_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pac
                            const hh_buf* norm, size_t norm_off, float eps, const hh_buf* x, size_t x_off, hh_buf* y,
                            size_t y_off);
 
+/* n_layers FFN residual blocks of one token back to back: x_{l+1} = x_l + FFN_l(RMSNorm(x_l)
+ * with norm_l), y = x_{n_layers}; layer l's pack at pack_off + l * layer_stride bytes, its
+ * norm at norm_off + l * norm_stride * 4 bytes (norm_stride in floats; 0 reuses one vector).
+ * y may be x.  No counterpart in the reference: its decode loop calls ffn_apply
+ * (hybrid_infer.rs:883-936) once per layer with attention between.  This entry point is for
+ * callers that run FFN blocks with no other op between them (FFN-only layer stacks, the
+ * chained-layer benchmark): small all-Q4_0 / all-Q8_0 layers (d_model, d_ff <= 2048) run
+ * every layer in one persistent launch that requests each layer's weights ahead of the
+ * activation exchanges; other layouts run hh_ffn_block_dev per layer.  Results match
+ * hh_ffn_block_dev applied layer by layer to f32 rounding (sums in another order).
+ * HH_ERR_INVALID for n_layers 0 or ranges outside the buffers.  Enqueue only. */
+hh_status hh_ffn_block_stack_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
+                                 size_t layer_stride, size_t n_layers, const hh_buf* norm, size_t norm_off,
+                                 size_t norm_stride, float eps, const hh_buf* x, size_t x_off, hh_buf* y,
+                                 size_t y_off);
+
 /* The FFN op for `batch` tokens (x, y: batch rows of d_model floats): the batched-prefill
  * form of the op (prefill_wave.rs:577-584 drives execute_quant_gemv_batched for FFN
  * matrices).  All-Q4_K FFNs run gate/up(+act) and down on the matrix cores; other formats
