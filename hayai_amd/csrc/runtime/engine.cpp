@@ -1428,6 +1428,7 @@ struct hh_moe_args {
     hh_route_args r;
 };
 constexpr int kMoeBlock = 256;
+constexpr size_t kLdsBytes = 160 * 1024;  // LDS per workgroup on gfx950
 constexpr size_t kMoeDownRows = 4;  // output rows per down workgroup (moe.hip)
 constexpr size_t kMoegGuRows = 2, kMoegDnRows = 4;  // grouped MoE rows per team (HH_MOEG_*_RPT, moe_group.hip)
 
@@ -1538,6 +1539,43 @@ hh_status hh_engine::enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* expert
         hipFunction_t fn;
         HH_TRY(kernel("hh_moe_prep", &fn));
         HH_TRY(launch(fn, (uint32_t)(1 + T), 256, g));
+        // The ring form (moe_gring.hip, opt-in): one workgroup per CU streams its share of the
+        // selected experts' concatenated rows; the gate/up kernel writes the intermediate's digits.
+        // Its per-(row, pair) dot and reduction chains leave it slower than the per-expert
+        // grouped kernels below at 32 tokens (192 vs 114 us per 128-expert layer).
+        const size_t cus = (size_t)props.multiProcessorCount;
+        const size_t u1 = dm / 64, u2 = (size_t)moe_team(df / 64);
+        const size_t emax = std::min(E, P);                        // active experts at most
+        const size_t rmax = 32 * ((emax * (df / 32) + cus - 1) / cus);  // rows of the largest gate/up share
+        const size_t gu_pair = xqb + 12 * rmax;                    // LDS per staged pair (digits, sums, h)
+        const size_t ns_cap = moe_gring_ns > 0 ? std::min<size_t>((size_t)moe_gring_ns, 64) : 64;  // HH_GRING_MAX_NS
+        const size_t ns_gu = std::min<size_t>(std::min<size_t>(32, ns_cap), (kLdsBytes - 1024) / gu_pair);
+        const size_t ns_dn = std::min<size_t>(ns_cap, (kLdsBytes - 1024) / hqb);
+        if (moe_gring && (u1 == 16 || u1 == 32 || u1 == 64) && df % 256 == 0 && dm % 256 == 0 && ns_gu >= 1 &&
+            rmax / df + 2 <= 64 && ((emax * (dm / 8) + cus - 1) / cus) * 8 / dm + 2 <= 64) {
+            struct {
+                decltype(g) m;
+                uint32_t ns, rmax;
+            } gr{g, (uint32_t)ns_gu, (uint32_t)rmax};
+            HH_TRY(kernel("hh_moe_gu_gring_u" + std::to_string(u1), &fn));
+            void* p1[] = {&gr};
+            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)cus, 1, 1, 8 * 64, 1, 1, (unsigned)(ns_gu * gu_pair), stream,
+                                             p1, nullptr),
+                       "launch(moe grouped ring gate/up)");
+            gr.ns = (uint32_t)ns_dn;
+            HH_TRY(kernel("hh_moe_dn_gring_u" + std::to_string(u2), &fn));
+            void* p2[] = {&gr};
+            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)cus, 1, 1, 8 * 64, 1, 1, (unsigned)(ns_dn * hqb), stream, p2,
+                                             nullptr),
+                       "launch(moe grouped ring down)");
+            HH_TRY(kernel("hh_moe_combine", &fn));
+            void* gp[] = {&g};
+            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)((dm + 255) / 256), (uint32_t)T, 1, 256, 1, 1, 0, stream, gp,
+                                             nullptr),
+                       "launch(moe combine)");
+            ffn_calls += 3 * T;
+            return HH_OK;
+        }
         const uint32_t gy = (uint32_t)std::min(E, P);
         {
             const int team = moe_team(dm / 64);
@@ -1713,6 +1751,8 @@ hh_status engine_create(int device, hh_engine** out) {
     if (const char* f = getenv("HAYAI_HIP_SMALL_FFN")) e->small_ffn = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_SMALL_STACK")) e->small_stack = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_STACK_GRID")) e->stack_grid = atoi(f);
+    if (const char* f = getenv("HAYAI_HIP_MOE_GRING")) e->moe_gring = atoi(f) != 0;
+    if (const char* f = getenv("HAYAI_HIP_MOE_GRING_NS")) e->moe_gring_ns = atoi(f);
     if (const char* f = getenv("HAYAI_HIP_MMQ")) e->mmq = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_MMQ_S")) e->mmq_s = atoi(f);
     if (const char* f = getenv("HAYAI_HIP_MMQ_NW")) e->mmq_nw = std::min(8, std::max(0, atoi(f)));

@@ -216,6 +216,8 @@ struct hh_engine {
                                   const float* norm, size_t norm_stride, float eps, const float* x, float* y);
     bool small_stack = true;  // HAYAI_HIP_SMALL_STACK=0: FFN stacks as one block per layer
     int stack_grid = 0;       // HAYAI_HIP_STACK_GRID: workgroups of the persistent stack (0: one per CU)
+    bool moe_gring = false;   // HAYAI_HIP_MOE_GRING=1: several-token MoE on the ring-form kernels (slower today)
+    int moe_gring_ns = 0;     // HAYAI_HIP_MOE_GRING_NS: pairs staged per pass (0: as many as LDS holds)
     // The two halves of enqueue_ffn's two-launch path: gate/up(+act) into the engine's FFN
     // intermediate, then the down projection of that intermediate.
     // With norm: the begin step of the FFN residual block (x is RMSNorm'ed first); with res:
