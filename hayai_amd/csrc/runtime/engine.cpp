@@ -1288,6 +1288,83 @@ hh_status hh_engine::enqueue_q4k_mmq(bool ffn, size_t m, size_t n, const uint8_t
     return HH_OK;
 }
 
+// ---- int8 MFMA batched Q4_K, weights staged through LDS (q4k_mmd.hip) ----
+
+// Must match struct hh_mmd_args in kernels/q4k_mmd.hip.
+struct MmdArgs {
+    const uint8_t* w0;
+    const uint8_t* w1;
+    const uint8_t* xs;
+    float* y;
+    float* part;
+    unsigned* cnt;
+    uint64_t row_bytes;
+    uint32_t m, n, b, tiles;
+    int32_t act;
+    uint32_t pad;
+};
+// One kernel configuration: NT matrices, SU superblocks per step, KR per K-range, RING slots.
+struct mmd_plan {
+    const char* name = nullptr;
+    size_t nt = 0, su = 0, kr = 0, ring = 0;
+    size_t steps = 0, smem = 0;
+};
+static mmd_plan plan_mmd(bool ffn, size_t m, size_t n, size_t cus) {
+    mmd_plan p;
+    const size_t nsb = n / 256, tiles = (m + 15) / 16;
+    if (ffn && nsb == 16) p = {"hh_q4k_mmd_gu_k16", 2, 4, 16, 4};
+    else if (ffn && nsb % 8 == 0) p = {"hh_q4k_mmd_gu_k8", 2, 4, 8, 4};
+    else if (!ffn && nsb % 8 == 0) p = {"hh_q4k_mmd_k8", 1, 8, 8, 4};
+    else return mmd_plan{};
+    const size_t nr = nsb / p.kr, per_r = tiles * (p.kr / p.su);
+    p.steps = nr * per_r;
+    const size_t per_wg = (p.steps + cus - 1) / cus;
+    if (per_wg > 32 || per_wg > per_r) return mmd_plan{};  // HH_MMD_MAX_SEG; at most two K-ranges
+    p.smem = (nr > 1 ? 2 : 1) * p.kr * 320 * 16 + p.ring * p.nt * 16 * (p.su * 144 + 16);
+    return p;
+}
+
+bool hh_engine::mmd_ok(bool ffn, size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const {
+    if (!mmd || !mmq || q4k_generic || b < (size_t)std::max(1, mmd_min) || b > 16 || m < 1 || m > 0xFFFFFFF0u || n < 256 ||
+        n % 256 != 0 || n > 0xFFFFFFFFu || ((((uintptr_t)w0 | (uintptr_t)w1 | (uintptr_t)x) & 15u) != 0))
+        return false;
+    const mmd_plan p = plan_mmd(ffn, m, n, (size_t)props.multiProcessorCount);
+    return p.name && p.smem + 512 <= (size_t)props.sharedMemPerBlock;
+}
+
+hh_status hh_engine::enqueue_q4k_mmd(bool ffn, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1,
+                                     const void* xs, size_t b, float* y, int act) {
+    const size_t cus = (size_t)props.multiProcessorCount;
+    const mmd_plan p = plan_mmd(ffn, m, n, cus);
+    if (!p.name) return HH_ERR_UNSUPPORTED_DEVICE;
+    const size_t tiles = (m + 15) / 16, ks = (n / 256) / p.su;
+    HH_TRY(grow(&ws_part, &ws_part_cap, tiles * ks * p.nt * 256 * sizeof(float)));
+    if (ws_cnt_cap < tiles * sizeof(unsigned)) {
+        HH_TRY(grow(&ws_cnt, &ws_cnt_cap, tiles * sizeof(unsigned)));
+        HH_TRY_HIP(hipMemsetAsync(ws_cnt, 0, ws_cnt_cap, stream), "hipMemsetAsync(counters)");
+    }
+    hipFunction_t fn;
+    HH_TRY(kernel(p.name, &fn));
+    MmdArgs a{};
+    a.w0 = w0;
+    a.w1 = ffn ? w1 : w0;
+    a.xs = (const uint8_t*)xs;
+    a.y = y;
+    a.part = (float*)ws_part;
+    a.cnt = (unsigned*)ws_cnt;
+    a.row_bytes = (uint64_t)((n / 256) * 144);
+    a.m = (uint32_t)m;
+    a.n = (uint32_t)n;
+    a.b = (uint32_t)b;
+    a.tiles = (uint32_t)tiles;
+    a.act = act;
+    void* params[] = {&a};
+    // 16 waves (HH_MMD_WAVES): two per (matrix, superblock) item of a step
+    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)cus, 1, 1, 16 * 64, 1, 1, (unsigned)p.smem, stream, params, nullptr);
+    if (err != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel(q4k_mmd)");
+    return HH_OK;
+}
+
 hh_status hh_engine::enqueue_gemv_batched(int type, size_t m, size_t n, const uint8_t* w, const float* x, size_t batch,
                                           float* y) {
     if (batch == 0) return HH_OK;
@@ -1301,6 +1378,12 @@ hh_status hh_engine::enqueue_gemv_batched(int type, size_t m, size_t n, const ui
         const size_t nb = std::min(kMmMaxTokens, batch - b0);
         if (nb == 1) {
             HH_TRY(enqueue_gemv(type, m, n, w, x + b0 * n, y + b0 * m));
+            continue;
+        }
+        if (mmd_ok(false, m, n, nb, w, w, x + b0 * n)) {  // 16 tokens: int8 MFMA, weights via LDS
+            HH_TRY(grow(&ws_xop, &ws_xop_cap, (n / 256) * mmq_stage_bytes(16)));
+            HH_TRY(enqueue_mmq_prep(x + b0 * n, nb, n, 16, ws_xop));
+            HH_TRY(enqueue_q4k_mmd(false, m, n, w, nullptr, ws_xop, nb, y + b0 * m, 0));
             continue;
         }
         if (mmq_ok(m, n, nb, w, w, x + b0 * n)) {  // 17..64 tokens: int8 MFMA
@@ -1365,6 +1448,19 @@ hh_status hh_engine::enqueue_ffn_batched(const hh_ffn_desc* d, const uint8_t* pa
         const size_t nb = std::min(kMmMaxTokens, batch - b0);
         if (nb == 1) {
             HH_TRY(enqueue_ffn(d, pack, x + b0 * dm, y + b0 * dm));
+            continue;
+        }
+        if (df % 256 == 0 && mmd_ok(true, df, dm, nb, wg, wu, x + b0 * dm) && mmd_ok(false, dm, df, nb, wd, wd, wd)) {
+            // 16 tokens on the int8 matrix cores with the weights staged through LDS
+            HH_TRY(grow(&ws_xop, &ws_xop_cap, (dm / 256) * mmq_stage_bytes(16)));
+            HH_TRY(grow(&ws_hop, &ws_hop_cap, (df / 256) * mmq_stage_bytes(16)));
+            HH_TRY(grow(&ws_h, &ws_h_cap, nb * df * sizeof(float)));
+            HH_TRY(enqueue_mmq_prep(x + b0 * dm, nb, dm, 16, ws_xop));
+            HH_TRY(enqueue_q4k_mmd(true, df, dm, wg, wu, ws_xop, nb, (float*)ws_h, d->act));
+            HH_TRY(enqueue_mmq_prep((const float*)ws_h, nb, df, 16, ws_hop));
+            HH_TRY(enqueue_q4k_mmd(false, dm, df, wd, nullptr, ws_hop, nb, y + b0 * dm, 0));
+            ffn_stage_valid = false;
+            ffn_calls += 3 * nb;
             continue;
         }
         if (df % 256 == 0 && mmq_ok(df, dm, nb, wg, wu, x + b0 * dm) && mmq_ok(dm, df, nb, wd, wd, wd)) {
@@ -1660,6 +1756,7 @@ static std::vector<std::string> required_kernels() {
         for (const char* kind : {"hh_q4k_mmr_s", "hh_q4k_mmr_gu_s"}) k.push_back(std::string(kind) + std::to_string(S));
     for (int S : {2, 4, 7, 8, 14, 16}) k.push_back("hh_q4k_mmr_dn_s" + std::to_string(S));
     k.push_back("hh_mmq_prep");
+    for (const char* kn : {"hh_q4k_mmd_gu_k16", "hh_q4k_mmd_gu_k8", "hh_q4k_mmd_k8"}) k.push_back(kn);
     for (const char* st : {"s2_t1", "s4_t1", "s7_t1", "s8_t1", "s14_t1", "s16_t1", "s2_t2", "s4_t2", "s7_t2", "s8_t2",
                            "s14_t2", "s2_t3", "s4_t3", "s7_t3", "s8_t3", "s2_t4", "s4_t4", "s6_t4", "s7_t4"})
         for (const char* kind : {"hh_q4k_mmq_", "hh_q4k_mmq_gu_"}) k.push_back(std::string(kind) + st);
@@ -1754,6 +1851,8 @@ hh_status engine_create(int device, hh_engine** out) {
     if (const char* f = getenv("HAYAI_HIP_MOE_GRING")) e->moe_gring = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_MOE_GRING_NS")) e->moe_gring_ns = atoi(f);
     if (const char* f = getenv("HAYAI_HIP_MMQ")) e->mmq = atoi(f) != 0;
+    if (const char* f = getenv("HAYAI_HIP_MMD")) e->mmd = atoi(f) != 0;
+    if (const char* f = getenv("HAYAI_HIP_MMD_MIN")) e->mmd_min = atoi(f);
     if (const char* f = getenv("HAYAI_HIP_MMQ_S")) e->mmq_s = atoi(f);
     if (const char* f = getenv("HAYAI_HIP_MMQ_NW")) e->mmq_nw = std::min(8, std::max(0, atoi(f)));
     if (const char* f = getenv("HAYAI_HIP_DMA_SPLIT")) e->dma_split = atoi(f) != 0;

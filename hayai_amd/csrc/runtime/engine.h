@@ -160,6 +160,8 @@ struct hh_engine {
     int ring_dn_per_cu = 1;     // HAYAI_HIP_RING_DN_PER_CU: ring down workgroups per CU
     bool mmr = true;            // HAYAI_HIP_MMR=0: batched Q4_K (<= 16 tokens) on the q4k_mm kernels
     bool mmq = true;            // HAYAI_HIP_MMQ=0: batched Q4_K (>= 17 tokens) on the f16 kernels, not int8
+    bool mmd = false;           // HAYAI_HIP_MMD=1: up to 16 tokens on the LDS-staged int8 kernels (q4k_mmd; slower today)
+    int mmd_min = 16;           // HAYAI_HIP_MMD_MIN: fewest tokens sent to the q4k_mmd kernels (1..16)
     int mmq_s = 0;              // HAYAI_HIP_MMQ_S: superblocks per chunk of an int8 batched launch (0: chosen)
     int mmq_nw = 0;             // HAYAI_HIP_MMQ_NW: units (waves) per workgroup (0: 8)
     bool coop_launch = false;   // HAYAI_HIP_COOP=1: cooperative launch API for the fused kernel
@@ -273,6 +275,9 @@ struct hh_engine {
     // stages (per 32-element block: s = amax / 127, q = round_half_away(x / s)) in `xs`,
     // then Y[b][m] = W . X (ffn == false) or H[b][m] = act(W_gate . X) * (W_up . X).
     bool mmq_ok(size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const;
+    bool mmd_ok(bool ffn, size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const;
+    hh_status enqueue_q4k_mmd(bool ffn, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* xs,
+                              size_t b, float* y, int act);
     hh_status enqueue_mmq_prep(const float* x, size_t b, size_t n, size_t tp, void* xs);
     hh_status enqueue_q4k_mmq(bool ffn, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* xs,
                               size_t b, float* y, int act);
