@@ -163,12 +163,23 @@ HH_DEV void hh_moe_gu_grp_body(const hh_moeg_args& a) {
             const uint32_t p = (uint32_t)a.order[p0 + i0 + i];
             hh_q4k_x xr;
             hh_q4k_load_lane_x(hh_moe_digits((char*)stage + i * xbytes, dm), u, xr);
+            // every lane computes (a lane past the row's units holds unit 0's data and
+            // contributes zero): no branch, so the rows' dot and DPP chains interleave
+            float gt[HH_MOEG_GU_RPT], ut[HH_MOEG_GU_RPT];
 #pragma unroll
             for (int r = 0; r < HH_MOEG_GU_RPT; r++) {
-                const float gv = hh_moeg_team_sum<TEAM>(act ? hh_q4k_unit(g[r], xr) : 0.f);
-                const float uv = hh_moeg_team_sum<TEAM>(act ? hh_q4k_unit(up[r], xr) : 0.f);
-                if (l == TEAM - 1 && j0 + r < df) a.h[(size_t)p * df + j0 + r] = hh_act_mul(gv, uv, a.act);
+                const float gx = hh_q4k_unit(g[r], xr), ux = hh_q4k_unit(up[r], xr);
+                gt[r] = act ? gx : 0.f;
+                ut[r] = act ? ux : 0.f;
             }
+#pragma unroll
+            for (int r = 0; r < HH_MOEG_GU_RPT; r++) {
+                gt[r] = hh_moeg_team_sum<TEAM>(gt[r]);
+                ut[r] = hh_moeg_team_sum<TEAM>(ut[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < HH_MOEG_GU_RPT; r++)
+                if (l == TEAM - 1 && j0 + r < df) a.h[(size_t)p * df + j0 + r] = hh_act_mul(gt[r], ut[r], a.act);
         }
     }
 }
@@ -201,11 +212,17 @@ HH_DEV void hh_moe_dn_grp_body(const hh_moeg_args& a) {
             const uint32_t p = (uint32_t)a.order[p0 + i0 + i];
             hh_q4k_x hr;
             hh_q4k_load_lane_x(hh_moe_digits((char*)stage + i * hbytes, df), u, hr);
+            float dt[HH_MOEG_DN_RPT];
 #pragma unroll
             for (int r = 0; r < HH_MOEG_DN_RPT; r++) {
-                const float d = hh_moeg_team_sum<TEAM>(act ? hh_q4k_unit(w[r], hr) : 0.f);
-                if (l == TEAM - 1 && j0 + r < dm) a.yp[(size_t)p * dm + j0 + r] = d;
+                const float dx = hh_q4k_unit(w[r], hr);
+                dt[r] = act ? dx : 0.f;
             }
+#pragma unroll
+            for (int r = 0; r < HH_MOEG_DN_RPT; r++) dt[r] = hh_moeg_team_sum<TEAM>(dt[r]);
+#pragma unroll
+            for (int r = 0; r < HH_MOEG_DN_RPT; r++)
+                if (l == TEAM - 1 && j0 + r < dm) a.yp[(size_t)p * dm + j0 + r] = dt[r];
         }
     }
 }
@@ -221,8 +238,9 @@ extern "C" __global__ void __launch_bounds__(256) hh_moe_combine(const hh_moeg_a
     a.y[(size_t)t * a.d_model + j] = acc;
 }
 
+// gate/up held to 128 VGPRs: four of its 4-wave workgroups per CU (the LDS stage allows four)
 #define HH_MOEG_KERNELS(TEAM)                                                                          \
-    extern "C" __global__ void __launch_bounds__(256) hh_moe_gu_grp_t##TEAM(const hh_moeg_args a) {     \
+    extern "C" __global__ void __launch_bounds__(256, 4) hh_moe_gu_grp_t##TEAM(const hh_moeg_args a) {  \
         hh_moe_gu_grp_body<TEAM>(a);                                                                   \
     }                                                                                                  \
     extern "C" __global__ void __launch_bounds__(256) hh_moe_dn_grp_t##TEAM(const hh_moeg_args a) {     \
