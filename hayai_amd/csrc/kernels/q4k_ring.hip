@@ -446,17 +446,25 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
     HH_RING_MARK(1, a.wd, 3, lane == 0);
 }
 
+// Ring depths (items per wave) of the Q4_K ring kernels.
+#ifndef HH_Q4K_GU_RING_D
+#define HH_Q4K_GU_RING_D 3
+#endif
+#ifndef HH_Q4K_DN_RING_D
+#define HH_Q4K_DN_RING_D 3
+#endif
+
 // _n: with the RMSNorm prologue (the FFN residual block)
 #define HH_GU_RING(G1)                                                                          \
     extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_q4k_gu_ring_g##G1(const hh_gur_args a) { \
-        hh_gu_ring_body<hh_ring_q4k, G1, 3, 1, false>(a);                                       \
+        hh_gu_ring_body<hh_ring_q4k, G1, HH_Q4K_GU_RING_D, 1, false>(a);                        \
     }                                                                                           \
     extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_q4k_gu_ring_g##G1##_n(const hh_gur_args a) { \
-        hh_gu_ring_body<hh_ring_q4k, G1, 3, 1, true>(a);                                        \
+        hh_gu_ring_body<hh_ring_q4k, G1, HH_Q4K_GU_RING_D, 1, true>(a);                         \
     }
 #define HH_DN_RING(G2)                                                                          \
     extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) hh_q4k_dn_ring_d##G2(const hh_dnr_args a) { \
-        hh_dn_ring_body<hh_ring_q4k, G2, 3>(a);                                                 \
+        hh_dn_ring_body<hh_ring_q4k, G2, HH_Q4K_DN_RING_D>(a);                                  \
     }
 HH_GU_RING(1)
 HH_GU_RING(2)

@@ -695,6 +695,7 @@ hh_status hh_engine::check_device_error() {
         // exchange words go back to tag 0, which no launch uses.
         HH_TRY_HIP(hipMemset(grid_sync, 0, kBarEpochOffset), "hipMemset(grid_sync)");
         if (ws_stk) HH_TRY_HIP(hipMemset(ws_stk, 0, ws_stk_cap), "hipMemset(stack exchange)");
+        if (ws_qstk) HH_TRY_HIP(hipMemset(ws_qstk, 0, ws_qstk_cap), "hipMemset(stack exchange)");
         return fail(HH_ERR_RUNTIME, "grid-wide exchange timed out (workgroups not co-resident)");
     }
     return HH_OK;
@@ -947,11 +948,83 @@ hh_status hh_engine::enqueue_small_stack(const hh_ffn_desc* d, const uint8_t* pa
     return HH_OK;
 }
 
+// Must match struct hh_qstk_args in kernels/q4k_stack.hip.
+struct QstkArgs {
+    const uint8_t* pack;
+    const float* norm;
+    const float* x;
+    float* y;
+    uint64_t* hx;
+    uint64_t* xx;
+    unsigned* bar;
+    uint64_t stride, off_g, off_u, off_d, rb1, rb2;
+    uint32_t norm_stride, d_model, d_ff, n_layers;
+    uint32_t lds_wd, lds_hx;
+    float eps;
+    int32_t act;
+};
+
+// Consecutive all-Q4_K FFN residual blocks in one persistent launch (q4k_stack.hip), opt-in
+// (HAYAI_HIP_Q4K_STACK=1: measured slower than one ring block per layer, 32 vs 23.7 us per
+// 8B layer): one workgroup per CU (every one resident: the exchanges poll), 8 compute waves
+// + 3 exchange waves + 1 DMA wave; each workgroup's share of W_down (its d_model / G rows)
+// lives in LDS, at most 16 rows.
+// Needs d_model <= 4096 (one wave per gate/up row), d_ff <= 16384 (four waves per down row),
+// both multiples of 256, a grid that gives every workgroup a down row and an h granule, and
+// a down share that fits beside the digits.
+hh_status hh_engine::enqueue_q4k_stack(const hh_ffn_desc* d, const uint8_t* pack, size_t stride, size_t n_layers,
+                                       const float* norm, size_t norm_stride, float eps, const float* x, float* y) {
+    const size_t dm = d->d_model, df = d->d_ff;
+    const size_t G = (size_t)props.multiProcessorCount;
+    if (!q4k_stack || q4k_generic || d->type_gate != HH_TYPE_Q4_K || d->type_up != HH_TYPE_Q4_K ||
+        d->type_down != HH_TYPE_Q4_K || dm % 256 || df % 256 || dm > 4096 || df > 16384 || dm < G || df / 8 < G ||
+        (dm + G - 1) / G > 16 ||
+        n_layers > 0x3FFFFFFFu || norm_stride > 0xFFFFFFFFu || (norm_stride & 3u) ||
+        (((uintptr_t)pack | d->gate_off | d->up_off | d->down_off | stride) & 15u) || ((uintptr_t)x & 15u) ||
+        ((uintptr_t)norm & 15u) || ((uintptr_t)y & 3u))
+        return HH_ERR_UNSUPPORTED_DEVICE;
+    const size_t wpt2 = df <= 8192 ? 2 : 4;
+    const size_t rb1 = (dm / 256) * 144, rb2 = (df / 256) * 144;
+    const size_t nrow_max = (dm + G - 1) / G;
+    const size_t lds_wd = (nrow_max * rb2 + 15) & ~(size_t)15;
+    // h digits (q1, q2, bf16 scales), or x's digits and x itself staged after them
+    const size_t lds_hx =
+        (std::max(2 * df + 2 * (df / 8), ((2 * dm + (dm / 32) * 8 + 15) & ~(size_t)15) + 4 * dm) + 15) & ~(size_t)15;
+    auto al4 = [](size_t n) { return (n + 3) & ~(size_t)3; };
+    const size_t tail = al4(16 * ((df / 8 + G - 1) / G)) + al4(nrow_max * wpt2) + al4(3) + al4(2 * nrow_max);
+    const size_t smem = lds_wd + lds_hx + 4 * tail;
+    if (smem + 16 > (size_t)props.sharedMemPerBlock) return HH_ERR_UNSUPPORTED_DEVICE;
+    // ring depth 3, at most 24 W_down copies of 1 KB in flight per CU
+    const std::string name = "hh_q4k_stk_d" + std::to_string(wpt2) + "_r3_t24";
+    hipFunction_t fn;
+    HH_TRY(kernel(name, &fn));
+    int per_cu = 0;
+    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 12 * 64, smem) != hipSuccess || per_cu < 1)
+        return HH_ERR_UNSUPPORTED_DEVICE;
+    // h words padded to whole gather passes (3 exchange waves x 64 lanes x 14 words), x words
+    // by one exchange wave's reach (64 lanes x 22 words) past d_model (q4k_stack.hip)
+    const size_t hpad = (3 * (df / 8) + 2687) / 2688 * 2688, xpad = dm + 64 * 22;
+    const size_t need = (hpad + xpad) * sizeof(uint64_t);
+    if (ws_qstk_cap < need) {
+        HH_TRY(grow(&ws_qstk, &ws_qstk_cap, need));
+        HH_TRY_HIP(hipMemset(ws_qstk, 0, ws_qstk_cap), "hipMemset(stack exchange)");
+    }
+    QstkArgs a{pack, norm, x, y, (uint64_t*)ws_qstk, (uint64_t*)ws_qstk + hpad, (unsigned*)grid_sync,
+               (uint64_t)stride, (uint64_t)d->gate_off, (uint64_t)d->up_off, (uint64_t)d->down_off, (uint64_t)rb1,
+               (uint64_t)rb2, (uint32_t)norm_stride, (uint32_t)dm, (uint32_t)df, (uint32_t)n_layers,
+               (uint32_t)lds_wd, (uint32_t)lds_hx, eps, d->act};
+    void* params[] = {&a};
+    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)G, 1, 1, 12 * 64, 1, 1, (unsigned)smem, stream, params, nullptr);
+    if (err != hipSuccess) return hip_fail(err, "launch(q4k ffn stack)");
+    return HH_OK;
+}
+
 hh_status hh_engine::enqueue_ffn_block_stack(const hh_ffn_desc* d, const uint8_t* pack, size_t stride,
                                              size_t n_layers, const float* norm, size_t norm_stride, float eps,
                                              const float* x, float* y) {
     if (n_layers == 0) return HH_OK;
-    const hh_status st = enqueue_small_stack(d, pack, stride, n_layers, norm, norm_stride, eps, x, y);
+    hh_status st = enqueue_small_stack(d, pack, stride, n_layers, norm, norm_stride, eps, x, y);
+    if (st == HH_ERR_UNSUPPORTED_DEVICE) st = enqueue_q4k_stack(d, pack, stride, n_layers, norm, norm_stride, eps, x, y);
     if (st == HH_OK) {
         ffn_stage_valid = false;
         ffn_calls += 3 * n_layers;
@@ -1848,6 +1921,7 @@ hh_status engine_create(int device, hh_engine** out) {
     if (const char* f = getenv("HAYAI_HIP_SMALL_FFN")) e->small_ffn = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_SMALL_STACK")) e->small_stack = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_STACK_GRID")) e->stack_grid = atoi(f);
+    if (const char* f = getenv("HAYAI_HIP_Q4K_STACK")) e->q4k_stack = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_MOE_GRING")) e->moe_gring = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_MOE_GRING_NS")) e->moe_gring_ns = atoi(f);
     if (const char* f = getenv("HAYAI_HIP_MMQ")) e->mmq = atoi(f) != 0;
@@ -1875,7 +1949,7 @@ void engine_destroy(hh_engine* e) {
     if (e->copy_stream) (void)hipStreamSynchronize(e->copy_stream);
     if (e->copy_stream2) (void)hipStreamSynchronize(e->copy_stream2);
     for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq, e->ws_xop, e->ws_hop, e->ws_part,
-                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->ws_xn, e->ws_f, e->ws_xq, e->ws_moe_yp, e->ws_moe_grp, e->ws_moe_q, e->ws_stk, e->grid_sync})
+                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->ws_xn, e->ws_f, e->ws_xq, e->ws_moe_yp, e->ws_moe_grp, e->ws_moe_q, e->ws_stk, e->ws_qstk, e->grid_sync})
         if (p) (void)hipFree(p);
     for (void* p : e->ws_retired) (void)hipFree(p);
     if (e->stream) (void)hipStreamDestroy(e->stream);

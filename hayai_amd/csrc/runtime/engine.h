@@ -146,6 +146,8 @@ struct hh_engine {
     size_t ws_moe_q_cap = 0;
     void* ws_stk = nullptr;     // FFN-stack exchange: tagged words of h (d_ff) then x (d_model); zeroed
     size_t ws_stk_cap = 0;      // when allocated and after a device error
+    void* ws_qstk = nullptr;    // Q4_K FFN-stack exchange: h granule words (3 d_ff / 8) then x (d_model);
+    size_t ws_qstk_cap = 0;     // zeroed when allocated and after a device error
     void* grid_sync = nullptr;  // grid-barrier state (counters, flags, error word, epochs)
     hh_ffn_desc ffn_stage{};    // FFN whose gate/up output is pending in ws_h (/ws_hq)
     bool ffn_stage_valid = false;
@@ -216,7 +218,10 @@ struct hh_engine {
                                       const float* norm, size_t norm_stride, float eps, const float* x, float* y);
     hh_status enqueue_small_stack(const hh_ffn_desc* d, const uint8_t* pack, size_t stride, size_t n_layers,
                                   const float* norm, size_t norm_stride, float eps, const float* x, float* y);
+    hh_status enqueue_q4k_stack(const hh_ffn_desc* d, const uint8_t* pack, size_t stride, size_t n_layers,
+                                const float* norm, size_t norm_stride, float eps, const float* x, float* y);
     bool small_stack = true;  // HAYAI_HIP_SMALL_STACK=0: FFN stacks as one block per layer
+    bool q4k_stack = false;   // HAYAI_HIP_Q4K_STACK=1: all-Q4_K FFN stacks in one persistent launch
     int stack_grid = 0;       // HAYAI_HIP_STACK_GRID: workgroups of the persistent stack (0: one per CU)
     bool moe_gring = false;   // HAYAI_HIP_MOE_GRING=1: several-token MoE on the ring-form kernels (slower today)
     int moe_gring_ns = 0;     // HAYAI_HIP_MOE_GRING_NS: pairs staged per pass (0: as many as LDS holds)

@@ -265,7 +265,9 @@ hh_status hh_ffn_block_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pac
  * callers that run FFN blocks with no other op between them (FFN-only layer stacks, the
  * chained-layer benchmark): small all-Q4_0 / all-Q8_0 layers (d_model, d_ff <= 2048) run
  * every layer in one persistent launch that requests each layer's weights ahead of the
- * activation exchanges; other layouts run hh_ffn_block_dev per layer.  Results match
+ * activation exchanges; all-Q4_K layers (d_model <= 4096, d_ff <= 16384) do so when the
+ * engine was created with HAYAI_HIP_Q4K_STACK=1; other layouts run hh_ffn_block_dev per
+ * layer.  Results match
  * hh_ffn_block_dev applied layer by layer to f32 rounding (sums in another order).
  * HH_ERR_INVALID for n_layers 0 or ranges outside the buffers.  Enqueue only. */
 hh_status hh_ffn_block_stack_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
