@@ -5,7 +5,7 @@
 // w[t][s] * down_e(act(gate_e x_t) * up_e x_t), e = ids[t][s]):
 //   hh_moe_prep:         (token, slot) pairs p = t * k + s grouped by expert, in p order
 //                        within an expert, the active experts in ascending order; and every
-//                        token's x as int8 digits
+//                        token's x as int8 digits (hh_moe_route_prep: the routing too)
 //   hh_moe_gu_grp_t<TM>: grid.y = active expert; every row of gate and up is read once and
 //                        dotted with each of the expert's tokens: h[p][row] = act(g) * u
 //   hh_moe_hdigits:      h as digits, by pair
@@ -62,39 +62,89 @@ HH_DEV int hh_moeg_valid(const hh_moeg_args& a, int e) { return (e < 0 || (uint3
 
 // Workgroup 0 groups the pairs; workgroup 1 + t turns token t's x into digits (global, read
 // by every expert's gate/up workgroups from L2).  Grouping: pair p's position is its expert's
-// start plus the number of earlier pairs with the same expert; an expert's start is the sum
-// of the counts of the experts before it; all sums are over LDS copies, one thread per pair or
-// expert, so the order is deterministic.
-extern "C" __global__ void __launch_bounds__(256) hh_moe_prep(const hh_moeg_args a) {
+// start plus the number of earlier pairs with the same expert (its rank); an expert's start
+// is the sum of the counts of the experts before it.  The starts (and the list of active
+// experts) come from one exclusive scan over the counts; a rank is a few popcounts of the
+// expert's bitmask of pairs (built with atomicOr: order-free), or, when the masks would not
+// fit LDS, a count over the earlier pairs.  Every result is a pure function of ids.
+#define HH_MOEG_MASK_WORDS 4096  // LDS words for the per-expert pair bitmasks
+
+// Exclusive scan over the workgroup of (a, b) pairs, one pair per thread (256 threads):
+// returns the sums of the pairs of lower threads; *ta, *tb get the totals.
+HH_DEV int2 hh_moeg_scan256(int a, int b, int* ta, int* tb) {
+    __shared__ int ws[2][4];
+    const uint32_t tid = threadIdx.x, lane = tid % 64, w = tid / 64;
+    int ia = a, ib = b;  // inclusive scan within the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int xa = __shfl_up(ia, d, 64), xb = __shfl_up(ib, d, 64);
+        if ((int)lane >= d) {
+            ia += xa;
+            ib += xb;
+        }
+    }
+    if (lane == 63) {
+        ws[0][w] = ia;
+        ws[1][w] = ib;
+    }
+    __syncthreads();
+    int oa = 0, ob = 0, sa = 0, sb = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < 4; k++) {
+        if (k < w) {
+            oa += ws[0][k];
+            ob += ws[1][k];
+        }
+        sa += ws[0][k];
+        sb += ws[1][k];
+    }
+    *ta = sa;
+    *tb = sb;
+    return make_int2(oa + ia - a, ob + ib - b);
+}
+
+// The grouping, by one workgroup of 256 threads.
+HH_DEV void hh_moeg_group(const hh_moeg_args& a) {
     __shared__ int cnt[HH_MOEG_MAX_E];
     __shared__ int first[HH_MOEG_MAX_E];
     __shared__ int pid[HH_MOEG_MAX_P];
+    __shared__ uint32_t mask[HH_MOEG_MASK_WORDS];
     const uint32_t tid = threadIdx.x;
-    if (blockIdx.x > 0) {
-        const uint32_t t = blockIdx.x - 1;
-        hh_quantize_digits(a.x + (size_t)t * a.d_model, a.d_model,
-                           hh_moe_digits((char*)a.xq + t * hh_digits_bytes_dev(a.d_model), a.d_model));
-        return;
-    }
     const uint32_t E = a.n_experts, P = a.T * a.k;
+    const uint32_t PW = (P + 31) / 32;                     // mask words per expert
+    const bool masks = (size_t)E * PW <= HH_MOEG_MASK_WORDS;  // else: count earlier pairs
     for (uint32_t e = tid; e < E; e += 256) cnt[e] = 0;
+    if (masks)
+        for (uint32_t i = tid; i < E * PW; i += 256) mask[i] = 0u;
     for (uint32_t p = tid; p < P; p += 256) pid[p] = hh_moeg_valid(a, a.ids[p]);
     __syncthreads();
-    for (uint32_t p = tid; p < P; p += 256)
-        if (pid[p] >= 0) atomicAdd(&cnt[pid[p]], 1);  // counts only: order-free
+    for (uint32_t p = tid; p < P; p += 256) {
+        const int e = pid[p];
+        if (e < 0) continue;
+        atomicAdd(&cnt[e], 1);  // counts and masks only: order-free
+        if (masks) atomicOr(&mask[(uint32_t)e * PW + p / 32], 1u << (p % 32));
+    }
     __syncthreads();
-    for (uint32_t e = tid; e < E; e += 256) {
-        int s = 0, na = 0;
-        for (uint32_t f = 0; f < e; f++) {
-            s += cnt[f];
-            na += cnt[f] > 0;
+    // starts and active-expert positions: each thread owns experts 2 tid and 2 tid + 1
+    // (E <= HH_MOEG_MAX_E = 512)
+    {
+        const uint32_t e0 = 2 * tid, e1 = e0 + 1;
+        const int c0 = e0 < E ? cnt[e0] : 0, c1 = e1 < E ? cnt[e1] : 0;
+        int tot, tot_a;
+        const int2 ex = hh_moeg_scan256(c0 + c1, (c0 > 0) + (c1 > 0), &tot, &tot_a);
+        if (e0 < E) {
+            first[e0] = ex.x;
+            a.estart[e0] = ex.x;
+            if (c0) a.elist[ex.y] = (int)e0;
         }
-        first[e] = s;
-        a.estart[e] = s;
-        if (cnt[e]) a.elist[na] = (int)e;
-        if (e == E - 1) {
-            a.estart[E] = s + cnt[e];
-            a.elist[E] = na + (cnt[e] > 0);
+        if (e1 < E) {
+            first[e1] = ex.x + c0;
+            a.estart[e1] = ex.x + c0;
+            if (c1) a.elist[ex.y + (c0 > 0)] = (int)e1;
+        }
+        if (tid == 0) {
+            a.estart[E] = tot;
+            a.elist[E] = tot_a;
         }
     }
     __syncthreads();
@@ -102,9 +152,69 @@ extern "C" __global__ void __launch_bounds__(256) hh_moe_prep(const hh_moeg_args
         const int e = pid[p];
         if (e < 0) continue;
         int r = 0;
-        for (uint32_t q = 0; q < p; q++) r += pid[q] == e;
+        if (masks) {
+            const uint32_t* m = mask + (uint32_t)e * PW;
+            for (uint32_t wi = 0; wi < p / 32; wi++) r += __popc(m[wi]);
+            r += __popc(m[p / 32] & ((1u << (p % 32)) - 1u));
+        } else {
+            for (uint32_t q = 0; q < p; q++) r += pid[q] == e;
+        }
         a.order[first[e] + r] = (int)p;
     }
+}
+
+// Token t's x -> digits (global, read by every expert's gate/up workgroups from L2).
+HH_DEV void hh_moeg_x_digits(const hh_moeg_args& a, uint32_t t) {
+    hh_quantize_digits(a.x + (size_t)t * a.d_model, a.d_model,
+                       hh_moe_digits((char*)a.xq + t * hh_digits_bytes_dev(a.d_model), a.d_model));
+}
+
+extern "C" __global__ void __launch_bounds__(256) hh_moe_prep(const hh_moeg_args a) {
+    if (blockIdx.x > 0) {
+        hh_moeg_x_digits(a, blockIdx.x - 1);
+        return;
+    }
+    hh_moeg_group(a);
+}
+
+// Routing and hh_moe_prep in one launch: workgroups 0 .. R-1 route four tokens each (one per
+// wave, as hh_moe_route), workgroups R .. R+T-1 turn token t's x into digits.  A routing
+// workgroup publishes its ids (device-scope fence) and counts itself on a device counter;
+// the last one to arrive fences again, groups every pair (hh_moeg_group) and resets the
+// counter for the next launch.  No workgroup waits for another, so the launch needs no
+// co-residency and is captured into graphs as it is.
+struct hh_moeg_rp_args {
+    hh_route_args r;
+    hh_moeg_args g;
+    unsigned* arrivals;  // one word, 0 between launches
+};
+extern "C" __global__ void __launch_bounds__(HH_MOE_BLOCK) hh_moe_route_prep(const hh_moeg_rp_args a) {
+    const uint32_t R = (a.r.T + HH_MOE_BLOCK / HH_WAVE - 1) / (HH_MOE_BLOCK / HH_WAVE);
+    if (blockIdx.x >= R) {
+        hh_moeg_x_digits(a.g, blockIdx.x - R);
+        return;
+    }
+    {
+        __shared__ __attribute__((aligned(16))) hh_route_lds lds[HH_MOE_BLOCK / HH_WAVE];
+        const uint32_t lane = threadIdx.x % HH_WAVE, w = threadIdx.x / HH_WAVE;
+        const uint32_t t = blockIdx.x * (HH_MOE_BLOCK / HH_WAVE) + w;
+        int id;
+        float wv;
+        const uint32_t kk = hh_route_token(a.r, t, t < a.r.T, lds[w], &id, &wv);
+        if (t < a.r.T && lane < a.r.k_out) {
+            a.r.ids[(size_t)t * a.r.k_out + lane] = lane < kk ? id : -1;
+            a.r.wts[(size_t)t * a.r.k_out + lane] = lane < kk ? wv : 0.f;
+        }
+    }
+    __shared__ int last;
+    __threadfence();  // this workgroup's ids are visible device-wide before it counts itself
+    __syncthreads();
+    if (threadIdx.x == 0) last = atomicAdd(a.arrivals, 1u) == R - 1u;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();  // every workgroup's ids are visible to this one
+    hh_moeg_group(a.g);
+    if (threadIdx.x == 0) __hip_atomic_store(a.arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // h (f32, by pair) -> digits, one workgroup per pair.

@@ -387,6 +387,8 @@ constexpr size_t kBarLine = 128;
 constexpr size_t kBarBytes = kBarLine * (2 * 16 + 4);
 constexpr size_t kBarEpochOffset = kBarLine * (2 * 16 + 2);  // the epochs survive an error reset
 constexpr size_t kBarErrOffset = kBarLine * (2 * 16 + 1);
+// the grouped MoE's routing-arrival counter (hh_moe_route_prep): word 4 of the last line
+constexpr size_t kBarMoeArrivalsOffset = kBarLine * (2 * 16 + 3) + 4 * 4;
 
 hh_status hh_engine::enqueue_q4k_ffn(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
                                      const float* x, float* y) {
@@ -1685,7 +1687,6 @@ hh_status hh_engine::enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* expert
     const size_t P = T * k, E = d->n_experts;
     if (moe_grouped && P <= 4096 && E <= 512 && dm / 64 <= 64 && df / 64 <= 64 &&
         ((d->expert_stride | d->gate_off | d->up_off | d->down_off | (uintptr_t)experts | (uintptr_t)x) & 15u) == 0) {
-        if (logits) HH_TRY(enqueue_moe_route(d, logits, bias, T, ids, wts));
         HH_TRY(grow(&ws_moe_yp, &ws_moe_yp_cap, P * dm * sizeof(float)));
         HH_TRY(grow(&ws_moe_grp, &ws_moe_grp_cap, (P + 2 * (E + 1)) * sizeof(int32_t)));
         const size_t xqb = hh_digits_bytes(dm), hqb = hh_digits_bytes(df);
@@ -1706,8 +1707,24 @@ hh_status hh_engine::enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* expert
             (int32_t*)ws_moe_grp + P + E + 1, (uint8_t*)ws_moe_q, (uint8_t*)ws_moe_q + T * xqb, (uint32_t)T,
             (uint32_t)k, (uint32_t)dm, (uint32_t)df, (uint32_t)E, d->act};
         hipFunction_t fn;
-        HH_TRY(kernel("hh_moe_prep", &fn));
-        HH_TRY(launch(fn, (uint32_t)(1 + T), 256, g));
+        if (logits) {
+            // routing, grouping and x's digits in one launch (hh_moe_route_prep): the last
+            // routing workgroup to finish groups the pairs; its arrival counter is a word of
+            // the grid-barrier state that every launch leaves at zero
+            struct {
+                hh_route_args r;
+                decltype(g) m;
+                unsigned* arrivals;
+            } rp{route_args(d, logits, bias, T, ids, wts), g, (unsigned*)((char*)grid_sync + kBarMoeArrivalsOffset)};
+            HH_TRY(kernel("hh_moe_route_prep", &fn));
+            void* rpp[] = {&rp};
+            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)((T + 3) / 4 + T), 1, 1, kMoeBlock, 1, 1, 0, stream, rpp,
+                                             nullptr),
+                       "launch(moe route + prep)");
+        } else {
+            HH_TRY(kernel("hh_moe_prep", &fn));
+            HH_TRY(launch(fn, (uint32_t)(1 + T), 256, g));
+        }
         // The ring form (moe_gring.hip, opt-in): one workgroup per CU streams its share of the
         // selected experts' concatenated rows; the gate/up kernel writes the intermediate's digits.
         // Its per-(row, pair) dot and reduction chains leave it slower than the per-expert
@@ -1854,7 +1871,7 @@ static std::vector<std::string> required_kernels() {
         for (int t1 : {16, 32, 64})
             for (int t2 : {16, 32, 64})
                 k.push_back(std::string("hh_sffn_") + fmt + "_t" + std::to_string(t1) + "_" + std::to_string(t2));
-    for (const char* f : {"hh_moe_prep", "hh_moe_hdigits", "hh_moe_combine", "hh_moe_gu_grp_t16", "hh_moe_gu_grp_t32", "hh_moe_gu_grp_t64",
+    for (const char* f : {"hh_moe_prep", "hh_moe_route_prep", "hh_moe_hdigits", "hh_moe_combine", "hh_moe_gu_grp_t16", "hh_moe_gu_grp_t32", "hh_moe_gu_grp_t64",
                           "hh_moe_dn_grp_t16", "hh_moe_dn_grp_t32", "hh_moe_dn_grp_t64"})
         k.push_back(f);
     k.push_back("hh_rmsnorm_kernel");
