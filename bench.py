@@ -908,6 +908,9 @@ def bench_block(eng, pack, lay, stride, desc, args) -> int:
         for l in range(LAYERS):
             eng.ffn_dev(desc, pack, l * stride, xs, 4 * D_MODEL * l, ys, 4 * D_MODEL * l)
 
+    def stack_step():  # the same chain as one hh_ffn_block_stack_dev call
+        eng.ffn_block_stack_dev(desc, pack, 0, stride, LAYERS, norms, 0, D_MODEL, 1e-5, xres, 0, xres, 0)
+
     def timed(run, n):
         e0, e1 = eng.event(), eng.event()
         e0.record()
@@ -921,14 +924,28 @@ def bench_block(eng, pack, lay, stride, desc, args) -> int:
         xres.write(x0)
         block_step()
         ffn_step()
+        stack_step()
     eng.sync()
+    xres.write(x0)
+    block_step()
+    eng.sync()
+    y_block = xres.read(np.float32, D_MODEL)
+    xres.write(x0)
+    stack_step()
+    eng.sync()
+    y_stack = xres.read(np.float32, D_MODEL)
+    stack_diff = float(np.max(np.abs(y_stack - y_block)) / max(float(np.max(np.abs(y_block - x0))), 1e-30))
     xres.write(x0)
     ms_block = timed(block_step, args.steps)
     ms_ffn = timed(ffn_step, args.steps)
+    ms_stack = timed(stack_step, args.steps)
     bytes_step = LAYERS * (layer_bytes() + 4 * D_MODEL)  # + the norm weights
     gbs = bytes_step / (ms_block / 1e3) / 1e9
+    persistent = os.environ.get("HAYAI_HIP_Q4K_STACK", "0") not in ("", "0")
     log(f"[bench] block: {ms_block * 1e3:.1f} us/step ({ms_block * 1e3 / LAYERS:.2f} us/layer), {gbs:.1f} GB/s; "
-        f"plain FFN op {ms_ffn * 1e3 / LAYERS:.2f} us/layer")
+        f"plain FFN op {ms_ffn * 1e3 / LAYERS:.2f} us/layer; one stack call "
+        f"({'persistent Q4_K stack' if persistent else 'blocks per layer'}) {ms_stack * 1e3 / LAYERS:.2f} us/layer, "
+        f"max diff vs the blocks {stack_diff:.2e} of max|FFN part|")
     cpu = None
     if not args.no_cpu_baseline:
         import oracle
@@ -957,6 +974,8 @@ def bench_block(eng, pack, lay, stride, desc, args) -> int:
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "us_per_layer": round(ms_block * 1e3 / LAYERS, 3),
         "plain_ffn_us_per_layer": round(ms_ffn * 1e3 / LAYERS, 3),
+        "stack_call": {"us_per_layer": round(ms_stack * 1e3 / LAYERS, 3), "persistent_q4k_stack": persistent,
+                       "max_rel_diff_vs_blocks": stack_diff},
         "roofline": roofline_step(gbs, "ring gate/up with the RMSNorm prologue + ring down with the residual epilogue"),
         "cpu_baseline": cpu,
     }
@@ -1239,6 +1258,9 @@ def main() -> int:
                     help="--workload ffn / gemv weight format")
     ap.add_argument("--shape", default="8b", choices=["8b", "70b", "smollm"], help="--workload ffn shape")
     ap.add_argument("--layers", type=int, default=0, help="--workload ffn: layers (0: the shape's own count)")
+    ap.add_argument("--q4k-stack", action="store_true",
+                    help="--workload block: run the chain's one-call form on the persistent Q4_K stack "
+                         "(HAYAI_HIP_Q4K_STACK=1, set before the engine is created)")
     ap.add_argument("--m", type=int, default=4096, help="--workload gemv rows")
     ap.add_argument("--n", type=int, default=4096, help="--workload gemv columns")
     args = ap.parse_args()
@@ -1247,6 +1269,8 @@ def main() -> int:
               "d_ff across GPUs with one d_model all-reduce per layer, which is not built here.", file=sys.stderr)
         return 2
 
+    if args.q4k_stack:
+        os.environ["HAYAI_HIP_Q4K_STACK"] = "1"
     import hayai_amd
     from hayai_amd import synth
 
