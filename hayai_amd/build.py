@@ -35,6 +35,9 @@ KERNEL_FLAGS = [
     "-ffp-contract=off",
     # packed FP32 (v_pk_*_f32) stays off on this platform
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # kernel-argument preload: the first 16 dwords of a kernel's scalar parameters arrive in
+    # SGPRs (kernels taking a struct by value keep the scalar load)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

@@ -384,15 +384,15 @@ struct hh_ring_iq3 {
 #define HH_IQ_WDN_DEPTH 2  // the down kernels' 9-wave workgroups leave 168 VGPRs per lane
 #endif
 #define HH_IQ_GU(NAME, F, W1, D)                                                                               \
-    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) NAME##_gu_ring_g##W1(const hh_gur_args a) {   \
-        hh_gu_ring_body<F, W1, D, 2, false>(a);                                                               \
+    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) NAME##_gu_ring_g##W1(HH_GUR_PARAMS) {       \
+        hh_gu_ring_body<F, W1, D, 2, false>(HH_GUR_ARGS);                                                     \
     }                                                                                                          \
-    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) NAME##_gu_ring_g##W1##_n(const hh_gur_args a) { \
-        hh_gu_ring_body<F, W1, D, 2, true>(a);                                                                \
+    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) NAME##_gu_ring_g##W1##_n(HH_GUR_PARAMS) {   \
+        hh_gu_ring_body<F, W1, D, 2, true>(HH_GUR_ARGS);                                                      \
     }
 #define HH_IQ_DN(NAME, F, W2, D)                                                                               \
-    extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) NAME##_dn_ring_d##W2(const hh_dnr_args a) {     \
-        hh_dn_ring_body<F, W2, D>(a);                                                                         \
+    extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) NAME##_dn_ring_d##W2(HH_DNR_PARAMS) {         \
+        hh_dn_ring_body<F, W2, D>(HH_DNR_ARGS);                                                               \
     }
 HH_IQ_GU(hh_iq2, hh_ring_iq2<2>, 1, HH_IQ_GU_DEPTH)
 HH_IQ_GU(hh_iq2, hh_ring_iq2<2>, 2, HH_IQ_GU_DEPTH)

@@ -454,17 +454,30 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
 #define HH_Q4K_DN_RING_D 3
 #endif
 
+// The ring kernels (Q4_K here, Q6_K and IQ in their files) take hh_gur_args' / hh_dnr_args'
+// fields as separate scalar parameters (the same kernel-argument layout; the host passes the
+// struct's bytes), so the code object's kernel-argument preload (build flag) puts the leading
+// dwords in SGPRs before the waves start instead of a scalar load at the head of every wave
+// (the down kernel 9.65 -> 9.3 us per 8B layer).
+#define HH_GUR_PARAMS                                                                            \
+    const uint8_t *wg, const uint8_t *wu, const float *x, uint8_t *hx, const float *nw, uint64_t rb1, \
+        uint32_t d_model, uint32_t d_ff, int32_t act, float eps
+#define HH_GUR_ARGS hh_gur_args{wg, wu, x, hx, nw, rb1, d_model, d_ff, act, eps}
+#define HH_DNR_PARAMS \
+    const uint8_t *wd, const uint8_t *hx, float *y, const float *res, uint64_t rb2, uint32_t d_model, uint32_t d_ff
+#define HH_DNR_ARGS hh_dnr_args{wd, hx, y, res, rb2, d_model, d_ff}
+
 // _n: with the RMSNorm prologue (the FFN residual block)
 #define HH_GU_RING(G1)                                                                          \
-    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_q4k_gu_ring_g##G1(const hh_gur_args a) { \
-        hh_gu_ring_body<hh_ring_q4k, G1, HH_Q4K_GU_RING_D, 1, false>(a);                        \
+    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_q4k_gu_ring_g##G1(HH_GUR_PARAMS) { \
+        hh_gu_ring_body<hh_ring_q4k, G1, HH_Q4K_GU_RING_D, 1, false>(HH_GUR_ARGS);              \
     }                                                                                           \
-    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_q4k_gu_ring_g##G1##_n(const hh_gur_args a) { \
-        hh_gu_ring_body<hh_ring_q4k, G1, HH_Q4K_GU_RING_D, 1, true>(a);                         \
+    extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_q4k_gu_ring_g##G1##_n(HH_GUR_PARAMS) { \
+        hh_gu_ring_body<hh_ring_q4k, G1, HH_Q4K_GU_RING_D, 1, true>(HH_GUR_ARGS);               \
     }
 #define HH_DN_RING(G2)                                                                          \
-    extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) hh_q4k_dn_ring_d##G2(const hh_dnr_args a) { \
-        hh_dn_ring_body<hh_ring_q4k, G2, HH_Q4K_DN_RING_D>(a);                                  \
+    extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) hh_q4k_dn_ring_d##G2(HH_DNR_PARAMS) { \
+        hh_dn_ring_body<hh_ring_q4k, G2, HH_Q4K_DN_RING_D>(HH_DNR_ARGS);                        \
     }
 HH_GU_RING(1)
 HH_GU_RING(2)

@@ -161,8 +161,8 @@ struct hh_ring_q6k {
 // Two rows in flight per wave: deeper rings measured slower here (8B down, 4096 x 14336:
 // 14.2 us at D = 2, 14.8 at 3, 15.8 at 4, 17.3 at 5).
 #define HH_Q6K_DN_RING(W2)                                                                              \
-    extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) hh_q6k_dn_ring_d##W2(const hh_dnr_args a) { \
-        hh_dn_ring_body<hh_ring_q6k, W2, 2>(a);                                                         \
+    extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) hh_q6k_dn_ring_d##W2(HH_DNR_PARAMS) {     \
+        hh_dn_ring_body<hh_ring_q6k, W2, 2>(HH_DNR_ARGS);                                               \
     }
 HH_Q6K_DN_RING(1)
 HH_Q6K_DN_RING(2)

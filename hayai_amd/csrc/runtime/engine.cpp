@@ -620,8 +620,11 @@ hh_status hh_engine::enqueue_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, co
         hx = (uint8_t*)ws_hq;
     }
     GurArgs a{wg, wu, x, hx, norm, (uint64_t)((dm / 256) * f->block_bytes), (uint32_t)dm, (uint32_t)df, d->act, eps};
-    void* params[] = {&a};
-    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
+    // the argument block as raw kernel-argument bytes: the Q4_K kernels take its fields as
+    // separate scalar parameters (same layout), so their leading dwords can be preloaded
+    size_t asz = sizeof a;
+    void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &a, HIP_LAUNCH_PARAM_BUFFER_SIZE, &asz, HIP_LAUNCH_PARAM_END};
+    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, nullptr, cfg);
     if (err != hipSuccess) return hip_fail(err, "launch(ring gate/up)");
     return HH_OK;
 }
@@ -662,8 +665,9 @@ hh_status hh_engine::launch_dn_ring(int type, size_t m, size_t n, const uint8_t*
     const size_t rows_max = (m + grid - 1) / grid;
     const size_t smem = hb + rows_max * per_row;
     DnrArgs a{w, hx, y, res, (uint64_t)((n / 256) * f->block_bytes), (uint32_t)m, (uint32_t)n};
-    void* params[] = {&a};
-    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
+    size_t asz = sizeof a;  // raw argument bytes, as for the gate/up kernel
+    void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &a, HIP_LAUNCH_PARAM_BUFFER_SIZE, &asz, HIP_LAUNCH_PARAM_END};
+    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, nullptr, cfg);
     if (err != hipSuccess) return hip_fail(err, "launch(ring down)");
     return HH_OK;
 }

@@ -113,11 +113,14 @@ int main(int argc, char** argv) {
         for (int l = 0; l < L; l++) {
             const uint8_t* base = w + (size_t)l * stride;
             GurArgs ga{base, base + gsz, x, hx, nw + (size_t)l * dm, rb1, (uint32_t)dm, (uint32_t)df, 0, 1e-5f};
-            void* p1[] = {&ga};
-            CK(hipModuleLaunchKernel(fgu, (unsigned)cus, 1, 1, 512, 1, 1, (unsigned)smem_gu, 0, p1, nullptr));
+            // the kernels take the blocks' fields as scalar parameters: pass the raw bytes
+            size_t gsz = sizeof ga;
+            void* c1[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ga, HIP_LAUNCH_PARAM_BUFFER_SIZE, &gsz, HIP_LAUNCH_PARAM_END};
+            CK(hipModuleLaunchKernel(fgu, (unsigned)cus, 1, 1, 512, 1, 1, (unsigned)smem_gu, 0, nullptr, c1));
             DnrArgs da{base + 2 * gsz, hx, x, x, rb2, (uint32_t)dm, (uint32_t)df};
-            void* p2[] = {&da};
-            CK(hipModuleLaunchKernel(fdn, (unsigned)cus, 1, 1, 576, 1, 1, (unsigned)smem_dn, 0, p2, nullptr));
+            size_t dsz = sizeof da;
+            void* c2[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &da, HIP_LAUNCH_PARAM_BUFFER_SIZE, &dsz, HIP_LAUNCH_PARAM_END};
+            CK(hipModuleLaunchKernel(fdn, (unsigned)cus, 1, 1, 576, 1, 1, (unsigned)smem_dn, 0, nullptr, c2));
         }
         if (s == steps - 1) CK(hipEventRecord(e1, 0));
     }
