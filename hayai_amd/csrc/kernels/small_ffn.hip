@@ -23,6 +23,8 @@ struct hh_sffn_args {
     int32_t act;
 };
 
+// The kernels take these fields as scalar parameters (the same kernel-argument layout, the
+// host passes the struct's bytes), so the leading dwords arrive preloaded in SGPRs.
 template <class Q, int TEAM1, int TEAM2>
 HH_DEV void hh_sffn_body(const hh_sffn_args& a) {
     __shared__ int s_good;
@@ -81,8 +83,10 @@ HH_DEV void hh_sffn_body(const hh_sffn_args& a) {
 }
 
 #define HH_SFFN(NAME, Q, T1, T2)                                                                        \
-    extern "C" __global__ void __launch_bounds__(256) hh_sffn_##NAME##_t##T1##_##T2(const hh_sffn_args a) { \
-        hh_sffn_body<Q, T1, T2>(a);                                                                     \
+    extern "C" __global__ void __launch_bounds__(256) hh_sffn_##NAME##_t##T1##_##T2(                   \
+        const uint8_t* wg, const uint8_t* wu, const uint8_t* wd, const float* x, float* y, float* h,     \
+        unsigned* bar, uint64_t rb_in, uint64_t rb_ff, uint32_t d_model, uint32_t d_ff, int32_t act) {   \
+        hh_sffn_body<Q, T1, T2>(hh_sffn_args{wg, wu, wd, x, y, h, bar, rb_in, rb_ff, d_model, d_ff, act}); \
     }
 #define HH_SFFN_TEAMS(NAME, Q)  \
     HH_SFFN(NAME, Q, 16, 16)    \

@@ -3,6 +3,7 @@
 #include "engine.h"
 
 #include <algorithm>
+#include <cstddef>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -889,8 +890,10 @@ hh_status hh_engine::enqueue_small_ffn(const hh_ffn_desc* d, const uint8_t* wg, 
     HH_TRY(row_bytes(d->type_down, df, &rff));
     SffnArgs a{wg, wu, wd, x, y, (float*)ws_h, (unsigned*)grid_sync, (uint64_t)rin, (uint64_t)rff, (uint32_t)dm,
                (uint32_t)df, d->act};
-    void* params[] = {&a};
-    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)G, 1, 1, 256, 1, 1, 0, stream, params, nullptr);
+    // raw argument bytes (the kernel takes the fields as scalar parameters): up to act
+    size_t asz = offsetof(SffnArgs, act) + sizeof a.act;
+    void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &a, HIP_LAUNCH_PARAM_BUFFER_SIZE, &asz, HIP_LAUNCH_PARAM_END};
+    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)G, 1, 1, 256, 1, 1, 0, stream, nullptr, cfg);
     if (err != hipSuccess) return hip_fail(err, "launch(small ffn)");
     return HH_OK;
 }
