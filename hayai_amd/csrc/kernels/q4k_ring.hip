@@ -77,6 +77,7 @@ struct hh_gur_args {
     uint32_t d_ff;
     int32_t act;
     float eps;          // RMSNorm epsilon (with nw)
+    uint32_t grid;      // workgroups of the launch
 };
 
 struct hh_dnr_args {
@@ -140,7 +141,7 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % HH_WAVE;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / HH_WAVE);
-    const uint32_t G = gridDim.x, w = blockIdx.x;
+    const uint32_t G = a.grid, w = blockIdx.x;
     const uint32_t dm = a.d_model, dff = a.d_ff;
     const uint32_t NG = dff / 8;
     const uint32_t r0 = 8u * (uint32_t)(((uint64_t)w * NG) / G);
@@ -459,10 +460,13 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
 // struct's bytes), so the code object's kernel-argument preload (build flag) puts the leading
 // dwords in SGPRs before the waves start instead of a scalar load at the head of every wave
 // (the down kernel 9.65 -> 9.3 us per 8B layer).
-#define HH_GUR_PARAMS                                                                            \
-    const uint8_t *wg, const uint8_t *wu, const float *x, uint8_t *hx, const float *nw, uint64_t rb1, \
-        uint32_t d_model, uint32_t d_ff, int32_t act, float eps
-#define HH_GUR_ARGS hh_gur_args{wg, wu, x, hx, nw, rb1, d_model, d_ff, act, eps}
+// Gate/up packs what its first addresses need into the 14 dwords the preload can hold: five
+// pointers, the row bytes, d_model | d_ff << 16 and the grid size (in place of the dispatch's
+// own count, which would sit past them); act and eps follow.
+#define HH_GUR_PARAMS                                                                             \
+    const uint8_t *wg, const uint8_t *wu, const float *x, uint8_t *hx, const float *nw, uint32_t rb1, \
+        uint32_t dims, uint32_t grid, int32_t act, float eps
+#define HH_GUR_ARGS hh_gur_args{wg, wu, x, hx, nw, rb1, dims & 0xFFFFu, dims >> 16, act, eps, grid}
 #define HH_DNR_PARAMS \
     const uint8_t *wd, const uint8_t *hx, float *y, const float *res, uint64_t rb2, uint32_t d_model, uint32_t d_ff
 #define HH_DNR_ARGS hh_dnr_args{wd, hx, y, res, rb2, d_model, d_ff}

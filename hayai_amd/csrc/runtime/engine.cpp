@@ -510,14 +510,15 @@ hh_status hh_engine::enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, c
 }
 
 // Must match struct hh_gur_args / hh_dnr_args in kernels/q4k_ring.hip.
-struct GurArgs {
+struct GurArgs {  // the ring gate/up kernels' scalar parameters (HH_GUR_PARAMS, q4k_ring.hip)
     const uint8_t* wg;
     const uint8_t* wu;
     const float* x;
     uint8_t* hx;
     const float* nw;
-    uint64_t rb1;
-    uint32_t d_model, d_ff;
+    uint32_t rb1;
+    uint32_t dims;  // d_model | d_ff << 16
+    uint32_t grid;
     int32_t act;
     float eps;
 };
@@ -620,7 +621,8 @@ hh_status hh_engine::enqueue_ring_gu(const hh_ffn_desc* d, const uint8_t* wg, co
         HH_TRY(grow(&ws_hq, &ws_hq_cap, hh::ring_digits_bytes(df)));
         hx = (uint8_t*)ws_hq;
     }
-    GurArgs a{wg, wu, x, hx, norm, (uint64_t)((dm / 256) * f->block_bytes), (uint32_t)dm, (uint32_t)df, d->act, eps};
+    GurArgs a{wg, wu, x, hx, norm, (uint32_t)((dm / 256) * f->block_bytes), (uint32_t)(dm | (df << 16)), (uint32_t)grid,
+              d->act, eps};
     // the argument block as raw kernel-argument bytes: the Q4_K kernels take its fields as
     // separate scalar parameters (same layout), so their leading dwords can be preloaded
     size_t asz = sizeof a;

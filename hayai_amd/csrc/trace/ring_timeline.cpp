@@ -27,13 +27,14 @@
     } while (0)
 
 // kernels/q4k_ring.hip: struct hh_gur_args, struct hh_dnr_args
-struct GurArgs {
+struct GurArgs {  // the gate/up kernel's scalar parameters
     const uint8_t *wg, *wu;
     const float* x;
     uint8_t* hx;
     const float* nw;
-    uint64_t rb1;
-    uint32_t d_model, d_ff;
+    uint32_t rb1;
+    uint32_t dims;  // d_model | d_ff << 16
+    uint32_t grid;
     int32_t act;
     float eps;
 };
@@ -112,7 +113,8 @@ int main(int argc, char** argv) {
         if (s == steps - 1) CK(hipEventRecord(e0, 0));
         for (int l = 0; l < L; l++) {
             const uint8_t* base = w + (size_t)l * stride;
-            GurArgs ga{base, base + gsz, x, hx, nw + (size_t)l * dm, rb1, (uint32_t)dm, (uint32_t)df, 0, 1e-5f};
+            GurArgs ga{base, base + gsz, x, hx, nw + (size_t)l * dm, (uint32_t)rb1, (uint32_t)(dm | (df << 16)), (uint32_t)cus, 0,
+                       1e-5f};
             // the kernels take the blocks' fields as scalar parameters: pass the raw bytes
             size_t gsz = sizeof ga;
             void* c1[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ga, HIP_LAUNCH_PARAM_BUFFER_SIZE, &gsz, HIP_LAUNCH_PARAM_END};
