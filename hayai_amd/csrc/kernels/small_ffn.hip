@@ -21,15 +21,18 @@ struct hh_sffn_args {
     uint64_t rb_ff;
     uint32_t d_model, d_ff;
     int32_t act;
+    uint32_t grid;   // workgroups of the launch
 };
 
-// The kernels take these fields as scalar parameters (the same kernel-argument layout, the
-// host passes the struct's bytes), so the leading dwords arrive preloaded in SGPRs.
+// The kernels take what their first loads need as 14 scalar dwords, all preloaded into SGPRs
+// (the host passes the raw bytes): W_gate, x, y, h and the barrier state as pointers, W_up and
+// W_down as signed byte offsets from W_gate, d_model | d_ff << 16 and the grid size; act
+// follows.  Row bytes follow from the shape and the format.
 template <class Q, int TEAM1, int TEAM2>
 HH_DEV void hh_sffn_body(const hh_sffn_args& a) {
     __shared__ int s_good;
     constexpr uint32_t TPB1 = 256 / TEAM1, TPB2 = 256 / TEAM2;
-    const uint32_t tid = threadIdx.x, G = gridDim.x, w = blockIdx.x;
+    const uint32_t tid = threadIdx.x, G = a.grid, w = blockIdx.x;
     const uint32_t dm = a.d_model, df = a.d_ff;
     const uint32_t r0 = (uint32_t)(((uint64_t)w * df) / G), r1 = (uint32_t)(((uint64_t)(w + 1) * df) / G);
     const uint32_t q0 = (uint32_t)(((uint64_t)w * dm) / G), q1 = (uint32_t)(((uint64_t)(w + 1) * dm) / G);
@@ -84,9 +87,12 @@ HH_DEV void hh_sffn_body(const hh_sffn_args& a) {
 
 #define HH_SFFN(NAME, Q, T1, T2)                                                                        \
     extern "C" __global__ void __launch_bounds__(256) hh_sffn_##NAME##_t##T1##_##T2(                   \
-        const uint8_t* wg, const uint8_t* wu, const uint8_t* wd, const float* x, float* y, float* h,     \
-        unsigned* bar, uint64_t rb_in, uint64_t rb_ff, uint32_t d_model, uint32_t d_ff, int32_t act) {   \
-        hh_sffn_body<Q, T1, T2>(hh_sffn_args{wg, wu, wd, x, y, h, bar, rb_in, rb_ff, d_model, d_ff, act}); \
+        const uint8_t* wg, const float* x, float* y, float* h, unsigned* bar, int32_t du, int32_t dd,    \
+        uint32_t dims, uint32_t grid, int32_t act) {                                                     \
+        const uint32_t dm = dims & 0xFFFFu, df = dims >> 16;                                             \
+        hh_sffn_body<Q, T1, T2>(hh_sffn_args{wg, wg + du, wg + dd, x, y, h, bar,                         \
+                                             (uint64_t)(dm / Q::BLOCK) * Q::BLOCK_BYTES,                 \
+                                             (uint64_t)(df / Q::BLOCK) * Q::BLOCK_BYTES, dm, df, act, grid}); \
     }
 #define HH_SFFN_TEAMS(NAME, Q)  \
     HH_SFFN(NAME, Q, 16, 16)    \

@@ -859,14 +859,15 @@ hh_status hh_engine::enqueue_ffn_noalloc(const hh_ffn_desc* d, const uint8_t* pa
 }
 
 // Must match struct hh_sffn_args in kernels/small_ffn.hip.
-struct SffnArgs {
-    const uint8_t *wg, *wu, *wd;
+struct SffnArgs {  // the small FFN kernels' scalar parameters (small_ffn.hip)
+    const uint8_t* wg;
     const float* x;
     float* y;
     float* h;
     unsigned* bar;
-    uint64_t rb_in, rb_ff;
-    uint32_t d_model, d_ff;
+    int32_t du, dd;  // W_up, W_down - W_gate in bytes
+    uint32_t dims;   // d_model | d_ff << 16
+    uint32_t grid;
     int32_t act;
 };
 
@@ -890,10 +891,13 @@ hh_status hh_engine::enqueue_small_ffn(const hh_ffn_desc* d, const uint8_t* wg, 
     size_t rin, rff;
     HH_TRY(row_bytes(d->type_gate, dm, &rin));
     HH_TRY(row_bytes(d->type_down, df, &rff));
-    SffnArgs a{wg, wu, wd, x, y, (float*)ws_h, (unsigned*)grid_sync, (uint64_t)rin, (uint64_t)rff, (uint32_t)dm,
-               (uint32_t)df, d->act};
-    // raw argument bytes (the kernel takes the fields as scalar parameters): up to act
-    size_t asz = offsetof(SffnArgs, act) + sizeof a.act;
+    const int64_t du = (int64_t)(wu - wg), dd = (int64_t)(wd - wg);
+    if (du != (int32_t)du || dd != (int32_t)dd) return HH_ERR_UNSUPPORTED_DEVICE;
+    (void)rin;
+    (void)rff;
+    SffnArgs a{wg, x, y, (float*)ws_h, (unsigned*)grid_sync, (int32_t)du, (int32_t)dd, (uint32_t)(dm | (df << 16)),
+               (uint32_t)G, d->act};
+    size_t asz = sizeof a;  // raw argument bytes (the kernel takes the fields as scalar parameters)
     void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &a, HIP_LAUNCH_PARAM_BUFFER_SIZE, &asz, HIP_LAUNCH_PARAM_END};
     hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)G, 1, 1, 256, 1, 1, 0, stream, nullptr, cfg);
     if (err != hipSuccess) return hip_fail(err, "launch(small ffn)");
