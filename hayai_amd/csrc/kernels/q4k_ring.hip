@@ -454,6 +454,9 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
 #ifndef HH_Q4K_DN_RING_D
 #define HH_Q4K_DN_RING_D 3
 #endif
+#ifndef HH_Q4K_GU_RING_P
+#define HH_Q4K_GU_RING_P 1  // gate/up ring items issued before x is quantized
+#endif
 
 // The ring kernels (Q4_K here, Q6_K and IQ in their files) take hh_gur_args' / hh_dnr_args'
 // fields as separate scalar parameters (the same kernel-argument layout; the host passes the
@@ -474,10 +477,10 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
 // _n: with the RMSNorm prologue (the FFN residual block)
 #define HH_GU_RING(G1)                                                                          \
     extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_q4k_gu_ring_g##G1(HH_GUR_PARAMS) { \
-        hh_gu_ring_body<hh_ring_q4k, G1, HH_Q4K_GU_RING_D, 1, false>(HH_GUR_ARGS);              \
+        hh_gu_ring_body<hh_ring_q4k, G1, HH_Q4K_GU_RING_D, HH_Q4K_GU_RING_P, false>(HH_GUR_ARGS);              \
     }                                                                                           \
     extern "C" __global__ void __launch_bounds__(HH_RING_BLOCK) hh_q4k_gu_ring_g##G1##_n(HH_GUR_PARAMS) { \
-        hh_gu_ring_body<hh_ring_q4k, G1, HH_Q4K_GU_RING_D, 1, true>(HH_GUR_ARGS);               \
+        hh_gu_ring_body<hh_ring_q4k, G1, HH_Q4K_GU_RING_D, HH_Q4K_GU_RING_P, true>(HH_GUR_ARGS);               \
     }
 #define HH_DN_RING(G2)                                                                          \
     extern "C" __global__ void __launch_bounds__(HH_DN_BLOCK) hh_q4k_dn_ring_d##G2(HH_DNR_PARAMS) { \
