@@ -27,6 +27,7 @@
 //   LANE_PARTIALS    gate/up: each lane's contribution goes to LDS and rows are summed once
 //                    after the loop (formats with long per-row arithmetic), instead of a
 //                    wave reduction per row
+//   DIRECT_H         down: each lane loads its h digits from global memory itself
 
 #define HH_RING_BLOCK (HH_FFNP_CW * HH_WAVE)
 
@@ -105,6 +106,7 @@ HH_DEV char* hh_ring_tables_lds<0>() {
 struct hh_ring_q4k {
     static constexpr uint32_t UNIT = 64;
     static constexpr uint32_t TAB_BYTES = 0;
+    static constexpr bool DIRECT_H = true;  // down: h digits loaded per lane (no LDS copy)
     static constexpr bool LANE_PARTIALS = false;
     struct lane_t {
         uint32_t oh, oq;  // block header, this unit's 32 qs bytes
@@ -377,11 +379,24 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
         F::issue(wdp + (size_t)(r < q1 ? r : q0) * a.rb2, lo, s);  // padding re-reads row q0
     };
 
+    // F::DIRECT_H (Q4_K): every compute lane loads its own unit's digits of the intermediate
+    // straight into registers, ahead of its ring, so a wave starts as soon as its own ~160
+    // bytes per lane arrive (no copy into LDS, no barrier before the loop; 8B down 9.3 ->
+    // 9.15 us).  Otherwise (Q6_K: slower that way, its LM-head grids re-read h per workgroup
+    // many times; the IQ formats: LDS tables) the copy wave brings the intermediate (and the
+    // tables) into LDS as below.
+    constexpr bool DIRECT_H = F::DIRECT_H;
+    static_assert(!DIRECT_H || F::TAB_BYTES == 0, "direct h loads leave no wave to copy tables");
     typename F::data ring[D];
+    typename F::hr_t hr;
     if (wave < HH_FFNP_CW) {
+        if constexpr (DIRECT_H) {
+            const int8_t* gq1 = reinterpret_cast<const int8_t*>(a.hx);
+            F::load_h(gq1, gq1 + dff, reinterpret_cast<const float*>(gq1 + 2 * (size_t)dff), u2, hr);
+        }
 #pragma unroll
         for (int s = 0; s < D; s++) issue((uint32_t)s, ring[s]);
-    } else {
+    } else if constexpr (!DIRECT_H) {
         // the format's tables and the intermediate -> LDS, every 16-byte chunk in flight at once
         constexpr uint32_t TAB16 = F::TAB_BYTES / 16u;
         if constexpr (TAB16 > 0) {
@@ -401,12 +416,11 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
         }
         __builtin_amdgcn_s_waitcnt(0);
     }
-    __syncthreads();  // the intermediate is in LDS (the rings stay in flight)
+    if constexpr (!DIRECT_H) __syncthreads();  // the intermediate is in LDS (the rings stay in flight)
     HH_RING_MARK(1, a.wd, 1, tid == 0);
 
     if (wave < HH_FFNP_CW) {
-        typename F::hr_t hr;
-        F::load_h(hq1, hq2, hsc, u2, hr);
+        if constexpr (!DIRECT_H) F::load_h(hq1, hq2, hsc, u2, hr);
         for (uint32_t j0 = 0; j0 < n2p; j0 += D) {
 #pragma unroll
             for (int s = 0; s < D; s++) {
