@@ -225,26 +225,18 @@ HH_DEV void hh_moe_dn_ring_body(const hh_moe_ring_args& ra) {
         s.q1 = hh_ld16(row + oq + 16);
     };
 
+    // every compute lane loads its own unit's digits of h' from global memory, ahead of its
+    // ring, and starts as soon as they arrive (no copy into LDS, no barrier before the loop)
     hh_q4k_data ring[D];
+    hh_ffnp_h hr;
     if (wave < HH_FFNP_CW) {
+        const int8_t* g1 = reinterpret_cast<const int8_t*>(ra.hx);
+        hh_ffnp_load_h(g1, g1 + K, reinterpret_cast<const float*>(g1 + 2 * (size_t)K), u2, hr);  // (lu & 3 = u2 & 3)
 #pragma unroll
         for (int s = 0; s < D; s++) issue((uint32_t)s, ring[s]);
-    } else {
-        // h' digits -> LDS, every 16-byte chunk in flight at once
-        const uint32_t chunks = hbytes / 16u;
-        for (uint32_t c0 = 0; c0 < chunks; c0 += HH_WAVE) {
-            if (c0 + lane < chunks)
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void*)(ra.hx + (size_t)(c0 + lane) * 16),
-                    (__attribute__((address_space(3))) void*)(hh_smem + (size_t)c0 * 16), 16, 0, 0);
-        }
-        __builtin_amdgcn_s_waitcnt(0);
     }
-    __syncthreads();  // h' is in LDS (the rings stay in flight)
 
     if (wave < HH_FFNP_CW) {
-        hh_ffnp_h hr;
-        hh_ffnp_load_h(hq1, hq2, hsc, u2, hr);  // (unit position in its superblock: lu & 3 = u2 & 3)
         for (uint32_t j0 = 0; j0 < n2p; j0 += D) {
 #pragma unroll
             for (int s = 0; s < D; s++) {
