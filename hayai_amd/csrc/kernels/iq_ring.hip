@@ -218,7 +218,7 @@ struct hh_ring_iq2 {
     static constexpr uint32_t BB = 66;  // block bytes: d (f16) + 8 groups x (4 codebook indices, 4 sign/scale bytes)
     static constexpr uint32_t UPB = 8 / NG;  // units per block
     static constexpr uint32_t TAB_BYTES = sizeof(hh_iq2_tab);
-    static constexpr bool DIRECT_H = false;  // down: tables and h through the copy wave
+    static constexpr bool DIRECT_H = true;  // down: h digits per lane, the tables by the copy wave
     static constexpr bool LANE_PARTIALS = true;
     static constexpr int RUN = 2 * NG + 1;  // dwords covering the lane's 8 NG index/sign bytes
     struct lane_t {
@@ -291,7 +291,7 @@ struct hh_ring_iq3 {
     static constexpr uint32_t BB = 98;  // d (f16) + 64 codebook indices + 8 x (4 sign/scale bytes)
     static constexpr uint32_t UPB = 8 / NG;
     static constexpr uint32_t TAB_BYTES = sizeof(hh_iq3_tab);
-    static constexpr bool DIRECT_H = false;  // down: tables and h through the copy wave
+    static constexpr bool DIRECT_H = true;  // down: h digits per lane, the tables by the copy wave
     static constexpr bool LANE_PARTIALS = true;
     static constexpr int RUN = 2 * NG + 1;  // dwords covering the 8 NG index bytes
     static constexpr int ARUN = NG + 1;     // dwords covering the NG sign/scale words

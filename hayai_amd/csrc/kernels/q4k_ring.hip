@@ -382,11 +382,11 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
     // F::DIRECT_H (Q4_K): every compute lane loads its own unit's digits of the intermediate
     // straight into registers, ahead of its ring, so a wave starts as soon as its own ~160
     // bytes per lane arrive (no copy into LDS, no barrier before the loop; 8B down 9.3 ->
-    // 9.15 us).  Otherwise (Q6_K: slower that way, its LM-head grids re-read h per workgroup
-    // many times; the IQ formats: LDS tables) the copy wave brings the intermediate (and the
-    // tables) into LDS as below.
+    // 9.15 us), the copy wave then bringing only the format's LDS tables (if any).  Otherwise
+    // (Q6_K: slower that way, its LM-head grids re-read h per workgroup many times) the copy
+    // wave brings the intermediate (and the tables) into LDS as below.
     constexpr bool DIRECT_H = F::DIRECT_H;
-    static_assert(!DIRECT_H || F::TAB_BYTES == 0, "direct h loads leave no wave to copy tables");
+    constexpr bool TABLES = F::TAB_BYTES > 0;  // with direct h loads the copy wave brings only these
     typename F::data ring[D];
     typename F::hr_t hr;
     if (wave < HH_FFNP_CW) {
@@ -396,7 +396,7 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
         }
 #pragma unroll
         for (int s = 0; s < D; s++) issue((uint32_t)s, ring[s]);
-    } else if constexpr (!DIRECT_H) {
+    } else {
         // the format's tables and the intermediate -> LDS, every 16-byte chunk in flight at once
         constexpr uint32_t TAB16 = F::TAB_BYTES / 16u;
         if constexpr (TAB16 > 0) {
@@ -407,7 +407,7 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
                         (__attribute__((address_space(3))) void*)(tabs + (size_t)c0 * 16), 16, 0, 0);
             }
         }
-        const uint32_t chunks = hbytes / 16u;
+        const uint32_t chunks = DIRECT_H ? 0u : hbytes / 16u;
         for (uint32_t c0 = 0; c0 < chunks; c0 += HH_WAVE) {
             if (c0 + lane < chunks)
                 __builtin_amdgcn_global_load_lds(
@@ -416,7 +416,8 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
         }
         __builtin_amdgcn_s_waitcnt(0);
     }
-    if constexpr (!DIRECT_H) __syncthreads();  // the intermediate is in LDS (the rings stay in flight)
+    // the intermediate (or, with direct h loads, only the tables) is in LDS; the rings stay in flight
+    if constexpr (!DIRECT_H || TABLES) __syncthreads();
     HH_RING_MARK(1, a.wd, 1, tid == 0);
 
     if (wave < HH_FFNP_CW) {
