@@ -129,34 +129,5 @@ def build(verbose: bool = False) -> str:
     return lib
 
 
-TRACE_DIR = os.path.join(HERE, "trace_build")
-
-
-def build_timeline(verbose: bool = False) -> str:
-    """The timeline tools (csrc/trace/ring_timeline.cpp, stack_timeline.cpp,
-    q4k_stack_timeline.cpp) and the code object they run: the kernels again with
-    HH_RING_TRACE, HH_SSTK_TRACE and HH_QSTK_TRACE (per-workgroup phase timestamps); and the
-    streaming-ceiling probe (csrc/trace/stream_ceiling.cpp).  Measurement tools, not part of
-    the library; outputs under hayai_amd/trace_build/."""
-    os.makedirs(TRACE_DIR, exist_ok=True)
-    hipcc = os.path.join(rocm_path(), "bin", "hipcc")
-    co = os.path.join(TRACE_DIR, "hayai_kernels_trace.hsaco")
-    _run([hipcc, *KERNEL_FLAGS, "-DHH_RING_TRACE", "-DHH_SSTK_TRACE", "-DHH_QSTK_TRACE", "-o", co,
-          os.path.join(CSRC, "kernels", "all.hip")], verbose)
-    tool = os.path.join(TRACE_DIR, "ring_timeline")
-    _run([hipcc, "-O2", "-std=c++17", "-o", tool, os.path.join(CSRC, "trace", "ring_timeline.cpp")], verbose)
-    _run([hipcc, "-O2", "-std=c++17", "-o", os.path.join(TRACE_DIR, "stack_timeline"),
-          os.path.join(CSRC, "trace", "stack_timeline.cpp")], verbose)
-    _run([hipcc, "-O2", "-std=c++17", "-o", os.path.join(TRACE_DIR, "q4k_stack_timeline"),
-          os.path.join(CSRC, "trace", "q4k_stack_timeline.cpp")], verbose)
-    _run([hipcc, f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
-          "-packed-fp32-ops", "-o", os.path.join(TRACE_DIR, "stream_ceiling"),
-          os.path.join(CSRC, "trace", "stream_ceiling.cpp")], verbose)
-    return tool
-
-
 if __name__ == "__main__":
-    if "--timeline" in sys.argv:
-        print(build_timeline(verbose="-q" not in sys.argv))
-    else:
-        build(verbose="-q" not in sys.argv)
+    build(verbose="-q" not in sys.argv)

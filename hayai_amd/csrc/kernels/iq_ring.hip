@@ -114,20 +114,47 @@ HH_DEV void hh_iq_load_x(const hh_digits_ptr& xd, uint32_t u, hh_iq_x<NG>& x) {
 #pragma unroll
     for (int g = 0; g < NG; g++) x.s[g] = xd.sc[NG * u + g] * (1.0f / 256.0f);
 }
+// A lane's h bytes as loaded, apart from the arithmetic (as hh_ffnp_hraw).
 template <int NG>
-HH_DEV void hh_iq_load_h(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hh_iq_h<NG>& h) {
-    hh_iq_load_digits<NG>(q1, q2, u, h.q1, h.q2);
+struct hh_iq_hraw {
+    uint4 a[2 * NG], b[2 * NG];
+    float4 s[NG];
+};
+template <int NG>
+HH_DEV void hh_iq_load_h_raw(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hh_iq_hraw<NG>& r) {
+    const uint4* a = reinterpret_cast<const uint4*>(q1 + (size_t)u * 32 * NG);
+    const uint4* b = reinterpret_cast<const uint4*>(q2 + (size_t)u * 32 * NG);
+#pragma unroll
+    for (int i = 0; i < 2 * NG; i++) {
+        r.a[i] = a[i];
+        r.b[i] = b[i];
+    }
+#pragma unroll
+    for (int i = 0; i < NG; i++) r.s[i] = reinterpret_cast<const float4*>(sc)[NG * u + i];
+}
+template <int NG>
+HH_DEV void hh_iq_make_h(const hh_iq_hraw<NG>& r, hh_iq_h<NG>& h) {
+#pragma unroll
+    for (int i = 0; i < 2 * NG; i++) {
+        hh_unpack4(r.a[i], h.q1 + 4 * i);
+        hh_unpack4(r.b[i], h.q2 + 4 * i);
+    }
     float s[4 * NG];
 #pragma unroll
     for (int i = 0; i < NG; i++) {
-        const float4 v = reinterpret_cast<const float4*>(sc)[NG * u + i];
-        s[4 * i] = v.x;
-        s[4 * i + 1] = v.y;
-        s[4 * i + 2] = v.z;
-        s[4 * i + 3] = v.w;
+        s[4 * i] = r.s[i].x;
+        s[4 * i + 1] = r.s[i].y;
+        s[4 * i + 2] = r.s[i].z;
+        s[4 * i + 3] = r.s[i].w;
     }
 #pragma unroll
     for (int k = 0; k < 4 * NG; k++) h.w[k] = (s[k] - ((k & 3) < 3 ? s[k + 1] : 0.f)) * (1.0f / 256.0f);
+}
+template <int NG>
+HH_DEV void hh_iq_load_h(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hh_iq_h<NG>& h) {
+    hh_iq_hraw<NG> r;
+    hh_iq_load_h_raw<NG>(q1, q2, sc, u, r);
+    hh_iq_make_h<NG>(r, h);
 }
 
 // One signed 8-element codebook entry against the digits of elements 8l..8l+7 of group g,
@@ -247,6 +274,11 @@ struct hh_ring_iq2 {
     static HH_DEV void load_h(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hr_t& h) {
         hh_iq_load_h<NG>(q1, q2, sc, u, h);
     }
+    typedef hh_iq_hraw<NG> hraw_t;
+    static HH_DEV void load_h_raw(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hraw_t& r) {
+        hh_iq_load_h_raw<NG>(q1, q2, sc, u, r);
+    }
+    static HH_DEV void make_h(const hraw_t& r, uint32_t, hr_t& h) { hh_iq_make_h<NG>(r, h); }
     // d/8 * sum_g (2 s_g + 1) t_g  ==  sum_g d (0.5 + s_g) / 4 * t_g   (iq2.rs:513)
     template <class X>
     static HH_DEV float unit(const data& s, const lane_t& l, const X& x, const char* tab) {
@@ -325,6 +357,11 @@ struct hh_ring_iq3 {
     static HH_DEV void load_h(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hr_t& h) {
         hh_iq_load_h<NG>(q1, q2, sc, u, h);
     }
+    typedef hh_iq_hraw<NG> hraw_t;
+    static HH_DEV void load_h_raw(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hraw_t& r) {
+        hh_iq_load_h_raw<NG>(q1, q2, sc, u, r);
+    }
+    static HH_DEV void make_h(const hraw_t& r, uint32_t, hr_t& h) { hh_iq_make_h<NG>(r, h); }
     // d/4 * sum_g (2 s_g + 1) t_g  ==  sum_g d (0.5 + s_g) / 2 * t_g   (iq3.rs:160)
     template <class X>
     static HH_DEV float unit(const data& s, const lane_t& l, const X& x, const char* tab) {

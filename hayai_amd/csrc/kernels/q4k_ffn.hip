@@ -78,19 +78,33 @@ HH_DEV float hh_ffnp_sub_sum(const uint32_t (&q1)[8], const uint32_t (&q2)[8], c
     return t;
 }
 
-HH_DEV void hh_ffnp_load_h(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hh_ffnp_h& h) {
+// A lane's h bytes as loaded (digits of its 64 columns, the 8 granule scales): the loads are
+// issued apart from the arithmetic, so a caller can put its weight loads between them.
+struct hh_ffnp_hraw {
+    uint4 a[4], b[4];
+    float4 s0, s1;
+};
+HH_DEV void hh_ffnp_load_h_raw(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hh_ffnp_hraw& r) {
     const uint4* a = reinterpret_cast<const uint4*>(q1 + (size_t)u * 64);
     const uint4* b = reinterpret_cast<const uint4*>(q2 + (size_t)u * 64);
-    hh_unpack4(a[0], h.q1lo);
-    hh_unpack4(a[1], h.q1lo + 4);
-    hh_unpack4(a[2], h.q1hi);
-    hh_unpack4(a[3], h.q1hi + 4);
-    hh_unpack4(b[0], h.q2lo);
-    hh_unpack4(b[1], h.q2lo + 4);
-    hh_unpack4(b[2], h.q2hi);
-    hh_unpack4(b[3], h.q2hi + 4);
-    const float4 s0 = reinterpret_cast<const float4*>(sc)[2 * u];
-    const float4 s1 = reinterpret_cast<const float4*>(sc)[2 * u + 1];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        r.a[i] = a[i];
+        r.b[i] = b[i];
+    }
+    r.s0 = reinterpret_cast<const float4*>(sc)[2 * u];
+    r.s1 = reinterpret_cast<const float4*>(sc)[2 * u + 1];
+}
+HH_DEV void hh_ffnp_make_h(const hh_ffnp_hraw& r, uint32_t u, hh_ffnp_h& h) {
+    hh_unpack4(r.a[0], h.q1lo);
+    hh_unpack4(r.a[1], h.q1lo + 4);
+    hh_unpack4(r.a[2], h.q1hi);
+    hh_unpack4(r.a[3], h.q1hi + 4);
+    hh_unpack4(r.b[0], h.q2lo);
+    hh_unpack4(r.b[1], h.q2lo + 4);
+    hh_unpack4(r.b[2], h.q2hi);
+    hh_unpack4(r.b[3], h.q2hi + 4);
+    const float4 s0 = r.s0, s1 = r.s1;
     const float slo[4] = {s0.x, s0.y, s0.z, s0.w}, shi[4] = {s1.x, s1.y, s1.z, s1.w};
     const float k = 1.0f / 256.0f;
 #pragma unroll
@@ -105,6 +119,11 @@ HH_DEV void hh_ffnp_load_h(const int8_t* q1, const int8_t* q2, const float* sc, 
     h.sel_yz = kk | ((kk + 1u) << 8) | ((kk + 4u) << 16) | ((kk + 5u) << 24);
     h.sel_w = kk | ((kk + 1u) << 8) | (kk << 16) | ((kk + 1u) << 24);
     h.hi_form = g >= 2;
+}
+HH_DEV void hh_ffnp_load_h(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hh_ffnp_h& h) {
+    hh_ffnp_hraw r;
+    hh_ffnp_load_h_raw(q1, q2, sc, u, r);
+    hh_ffnp_make_h(r, u, h);
 }
 
 // Contribution of one (row, unit) with per-8 granule digit scales.

@@ -36,9 +36,9 @@
 // timestamp of the 100 MHz realtime counter per workgroup and phase, indexed by the layer
 // that the weight pointer falls in ((w - base) / stride, set by the tool).
 #ifdef HH_RING_TRACE
-__device__ unsigned long long hh_ring_trace[2][64][512][4];  // [gate/up, down][layer][workgroup][phase]
-__device__ const uint8_t* hh_ring_trace_base;
-__device__ unsigned long long hh_ring_trace_stride;
+__device__ unsigned long long hh_ring_trace[2][64][512][8];  // [gate/up, down][layer][workgroup][phase]
+__constant__ const uint8_t* hh_ring_trace_base;  // constant: scalar loads, no vector-memory wait
+__constant__ unsigned long long hh_ring_trace_stride;
 HH_DEV void hh_ring_mark(int kind, const uint8_t* w, int phase) {
     const long long l = (long long)((w - hh_ring_trace_base) / (long long)hh_ring_trace_stride);
     if (l >= 0 && l < 64 && blockIdx.x < 512) hh_ring_trace[kind][l][blockIdx.x][phase] = __builtin_amdgcn_s_memrealtime();
@@ -128,6 +128,11 @@ struct hh_ring_q4k {
     static HH_DEV void load_h(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hr_t& h) {
         hh_ffnp_load_h(q1, q2, sc, u, h);
     }
+    typedef hh_ffnp_hraw hraw_t;
+    static HH_DEV void load_h_raw(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hraw_t& r) {
+        hh_ffnp_load_h_raw(q1, q2, sc, u, r);
+    }
+    static HH_DEV void make_h(const hraw_t& r, uint32_t u, hr_t& h) { hh_ffnp_make_h(r, u, h); }
     static HH_DEV float unit_x(const data& s, const lane_t&, const xr_t& xr, const char*) { return hh_q4k_unit(s, xr); }
     static HH_DEV float unit_h(const data& s, const lane_t&, const hr_t& h, const char*) { return hh_ffnp_unit_g8(s, h); }
 };
@@ -216,6 +221,8 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
         float ss = has ? hh_sq8(t0, t1) : 0.f;
         for (uint32_t c2 = c + HH_RING_BLOCK; c2 < dm / 8; c2 += HH_RING_BLOCK) ss += hh_sq8(x4[2 * c2], x4[2 * c2 + 1]);
         ss = hh_wave_sum(ss);
+        HH_RING_MARK(0, a.wg, 4, tid == 0 && ss != -1.f);                    // x arrived (wave 0)
+        HH_RING_MARK(0, a.wg, 5, tid == HH_RING_BLOCK - HH_WAVE && ss != -1.f);  // x arrived (last wave)
         float* red = reinterpret_cast<float*>(stage);  // free until the epilogue
         if (lane == 0) red[wave] = ss;                   // read after the main loop's barrier
         hh_norm8(t0, t1, m0, m1, 1.f);
@@ -237,23 +244,30 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
     {
         typename F::xr_t xr;
         F::load_x(xd, u1, xr);
-        for (uint32_t j0 = 0; j0 < n1p; j0 += D) {
+        auto consume = [&](uint32_t j, const typename F::data& s) {
+            const uint32_t i = team1 + j * TPW1;
+            if (i < RR) {  // wave-uniform
+                float v = F::unit_x(s, lo, xr, tabs);
+                if constexpr (LP) {
+                    gu[i * TEAM1 + lane1] = act1 ? v : 0.f;  // summed after the loop
+                } else {
+                    v = hh_wave_sum(act1 ? v : 0.f);
+                    if (lane == 0) gu[i * WPT1 + wave % WPT1] = v;
+                }
+                HH_RING_MARK(0, a.wg, 6, j == 0 && tid == 0 && v != -1.f);  // first item done (wave 0)
+            }
+        };
+        // every round but the last issues the items D ahead; the last issues nothing
+        uint32_t j0 = 0;
+        for (; j0 + D < n1p; j0 += D) {
 #pragma unroll
             for (int s = 0; s < D; s++) {
-                const uint32_t j = j0 + (uint32_t)s;
-                const uint32_t i = team1 + j * TPW1;
-                if (i < RR) {  // wave-uniform
-                    float v = F::unit_x(ring[s], lo, xr, tabs);
-                    if constexpr (LP) {
-                        gu[i * TEAM1 + lane1] = act1 ? v : 0.f;  // summed after the loop
-                    } else {
-                        v = hh_wave_sum(act1 ? v : 0.f);
-                        if (lane == 0) gu[i * WPT1 + wave % WPT1] = v;
-                    }
-                }
-                issue(j + D, ring[s]);
+                consume(j0 + (uint32_t)s, ring[s]);
+                issue(j0 + (uint32_t)s + D, ring[s]);
             }
         }
+#pragma unroll
+        for (int s = 0; s < D; s++) consume(j0 + (uint32_t)s, ring[s]);
     }
     __syncthreads();  // row sums (or lane partials) are in LDS
     HH_RING_MARK(0, a.wg, 2, tid == 0);
@@ -336,15 +350,17 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
 }
 
 // Down: workgroup w owns output rows [w*M/G, (w+1)*M/G); a team of WPT2 waves covers one row
-// (lane = unit).  A ninth wave copies the intermediate into LDS (global->LDS DMA) while the
-// compute waves' rings are already in flight, so neither waits behind the other's requests;
-// lane partials meet in LDS and a 32-lane DPP reduction per row writes y (fixed order:
-// deterministic).
+// (lane = unit).  A ninth wave copies into LDS by global->LDS DMA, at kernel start, what the
+// compute waves read from there (the format's tables, the intermediate unless F::DIRECT_H),
+// so neither queues behind the other's requests; lane partials meet in LDS and a 32-lane DPP
+// reduction per row writes y (fixed order: deterministic).
 #define HH_DN_BLOCK ((HH_FFNP_CW + 1) * HH_WAVE)
 template <class F, int WPT2, int D>
 HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
     extern __shared__ __attribute__((aligned(16))) char hh_smem[];
     constexpr uint32_t TEAM2 = WPT2 * HH_WAVE, TPW2 = HH_FFNP_CW / WPT2;
+    constexpr bool DIRECT_H = F::DIRECT_H;
+    constexpr bool TABLES = F::TAB_BYTES > 0;  // with direct h loads the copy wave brings only these
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % HH_WAVE;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / HH_WAVE);
@@ -352,18 +368,20 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
     const uint32_t dm = a.d_model, dff = a.d_ff;
     const uint32_t q0 = (uint32_t)(((uint64_t)w * dm) / G);
     const uint32_t q1 = (uint32_t)(((uint64_t)(w + 1) * dm) / G);
-    const uint32_t n2 = (q1 - q0 + TPW2 - 1) / TPW2;
+    const uint32_t nrows = q1 - q0;
+    const uint32_t n2 = (nrows + TPW2 - 1) / TPW2;
     const uint32_t n2p = (n2 + D - 1) / D * D;
     HH_RING_MARK(1, a.wd, 0, tid == 0);
 
     // the residual of the first row this thread stores, fetched now rather than on the tail
     float res0 = 0.f;
-    if (a.res && tid % 32 == 31 && tid / 32 < q1 - q0) res0 = a.res[q0 + tid / 32];
+    if (a.res && tid % 32 == 31 && tid / 32 < nrows) res0 = a.res[q0 + tid / 32];
 
-    // LDS: static: the format's tables; dynamic: [intermediate][lane partials: rows x TEAM2]
+    // LDS: static: the format's tables; dynamic: [intermediate (unless DIRECT_H)][lane
+    // partials: rows x TEAM2]
     char* const tabs = hh_ring_tables_lds<F::TAB_BYTES>();
     char* const lds = hh_smem;
-    const uint32_t hbytes = 2u * dff + (dff / 8u) * 4u;
+    const uint32_t hbytes = DIRECT_H ? 0u : 2u * dff + (dff / 8u) * 4u;
     int8_t* hq1 = reinterpret_cast<int8_t*>(lds);
     int8_t* hq2 = hq1 + dff;
     float* hsc = reinterpret_cast<float*>(hq2 + dff);
@@ -379,41 +397,47 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
         F::issue(wdp + (size_t)(r < q1 ? r : q0) * a.rb2, lo, s);  // padding re-reads row q0
     };
 
-    // F::DIRECT_H (Q4_K): every compute lane loads its own unit's digits of the intermediate
-    // straight into registers, ahead of its ring, so a wave starts as soon as its own ~160
-    // bytes per lane arrive (no copy into LDS, no barrier before the loop; 8B down 9.3 ->
-    // 9.15 us), the copy wave then bringing only the format's LDS tables (if any).  Otherwise
-    // (Q6_K: slower that way, its LM-head grids re-read h per workgroup many times) the copy
-    // wave brings the intermediate (and the tables) into LDS as below.
-    constexpr bool DIRECT_H = F::DIRECT_H;
-    constexpr bool TABLES = F::TAB_BYTES > 0;  // with direct h loads the copy wave brings only these
+    // F::DIRECT_H (Q4_K, IQ): every compute lane loads its own unit's digits of the
+    // intermediate straight into registers, ahead of its ring, so a wave starts as soon as its
+    // own ~160 bytes per lane arrive (no copy into LDS, no barrier before the loop; 8B down
+    // 9.3 -> 9.15 us), the copy wave then bringing only the format's LDS tables (if any).
+    // Otherwise (Q6_K: slower that way, its LM-head grids re-read h per
+    // workgroup many times) the copy wave brings the intermediate (and the tables) into LDS.
     typename F::data ring[D];
     typename F::hr_t hr;
     if (wave < HH_FFNP_CW) {
         if constexpr (DIRECT_H) {
+            // h's loads, then every ring item's, and only then the arithmetic on h (which
+            // waits for h): no ring load is held back behind the intermediate's arrival
+            typename F::hraw_t hraw;
             const int8_t* gq1 = reinterpret_cast<const int8_t*>(a.hx);
-            F::load_h(gq1, gq1 + dff, reinterpret_cast<const float*>(gq1 + 2 * (size_t)dff), u2, hr);
-        }
+            F::load_h_raw(gq1, gq1 + dff, reinterpret_cast<const float*>(gq1 + 2 * (size_t)dff), u2, hraw);
 #pragma unroll
-        for (int s = 0; s < D; s++) issue((uint32_t)s, ring[s]);
+            for (int s = 0; s < D; s++) issue((uint32_t)s, ring[s]);
+            __builtin_amdgcn_sched_barrier(0);
+            F::make_h(hraw, u2, hr);
+#ifdef HH_RING_TRACE
+            const float hchk = __builtin_bit_cast(float, hraw.a[0].x ^ hraw.b[3].w) + hraw.s1.w;
+            HH_RING_MARK(1, a.wd, 4, tid == 0 && hchk != -1.f);                     // h arrived (wave 0)
+            HH_RING_MARK(1, a.wd, 5, tid == HH_RING_BLOCK - HH_WAVE && hchk != -1.f);  // h arrived (last wave)
+#endif
+        } else {
+#pragma unroll
+            for (int s = 0; s < D; s++) issue((uint32_t)s, ring[s]);
+        }
     } else {
-        // the format's tables and the intermediate -> LDS, every 16-byte chunk in flight at once
-        constexpr uint32_t TAB16 = F::TAB_BYTES / 16u;
-        if constexpr (TAB16 > 0) {
-            for (uint32_t c0 = 0; c0 < TAB16; c0 += HH_WAVE) {
-                if (c0 + lane < TAB16)
+        // every 16-byte chunk in flight at once (the hardware holds the wave's issue while its
+        // count of outstanding loads is full)
+        auto dma = [&](const uint8_t* src, char* dst, uint32_t chunks) {
+            for (uint32_t c0 = 0; c0 < chunks; c0 += HH_WAVE) {
+                if (c0 + lane < chunks)
                     __builtin_amdgcn_global_load_lds(
-                        (const __attribute__((address_space(1))) void*)(F::tables() + c0 + lane),
-                        (__attribute__((address_space(3))) void*)(tabs + (size_t)c0 * 16), 16, 0, 0);
+                        (const __attribute__((address_space(1))) void*)(src + (size_t)(c0 + lane) * 16),
+                        (__attribute__((address_space(3))) void*)(dst + (size_t)c0 * 16), 16, 0, 0);
             }
-        }
-        const uint32_t chunks = DIRECT_H ? 0u : hbytes / 16u;
-        for (uint32_t c0 = 0; c0 < chunks; c0 += HH_WAVE) {
-            if (c0 + lane < chunks)
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void*)(a.hx + (size_t)(c0 + lane) * 16),
-                    (__attribute__((address_space(3))) void*)(lds + (size_t)c0 * 16), 16, 0, 0);
-        }
+        };
+        if constexpr (TABLES) dma(reinterpret_cast<const uint8_t*>(F::tables()), tabs, F::TAB_BYTES / 16u);
+        if constexpr (!DIRECT_H) dma(a.hx, lds, hbytes / 16u);
         __builtin_amdgcn_s_waitcnt(0);
     }
     // the intermediate (or, with direct h loads, only the tables) is in LDS; the rings stay in flight
@@ -422,18 +446,25 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
 
     if (wave < HH_FFNP_CW) {
         if constexpr (!DIRECT_H) F::load_h(hq1, hq2, hsc, u2, hr);
-        for (uint32_t j0 = 0; j0 < n2p; j0 += D) {
+        auto consume = [&](uint32_t k, const typename F::data& s) {
+            const uint32_t rl = team2 + k * TPW2;  // local row
+            if (rl < nrows) {                      // wave-uniform
+                const float v = F::unit_h(s, lo, hr, tabs);
+                part[rl * TEAM2 + lane2] = act2 ? v : 0.f;  // reduced after the loop
+                HH_RING_MARK(1, a.wd, 6, k == 0 && tid == 0 && v != -1.f);  // first item done (wave 0)
+            }
+        };
+        // every round but the last issues the items D ahead; the last issues nothing
+        uint32_t j0 = 0;
+        for (; j0 + D < n2p; j0 += D) {
 #pragma unroll
             for (int s = 0; s < D; s++) {
-                const uint32_t k = j0 + (uint32_t)s;
-                const uint32_t rl = team2 + k * TPW2;  // local row
-                if (q0 + rl < q1) {                    // wave-uniform
-                    const float v = F::unit_h(ring[s], lo, hr, tabs);
-                    part[rl * TEAM2 + lane2] = act2 ? v : 0.f;  // reduced after the loop
-                }
-                issue(k + D, ring[s]);
+                consume(j0 + (uint32_t)s, ring[s]);
+                issue(j0 + (uint32_t)s + D, ring[s]);
             }
         }
+#pragma unroll
+        for (int s = 0; s < D; s++) consume(j0 + (uint32_t)s, ring[s]);
     }
     __syncthreads();  // lane partials are in LDS
     HH_RING_MARK(1, a.wd, 2, tid == 0);
@@ -442,7 +473,6 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
     // 32-lane halves of a wave)
     {
         constexpr uint32_t PER = TEAM2 / 32;
-        const uint32_t nrows = q1 - q0;
         for (uint32_t rl0 = 0; rl0 < nrows; rl0 += HH_DN_BLOCK / 32) {
             const uint32_t rl = rl0 + tid / 32, seg = tid % 32;
             float s = 0.f;
@@ -467,7 +497,7 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
 #define HH_Q4K_GU_RING_D 3
 #endif
 #ifndef HH_Q4K_DN_RING_D
-#define HH_Q4K_DN_RING_D 3
+#define HH_Q4K_DN_RING_D 2
 #endif
 #ifndef HH_Q4K_GU_RING_P
 #define HH_Q4K_GU_RING_P 1  // gate/up ring items issued before x is quantized
@@ -485,7 +515,7 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
     const uint8_t *wg, const uint8_t *wu, const float *x, uint8_t *hx, const float *nw, uint32_t rb1, \
         uint32_t dims, uint32_t grid, int32_t act, float eps
 #define HH_GUR_ARGS hh_gur_args{wg, wu, x, hx, nw, rb1, dims & 0xFFFFu, dims >> 16, act, eps, grid}
-#define HH_DNR_PARAMS \
+#define HH_DNR_PARAMS                                                                                 \
     const uint8_t *wd, const uint8_t *hx, float *y, const float *res, uint64_t rb2, uint32_t d_model, uint32_t d_ff
 #define HH_DNR_ARGS hh_dnr_args{wd, hx, y, res, rb2, d_model, d_ff}
 

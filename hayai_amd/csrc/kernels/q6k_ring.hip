@@ -120,7 +120,7 @@ HH_DEV float hh_q6k_unit(const hh_q6k_raw& raw, uint32_t sh, uint32_t is, const 
 struct hh_ring_q6k {
     static constexpr uint32_t UNIT = 64;
     static constexpr uint32_t TAB_BYTES = 0;
-    static constexpr bool DIRECT_H = false;  // down: h digits loaded per lane (no LDS copy)
+    static constexpr bool DIRECT_H = false;  // down: the copy wave brings h's digits into LDS
     static constexpr bool LANE_PARTIALS = false;
     struct lane_t {
         uint32_t oa, ob, oh, os, od;  // dword-aligned offsets of the lane's pieces

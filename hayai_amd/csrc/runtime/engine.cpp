@@ -547,12 +547,13 @@ struct RingFmt {
     bool lane_partials;  // the gate/up kernel keeps every lane's row contribution in LDS
     bool wide_gu;        // 128-column lanes for gate/up at d_model 8192 (kernel stem + "w")
     bool wide_dn;        // 128-column lanes for down rows of at least 8192 columns
+    bool direct_h;       // down: lanes load h's digits themselves (no LDS copy of h)
 };
 static const RingFmt kRingFmts[] = {
-    {HH_TYPE_Q4_K, "q4k", 144, 0, true, false, false, false},
-    {HH_TYPE_Q6_K, "q6k", 210, 0, false, false, false, false},
-    {HH_TYPE_IQ2_XXS, "iq2", 66, 3072, true, true, true, true},
-    {HH_TYPE_IQ3_XXS, "iq3", 98, 2048, true, true, true, false},
+    {HH_TYPE_Q4_K, "q4k", 144, 0, true, false, false, false, true},
+    {HH_TYPE_Q6_K, "q6k", 210, 0, false, false, false, false, false},
+    {HH_TYPE_IQ2_XXS, "iq2", 66, 3072, true, true, true, true, true},
+    {HH_TYPE_IQ3_XXS, "iq3", 98, 2048, true, true, true, false, true},
 };
 static const RingFmt* ring_fmt(int type) {
     for (const RingFmt& f : kRingFmts)
@@ -650,10 +651,12 @@ hh_status hh_engine::launch_dn_ring(int type, size_t m, size_t n, const uint8_t*
     const std::string name = std::string("hh_") + f->stem + (wide ? "w" : "") + "_dn_ring_d" + std::to_string(w2);
     hipFunction_t fn;
     HH_TRY(kernel(name, &fn));
-    const int block = 9 * 64;  // 8 compute waves + the wave that copies the intermediate
+    const int block = 9 * 64;  // 8 compute waves + the wave that copies into LDS
     const size_t cus = (size_t)props.multiProcessorCount;
     const size_t lds = (size_t)props.sharedMemPerBlock - f->tab_bytes;  // the tables are static LDS
-    const size_t hb = ((2 * n + (n / 8) * 4) + 15) & ~size_t(15), per_row = (size_t)w2 * 64 * 4;
+    // the intermediate's copy in LDS (formats whose lanes do not load it themselves)
+    const size_t hb = f->direct_h ? 0 : ((2 * n + (n / 8) * 4) + 15) & ~size_t(15);
+    const size_t per_row = (size_t)w2 * 64 * 4;
     if (hb + per_row > lds) return HH_ERR_UNSUPPORTED_DEVICE;
     const size_t rows_fit = (lds - hb) / per_row;
     int occ = 0;
