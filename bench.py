@@ -941,10 +941,9 @@ def bench_block(eng, pack, lay, stride, desc, args) -> int:
     ms_stack = timed(stack_step, args.steps)
     bytes_step = LAYERS * (layer_bytes() + 4 * D_MODEL)  # + the norm weights
     gbs = bytes_step / (ms_block / 1e3) / 1e9
-    persistent = os.environ.get("HAYAI_HIP_Q4K_STACK", "0") not in ("", "0")
     log(f"[bench] block: {ms_block * 1e3:.1f} us/step ({ms_block * 1e3 / LAYERS:.2f} us/layer), {gbs:.1f} GB/s; "
         f"plain FFN op {ms_ffn * 1e3 / LAYERS:.2f} us/layer; one stack call "
-        f"({'persistent Q4_K stack' if persistent else 'blocks per layer'}) {ms_stack * 1e3 / LAYERS:.2f} us/layer, "
+        f"(blocks per layer) {ms_stack * 1e3 / LAYERS:.2f} us/layer, "
         f"max diff vs the blocks {stack_diff:.2e} of max|FFN part|")
     cpu = None
     if not args.no_cpu_baseline:
@@ -974,7 +973,7 @@ def bench_block(eng, pack, lay, stride, desc, args) -> int:
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "us_per_layer": round(ms_block * 1e3 / LAYERS, 3),
         "plain_ffn_us_per_layer": round(ms_ffn * 1e3 / LAYERS, 3),
-        "stack_call": {"us_per_layer": round(ms_stack * 1e3 / LAYERS, 3), "persistent_q4k_stack": persistent,
+        "stack_call": {"us_per_layer": round(ms_stack * 1e3 / LAYERS, 3),
                        "max_rel_diff_vs_blocks": stack_diff},
         "roofline": roofline_step(gbs, "ring gate/up with the RMSNorm prologue + ring down with the residual epilogue"),
         "cpu_baseline": cpu,
@@ -1258,9 +1257,6 @@ def main() -> int:
                     help="--workload ffn / gemv weight format")
     ap.add_argument("--shape", default="8b", choices=["8b", "70b", "smollm"], help="--workload ffn shape")
     ap.add_argument("--layers", type=int, default=0, help="--workload ffn: layers (0: the shape's own count)")
-    ap.add_argument("--q4k-stack", action="store_true",
-                    help="--workload block: run the chain's one-call form on the persistent Q4_K stack "
-                         "(HAYAI_HIP_Q4K_STACK=1, set before the engine is created)")
     ap.add_argument("--m", type=int, default=4096, help="--workload gemv rows")
     ap.add_argument("--n", type=int, default=4096, help="--workload gemv columns")
     args = ap.parse_args()
@@ -1269,8 +1265,6 @@ def main() -> int:
               "d_ff across GPUs with one d_model all-reduce per layer, which is not built here.", file=sys.stderr)
         return 2
 
-    if args.q4k_stack:
-        os.environ["HAYAI_HIP_Q4K_STACK"] = "1"
     import hayai_amd
     from hayai_amd import synth
 

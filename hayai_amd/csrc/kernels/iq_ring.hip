@@ -14,7 +14,7 @@
 //   v = (g ^ m) + (m & 0x01010101),   m = 0xFF in every byte whose sign bit is set
 // and dotted with the activation's two int8 digits (v_dot4), the int32 sums of a group
 // meeting its scale once (per-32 x digits) or per granule of 8 (h digits, prefix-summed as
-// in hh_ffnp_h).  Codebook and sign masks sit in LDS (the lanes' indices diverge).
+// in hh_hd).  Codebook and sign masks sit in LDS (the lanes' indices diverge).
 //
 // Unit (lane) = 64 columns = two groups = 16 qs bytes (IQ3_XXS: + 8 scale/sign bytes) of a
 // 66- or 98-byte block.  Rows start 4-byte aligned (the host requires an even number of
@@ -114,7 +114,7 @@ HH_DEV void hh_iq_load_x(const hh_digits_ptr& xd, uint32_t u, hh_iq_x<NG>& x) {
 #pragma unroll
     for (int g = 0; g < NG; g++) x.s[g] = xd.sc[NG * u + g] * (1.0f / 256.0f);
 }
-// A lane's h bytes as loaded, apart from the arithmetic (as hh_ffnp_hraw).
+// A lane's h bytes as loaded, apart from the arithmetic (as hh_hd_raw).
 template <int NG>
 struct hh_iq_hraw {
     uint4 a[2 * NG], b[2 * NG];

@@ -52,7 +52,7 @@ HH_DEV void hh_moe_gu_ring_body(const hh_moe_ring_args& ra) {
     const uint32_t r1 = 8u * (uint32_t)(((uint64_t)(w + 1) * NG) / G);
     const uint32_t RR = 2u * (r1 - r0);  // row reads: (gate, up) of each row
     const uint32_t NI = (RR + RPI - 1) / RPI;
-    const uint32_t n1 = (NI + HH_FFNP_CW - 1) / HH_FFNP_CW;
+    const uint32_t n1 = (NI + HH_RING_CW - 1) / HH_RING_CW;
     const uint32_t n1p = (n1 + D - 1) / D * D;
 
     // LDS: [x digits][gate/up row sums][staging 128 B]
@@ -71,8 +71,8 @@ HH_DEV void hh_moe_gu_ring_body(const hh_moe_ring_args& ra) {
     __shared__ int s_sel[64];
     __shared__ float s_inv;
     __shared__ uint32_t s_kk;
-    constexpr uint32_t XT = (HH_FFNP_CW - 2) * HH_WAVE;
-    if (wave == HH_FFNP_CW - 1) {
+    constexpr uint32_t XT = (HH_RING_CW - 2) * HH_WAVE;
+    if (wave == HH_RING_CW - 1) {
         if (a.route) {
             int sel;
             const uint32_t kk = hh_route_select(a.r, 0, true, rl, &sel);
@@ -85,7 +85,7 @@ HH_DEV void hh_moe_gu_ring_body(const hh_moe_ring_args& ra) {
             s_ids[lane] = hh_moe_valid(a, a.ids[lane]);
             s_w[lane] = a.wts[lane];
         }
-    } else if (wave == HH_FFNP_CW - 2) {
+    } else if (wave == HH_RING_CW - 2) {
         if (a.route && a.r.gating != 1) {
             const float inv = hh_route_softmax(a.r, 0, true, rex);
             if (lane == 0) s_inv = inv;
@@ -99,7 +99,7 @@ HH_DEV void hh_moe_gu_ring_body(const hh_moe_ring_args& ra) {
     const uint32_t rin = lane / U1, u1 = lane % U1;
     const uint32_t oh = (u1 >> 2) * 144u, oq = oh + 16u + (u1 & 3u) * 32u;
     auto issue = [&](uint32_t j, hh_q4k_data& s) {
-        const uint32_t i = (wave + j * HH_FFNP_CW) * RPI + rin;
+        const uint32_t i = (wave + j * HH_RING_CW) * RPI + rin;
         const uint8_t* row = a.experts;  // padding, rows past the share, empty slots: expert 0's bytes
         if (i < RR) {
             const uint32_t r = r0 + (i >> 1), slot = r / dff;
@@ -122,7 +122,7 @@ HH_DEV void hh_moe_gu_ring_body(const hh_moe_ring_args& ra) {
 #pragma unroll
             for (int s = 0; s < D; s++) {
                 const uint32_t j = j0 + (uint32_t)s;
-                const uint32_t ib = (wave + j * HH_FFNP_CW) * RPI;  // first row read of the item
+                const uint32_t ib = (wave + j * HH_RING_CW) * RPI;  // first row read of the item
                 if (ib < RR) {                                       // wave-uniform
                     const float v = hh_group_sum<U1>(hh_q4k_unit(ring[s], xr));
                     const uint32_t i = ib + rin;
@@ -188,7 +188,7 @@ HH_DEV void hh_moe_dn_ring_body(const hh_moe_ring_args& ra) {
     extern __shared__ __attribute__((aligned(16))) char hh_smem[];
     __shared__ int s_ids[64];
     const hh_moe_args& a = ra.m;
-    constexpr uint32_t TEAM2 = WPT2 * HH_WAVE, TPW2 = HH_FFNP_CW / WPT2;
+    constexpr uint32_t TEAM2 = WPT2 * HH_WAVE, TPW2 = HH_RING_CW / WPT2;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % HH_WAVE;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / HH_WAVE);
@@ -228,22 +228,22 @@ HH_DEV void hh_moe_dn_ring_body(const hh_moe_ring_args& ra) {
     // every compute lane loads its own unit's digits of h' from global memory, ahead of its
     // ring, and starts as soon as they arrive (no copy into LDS, no barrier before the loop)
     hh_q4k_data ring[D];
-    hh_ffnp_h hr;
-    if (wave < HH_FFNP_CW) {
+    hh_hd hr;
+    if (wave < HH_RING_CW) {
         const int8_t* g1 = reinterpret_cast<const int8_t*>(ra.hx);
-        hh_ffnp_load_h(g1, g1 + K, reinterpret_cast<const float*>(g1 + 2 * (size_t)K), u2, hr);  // (lu & 3 = u2 & 3)
+        hh_hd_load(g1, g1 + K, reinterpret_cast<const float*>(g1 + 2 * (size_t)K), u2, hr);  // (lu & 3 = u2 & 3)
 #pragma unroll
         for (int s = 0; s < D; s++) issue((uint32_t)s, ring[s]);
     }
 
-    if (wave < HH_FFNP_CW) {
+    if (wave < HH_RING_CW) {
         for (uint32_t j0 = 0; j0 < n2p; j0 += D) {
 #pragma unroll
             for (int s = 0; s < D; s++) {
                 const uint32_t kk = j0 + (uint32_t)s;
                 const uint32_t rl = team2 + kk * TPW2;
                 if (q0 + rl < q1) {
-                    const float v = hh_ffnp_unit_g8(ring[s], hr);
+                    const float v = hh_q4k_unit_h(ring[s], hr);
                     part[rl * TEAM2 + lane2] = act2 ? v : 0.f;
                 }
                 issue(kk + D, ring[s]);

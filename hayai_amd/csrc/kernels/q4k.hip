@@ -100,9 +100,6 @@ HH_DEV void hh_digits8(const float (&v)[8], float scale, float inv, uint2& o1, u
 HH_DEV void hh_store_coherent(uint32_t* p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-HH_DEV uint64_t hh_load_coherent(const uint64_t* p) {
-    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Quantize n f32 values (n % 32 == 0) into digits: 4 lanes per 32-element sub-block,
 // chunk c = 8 elements.  Threads first, first + stride, ... take chunks (by default the
@@ -245,14 +242,8 @@ HH_DEV float hh_q4k_unit(const hh_q4k_data& d, const hh_q4k_x& xr) {
 //   R       rows per team step
 //   GATEUP  two matrices, output act(gate)*up (and optionally the digits of that output)
 //   XDIG    x arrives as pre-built digits (a.xq) instead of f32 (a.x)
-//   COH     digits exchanged with other workgroups of the same launch (fused FFN): the h
-//           digits are written and read with device-coherent accesses
-struct hh_no_gate {
-    HH_DEV bool operator()() const { return true; }
-};
-
-template <int WPT, int R, bool GATEUP, bool XDIG, bool COH = false, class Gate = hh_no_gate>
-HH_DEV void hh_q4k_body(const hh_q4k_args& a, Gate gate = {}) {
+template <int WPT, int R, bool GATEUP, bool XDIG>
+HH_DEV void hh_q4k_body(const hh_q4k_args& a) {
     extern __shared__ __attribute__((aligned(16))) char hh_smem[];
     constexpr int TEAM = WPT * HH_WAVE;
     constexpr int TPW = HH_Q4K_WAVES / WPT;  // teams per workgroup
@@ -278,18 +269,9 @@ HH_DEV void hh_q4k_body(const hh_q4k_args& a, Gate gate = {}) {
     constexpr uint32_t ROWS_PER_STEP = TPW * R;
     const uint32_t nsteps = (r1 - r0 + ROWS_PER_STEP - 1) / ROWS_PER_STEP;
 
-    // LDS: [x digits (f32 input mode, or staged copies of digits from other workgroups)]
-    //      [h rows (gate/up)] [team reduction slots]
+    // LDS: [x digits (f32 input mode)] [h rows (gate/up)] [team reduction slots]
     char* lds = hh_smem;
     hh_digits_ptr xd = a.xq;
-    if constexpr (XDIG && COH) {
-        // Staged copy of digits written by other workgroups of this launch (filled below).
-        xd.q1 = reinterpret_cast<int8_t*>(lds);
-        xd.q2 = xd.q1 + a.n;
-        xd.sc = reinterpret_cast<float*>(xd.q2 + a.n);
-        xd.sum = xd.sc + a.n / 32;
-        lds = reinterpret_cast<char*>(xd.sum + a.n / 32);
-    }
     if constexpr (!XDIG) {
         xd.q1 = reinterpret_cast<int8_t*>(lds);
         xd.q2 = xd.q1 + a.n;
@@ -361,18 +343,6 @@ HH_DEV void hh_q4k_body(const hh_q4k_args& a, Gate gate = {}) {
     // x prologue so HBM latency overlaps the digit conversion.
     hh_q4k_data A[NV][R], B[NV][R];
     if (nsteps > 0) load_step(0, A);
-    if constexpr (XDIG && COH) {
-        // Digits produced by other workgroups: the first two row steps' weights are in
-        // flight while this workgroup waits for them (gate), then they are copied once into
-        // LDS with coalesced device-coherent loads (q1, q2, sc, sum are contiguous).
-        if (nsteps > 1) load_step(1, B);
-        if (!gate()) return;
-        const uint32_t words = (2 * a.n + (a.n / 32) * 8) / 8;
-        const uint64_t* src = reinterpret_cast<const uint64_t*>(a.xq.q1);
-        uint64_t* dst = reinterpret_cast<uint64_t*>(xd.q1);
-        for (uint32_t i = tid; i < words; i += blockDim.x) dst[i] = hh_load_coherent(src + i);
-        __syncthreads();
-    }
     if constexpr (!XDIG) {
         hh_quantize_digits(a.x, a.n, xd);
         __syncthreads();
@@ -380,7 +350,7 @@ HH_DEV void hh_q4k_body(const hh_q4k_args& a, Gate gate = {}) {
     if (act) hh_q4k_load_lane_x(xd, lane, xr);
 
     for (uint32_t k = 0; k < nsteps; k += 2) {
-        if (k + 1 < nsteps && !(XDIG && COH && k == 0)) load_step(k + 1, B);
+        if (k + 1 < nsteps) load_step(k + 1, B);
         compute_step(k, A);
         if (k + 1 >= nsteps) break;
         if (k + 2 < nsteps) load_step(k + 2, A);
@@ -392,7 +362,7 @@ HH_DEV void hh_q4k_body(const hh_q4k_args& a, Gate gate = {}) {
         if (a.hq.q1 != nullptr && r1 > r0) {
             __syncthreads();
             const hh_digits_ptr dst{a.hq.q1 + r0, a.hq.q2 + r0, a.hq.sc + r0 / 32, a.hq.sum + r0 / 32};
-            hh_quantize_digits<COH>(hl, r1 - r0, dst);
+            hh_quantize_digits(hl, r1 - r0, dst);
         }
     }
 }
@@ -415,7 +385,8 @@ HH_Q4K_WPT(4)
 HH_Q4K_WPT(8)
 
 // ----------------------------------------------------------------------------------------
-// One launch per FFN layer: gate/up phase, grid-wide barrier, down phase.
+// Grid-wide barrier of the persistent launches (small_ffn.hip, small_stack.hip, the grouped
+// MoE kernels).
 //
 // All workgroups are co-resident (the host sizes the grid from the occupancy API), so a
 // grid barrier is safe; it is still bounded: a wait that exceeds ~2^20 sleeps gives up,
@@ -437,19 +408,13 @@ HH_Q4K_WPT(8)
 // The epoch changes only at a release, which needs every workgroup's arrival, so all
 // workgroups of a launch read the same value: the one the previous launch on this state
 // released (launches on one stream do not overlap).  No argument changes between
-// launches, so a captured graph replays them as they are.  The h digits cross workgroups
-// (and XCDs) through device-coherent stores and loads, ordered by s_waitcnt before the
-// arrival and by the barrier.
+// launches, so a captured graph replays them as they are.  Data that crosses workgroups
+// (and XCDs) goes through device-coherent stores and loads, ordered by s_waitcnt before
+// the arrival and by the barrier.
 #define HH_BAR_GROUPS 16
 #define HH_BAR_LINE 32  // u32 words per 128-byte line
 #define HH_BAR_WORDS (HH_BAR_LINE * (2 * HH_BAR_GROUPS + 4))
 #define HH_BAR_STACK_EPOCH ((2 * HH_BAR_GROUPS + 3) * HH_BAR_LINE)
-
-struct hh_q4k_ffn_args {
-    hh_q4k_args gu;  // gate/up: writes h (f32) and the digits of h
-    hh_q4k_args dn;  // down: reads the digits of h
-    unsigned* bar;   // HH_BAR_WORDS words
-};
 
 HH_DEV unsigned hh_atomic_add_agent(unsigned* p, unsigned v) {
     return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -470,64 +435,3 @@ HH_DEV unsigned hh_barrier_epoch(unsigned* bar) { return hh_load_agent(bar + (2 
 // arrival that overtook it could complete a release whose epoch store the load then sees.
 HH_DEV void hh_barrier_gen_ready(unsigned gen) { asm volatile("" ::"v"(gen) : "memory"); }
 
-// The caller has completed (s_waitcnt + workgroup barrier) every store that other
-// workgroups read after this barrier.
-HH_DEV bool hh_grid_barrier(unsigned* bar, unsigned gen) {
-    __shared__ int ok;
-    if (threadIdx.x == 0) {
-        const unsigned G = gridDim.x < HH_BAR_GROUPS ? gridDim.x : HH_BAR_GROUPS;
-        const unsigned g = blockIdx.x % HH_BAR_GROUPS;
-        const unsigned members = (gridDim.x - g + HH_BAR_GROUPS - 1) / HH_BAR_GROUPS;
-        unsigned* cnt = bar + g * HH_BAR_LINE;
-        unsigned* flag = bar + (HH_BAR_GROUPS + g) * HH_BAR_LINE;
-        unsigned* top = bar + 2 * HH_BAR_GROUPS * HH_BAR_LINE;
-        unsigned* err = top + HH_BAR_LINE;
-        hh_barrier_gen_ready(gen);
-        if (hh_atomic_add_agent(cnt, 1u) == members - 1) {
-            hh_store_agent(cnt, 0u);
-            if (hh_atomic_add_agent(top, 1u) == G - 1) {
-                hh_store_agent(top, 0u);
-                __builtin_amdgcn_s_waitcnt(0);
-                for (unsigned k = 0; k < G; k++) hh_store_agent(bar + (HH_BAR_GROUPS + k) * HH_BAR_LINE, gen);
-                hh_store_agent(top + 2 * HH_BAR_LINE, gen);
-            }
-        }
-        int good = 1;
-        for (unsigned spins = 0; hh_load_agent(flag) != gen; spins++) {
-            __builtin_amdgcn_s_sleep(4);
-            if (spins > (1u << 20)) {
-                good = 0;
-                hh_store_agent(err, 1u);
-                break;
-            }
-        }
-        ok = good;
-    }
-    __syncthreads();  // later device-coherent loads are issued after the wait completed
-    return ok != 0;
-}
-
-template <int WPT_GU, int WPT_D>
-HH_DEV void hh_q4k_ffn_body(const hh_q4k_ffn_args& a) {
-    const unsigned epoch = hh_barrier_epoch(a.bar);
-    hh_q4k_body<WPT_GU, 1, true, false, true>(a.gu);
-    // Every thread's device-coherent h-digit stores are complete before the workgroup
-    // arrives (vmcnt covers stores on this architecture).  No fence: a release/acquire
-    // fence at agent scope writes back and invalidates the whole L2 of the XCD.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    // The down phase issues its first weight loads, then waits at the grid barrier.
-    hh_q4k_body<WPT_D, 2, false, true, true>(a.dn, [&]() { return hh_grid_barrier(a.bar, epoch + 1u); });
-}
-
-// hh_q4k_ffn_g<WPT gate/up>_d<WPT down>
-#define HH_Q4K_FFN(G, D)                                                                     \
-    extern "C" __global__ void __launch_bounds__(HH_Q4K_BLOCK) hh_q4k_ffn_g##G##_d##D(const hh_q4k_ffn_args a) { \
-        hh_q4k_ffn_body<G, D>(a);                                                            \
-    }
-HH_Q4K_FFN(1, 1)
-HH_Q4K_FFN(1, 2)
-HH_Q4K_FFN(1, 4)
-HH_Q4K_FFN(2, 4)
-HH_Q4K_FFN(2, 8)
-HH_Q4K_FFN(4, 8)

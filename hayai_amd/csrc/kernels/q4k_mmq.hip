@@ -10,7 +10,7 @@
 //   hh_q4k_mmq_gu_s<S>_t<TT> H[b][m] = act(W_gate . X) * (W_up . X) (prefill_batched's
 //                            gate/up and SiLU * up, crates/hayai-core/src/prefill_wave.rs:
 //                            569-584, fused)
-// (Compiled after q4k_mm.hip: shares its vector types and coherent partial-sum helpers.)
+// (Compiled after mm_common.hip: shares its vector types and coherent partial-sum helpers.)
 //
 // Arithmetic.  A Q4_K weight is d * sc_j * q - dmin * m_j for sub-block j (32 columns) and a
 // token element is s_tj * xq (its block's scale), so one output is

@@ -6,10 +6,10 @@
 //   hh_q4k_mmr_dn_s<S>  Y = W_down . H from those stages (prefill_wave.rs:579-584)
 //   hh_q4k_mmr_s<S>     Y = W . X (ggml_gemv_batched_q4_k, crates/hayai-opencl/src/
 //                       compute.rs:179-257)
-// (Compiled after q4k_mm.hip: the same MFMA arithmetic, tile decode and token-stage layout;
+// (Compiled after mm_common.hip: the same MFMA arithmetic, tile decode and token-stage layout;
 // hh_mm_prep writes the token stages of X once per call.)
 //
-// Token stages.  X enters as hi + lo f16 halves (the 17 KB stages of q4k_mm.hip: f32-level
+// Token stages.  X enters as hi + lo f16 halves (the 17 KB stages of mm_common.hip: f32-level
 // accuracy; a single f16 rounding of the FFN input costs up to ~2e-3 of relative output
 // error).  h enters the down projection as one f16 per element plus hi/lo sums (9 KB stages:
 // [0, 8192) operands, [8192, 8704) sums hi, [8704, 9216) sums lo); its rounding costs at most

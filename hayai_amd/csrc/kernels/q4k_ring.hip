@@ -3,11 +3,12 @@
 //                          (ffn_begin_gate_up_scratch, crates/hayai-core/src/
 //                          stream_infer.rs:3752-3808, with the activation of :3836-3840)
 //   hh_q4k_dn_ring_d<W2>:  y = W_down . h from those digits (ffn_finish_scratch, :3809-3864)
-// (Compiled after q4k_ffn.hip in the same translation unit; uses its ring and digit helpers.)
+// (Compiled after ring_common.hip in the same translation unit; uses its digit helpers.)
 //
 // Each launch is one weight stream with nothing else on its path: a kernel boundary costs
-// less than any exchange of h inside one launch (see q4k_ffn.hip), so the layer is split
-// there.  Both kernels use the persistent kernel's ring: every compute wave keeps D items
+// less than an exchange of h between the workgroups of one launch (measured: a grid barrier
+// plus the exchange under a full HBM stream took ~5 us, the boundary plus the h hop ~3 us),
+// so the layer is split there.  In both kernels every compute wave keeps D items
 // (one 64-column Q4_K unit of one row per lane: 16-byte block header + 32 qs bytes) in
 // flight, addressed by a wave-uniform row base plus fixed lane offsets, so the wait counts
 // are static and HBM never waits for the math.
@@ -29,7 +30,7 @@
 //                    wave reduction per row
 //   DIRECT_H         down: each lane loads its h digits from global memory itself
 
-#define HH_RING_BLOCK (HH_FFNP_CW * HH_WAVE)
+#define HH_RING_BLOCK (HH_RING_CW * HH_WAVE)
 
 // Phase timeline of the ring kernels, compiled in only for the timeline tool
 // (csrc/trace/ring_timeline.cpp builds a separate code object with HH_RING_TRACE): one
@@ -113,7 +114,7 @@ struct hh_ring_q4k {
     };
     typedef hh_q4k_data data;
     typedef hh_q4k_x xr_t;
-    typedef hh_ffnp_h hr_t;
+    typedef hh_hd hr_t;
     static HH_DEV lane_t lane(uint32_t u) {
         const uint32_t oh = (u >> 2) * 144u;
         return lane_t{oh, oh + 16u + (u & 3u) * 32u};
@@ -126,15 +127,15 @@ struct hh_ring_q4k {
     static HH_DEV const uint4* tables() { return nullptr; }
     static HH_DEV void load_x(const hh_digits_ptr& xd, uint32_t u, xr_t& xr) { hh_q4k_load_lane_x(xd, u, xr); }
     static HH_DEV void load_h(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hr_t& h) {
-        hh_ffnp_load_h(q1, q2, sc, u, h);
+        hh_hd_load(q1, q2, sc, u, h);
     }
-    typedef hh_ffnp_hraw hraw_t;
+    typedef hh_hd_raw hraw_t;
     static HH_DEV void load_h_raw(const int8_t* q1, const int8_t* q2, const float* sc, uint32_t u, hraw_t& r) {
-        hh_ffnp_load_h_raw(q1, q2, sc, u, r);
+        hh_hd_load_raw(q1, q2, sc, u, r);
     }
-    static HH_DEV void make_h(const hraw_t& r, uint32_t u, hr_t& h) { hh_ffnp_make_h(r, u, h); }
+    static HH_DEV void make_h(const hraw_t& r, uint32_t u, hr_t& h) { hh_hd_make(r, u, h); }
     static HH_DEV float unit_x(const data& s, const lane_t&, const xr_t& xr, const char*) { return hh_q4k_unit(s, xr); }
-    static HH_DEV float unit_h(const data& s, const lane_t&, const hr_t& h, const char*) { return hh_ffnp_unit_g8(s, h); }
+    static HH_DEV float unit_h(const data& s, const lane_t&, const hr_t& h, const char*) { return hh_q4k_unit_h(s, h); }
 };
 
 // Gate/up: workgroup w owns the 8-row granules [w*NG/G, (w+1)*NG/G) of W_gate and W_up; a
@@ -144,7 +145,7 @@ struct hh_ring_q4k {
 template <class F, int WPT1, int D, int P, bool NORM>
 HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
     extern __shared__ __attribute__((aligned(16))) char hh_smem[];
-    constexpr uint32_t TEAM1 = WPT1 * HH_WAVE, TPW1 = HH_FFNP_CW / WPT1;
+    constexpr uint32_t TEAM1 = WPT1 * HH_WAVE, TPW1 = HH_RING_CW / WPT1;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % HH_WAVE;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / HH_WAVE);
@@ -230,11 +231,11 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
     if constexpr (TAB16 > 0) {
         if (tid < TAB16) reinterpret_cast<uint4*>(tabs)[tid] = tab;
     }
-    hh_ffnp_digits_chunk(t0, t1, c, has, xd);
+    hh_x_digits_chunk(t0, t1, c, has, xd);
     for (uint32_t c2 = c + HH_RING_BLOCK; c2 < dm / 8; c2 += HH_RING_BLOCK) {
         float4 v0 = x4[2 * c2], v1 = x4[2 * c2 + 1];  // d_model > 4096: later passes
         if constexpr (NORM) hh_norm8(v0, v1, n4[2 * c2], n4[2 * c2 + 1], 1.f);
-        hh_ffnp_digits_chunk(v0, v1, c2, true, xd);
+        hh_x_digits_chunk(v0, v1, c2, true, xd);
     }
 #pragma unroll
     for (int s = P; s < D; s++) issue((uint32_t)s, ring[s]);
@@ -299,7 +300,7 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
             const float* red = reinterpret_cast<const float*>(stage);
             float tot = 0.f;
 #pragma unroll
-            for (int k = 0; k < HH_FFNP_CW; k++) tot += red[k];
+            for (int k = 0; k < HH_RING_CW; k++) tot += red[k];
             inv = 1.0f / sqrtf(tot / (float)dm + a.eps);
         }
         // h = act(g) * u, two int8 digits per element, one scale per granule of 8 rows: one
@@ -354,11 +355,11 @@ HH_DEV void hh_gu_ring_body(const hh_gur_args& a) {
 // compute waves read from there (the format's tables, the intermediate unless F::DIRECT_H),
 // so neither queues behind the other's requests; lane partials meet in LDS and a 32-lane DPP
 // reduction per row writes y (fixed order: deterministic).
-#define HH_DN_BLOCK ((HH_FFNP_CW + 1) * HH_WAVE)
+#define HH_DN_BLOCK ((HH_RING_CW + 1) * HH_WAVE)
 template <class F, int WPT2, int D>
 HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
     extern __shared__ __attribute__((aligned(16))) char hh_smem[];
-    constexpr uint32_t TEAM2 = WPT2 * HH_WAVE, TPW2 = HH_FFNP_CW / WPT2;
+    constexpr uint32_t TEAM2 = WPT2 * HH_WAVE, TPW2 = HH_RING_CW / WPT2;
     constexpr bool DIRECT_H = F::DIRECT_H;
     constexpr bool TABLES = F::TAB_BYTES > 0;  // with direct h loads the copy wave brings only these
     const uint32_t tid = threadIdx.x;
@@ -405,7 +406,7 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
     // workgroup many times) the copy wave brings the intermediate (and the tables) into LDS.
     typename F::data ring[D];
     typename F::hr_t hr;
-    if (wave < HH_FFNP_CW) {
+    if (wave < HH_RING_CW) {
         if constexpr (DIRECT_H) {
             // h's loads, then every ring item's, and only then the arithmetic on h (which
             // waits for h): no ring load is held back behind the intermediate's arrival
@@ -444,7 +445,7 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
     if constexpr (!DIRECT_H || TABLES) __syncthreads();
     HH_RING_MARK(1, a.wd, 1, tid == 0);
 
-    if (wave < HH_FFNP_CW) {
+    if (wave < HH_RING_CW) {
         if constexpr (!DIRECT_H) F::load_h(hq1, hq2, hsc, u2, hr);
         auto consume = [&](uint32_t k, const typename F::data& s) {
             const uint32_t rl = team2 + k * TPW2;  // local row

@@ -7,7 +7,7 @@
 // finishes its rows of y = W_down . h (:3809-3864) with the down weights already in
 // registers.  Teams of TEAM1 / TEAM2 lanes per row (lane = block unit, as the team kernels of
 // gemv.hip), at most two rows per team and phase.
-// (Compiled after q4k_ffn.hip in the same translation unit: the grid barrier.)
+// (Compiled after ring_common.hip in the same translation unit: the grid barrier.)
 
 struct hh_sffn_args {
     const uint8_t* wg;

@@ -376,138 +376,14 @@ hh_status hh_engine::enqueue_gateup(int tg, int tu, size_t d_ff, size_t d_model,
     return launch(fn, (uint32_t)((d_ff + 255) / 256), 256, a);
 }
 
-// Fused FFN kernel arguments and grid-barrier state (q4k.hip): 16 arrival-counter lines,
-// 16 release-flag lines, the group counter, the error word, the barrier epoch and the
-// FFN-stack epoch, 128 bytes each.
-struct hh_q4k_ffn_args {
-    hh_q4k_args gu;
-    hh_q4k_args dn;
-    unsigned* bar;
-};
+// Grid-barrier state (q4k.hip): 16 arrival-counter lines, 16 release-flag lines, the group
+// counter, the error word, the barrier epoch and the FFN-stack epoch, 128 bytes each.
 constexpr size_t kBarLine = 128;
 constexpr size_t kBarBytes = kBarLine * (2 * 16 + 4);
 constexpr size_t kBarEpochOffset = kBarLine * (2 * 16 + 2);  // the epochs survive an error reset
 constexpr size_t kBarErrOffset = kBarLine * (2 * 16 + 1);
 // the grouped MoE's routing-arrival counter (hh_moe_route_prep): word 4 of the last line
 constexpr size_t kBarMoeArrivalsOffset = kBarLine * (2 * 16 + 3) + 4 * 4;
-
-hh_status hh_engine::enqueue_q4k_ffn(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
-                                     const float* x, float* y) {
-    const size_t dm = d->d_model, df = d->d_ff;
-    // (the cooperative launch API is not captured into graphs)
-    if ((capturing && coop_launch) || !ffn_fused || q4k_generic || dm % 256 || df % 256 || dm / 64 > 512 || df / 64 > 512 ||
-        (((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd | (uintptr_t)x) & 15u))
-        return HH_ERR_UNSUPPORTED_DEVICE;
-    int wg_t = 1, wd_t = 1;
-    while ((size_t)wg_t * 64 < dm / 64) wg_t *= 2;
-    while ((size_t)wd_t * 64 < df / 64) wd_t *= 2;
-    const std::string name = "hh_q4k_ffn_g" + std::to_string(wg_t) + "_d" + std::to_string(wd_t);
-    hipFunction_t fn;
-    if (fns.find(name) == fns.end() && hipModuleGetFunction(&fn, module, name.c_str()) != hipSuccess)
-        return HH_ERR_UNSUPPORTED_DEVICE;
-    HH_TRY(kernel(name, &fn));
-    HH_TRY(grow(&ws_h, &ws_h_cap, df * sizeof(float)));
-    HH_TRY(grow(&ws_hq, &ws_hq_cap, hh_digits_bytes(df)));
-    const int waves = 8;
-    const size_t xbytes = hh_digits_bytes(dm);
-    const size_t red_bytes = (size_t)waves * 4 * sizeof(float);
-    int occ = blocks_per_cu_override;
-    if (occ <= 0) {
-        auto it = blocks_per_cu.find(name);
-        if (it != blocks_per_cu.end()) {
-            occ = it->second;
-        } else {
-            if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &occ, fn, waves * 64, std::max(xbytes + 64 * sizeof(float), hh_digits_bytes(df)) + red_bytes) !=
-                    hipSuccess ||
-                occ < 1)
-                occ = 1;
-            blocks_per_cu[name] = occ;
-        }
-    }
-    const size_t S = df / 32;
-    const size_t grid = std::max<size_t>(1, std::min((size_t)props.multiProcessorCount * occ, S));
-    const uint32_t hrows = (uint32_t)(32 * ((S + grid - 1) / grid));
-    // gate/up phase: x digits + h rows + reduction; down phase: staged h digits + reduction
-    const size_t smem = std::max(xbytes + (size_t)hrows * sizeof(float), hh_digits_bytes(df)) + red_bytes;
-    hh_q4k_ffn_args a{};
-    a.gu = hh_q4k_args{wg, wu, x, (float*)ws_h, hh_digits_ptr{}, digits_at(ws_hq, df), (uint32_t)df, (uint32_t)dm,
-                       (uint64_t)((dm / 256) * 144), d->act, hrows};
-    a.dn = hh_q4k_args{wd, nullptr, nullptr, y, digits_at(ws_hq, df), hh_digits_ptr{}, (uint32_t)dm, (uint32_t)df,
-                       (uint64_t)((df / 256) * 144), 0, 0};
-    a.bar = (unsigned*)grid_sync;
-    void* params[] = {&a};
-    hipError_t err;
-    if (coop_launch)
-        err = hipModuleLaunchCooperativeKernel(fn, (uint32_t)grid, 1, 1, waves * 64, 1, 1, (unsigned)smem, stream,
-                                               params);
-    else
-        err = hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, waves * 64, 1, 1, (unsigned)smem, stream, params,
-                                    nullptr);
-    if (err != hipSuccess) return hip_fail(err, "launch(fused q4k ffn)");
-    return HH_OK;
-}
-
-// Must match struct hh_ffnp_args in kernels/q4k_ffn.hip.
-struct FfnpArgs {
-    const uint8_t* wg;
-    const uint8_t* wu;
-    const uint8_t* wd;
-    const float* x;
-    float* y;
-    uint8_t* hx;
-    unsigned* bar;
-    uint64_t rb1, rb2;
-    uint32_t d_model, d_ff;
-    int32_t act;
-};
-
-hh_status hh_engine::enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu,
-                                      const uint8_t* wd, const float* x, float* y) {
-    const size_t dm = d->d_model, df = d->d_ff;
-    if (!ffnp || q4k_generic || dm % 256 || df % 256 || dm > 8192 || df > 32768 ||
-        (((uintptr_t)wg | (uintptr_t)wu | (uintptr_t)wd | (uintptr_t)x) & 15u))
-        return HH_ERR_UNSUPPORTED_DEVICE;
-    const int w1 = dm <= 4096 ? 1 : 2;
-    int w2 = 1;
-    while ((size_t)w2 * 64 < df / 64) w2 *= 2;
-    if (w2 < w1) w2 = w1;  // instantiated pairs: g1 with d1..d8, g2 with d2..d8
-    const std::string name = "hh_q4k_ffnp_g" + std::to_string(w1) + "_d" + std::to_string(w2);
-    hipFunction_t fn;
-    HH_TRY(kernel(name, &fn));
-    const int block = 9 * 64;  // 8 compute waves + the exchange wave
-    const size_t G0 = (size_t)props.multiProcessorCount;
-    // LDS: digits (x, then h) + gate/up row sums + down lane partials + 128 B staging (the
-    // kernel's layout)
-    const size_t NG = df / 8;
-    const size_t rr_max = 2 * 8 * ((NG + G0 - 1) / G0);
-    const size_t rows2_max = (dm + G0 - 1) / G0;
-    const size_t dig = std::max(2 * dm + (dm / 32) * 8, 2 * df + (df / 8) * 4);
-    const size_t smem = ((dig + 15) & ~size_t(15)) + ((rr_max * w1 + 3) & ~size_t(3)) * 4 +
-                        rows2_max * (size_t)w2 * 64 * 4 + 128;
-    if (smem > props.sharedMemPerBlock) return HH_ERR_UNSUPPORTED_DEVICE;
-    int occ = 0;
-    auto it = blocks_per_cu.find(name);
-    if (it != blocks_per_cu.end()) {
-        occ = it->second;
-    } else {
-        if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, block, smem) != hipSuccess) occ = 0;
-        blocks_per_cu[name] = occ;
-    }
-    // Every workgroup must be resident at once (grid barrier): one per CU.  Never more, even
-    // when the occupancy calculator reports room for two: it counts wave slots per CU, but a
-    // 9-wave workgroup puts 3 waves on one SIMD, so a second one may not fit beside it.
-    if (occ < 1) return HH_ERR_UNSUPPORTED_DEVICE;
-    const size_t grid = G0;
-    HH_TRY(grow(&ws_hq, &ws_hq_cap, 3 * df + 16));
-    FfnpArgs a{wg, wu, wd, x, y, (uint8_t*)ws_hq, (unsigned*)grid_sync, (uint64_t)((dm / 256) * 144),
-               (uint64_t)((df / 256) * 144), (uint32_t)dm, (uint32_t)df, d->act};
-    void* params[] = {&a};
-    hipError_t err =
-        hipModuleLaunchKernel(fn, (uint32_t)grid, 1, 1, block, 1, 1, (unsigned)smem, stream, params, nullptr);
-    if (err != hipSuccess) return hip_fail(err, "launch(persistent q4k ffn)");
-    return HH_OK;
-}
 
 // Must match struct hh_gur_args / hh_dnr_args in kernels/q4k_ring.hip.
 struct GurArgs {  // the ring gate/up kernels' scalar parameters (HH_GUR_PARAMS, q4k_ring.hip)
@@ -707,7 +583,6 @@ hh_status hh_engine::check_device_error() {
         // exchange words go back to tag 0, which no launch uses.
         HH_TRY_HIP(hipMemset(grid_sync, 0, kBarEpochOffset), "hipMemset(grid_sync)");
         if (ws_stk) HH_TRY_HIP(hipMemset(ws_stk, 0, ws_stk_cap), "hipMemset(stack exchange)");
-        if (ws_qstk) HH_TRY_HIP(hipMemset(ws_qstk, 0, ws_qstk_cap), "hipMemset(stack exchange)");
         return fail(HH_ERR_RUNTIME, "grid-wide exchange timed out (workgroups not co-resident)");
     }
     return HH_OK;
@@ -797,17 +672,6 @@ hh_status hh_engine::enqueue_ffn(const hh_ffn_desc* d, const uint8_t* pack, cons
         ffn_stage_valid = false;
         ffn_calls += 3;
         return HH_OK;
-    }
-    if (d->type_gate == HH_TYPE_Q4_K && d->type_up == HH_TYPE_Q4_K && d->type_down == HH_TYPE_Q4_K) {
-        hh_status fst = enqueue_q4k_ffnp(d, pack + d->gate_off, pack + d->up_off, pack + d->down_off, x, y);
-        if (fst == HH_ERR_UNSUPPORTED_DEVICE)
-            fst = enqueue_q4k_ffn(d, pack + d->gate_off, pack + d->up_off, pack + d->down_off, x, y);
-        if (fst == HH_OK) {
-            ffn_stage_valid = false;
-            ffn_calls += 3;
-            return HH_OK;
-        }
-        if (fst != HH_ERR_UNSUPPORTED_DEVICE) return fst;
     }
     if (d->type_gate == d->type_up && d->type_up == d->type_down &&
         (d->type_gate == HH_TYPE_Q4_0 || d->type_gate == HH_TYPE_Q8_0)) {
@@ -966,83 +830,11 @@ hh_status hh_engine::enqueue_small_stack(const hh_ffn_desc* d, const uint8_t* pa
     return HH_OK;
 }
 
-// Must match struct hh_qstk_args in kernels/q4k_stack.hip.
-struct QstkArgs {
-    const uint8_t* pack;
-    const float* norm;
-    const float* x;
-    float* y;
-    uint64_t* hx;
-    uint64_t* xx;
-    unsigned* bar;
-    uint64_t stride, off_g, off_u, off_d, rb1, rb2;
-    uint32_t norm_stride, d_model, d_ff, n_layers;
-    uint32_t lds_wd, lds_hx;
-    float eps;
-    int32_t act;
-};
-
-// Consecutive all-Q4_K FFN residual blocks in one persistent launch (q4k_stack.hip), opt-in
-// (HAYAI_HIP_Q4K_STACK=1: measured slower than one ring block per layer, 32 vs 23.7 us per
-// 8B layer): one workgroup per CU (every one resident: the exchanges poll), 8 compute waves
-// + 3 exchange waves + 1 DMA wave; each workgroup's share of W_down (its d_model / G rows)
-// lives in LDS, at most 16 rows.
-// Needs d_model <= 4096 (one wave per gate/up row), d_ff <= 16384 (four waves per down row),
-// both multiples of 256, a grid that gives every workgroup a down row and an h granule, and
-// a down share that fits beside the digits.
-hh_status hh_engine::enqueue_q4k_stack(const hh_ffn_desc* d, const uint8_t* pack, size_t stride, size_t n_layers,
-                                       const float* norm, size_t norm_stride, float eps, const float* x, float* y) {
-    const size_t dm = d->d_model, df = d->d_ff;
-    const size_t G = (size_t)props.multiProcessorCount;
-    if (!q4k_stack || q4k_generic || d->type_gate != HH_TYPE_Q4_K || d->type_up != HH_TYPE_Q4_K ||
-        d->type_down != HH_TYPE_Q4_K || dm % 256 || df % 256 || dm > 4096 || df > 16384 || dm < G || df / 8 < G ||
-        (dm + G - 1) / G > 16 ||
-        n_layers > 0x3FFFFFFFu || norm_stride > 0xFFFFFFFFu || (norm_stride & 3u) ||
-        (((uintptr_t)pack | d->gate_off | d->up_off | d->down_off | stride) & 15u) || ((uintptr_t)x & 15u) ||
-        ((uintptr_t)norm & 15u) || ((uintptr_t)y & 3u))
-        return HH_ERR_UNSUPPORTED_DEVICE;
-    const size_t wpt2 = df <= 8192 ? 2 : 4;
-    const size_t rb1 = (dm / 256) * 144, rb2 = (df / 256) * 144;
-    const size_t nrow_max = (dm + G - 1) / G;
-    const size_t lds_wd = (nrow_max * rb2 + 15) & ~(size_t)15;
-    // h digits (q1, q2, bf16 scales), or x's digits and x itself staged after them
-    const size_t lds_hx =
-        (std::max(2 * df + 2 * (df / 8), ((2 * dm + (dm / 32) * 8 + 15) & ~(size_t)15) + 4 * dm) + 15) & ~(size_t)15;
-    auto al4 = [](size_t n) { return (n + 3) & ~(size_t)3; };
-    const size_t tail = al4(16 * ((df / 8 + G - 1) / G)) + al4(nrow_max * wpt2) + al4(3) + al4(2 * nrow_max);
-    const size_t smem = lds_wd + lds_hx + 4 * tail;
-    if (smem + 16 > (size_t)props.sharedMemPerBlock) return HH_ERR_UNSUPPORTED_DEVICE;
-    // ring depth 3, at most 24 W_down copies of 1 KB in flight per CU
-    const std::string name = "hh_q4k_stk_d" + std::to_string(wpt2) + "_r3_t24";
-    hipFunction_t fn;
-    HH_TRY(kernel(name, &fn));
-    int per_cu = 0;
-    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 12 * 64, smem) != hipSuccess || per_cu < 1)
-        return HH_ERR_UNSUPPORTED_DEVICE;
-    // h words padded to whole gather passes (3 exchange waves x 64 lanes x 14 words), x words
-    // by one exchange wave's reach (64 lanes x 22 words) past d_model (q4k_stack.hip)
-    const size_t hpad = (3 * (df / 8) + 2687) / 2688 * 2688, xpad = dm + 64 * 22;
-    const size_t need = (hpad + xpad) * sizeof(uint64_t);
-    if (ws_qstk_cap < need) {
-        HH_TRY(grow(&ws_qstk, &ws_qstk_cap, need));
-        HH_TRY_HIP(hipMemset(ws_qstk, 0, ws_qstk_cap), "hipMemset(stack exchange)");
-    }
-    QstkArgs a{pack, norm, x, y, (uint64_t*)ws_qstk, (uint64_t*)ws_qstk + hpad, (unsigned*)grid_sync,
-               (uint64_t)stride, (uint64_t)d->gate_off, (uint64_t)d->up_off, (uint64_t)d->down_off, (uint64_t)rb1,
-               (uint64_t)rb2, (uint32_t)norm_stride, (uint32_t)dm, (uint32_t)df, (uint32_t)n_layers,
-               (uint32_t)lds_wd, (uint32_t)lds_hx, eps, d->act};
-    void* params[] = {&a};
-    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)G, 1, 1, 12 * 64, 1, 1, (unsigned)smem, stream, params, nullptr);
-    if (err != hipSuccess) return hip_fail(err, "launch(q4k ffn stack)");
-    return HH_OK;
-}
-
 hh_status hh_engine::enqueue_ffn_block_stack(const hh_ffn_desc* d, const uint8_t* pack, size_t stride,
                                              size_t n_layers, const float* norm, size_t norm_stride, float eps,
                                              const float* x, float* y) {
     if (n_layers == 0) return HH_OK;
     hh_status st = enqueue_small_stack(d, pack, stride, n_layers, norm, norm_stride, eps, x, y);
-    if (st == HH_ERR_UNSUPPORTED_DEVICE) st = enqueue_q4k_stack(d, pack, stride, n_layers, norm, norm_stride, eps, x, y);
     if (st == HH_OK) {
         ffn_stage_valid = false;
         ffn_calls += 3 * n_layers;
@@ -1086,30 +878,15 @@ hh_status hh_engine::enqueue_ffn_block(const hh_ffn_desc* d, const uint8_t* pack
 
 // ---------------------------------------------------------------- batched (MFMA) ------
 
-// Kernel argument blocks of q4k_mm.hip (same layout).
-struct hh_mm_args {
-    const uint8_t* w0;
-    const uint8_t* w1;
-    const void* xop;
-    float* y;
-    void* hop;
-    float* part;
-    unsigned* cnt;
-    uint32_t m, n, b, ksg;
-    uint64_t row_bytes;
-    int32_t act;
-    uint32_t pad;
-};
+// Kernel argument block of hh_mm_prep (mm_common.hip, same layout).
 struct hh_mm_prep_args {
     const float* x;
     void* xop;
     uint32_t b, n, T, pad;
 };
 constexpr size_t kMmMaxTokens = 64;  // tokens per MFMA launch (4 tiles of 16)
-constexpr int kMmBlock = 256;        // 4 waves, one row pair each
 constexpr size_t kMmStage = 17408;   // bytes of one (16-token tile, superblock) operand stage
 
-static size_t mm_tiles(size_t b) { return b <= 16 ? 1 : (b <= 32 ? 2 : 4); }
 static size_t mm_stage_bytes(size_t n, size_t tt) { return tt * (n / 256) * kMmStage; }
 
 hh_status hh_engine::enqueue_mm_prep(const float* x, size_t b, size_t n, size_t tt) {
@@ -1120,43 +897,6 @@ hh_status hh_engine::enqueue_mm_prep(const float* x, size_t b, size_t n, size_t 
     hh_mm_prep_args a{x, ws_xop, (uint32_t)b, (uint32_t)n, (uint32_t)T, 0};
     const size_t threads = T * (n / 16);
     return launch(fn, (uint32_t)((threads + 255) / 256), 256, a);
-}
-
-hh_status hh_engine::enqueue_q4k_mm(size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* xop,
-                                    size_t b, size_t tt, float* y, bool ffn, int act) {
-    const size_t nsb = n / 256;
-    const size_t T = 16 * tt;
-    const size_t pairs = ffn ? (m + 15) / 16 : (m + 31) / 32;
-    const size_t groups = (pairs + 3) / 4;
-    // Split the superblocks over workgroups until every CU has one (each keeps >= 2).
-    const size_t cus = (size_t)props.multiProcessorCount;
-    const size_t ksg = std::max<size_t>(1, std::min((cus + groups - 1) / groups, std::max<size_t>(1, nsb / 2)));
-    if (ksg > 1) {
-        HH_TRY(grow(&ws_part, &ws_part_cap, groups * ksg * 2 * T * 64 * sizeof(float)));
-        if (ws_cnt_cap < groups * sizeof(unsigned)) {
-            HH_TRY(grow(&ws_cnt, &ws_cnt_cap, groups * sizeof(unsigned)));
-            HH_TRY_HIP(hipMemsetAsync(ws_cnt, 0, ws_cnt_cap, stream), "hipMemsetAsync(counters)");
-        }
-    }
-    if (ffn) HH_TRY(grow(&ws_hop, &ws_hop_cap, mm_stage_bytes(m, tt)));
-    const std::string name = std::string(ffn ? "hh_q4k_mm_gateup_t" : "hh_q4k_mm_t") + std::to_string(tt);
-    hipFunction_t fn;
-    HH_TRY(kernel(name, &fn));
-    hh_mm_args a{};
-    a.w0 = w0;
-    a.w1 = w1;
-    a.xop = xop;
-    a.y = y;
-    a.hop = ws_hop;
-    a.part = (float*)ws_part;
-    a.cnt = (unsigned*)ws_cnt;
-    a.m = (uint32_t)m;
-    a.n = (uint32_t)n;
-    a.b = (uint32_t)b;
-    a.ksg = (uint32_t)ksg;
-    a.row_bytes = (uint64_t)(nsb * 144);
-    a.act = act;
-    return launch(fn, (uint32_t)(groups * ksg), kMmBlock, a);
 }
 
 // Kernel argument block of q4k_mmr.hip (same layout).
@@ -1379,83 +1119,6 @@ hh_status hh_engine::enqueue_q4k_mmq(bool ffn, size_t m, size_t n, const uint8_t
     return HH_OK;
 }
 
-// ---- int8 MFMA batched Q4_K, weights staged through LDS (q4k_mmd.hip) ----
-
-// Must match struct hh_mmd_args in kernels/q4k_mmd.hip.
-struct MmdArgs {
-    const uint8_t* w0;
-    const uint8_t* w1;
-    const uint8_t* xs;
-    float* y;
-    float* part;
-    unsigned* cnt;
-    uint64_t row_bytes;
-    uint32_t m, n, b, tiles;
-    int32_t act;
-    uint32_t pad;
-};
-// One kernel configuration: NT matrices, SU superblocks per step, KR per K-range, RING slots.
-struct mmd_plan {
-    const char* name = nullptr;
-    size_t nt = 0, su = 0, kr = 0, ring = 0;
-    size_t steps = 0, smem = 0;
-};
-static mmd_plan plan_mmd(bool ffn, size_t m, size_t n, size_t cus) {
-    mmd_plan p;
-    const size_t nsb = n / 256, tiles = (m + 15) / 16;
-    if (ffn && nsb == 16) p = {"hh_q4k_mmd_gu_k16", 2, 4, 16, 4};
-    else if (ffn && nsb % 8 == 0) p = {"hh_q4k_mmd_gu_k8", 2, 4, 8, 4};
-    else if (!ffn && nsb % 8 == 0) p = {"hh_q4k_mmd_k8", 1, 8, 8, 4};
-    else return mmd_plan{};
-    const size_t nr = nsb / p.kr, per_r = tiles * (p.kr / p.su);
-    p.steps = nr * per_r;
-    const size_t per_wg = (p.steps + cus - 1) / cus;
-    if (per_wg > 32 || per_wg > per_r) return mmd_plan{};  // HH_MMD_MAX_SEG; at most two K-ranges
-    p.smem = (nr > 1 ? 2 : 1) * p.kr * 320 * 16 + p.ring * p.nt * 16 * (p.su * 144 + 16);
-    return p;
-}
-
-bool hh_engine::mmd_ok(bool ffn, size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const {
-    if (!mmd || !mmq || q4k_generic || b < (size_t)std::max(1, mmd_min) || b > 16 || m < 1 || m > 0xFFFFFFF0u || n < 256 ||
-        n % 256 != 0 || n > 0xFFFFFFFFu || ((((uintptr_t)w0 | (uintptr_t)w1 | (uintptr_t)x) & 15u) != 0))
-        return false;
-    const mmd_plan p = plan_mmd(ffn, m, n, (size_t)props.multiProcessorCount);
-    return p.name && p.smem + 512 <= (size_t)props.sharedMemPerBlock;
-}
-
-hh_status hh_engine::enqueue_q4k_mmd(bool ffn, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1,
-                                     const void* xs, size_t b, float* y, int act) {
-    const size_t cus = (size_t)props.multiProcessorCount;
-    const mmd_plan p = plan_mmd(ffn, m, n, cus);
-    if (!p.name) return HH_ERR_UNSUPPORTED_DEVICE;
-    const size_t tiles = (m + 15) / 16, ks = (n / 256) / p.su;
-    HH_TRY(grow(&ws_part, &ws_part_cap, tiles * ks * p.nt * 256 * sizeof(float)));
-    if (ws_cnt_cap < tiles * sizeof(unsigned)) {
-        HH_TRY(grow(&ws_cnt, &ws_cnt_cap, tiles * sizeof(unsigned)));
-        HH_TRY_HIP(hipMemsetAsync(ws_cnt, 0, ws_cnt_cap, stream), "hipMemsetAsync(counters)");
-    }
-    hipFunction_t fn;
-    HH_TRY(kernel(p.name, &fn));
-    MmdArgs a{};
-    a.w0 = w0;
-    a.w1 = ffn ? w1 : w0;
-    a.xs = (const uint8_t*)xs;
-    a.y = y;
-    a.part = (float*)ws_part;
-    a.cnt = (unsigned*)ws_cnt;
-    a.row_bytes = (uint64_t)((n / 256) * 144);
-    a.m = (uint32_t)m;
-    a.n = (uint32_t)n;
-    a.b = (uint32_t)b;
-    a.tiles = (uint32_t)tiles;
-    a.act = act;
-    void* params[] = {&a};
-    // 16 waves (HH_MMD_WAVES): two per (matrix, superblock) item of a step
-    hipError_t err = hipModuleLaunchKernel(fn, (uint32_t)cus, 1, 1, 16 * 64, 1, 1, (unsigned)p.smem, stream, params, nullptr);
-    if (err != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel(q4k_mmd)");
-    return HH_OK;
-}
-
 hh_status hh_engine::enqueue_gemv_batched(int type, size_t m, size_t n, const uint8_t* w, const float* x, size_t batch,
                                           float* y) {
     if (batch == 0) return HH_OK;
@@ -1471,12 +1134,6 @@ hh_status hh_engine::enqueue_gemv_batched(int type, size_t m, size_t n, const ui
             HH_TRY(enqueue_gemv(type, m, n, w, x + b0 * n, y + b0 * m));
             continue;
         }
-        if (mmd_ok(false, m, n, nb, w, w, x + b0 * n)) {  // 16 tokens: int8 MFMA, weights via LDS
-            HH_TRY(grow(&ws_xop, &ws_xop_cap, (n / 256) * mmq_stage_bytes(16)));
-            HH_TRY(enqueue_mmq_prep(x + b0 * n, nb, n, 16, ws_xop));
-            HH_TRY(enqueue_q4k_mmd(false, m, n, w, nullptr, ws_xop, nb, y + b0 * m, 0));
-            continue;
-        }
         if (mmq_ok(m, n, nb, w, w, x + b0 * n)) {  // 17..64 tokens: int8 MFMA
             const size_t tp = 16 * ((nb + 15) / 16);
             HH_TRY(grow(&ws_xop, &ws_xop_cap, (n / 256) * mmq_stage_bytes(tp)));
@@ -1488,9 +1145,7 @@ hh_status hh_engine::enqueue_gemv_batched(int type, size_t m, size_t n, const ui
             HH_TRY(enqueue_q4k_mmr(MMR_GEMM, m, n, w, nullptr, x + b0 * n, nb, y + b0 * m, 0));
             continue;
         }
-        const size_t tt = mm_tiles(nb);
-        HH_TRY(enqueue_mm_prep(x + b0 * n, nb, n, tt));
-        HH_TRY(enqueue_q4k_mm(m, n, w, nullptr, ws_xop, nb, tt, y + b0 * m, false, 0));
+        for (size_t b = b0; b < b0 + nb; b++) HH_TRY(enqueue_gemv(type, m, n, w, x + b * n, y + b * m));
     }
     return HH_OK;
 }
@@ -1541,19 +1196,6 @@ hh_status hh_engine::enqueue_ffn_batched(const hh_ffn_desc* d, const uint8_t* pa
             HH_TRY(enqueue_ffn(d, pack, x + b0 * dm, y + b0 * dm));
             continue;
         }
-        if (df % 256 == 0 && mmd_ok(true, df, dm, nb, wg, wu, x + b0 * dm) && mmd_ok(false, dm, df, nb, wd, wd, wd)) {
-            // 16 tokens on the int8 matrix cores with the weights staged through LDS
-            HH_TRY(grow(&ws_xop, &ws_xop_cap, (dm / 256) * mmq_stage_bytes(16)));
-            HH_TRY(grow(&ws_hop, &ws_hop_cap, (df / 256) * mmq_stage_bytes(16)));
-            HH_TRY(grow(&ws_h, &ws_h_cap, nb * df * sizeof(float)));
-            HH_TRY(enqueue_mmq_prep(x + b0 * dm, nb, dm, 16, ws_xop));
-            HH_TRY(enqueue_q4k_mmd(true, df, dm, wg, wu, ws_xop, nb, (float*)ws_h, d->act));
-            HH_TRY(enqueue_mmq_prep((const float*)ws_h, nb, df, 16, ws_hop));
-            HH_TRY(enqueue_q4k_mmd(false, dm, df, wd, nullptr, ws_hop, nb, y + b0 * dm, 0));
-            ffn_stage_valid = false;
-            ffn_calls += 3 * nb;
-            continue;
-        }
         if (df % 256 == 0 && mmq_ok(df, dm, nb, wg, wu, x + b0 * dm) && mmq_ok(dm, df, nb, wd, wd, wd)) {
             // 17..64 tokens on the int8 matrix cores: x -> int8 stages, gate/up + act -> h (f32),
             // h -> int8 stages, down
@@ -1576,11 +1218,7 @@ hh_status hh_engine::enqueue_ffn_batched(const hh_ffn_desc* d, const uint8_t* pa
             ffn_calls += 3 * nb;
             continue;
         }
-        const size_t tt = mm_tiles(nb);
-        HH_TRY(enqueue_mm_prep(x + b0 * dm, nb, dm, tt));
-        HH_TRY(enqueue_q4k_mm(df, dm, wg, wu, ws_xop, nb, tt, nullptr, true, d->act));
-        HH_TRY(enqueue_q4k_mm(dm, df, wd, nullptr, ws_hop, nb, tt, y + b0 * dm, false, 0));
-        ffn_calls += 3 * nb;
+        for (size_t b = b0; b < b0 + nb; b++) HH_TRY(enqueue_ffn(d, pack, x + b * dm, y + b * dm));
     }
     return HH_OK;
 }
@@ -1741,43 +1379,6 @@ hh_status hh_engine::enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* expert
             HH_TRY(kernel("hh_moe_prep", &fn));
             HH_TRY(launch(fn, (uint32_t)(1 + T), 256, g));
         }
-        // The ring form (moe_gring.hip, opt-in): one workgroup per CU streams its share of the
-        // selected experts' concatenated rows; the gate/up kernel writes the intermediate's digits.
-        // Its per-(row, pair) dot and reduction chains leave it slower than the per-expert
-        // grouped kernels below at 32 tokens (192 vs 114 us per 128-expert layer).
-        const size_t cus = (size_t)props.multiProcessorCount;
-        const size_t u1 = dm / 64, u2 = (size_t)moe_team(df / 64);
-        const size_t emax = std::min(E, P);                        // active experts at most
-        const size_t rmax = 32 * ((emax * (df / 32) + cus - 1) / cus);  // rows of the largest gate/up share
-        const size_t gu_pair = xqb + 12 * rmax;                    // LDS per staged pair (digits, sums, h)
-        const size_t ns_cap = moe_gring_ns > 0 ? std::min<size_t>((size_t)moe_gring_ns, 64) : 64;  // HH_GRING_MAX_NS
-        const size_t ns_gu = std::min<size_t>(std::min<size_t>(32, ns_cap), (kLdsBytes - 1024) / gu_pair);
-        const size_t ns_dn = std::min<size_t>(ns_cap, (kLdsBytes - 1024) / hqb);
-        if (moe_gring && (u1 == 16 || u1 == 32 || u1 == 64) && df % 256 == 0 && dm % 256 == 0 && ns_gu >= 1 &&
-            rmax / df + 2 <= 64 && ((emax * (dm / 8) + cus - 1) / cus) * 8 / dm + 2 <= 64) {
-            struct {
-                decltype(g) m;
-                uint32_t ns, rmax;
-            } gr{g, (uint32_t)ns_gu, (uint32_t)rmax};
-            HH_TRY(kernel("hh_moe_gu_gring_u" + std::to_string(u1), &fn));
-            void* p1[] = {&gr};
-            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)cus, 1, 1, 8 * 64, 1, 1, (unsigned)(ns_gu * gu_pair), stream,
-                                             p1, nullptr),
-                       "launch(moe grouped ring gate/up)");
-            gr.ns = (uint32_t)ns_dn;
-            HH_TRY(kernel("hh_moe_dn_gring_u" + std::to_string(u2), &fn));
-            void* p2[] = {&gr};
-            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)cus, 1, 1, 8 * 64, 1, 1, (unsigned)(ns_dn * hqb), stream, p2,
-                                             nullptr),
-                       "launch(moe grouped ring down)");
-            HH_TRY(kernel("hh_moe_combine", &fn));
-            void* gp[] = {&g};
-            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)((dm + 255) / 256), (uint32_t)T, 1, 256, 1, 1, 0, stream, gp,
-                                             nullptr),
-                       "launch(moe combine)");
-            ffn_calls += 3 * T;
-            return HH_OK;
-        }
         const uint32_t gy = (uint32_t)std::min(E, P);
         {
             const int team = moe_team(dm / 64);
@@ -1855,20 +1456,15 @@ static std::vector<std::string> required_kernels() {
     for (int w : {1, 2, 4, 8})
         for (const char* kind : {"hh_q4k_gemv_w", "hh_q4k_gemvq_w", "hh_q4k_gateup_w"})
             k.push_back(std::string(kind) + std::to_string(w));
-    for (int tt : {1, 2, 4})
-        for (const char* kind : {"hh_q4k_mm_t", "hh_q4k_mm_gateup_t"}) k.push_back(std::string(kind) + std::to_string(tt));
     k.push_back("hh_mm_prep");
     for (int S : {2, 4, 7, 8})
         for (const char* kind : {"hh_q4k_mmr_s", "hh_q4k_mmr_gu_s"}) k.push_back(std::string(kind) + std::to_string(S));
     for (int S : {2, 4, 7, 8, 14, 16}) k.push_back("hh_q4k_mmr_dn_s" + std::to_string(S));
     k.push_back("hh_mmq_prep");
-    for (const char* kn : {"hh_q4k_mmd_gu_k16", "hh_q4k_mmd_gu_k8", "hh_q4k_mmd_k8"}) k.push_back(kn);
     for (const char* st : {"s2_t1", "s4_t1", "s7_t1", "s8_t1", "s14_t1", "s16_t1", "s2_t2", "s4_t2", "s7_t2", "s8_t2",
                            "s14_t2", "s2_t3", "s4_t3", "s7_t3", "s8_t3", "s2_t4", "s4_t4", "s6_t4", "s7_t4"})
         for (const char* kind : {"hh_q4k_mmq_", "hh_q4k_mmq_gu_"}) k.push_back(std::string(kind) + st);
     k.push_back("hh_lut_gemv");
-    for (const char* f : {"g1_d1", "g1_d2", "g1_d4", "g1_d8", "g2_d2", "g2_d4", "g2_d8"})
-        k.push_back(std::string("hh_q4k_ffnp_") + f);
     for (const char* f : {"gu_ring_g1", "gu_ring_g2", "gu_ring_g1_n", "gu_ring_g2_n", "dn_ring_d1", "dn_ring_d2", "dn_ring_d4", "dn_ring_d8"})
         k.push_back(std::string("hh_q4k_") + f);
     for (int w : {1, 2, 4, 8}) k.push_back("hh_q6k_dn_ring_d" + std::to_string(w));
@@ -1947,26 +1543,18 @@ hh_status engine_create(int device, hh_engine** out) {
     }
     if (const char* b = getenv("HAYAI_HIP_BLOCKS_PER_CU")) e->blocks_per_cu_override = atoi(b);
     if (const char* g = getenv("HAYAI_HIP_Q4K_GENERIC")) e->q4k_generic = atoi(g) != 0;
-    if (const char* f = getenv("HAYAI_HIP_FFN_FUSED")) e->ffn_fused = atoi(f) != 0;
-    if (const char* f = getenv("HAYAI_HIP_FFNP")) e->ffnp = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_RING")) e->ring = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_MOE_GROUPED")) e->moe_grouped = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_SMALL_FFN")) e->small_ffn = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_SMALL_STACK")) e->small_stack = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_STACK_GRID")) e->stack_grid = atoi(f);
-    if (const char* f = getenv("HAYAI_HIP_Q4K_STACK")) e->q4k_stack = atoi(f) != 0;
-    if (const char* f = getenv("HAYAI_HIP_MOE_GRING")) e->moe_gring = atoi(f) != 0;
-    if (const char* f = getenv("HAYAI_HIP_MOE_GRING_NS")) e->moe_gring_ns = atoi(f);
     if (const char* f = getenv("HAYAI_HIP_MMQ")) e->mmq = atoi(f) != 0;
-    if (const char* f = getenv("HAYAI_HIP_MMD")) e->mmd = atoi(f) != 0;
-    if (const char* f = getenv("HAYAI_HIP_MMD_MIN")) e->mmd_min = atoi(f);
     if (const char* f = getenv("HAYAI_HIP_MMQ_S")) e->mmq_s = atoi(f);
     if (const char* f = getenv("HAYAI_HIP_MMQ_NW")) e->mmq_nw = std::min(8, std::max(0, atoi(f)));
     if (const char* f = getenv("HAYAI_HIP_DMA_SPLIT")) e->dma_split = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_RING_GU_PER_CU")) e->ring_gu_per_cu = std::max(1, atoi(f));
     if (const char* f = getenv("HAYAI_HIP_RING_DN_PER_CU")) e->ring_dn_per_cu = std::max(1, atoi(f));
     if (const char* f = getenv("HAYAI_HIP_MMR")) e->mmr = atoi(f) != 0;
-    if (const char* c = getenv("HAYAI_HIP_COOP")) e->coop_launch = atoi(c) != 0;
     err = hipMalloc(&e->grid_sync, kBarBytes);
     if (err == hipSuccess) err = hipMemset(e->grid_sync, 0, kBarBytes);
     if (err != hipSuccess) return bail(hip_fail(err, "hipMalloc(grid_sync)"));
@@ -1982,7 +1570,7 @@ void engine_destroy(hh_engine* e) {
     if (e->copy_stream) (void)hipStreamSynchronize(e->copy_stream);
     if (e->copy_stream2) (void)hipStreamSynchronize(e->copy_stream2);
     for (void* p : {e->ws_x, e->ws_y, e->ws_h, e->ws_g, e->ws_u, e->ws_w, e->ws_hq, e->ws_xop, e->ws_hop, e->ws_part,
-                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->ws_xn, e->ws_f, e->ws_xq, e->ws_moe_yp, e->ws_moe_grp, e->ws_moe_q, e->ws_stk, e->ws_qstk, e->grid_sync})
+                    e->ws_cnt, e->ws_moe_h, e->ws_moe_ids, e->ws_moe_w, e->ws_moe_hx, e->ws_xn, e->ws_f, e->ws_xq, e->ws_moe_yp, e->ws_moe_grp, e->ws_moe_q, e->ws_stk, e->grid_sync})
         if (p) (void)hipFree(p);
     for (void* p : e->ws_retired) (void)hipFree(p);
     if (e->stream) (void)hipStreamDestroy(e->stream);

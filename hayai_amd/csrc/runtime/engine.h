@@ -146,27 +146,20 @@ struct hh_engine {
     size_t ws_moe_q_cap = 0;
     void* ws_stk = nullptr;     // FFN-stack exchange: tagged words of h (d_ff) then x (d_model); zeroed
     size_t ws_stk_cap = 0;      // when allocated and after a device error
-    void* ws_qstk = nullptr;    // Q4_K FFN-stack exchange: h granule words (3 d_ff / 8) then x (d_model);
-    size_t ws_qstk_cap = 0;     // zeroed when allocated and after a device error
     void* grid_sync = nullptr;  // grid-barrier state (counters, flags, error word, epochs)
     hh_ffn_desc ffn_stage{};    // FFN whose gate/up output is pending in ws_h (/ws_hq)
     bool ffn_stage_valid = false;
     bool ffn_stage_digits = false;  // ws_hq holds the digits of ws_h
     bool ffn_stage_ring = false;    // ws_hq holds the ring kernels' granule digits of h
-    bool ffn_fused = false;     // HAYAI_HIP_FFN_FUSED=1: one-launch Q4_K FFN (grid barrier)
-    bool ffnp = true;           // HAYAI_HIP_FFNP=0: skip the persistent pipelined Q4_K FFN
     bool ring = true;           // HAYAI_HIP_RING=0: skip the two-launch ring Q4_K FFN
     bool moe_grouped = true;    // HAYAI_HIP_MOE_GROUPED=0: several-token MoE per (token, expert)
     bool small_ffn = true;      // HAYAI_HIP_SMALL_FFN=0: small Q4_0/Q8_0 FFNs as two launches
     int ring_gu_per_cu = 1;     // HAYAI_HIP_RING_GU_PER_CU: ring gate/up workgroups per CU
     int ring_dn_per_cu = 1;     // HAYAI_HIP_RING_DN_PER_CU: ring down workgroups per CU
-    bool mmr = true;            // HAYAI_HIP_MMR=0: batched Q4_K (<= 16 tokens) on the q4k_mm kernels
-    bool mmq = true;            // HAYAI_HIP_MMQ=0: batched Q4_K (>= 17 tokens) on the f16 kernels, not int8
-    bool mmd = false;           // HAYAI_HIP_MMD=1: up to 16 tokens on the LDS-staged int8 kernels (q4k_mmd; slower today)
-    int mmd_min = 16;           // HAYAI_HIP_MMD_MIN: fewest tokens sent to the q4k_mmd kernels (1..16)
+    bool mmr = true;            // HAYAI_HIP_MMR=0: batched Q4_K (<= 16 tokens) one token at a time
+    bool mmq = true;            // HAYAI_HIP_MMQ=0: batched Q4_K (>= 17 tokens) one token at a time, not int8
     int mmq_s = 0;              // HAYAI_HIP_MMQ_S: superblocks per chunk of an int8 batched launch (0: chosen)
     int mmq_nw = 0;             // HAYAI_HIP_MMQ_NW: units (waves) per workgroup (0: 8)
-    bool coop_launch = false;   // HAYAI_HIP_COOP=1: cooperative launch API for the fused kernel
     int blocks_per_cu_override = 0;  // HAYAI_HIP_BLOCKS_PER_CU
     bool q4k_generic = false;        // HAYAI_HIP_Q4K_GENERIC=1: skip the int8-digit Q4_K kernels
 
@@ -218,13 +211,8 @@ struct hh_engine {
                                       const float* norm, size_t norm_stride, float eps, const float* x, float* y);
     hh_status enqueue_small_stack(const hh_ffn_desc* d, const uint8_t* pack, size_t stride, size_t n_layers,
                                   const float* norm, size_t norm_stride, float eps, const float* x, float* y);
-    hh_status enqueue_q4k_stack(const hh_ffn_desc* d, const uint8_t* pack, size_t stride, size_t n_layers,
-                                const float* norm, size_t norm_stride, float eps, const float* x, float* y);
     bool small_stack = true;  // HAYAI_HIP_SMALL_STACK=0: FFN stacks as one block per layer
-    bool q4k_stack = false;   // HAYAI_HIP_Q4K_STACK=1: all-Q4_K FFN stacks in one persistent launch
     int stack_grid = 0;       // HAYAI_HIP_STACK_GRID: workgroups of the persistent stack (0: one per CU)
-    bool moe_gring = false;   // HAYAI_HIP_MOE_GRING=1: several-token MoE on the ring-form kernels (slower today)
-    int moe_gring_ns = 0;     // HAYAI_HIP_MOE_GRING_NS: pairs staged per pass (0: as many as LDS holds)
     // The two halves of enqueue_ffn's two-launch path: gate/up(+act) into the engine's FFN
     // intermediate, then the down projection of that intermediate.
     // With norm: the begin step of the FFN residual block (x is RMSNorm'ed first); with res:
@@ -237,13 +225,6 @@ struct hh_engine {
     // x given as int8 digits (then x is unused); hdigits: gate/up also writes h's digits.
     hh_status enqueue_q4k(size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const float* x, float* y,
                           int act, bool gateup, const void* xdigits, void* hdigits);
-    // One-launch Q4_K FFN layer (gate/up, grid barrier, down); HH_ERR_UNSUPPORTED_DEVICE when
-    // the shape has no fused instantiation.
-    hh_status enqueue_q4k_ffn(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
-                              const float* x, float* y);
-    // Persistent one-launch Q4_K FFN layer with the down weights prefetched across the grid
-    // barrier (q4k_ffn.hip); HH_ERR_UNSUPPORTED_DEVICE when the shape, alignment or
-    // occupancy does not allow it.
     bool ring_ok(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd, const float* x) const;
     // Ring gate/up (Q4_K, IQ2_XXS, IQ3_XXS); hx: where h's digits go
     // (hh_ring_digits_bytes(d_ff)); null: ws_hq.
@@ -255,8 +236,6 @@ struct hh_engine {
                              const float* res);
     hh_status enqueue_ring_gemv(int type, size_t m, size_t n, const uint8_t* w, const float* x, float* y,
                                 void* xq_ws = nullptr);
-    hh_status enqueue_q4k_ffnp(const hh_ffn_desc* d, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
-                               const float* x, float* y);
     // Batched GEMV Y[b][m] = W . X[b] (x, y device pointers, row-major by token).  Q4_K with
     // 2 <= batch uses the MFMA kernels in chunks of up to 64 tokens; other formats (and
     // batch 1) run one GEMV per token, as the reference's orchestrator does
@@ -267,10 +246,6 @@ struct hh_engine {
     hh_status enqueue_ffn_batched(const hh_ffn_desc* d, const uint8_t* pack, const float* x, size_t batch, float* y);
     // Tokens [b][n] f32 -> operand stages in ws_xop for 16 * tt token slots.
     hh_status enqueue_mm_prep(const float* x, size_t b, size_t n, size_t tt);
-    // One MFMA launch: GEMM mode (ffn == false; w0, y) or gate/up mode (w0 = gate, w1 = up,
-    // act, writing the stages of h into ws_hop).  xop holds 16 * tt tokens of n columns.
-    hh_status enqueue_q4k_mm(size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* xop, size_t b,
-                             size_t tt, float* y, bool ffn, int act);
     // Weight-stream MFMA launch for 1..16 tokens (q4k_mmr.hip).  kind: MMR_GEMM (w0, f32 x,
     // y), MMR_GU (w0 = gate, w1 = up, f32 x, act; h stages into ws_hop) or MMR_DN (w0, x =
     // token stages, y).  HH_ERR_UNSUPPORTED_DEVICE when shape or alignment does not fit.
@@ -280,9 +255,6 @@ struct hh_engine {
     // stages (per 32-element block: s = amax / 127, q = round_half_away(x / s)) in `xs`,
     // then Y[b][m] = W . X (ffn == false) or H[b][m] = act(W_gate . X) * (W_up . X).
     bool mmq_ok(size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const;
-    bool mmd_ok(bool ffn, size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const;
-    hh_status enqueue_q4k_mmd(bool ffn, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* xs,
-                              size_t b, float* y, int act);
     hh_status enqueue_mmq_prep(const float* x, size_t b, size_t n, size_t tp, void* xs);
     hh_status enqueue_q4k_mmq(bool ffn, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* xs,
                               size_t b, float* y, int act);

@@ -7,11 +7,12 @@ other types token by token.  Two matrix-core paths:
   activations quantized to int8 per 32-element block, int8 MFMA (q4k_mmq.hip); parity against
   the oracle fed the same quantized activations (oracle.dequant_act_q8 / oracle.ffn_q8), the
   quantization's own error printed beside it;
-- 2..16 tokens: f16 operands with f32-level accuracy, against the oracle's f32 restatement;
-- opt-in (HAYAI_HIP_MMD=1, HAYAI_HIP_MMD_MIN): up to 16 tokens on the int8 kernels whose
-  weights are staged through LDS (q4k_mmd.hip), where the reduction dimension is a multiple of
-  2048, held to the same quantized-activation oracle.
-Both are held to the FFN tolerance (max |y - ref| / max |ref| <= 1e-3 per token).
+- 2..16 tokens: f16 operands with f32-level accuracy, against the oracle's f32 restatement.
+Both are held to the FFN tolerance (max |y - ref| / max |ref| <= 1e-3 per token).  The int8
+path's distance from the f32-activation result (the quantization itself, which configs[2]
+prescribes and the public contract states) is bounded too: QERR_GEMM for a GEMM, QERR_FFN for
+the FFN (h is heavy-tailed, so its per-block quantization costs more); measured 0.7-1.9% and
+3-13% of max|y|, so a wrong prep scale, rounding or clamp (errors of tens of percent) fails.
 """
 import numpy as np
 import pytest
@@ -22,6 +23,8 @@ from hayai_amd import synth
 
 pytestmark = pytest.mark.gpu
 REL_TOL = 1e-3
+QERR_GEMM = 0.04
+QERR_FFN = 0.25
 Q4_0, Q4_K = 2, 12
 
 
@@ -35,20 +38,18 @@ def per_token_err(Y, R):
     return max(rel_err(Y[b], R[b]) for b in range(Y.shape[0]))
 
 
-def int8_tokens(batch, ks, min16=17):
-    """Which tokens go through the int8 path: passes of up to 64 tokens, those of 17 or more,
-    and (q4k_mmd.hip enabled from min16 tokens) passes of min16..16 tokens when every reduction
-    dimension in ks is a multiple of 2048."""
+def int8_tokens(batch):
+    """Which tokens go through the int8 path: passes of up to 64 tokens, those of 17 or more."""
     on = np.zeros(batch, bool)
     for b0 in range(0, batch, 64):
         nb = min(64, batch - b0)
-        on[b0:b0 + nb] = nb >= 17 or (min16 <= nb <= 16 and all(k % 2048 == 0 for k in ks))
+        on[b0:b0 + nb] = nb >= 17
     return on
 
 
-def batched_ref(t, m, n, w, X, min16=17):
+def batched_ref(t, m, n, w, X):
     """Per token: the oracle GEMV of the activation the path computes with."""
-    on = int8_tokens(X.shape[0], (n,), min16)
+    on = int8_tokens(X.shape[0])
     Xq = np.stack([oracle.dequant_act_q8(X[b]) if on[b] else X[b] for b in range(X.shape[0])])
     return oracle.gemv_batched(t, m, n, w, Xq)
 
@@ -83,9 +84,10 @@ def test_q4_k_batched_matches_oracle(engine, m, n, batch):
     err = per_token_err(Y, R)
     qerr = per_token_err(Y, oracle.gemv_batched(Q4_K, m, n, w, X))
     print(f"  per-token max rel err {err:.3e} (vs f32 activations: {qerr:.3e}, "
-          f"int8 tokens {int(int8_tokens(batch, (n,)).sum())})", flush=True)
+          f"int8 tokens {int(int8_tokens(batch).sum())})", flush=True)
     assert np.isfinite(Y).all()
     assert err <= REL_TOL
+    assert qerr <= (QERR_GEMM if int8_tokens(batch).any() else REL_TOL), qerr
 
 
 def test_batched_is_deterministic_and_batch1_is_gemv(engine):
@@ -152,24 +154,26 @@ def test_ffn_batched_matches_oracle(engine, types, d_model, d_ff, batch, act):
     desc = engine.ffn_desc(types, d_model, d_ff, lay, act)
     X = synth.normal(synth.seed_for(3, batch, synth.ACT), batch * d_model).reshape(batch, d_model)
     Y = engine.ffn_batched(desc, pack, 0, X)
-    on = int8_tokens(batch, (d_model, d_ff)) if types == (12, 12, 12) else np.zeros(batch, bool)
+    on = int8_tokens(batch) if types == (12, 12, 12) else np.zeros(batch, bool)
     R = np.stack([(oracle.ffn_q8 if on[b] else oracle.ffn)(types, d_model, d_ff, wg, wu, wd, X[b], act=act)
                   for b in range(batch)])
     err = per_token_err(Y, R)
     R32 = np.stack([oracle.ffn(types, d_model, d_ff, wg, wu, wd, X[b], act=act) for b in range(batch)])
-    print(f"  per-token max rel err {err:.3e} (vs f32 activations: {per_token_err(Y, R32):.3e})", flush=True)
+    qerr = per_token_err(Y, R32)
+    print(f"  per-token max rel err {err:.3e} (vs f32 activations: {qerr:.3e})", flush=True)
     assert err <= REL_TOL
+    assert qerr <= (QERR_FFN if on.any() else REL_TOL), qerr
     if types == (2, 2, 2):
         for b in range(batch):  # non-Q4_K formats: the single-token op per token
             np.testing.assert_array_equal(Y[b], engine.ffn(desc, pack, 0, X[b]))
 
 
 @pytest.mark.parametrize("batch", [16, 40, 64])
-def test_int8_path_off_keeps_f16_kernels(monkeypatch, batch):
-    # HAYAI_HIP_MMQ=0: 17..64 tokens run the f16 kernels (f32-level accuracy) instead, held to
-    # the oracle fed the original f32 activations; the int8 engine's output differs from them
-    # by the activation quantization only
-    print(f"[case] batched f16 kernels batch={batch}", flush=True)
+def test_int8_path_off_keeps_f32_activations(monkeypatch, batch):
+    # HAYAI_HIP_MMQ=0: 17..64 tokens run one token at a time on the batch-1 kernels (16 stay
+    # on the f16 weight-stream MFMA kernels), held to the oracle fed the original f32
+    # activations: no int8 activation quantization on this path
+    print(f"[case] batched without int8 batch={batch}", flush=True)
     monkeypatch.setenv("HAYAI_HIP_MMQ", "0")
     eng = hayai_amd.HipEngine(0)
     try:
@@ -178,58 +182,5 @@ def test_int8_path_off_keeps_f16_kernels(monkeypatch, batch):
         X = synth.normal(72 + batch, batch * n).reshape(batch, n)
         Y = eng.ggml_gemv_batched_q4_k(m, n, w, X, batch).reshape(batch, m)
         assert per_token_err(Y, oracle.gemv_batched(Q4_K, m, n, w, X)) <= REL_TOL
-    finally:
-        eng.close()
-
-
-def _engine_with_env(monkeypatch, **env):
-    for k, v in env.items():
-        monkeypatch.setenv(k, v)
-    return hayai_amd.HipEngine(0)
-
-
-@pytest.mark.parametrize("m,n,batch", [
-    (14336, 4096, 16),   # one K-range of 16 superblocks
-    (4096, 14336, 16),   # seven K-ranges: every segment a partial
-    (2048, 2048, 16),    # one K-range of 8: tiles split between workgroups
-    (100, 2048, 16),     # fewer steps than workgroups, ragged last tile
-    (4104, 14336, 11),   # 11 tokens (5 padding rows of the token tile), ragged rows
-    (8192, 8192, 2),     # two tokens
-])
-def test_lds_staged_int8_gemm_matches_oracle(monkeypatch, m, n, batch):
-    # q4k_mmd.hip (stream-K over 16-row tiles, weights copied into an LDS ring): held to the
-    # oracle fed the same quantized activations far below the FFN tolerance (a lost or
-    # doubled segment, a wrong tile or K-range would show at the 1e-1 level), deterministic
-    print(f"[case] lds-staged int8 gemm m={m} n={n} batch={batch}", flush=True)
-    eng = _engine_with_env(monkeypatch, HAYAI_HIP_MMD="1", HAYAI_HIP_MMD_MIN="1")
-    try:
-        w = synth.matrix(Q4_K, m, n, synth.seed_for(8, batch, m))
-        X = synth.normal(synth.seed_for(8, batch, n), batch * n).reshape(batch, n)
-        Y = eng.ggml_gemv_batched_q4_k(m, n, w, X, batch).reshape(batch, m)
-        R = batched_ref(Q4_K, m, n, w, X, min16=1)
-        err = per_token_err(Y, R)
-        print(f"  per-token max rel err {err:.3e}", flush=True)
-        assert np.isfinite(Y).all()
-        assert err <= 1e-4
-        Y2 = eng.ggml_gemv_batched_q4_k(m, n, w, X, batch).reshape(batch, m)
-        np.testing.assert_array_equal(Y2.view(np.uint32), Y.view(np.uint32))
-    finally:
-        eng.close()
-
-
-@pytest.mark.parametrize("d_model,d_ff,batch,act", [(4096, 14336, 16, 0), (2048, 8192, 16, 1), (4096, 14336, 7, 0)])
-def test_lds_staged_int8_ffn_matches_oracle(monkeypatch, d_model, d_ff, batch, act):
-    print(f"[case] lds-staged int8 ffn {d_model}x{d_ff} batch={batch} act={act}", flush=True)
-    eng = _engine_with_env(monkeypatch, HAYAI_HIP_MMD="1", HAYAI_HIP_MMD_MIN="1")
-    try:
-        types = (12, 12, 12)
-        lay, (wg, wu, wd), pack = make_pack(eng, types, d_model, d_ff, 50 + batch)
-        desc = eng.ffn_desc(types, d_model, d_ff, lay, act)
-        X = synth.normal(synth.seed_for(5, batch, synth.ACT), batch * d_model).reshape(batch, d_model)
-        Y = eng.ffn_batched(desc, pack, 0, X)
-        R = np.stack([oracle.ffn_q8(types, d_model, d_ff, wg, wu, wd, X[b], act=act) for b in range(batch)])
-        err = per_token_err(Y, R)
-        print(f"  per-token max rel err {err:.3e}", flush=True)
-        assert err <= REL_TOL
     finally:
         eng.close()

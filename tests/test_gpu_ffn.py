@@ -131,23 +131,16 @@ def engine_with_env(**env):
 
 
 @pytest.fixture(scope="module")
-def persistent_engine():
-    """An engine whose Q4_K FFN is the persistent one-launch form (ring form off)."""
+def two_launch_engine():
+    """An engine with the ring kernels off: Q4_K FFNs run as the first two-launch kernels
+    (gate/up + activation with per-32 digits of h, then down), IQ formats on the generic f32
+    team kernels."""
     eng = engine_with_env(HAYAI_HIP_RING="0")
     yield eng
     eng.close()
 
 
-@pytest.fixture(scope="module")
-def two_launch_engine():
-    """An engine with the ring and persistent Q4_K FFN forms off: every FFN runs as the first
-    two-launch kernels (gate/up + activation with per-32 digits of h, then down)."""
-    eng = engine_with_env(HAYAI_HIP_RING="0", HAYAI_HIP_FFNP="0")
-    yield eng
-    eng.close()
-
-
-PERSISTENT_CASES = [
+Q4K_CASES = [
     # (d_model, d_ff): the 8B shape (1 wave per gate/up row, 4 per down row); d_model 8192
     # (2 waves per gate/up row); d_ff 28672 (8 waves per down row); fewer h granules and
     # down rows than workgroups (the expert shape, and a tiny layer)
@@ -155,16 +148,13 @@ PERSISTENT_CASES = [
 ]
 
 
-@pytest.mark.parametrize("form", ["ring", "persistent"])
-@pytest.mark.parametrize("d_model,d_ff", PERSISTENT_CASES)
-def test_q4k_ffn_forms_match_oracle_and_two_launch(engine, persistent_engine, two_launch_engine, form, d_model,
-                                                   d_ff):
-    # The ring form (two streaming launches, h as granule digits in between) and the
-    # persistent one-launch form (gate/up, grid barrier, down with its weights already in
-    # flight) against the oracle and against the first two-launch kernels on the same bytes.
+@pytest.mark.parametrize("d_model,d_ff", Q4K_CASES)
+def test_q4k_ffn_ring_matches_oracle_and_two_launch(engine, two_launch_engine, d_model, d_ff):
+    # The ring form (two streaming launches, h as granule digits in between) against the
+    # oracle and against the first two-launch kernels on the same bytes.
     types = (12, 12, 12)
-    eng = engine if form == "ring" else persistent_engine
-    print(f"[case] q4_k ffn ({form}) {d_model}x{d_ff}", flush=True)
+    eng = engine
+    print(f"[case] q4_k ffn (ring) {d_model}x{d_ff}", flush=True)
     oracle.set_threads(min(16, oracle.max_threads()))
     lay, (wg, wu, wd), pack = make_pack(eng, types, d_model, d_ff, 20)
     pack2 = two_launch_engine.alloc(lay.total)
@@ -216,14 +206,13 @@ def test_q4k_m_ffn_matches_oracle_and_two_launch(engine, two_launch_engine, d_mo
         print(f"  rel_err vs oracle {rel_err(y, ref):.2e}, vs two-launch {rel_err(y, y2):.2e}", flush=True)
 
 
-@pytest.mark.parametrize("form", ["ring", "persistent"])
-def test_q4k_ffn_chain_is_deterministic(engine, persistent_engine, form):
-    # 6 dependent launches with no host sync in between (the persistent form uses a new
-    # barrier generation per launch; the h buffer is reused), then the same chain call by
-    # call: the results are identical bit for bit, and every step is within tolerance of the
-    # oracle.
+@pytest.mark.parametrize("form", ["ring", "two-launch"])
+def test_q4k_ffn_chain_is_deterministic(engine, two_launch_engine, form):
+    # 6 dependent launches with no host sync in between (the h buffer is reused), then the
+    # same chain call by call: the results are identical bit for bit, and every step is within
+    # tolerance of the oracle.
     types, d_model, d_ff = (12, 12, 12), 4096, 14336
-    engine = engine if form == "ring" else persistent_engine
+    engine = engine if form == "ring" else two_launch_engine
     print(f"[case] q4_k ffn chain ({form}) {d_model}x{d_ff}", flush=True)
     lay, (wg, wu, wd), pack = make_pack(engine, types, d_model, d_ff, 2)
     desc = engine.ffn_desc(types, d_model, d_ff, lay)
@@ -282,7 +271,7 @@ IQ_RING_CASES = [
 
 
 @pytest.mark.parametrize("types,d_model,d_ff", IQ_RING_CASES)
-def test_iq_ring_ffn_matches_oracle_and_generic(engine, persistent_engine, types, d_model, d_ff):
+def test_iq_ring_ffn_matches_oracle_and_generic(engine, two_launch_engine, types, d_model, d_ff):
     # The IQ2_XXS / IQ3_XXS ring kernels (int8 codebook entries, v_dot4 against the
     # activation digits) and the generic f32 team kernels (ring form off) each meet the
     # FFN bar against the oracle; the two-call seam runs the ring kernels bit for bit.
@@ -291,7 +280,7 @@ def test_iq_ring_ffn_matches_oracle_and_generic(engine, persistent_engine, types
     x = synth.normal(synth.seed_for(40, d_model, synth.ACT), d_model)
     lay, (wg, wu, wd), pack0 = make_pack(engine, types, d_model, d_ff, 40)
     ys = {}
-    for name, eng in (("ring", engine), ("generic", persistent_engine)):
+    for name, eng in (("ring", engine), ("generic", two_launch_engine)):
         pack = pack0
         if eng is not engine:
             pack = eng.alloc(lay.total)

@@ -102,13 +102,10 @@ def engine_with_env(**env):
 
 
 BARRIER_CASES = [
-    # (types, d_model, d_ff, engine switches): the one-launch FFNs with a grid barrier.  The
-    # small Q4_0 / Q8_0 FFN at SmolLM2-135M's layer; the persistent Q4_K FFN (ring form off)
-    # at the 8B layer and at a layer with fewer h granules than workgroups.
+    # (types, d_model, d_ff, engine switches): the one-launch FFNs with a grid barrier, the
+    # small Q4_0 / Q8_0 FFN at SmolLM2-135M's layer.
     ((hayai_amd.Q4_0,) * 3, 576, 1536, {}),
     ((hayai_amd.Q8_0,) * 3, 576, 1536, {}),
-    ((hayai_amd.Q4_K,) * 3, 4096, 14336, {"HAYAI_HIP_RING": "0"}),
-    ((hayai_amd.Q4_K,) * 3, 2048, 768, {"HAYAI_HIP_RING": "0"}),
 ]
 
 
