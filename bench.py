@@ -23,6 +23,8 @@ rocprofv3 FETCH_SIZE / WRITE_SIZE passes (each scaled by what the counter reads 
 is timed the same way and reported beside it.
 cpu_baseline: the oracle's fp32 restatement of hayai-model's gemv_q4_k FFN (oracle/,
 OpenMP over rows) on a bounded sample of the same layers, host cores.
+configs: the other BASELINE.json configs in compact form (compact_configs), each with its own
+roofline, timed in the same run (--no-configs skips them).
 """
 from __future__ import annotations
 
@@ -171,7 +173,47 @@ def roofline_step(gbs: float, what: str) -> dict:
             "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": what}
 
 
-def bench_batched(eng, pack, lay, stride, desc, args) -> int:
+def emit(eng, out: dict) -> int:
+    """Print a workload's JSON line and release the engine."""
+    print(json.dumps(out), flush=True)
+    eng.close()
+    return 0
+
+
+def compact_configs(eng, pack, lay, stride, desc) -> dict:
+    """The other BASELINE.json configs in compact form, timed in the default run beside the
+    headline, on the same box and clock: configs[0] (SmolLM2-135M Q4_0, 30 layers), configs[2]
+    (the headline's own 32 resident 8B layers at 16 and 64 tokens), configs[3] (the MoE layer at
+    1 and 32 tokens, 4 resident layers) and configs[4] (the 70B IQ2_XXS FFN, 8 layers through
+    the two pinned slots, with the host link's plain hipMemcpy rate beside it).  Each entry keeps
+    its own roofline; the full forms are --workload smollm / batched / moe / stream."""
+    def ns(**kw):
+        base = dict(steps=10, warmup=2, no_cpu_baseline=True, cpu_budget=0.0, batch=1, layers=0)
+        base.update(kw)
+        return argparse.Namespace(**base)
+
+    keep = ("config", "dtype", "steps", "ms_per_step", "value", "unit", "pct_of_peak", "us_per_layer", "ffn_tok_s",
+            "tflops", "mfma", "roofline")
+
+    def pick(o, extra=()):
+        return {k: o[k] for k in keep + tuple(extra) if k in o}
+
+    t0 = time.perf_counter()
+    out = {}
+    out["c0_smollm_q4_0_bs1"] = pick(bench_smollm(eng, ns(steps=40, warmup=4)), ("graph_replay", "chained_stack"))
+    for B in (16, 64):
+        out[f"c2_8b_q4_k_batch{B}"] = pick(bench_batched(eng, pack, lay, stride, desc, ns(batch=B, steps=5, warmup=2)))
+    for T in (1, 32):
+        out[f"c3_moe_q4_k_t{T}"] = pick(bench_moe(eng, ns(batch=T, steps=20, warmup=3)),
+                                         ("mean_distinct_experts_per_layer",))
+    out["c4_70b_iq2_xxs_streamed"] = pick(bench_stream(eng, ns(layers=8, steps=3, warmup=1)),
+                                          ("h2d_copy_only_gbs", "h2d_pinned_memcpy_peak_gbs", "h2d_frac_of_memcpy_peak",
+                                           "overlap_efficiency", "ffn_resident_hbm_gbs", "ffn_resident_pct_of_peak"))
+    log(f"[bench] compact configs timed in {time.perf_counter() - t0:.1f}s")
+    return out
+
+
+def bench_batched(eng, pack, lay, stride, desc, args) -> dict:
     """the 8B Q4_K FFN for B tokens per step (all 32 layers
     resident), gate/up(+SiLU) and down on the matrix cores.  value = algorithmic bytes per
     step (weights once per layer + B tokens' f32 x in and y out) / step time."""
@@ -236,7 +278,8 @@ def bench_batched(eng, pack, lay, stride, desc, args) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16 MFMA operands (x as hi+lo pair), f32 accumulate",
+        "dtype": ("int8 MFMA (activations int8 per 32-element block, as configs[2]), i32 accumulate, f32 scales"
+                  if B >= 17 else "f16 MFMA operands (x as hi+lo pair), f32 accumulate"),
         "data": "synthetic (seeded Q4_K blocks, N(0,1) f32 activations)",
         "config": {"workload": f"llama3-8b-ffn-q4_k-batch{B}-32layers-resident", "d_model": D_MODEL, "d_ff": D_FF,
                    "layers": LAYERS, "batch": B, "weights": "Q4_K", "act": "silu"},
@@ -245,14 +288,16 @@ def bench_batched(eng, pack, lay, stride, desc, args) -> int:
         "tflops": round(tflops, 2),
         "roofline": roofline_step(gbs, "whole step: token prep + weight-stream f16 MFMA gate/up and down (B <= 16) or "
                                        "the int8 MFMA kernels (17..64 tokens); MFMA rate in tflops"),
+        "mfma": {"achieved": round(tflops, 2), "peak": 5000.0 if B >= 17 else 2500.0,
+                 "unit": "TOP/s (int8 dense)" if B >= 17 else "TFLOP/s (f16 dense)",
+                 "frac": round(tflops / (5000.0 if B >= 17 else 2500.0), 5),
+                 "counted": "useful multiply-adds only: 2 * B * 3 * d_model * d_ff per layer"},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(out), flush=True)
-    eng.close()
-    return 0
+    return out
 
 
-def bench_moe(eng, args) -> int:
+def bench_moe(eng, args) -> dict:
     """Qwen3-30B-A3B-shaped MoE layer (128 experts, top-8 softmax
     routing with renormalisation, d_model 2048, expert d_ff 768, Q4_K), T tokens per step.
     4 MoE layers are resident (4 x 340 MB, beyond the 256 MB last-level cache) and each step
@@ -345,12 +390,10 @@ def bench_moe(eng, args) -> int:
                                        "kernels (T = 1)"),
         "cpu_baseline": cpu,
     }
-    print(json.dumps(out), flush=True)
-    eng.close()
-    return 0
+    return out
 
 
-def bench_stream(eng, args) -> int:
+def bench_stream(eng, args) -> dict:
     """Llama-3-70B-shaped FFN (d_model 8192, d_ff 28672) in IQ2_XXS,
     80 layers streamed from pinned host memory through 2 ping-pong slots: the DMA of layer
     l+1 (hipMemcpyAsync on the copy stream) overlaps the FFN of layer l (compute stream).
@@ -363,7 +406,8 @@ def bench_stream(eng, args) -> int:
     from hayai_amd import synth
 
     T = hayai_amd.IQ2_XXS
-    DM, DF, L = 8192, 28672, 80
+    DM, DF = 8192, 28672
+    L = getattr(args, "layers", 0) or 80
     gate = hayai_amd.QuantMatrix("ffn_gate", DM, DF, T)
     up = hayai_amd.QuantMatrix("ffn_up", DM, DF, T)
     down = hayai_amd.QuantMatrix("ffn_down", DF, DM, T)
@@ -371,12 +415,15 @@ def bench_stream(eng, args) -> int:
     desc = eng.ffn_desc((T, T, T), DM, DF, lay)
     st = hayai_amd.StreamingScratch(eng, lay.total, k_chunk=1, n_slots=2)
     lo, hi = synth.SCALE_RANGE[T]
+    # the two slot images: seeded IQ2_XXS blocks generated on the device (synth.matrix's
+    # generator), copied once into the pinned host slots
+    img = eng.alloc(lay.total)
     for l in range(2):
-        view = st.host_slot(l)
         for mat, off, rows, cols in ((synth.GATE, lay.gate_off, DF, DM), (synth.UP, lay.up_off, DF, DM),
                                      (synth.DOWN, lay.down_off, DM, DF)):
-            w = synth.matrix(T, rows, cols, synth.seed_for(5, l, mat), lo, hi)
-            view[off:off + w.size] = w
+            eng.synth_weights_dev(T, img, off, rows * cols // 256, synth.seed_for(5, l, mat), lo, hi)
+        st.host_slot(l)[:] = img.read(np.uint8, lay.total)
+    img.free()
     wbytes = sum(ln for _, ln in (lay.ffn_region(r) for r in range(3)))
     xs = synth.normal(synth.seed_for(5, 0, synth.ACT), L * DM).reshape(L, DM)
     xbuf = eng.upload(xs)
@@ -415,6 +462,14 @@ def bench_stream(eng, args) -> int:
         st.weight_bind(L - 1)  # the compute stream waits for the last copy
 
     ms_copy = timed(copies_only, max(1, min(args.steps, 3)))
+    # the host link on its own: one hipMemcpyAsync of 256 MiB from pinned host memory to HBM
+    # (hh_buf_copy on the compute stream), the best of 3
+    pin, dev = eng.alloc(256 << 20, hayai_amd.BUF_PINNED_HOST), eng.alloc(256 << 20)
+    dev.copy_from(pin, 256 << 20)
+    ms_peak = min(timed(lambda: dev.copy_from(pin, 256 << 20), 1) for _ in range(3))
+    h2d_peak = (256 << 20) / (ms_peak / 1e3) / 1e9
+    pin.free()
+    dev.free()
     # FFN kernels alone on a staged layer (weights device-resident in the mirror)
     stage(0)
     mirror, off0 = st.weight_bind(0)
@@ -452,10 +507,12 @@ def bench_stream(eng, args) -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded IQ2_XXS layer images in 2 pinned host slots, N(0,1) f32 activations)",
-        "config": {"workload": "llama3-70b-ffn-iq2_xxs-bs1-80layers-streamed", "d_model": DM, "d_ff": DF,
+        "config": {"workload": f"llama3-70b-ffn-iq2_xxs-bs1-{L}layers-streamed", "d_model": DM, "d_ff": DF,
                    "layers": L, "batch": 1, "weights": "IQ2_XXS", "slots": 2, "layer_bytes": wbytes},
         "ffn_tok_s": round(1e3 / ms_tok, 3),
         "h2d_copy_only_gbs": round(h2d, 3),
+        "h2d_pinned_memcpy_peak_gbs": round(h2d_peak, 3),
+        "h2d_frac_of_memcpy_peak": round(h2d / h2d_peak, 4),
         "overlap_efficiency": round(ms_copy / ms_tok, 4),
         "ffn_resident_hbm_gbs": round(ffn_gbs, 1),
         "ffn_resident_pct_of_peak": round(100.0 * ffn_gbs / PEAK_HBM_GBS, 2),
@@ -465,10 +522,8 @@ def bench_stream(eng, args) -> int:
                                "host-link bound"},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(out), flush=True)
     st.free()
-    eng.close()
-    return 0
+    return out
 
 
 def bench_disk(eng, args) -> int:
@@ -677,7 +732,7 @@ def bench_lmhead(eng, args) -> int:
     return 0
 
 
-def bench_smollm(eng, args) -> int:
+def bench_smollm(eng, args) -> dict:
     """SmolLM2-135M-shaped SwiGLU FFN (d_model 576, d_ff 1536) in
     Q4_0, 30 layers, batch 1.  The 30-layer stack is 45 MB; 8 copies (360 MB, beyond the
     256 MB last-level cache) rotate across steps so weights come from HBM.  value =
@@ -804,9 +859,7 @@ def bench_smollm(eng, args) -> int:
         "roofline": roofline_step(gbs, "whole step: the one-launch Q4_0 FFN kernel per layer (launch-latency bound)"),
         "cpu_baseline": cpu,
     }
-    print(json.dumps(out), flush=True)
-    eng.close()
-    return 0
+    return out
 
 
 def bench_q4km(eng, args) -> int:
@@ -1235,6 +1288,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="default workload: skip the compact forms of the other BASELINE.json configs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 256 MiB device copy before timing (reference point for HBM counters)")
     ap.add_argument("--workload", default="bs1", choices=["bs1", "batched", "moe", "stream", "smollm", "q4km", "block", "disk",
@@ -1271,11 +1326,11 @@ def main() -> int:
     eng = hayai_amd.HipEngine(0)
     log(f"[bench] device {eng.device_name} {eng.arch} CUs={eng.device_info.compute_units}")
     if args.workload == "moe":
-        return bench_moe(eng, args)
+        return emit(eng, bench_moe(eng, args))
     if args.workload == "stream":
-        return bench_stream(eng, args)
+        return emit(eng, bench_stream(eng, args))
     if args.workload == "smollm":
-        return bench_smollm(eng, args)
+        return emit(eng, bench_smollm(eng, args))
     if args.workload == "q4km":
         return bench_q4km(eng, args)
     if args.workload == "disk":
@@ -1307,7 +1362,7 @@ def main() -> int:
     log(f"[bench] {LAYERS} layers resident: {stride * LAYERS / 2**30:.2f} GiB of Q4_K weights")
     desc = eng.ffn_desc((Q4_K, Q4_K, Q4_K), D_MODEL, D_FF, lay)
     if args.workload == "batched":
-        return bench_batched(eng, pack, lay, stride, desc, args)
+        return emit(eng, bench_batched(eng, pack, lay, stride, desc, args))
     if args.workload == "block":
         return bench_block(eng, pack, lay, stride, desc, args)
 
@@ -1397,6 +1452,8 @@ def main() -> int:
         f"({dn_gbs:.0f} GB/s)")
     layer_us = ms * 1e3 / LAYERS
 
+    configs = None if args.no_configs else compact_configs(eng, pack, lay, stride, desc)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(eng, pack, lay, stride, xs, args.cpu_budget)
@@ -1441,6 +1498,7 @@ def main() -> int:
         "down_kernel": {"kernel": "hh_q4k_dn_ring_d4 (residual epilogue)", "us": round(dn * 1e3, 3),
                         "gbs": round(dn_gbs, 1)},
         "cpu_baseline": cpu,
+        "configs": configs,
     }
     print(json.dumps(out), flush=True)
     eng.close()
