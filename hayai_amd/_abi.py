@@ -120,6 +120,10 @@ class MoeDesc(C.Structure):
         ("gating", C.c_int),
         ("norm_topk_prob", C.c_int),
         ("routed_scaling_factor", C.c_float),
+        ("shared_d_ff", C.c_size_t),
+        ("shared_gate_off", C.c_size_t),
+        ("shared_up_off", C.c_size_t),
+        ("shared_down_off", C.c_size_t),
     ]
 
 

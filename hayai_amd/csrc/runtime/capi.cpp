@@ -745,6 +745,17 @@ static hh_status validate_moe_experts(hh_engine* e, const hh_moe_desc* d, const 
     if (((uintptr_t)experts->ptr + off) % 16 || d->expert_stride % 16 || d->gate_off % 16 || d->up_off % 16 ||
         d->down_off % 16)
         return fail(HH_ERR_INVALID, "moe: expert packs and tensor offsets must be 16-byte aligned");
+    if (d->shared_d_ff) {  // the shared expert: an FFN of d_model x shared_d_ff in the same buffer
+        HH_TRY(validate_shape(d->type, d->shared_d_ff, d->d_model));
+        HH_TRY(validate_shape(d->type, d->d_model, d->shared_d_ff));
+        size_t rsf;
+        HH_TRY(row_bytes(d->type, d->shared_d_ff, &rsf));
+        const size_t g = d->shared_d_ff * rin, dn = d->d_model * rsf;
+        if (d->shared_gate_off > SIZE_MAX - g || d->shared_up_off > SIZE_MAX - g || d->shared_down_off > SIZE_MAX - dn)
+            return fail(HH_ERR_INVALID, "moe: shared expert layout overflows");
+        HH_TRY(check_range(experts, off, std::max({d->shared_gate_off + g, d->shared_up_off + g, d->shared_down_off + dn}),
+                           "moe shared expert"));
+    }
     return HH_OK;
 }
 
@@ -825,9 +836,12 @@ hh_status hh_moe_ffn_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* exper
     if (T == 0) return HH_OK;
     HH_TRY(e->select());
     std::lock_guard<std::mutex> lk(e->ws_mutex);
-    return e->enqueue_moe_ffn(d, (const uint8_t*)experts->ptr + experts_off, (const float*)((const char*)x->ptr + x_off),
-                              T, (int32_t*)((char*)ids->ptr + ids_off), (float*)((char*)weights->ptr + weights_off),
-                              (float*)((char*)y->ptr + y_off));
+    const uint8_t* ex = (const uint8_t*)experts->ptr + experts_off;
+    const float* xp = (const float*)((const char*)x->ptr + x_off);
+    float* yp = (float*)((char*)y->ptr + y_off);
+    HH_TRY(e->enqueue_moe_ffn(d, ex, xp, T, (int32_t*)((char*)ids->ptr + ids_off),
+                              (float*)((char*)weights->ptr + weights_off), yp));
+    return e->enqueue_moe_shared(d, ex, xp, T, yp);
 }
 
 hh_status hh_moe_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* experts, size_t experts_off,
@@ -857,10 +871,13 @@ hh_status hh_moe_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* experts, 
     HH_TRY(e->grow(&e->ws_moe_ids, &e->ws_moe_ids_cap, kb));
     HH_TRY(e->grow(&e->ws_moe_w, &e->ws_moe_w_cap, kb));
     // routing runs inside the gate/up kernel
-    return e->enqueue_moe_ffn(d, (const uint8_t*)experts->ptr + experts_off, (const float*)((const char*)x->ptr + x_off),
-                              T, (int32_t*)e->ws_moe_ids, (float*)e->ws_moe_w, (float*)((char*)y->ptr + y_off),
+    const uint8_t* ex = (const uint8_t*)experts->ptr + experts_off;
+    const float* xp = (const float*)((const char*)x->ptr + x_off);
+    float* yp = (float*)((char*)y->ptr + y_off);
+    HH_TRY(e->enqueue_moe_ffn(d, ex, xp, T, (int32_t*)e->ws_moe_ids, (float*)e->ws_moe_w, yp,
                               (const float*)((const char*)logits->ptr + logits_off),
-                              bias ? (const float*)((const char*)bias->ptr + bias_off) : nullptr);
+                              bias ? (const float*)((const char*)bias->ptr + bias_off) : nullptr));
+    return e->enqueue_moe_shared(d, ex, xp, T, yp);
 }
 
 // ---------------------------------------------------------------- events -------------

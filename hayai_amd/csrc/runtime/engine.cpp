@@ -1437,6 +1437,36 @@ hh_status hh_engine::enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* expert
     return HH_OK;
 }
 
+// The shared expert (DeepSeek-style, crates/hayai-core/src/moe_infer.rs:456-493): an FFN of
+// d_model x shared_d_ff added with weight 1 after the routed experts' sum (acc[j] += d[j],
+// then the caller's x += acc).  One token: the ring kernels, the down kernel adding its output
+// to y as it stores (y = y + down).  Several tokens: the batched FFN in passes of at most 16
+// tokens (the f16 weight-stream MFMA kernels, f32-level accuracy: no int8 activations here),
+// into a workspace, then y += it.
+hh_status hh_engine::enqueue_moe_shared(const hh_moe_desc* d, const uint8_t* experts, const float* x, size_t T,
+                                        float* y) {
+    if (d->shared_d_ff == 0 || T == 0) return HH_OK;
+    if (T * d->d_model > 0xFFFFFFFFu) return fail(HH_ERR_INVALID, "moe: %zu tokens too many for the shared expert", T);
+    const hh_ffn_desc s{d->type, d->type, d->type, d->act, d->d_model, d->shared_d_ff,
+                        d->shared_gate_off, d->shared_up_off, d->shared_down_off};
+    const size_t dm = d->d_model;
+    if (T == 1 && ring_ok(&s, experts + s.gate_off, experts + s.up_off, experts + s.down_off, x)) {
+        HH_TRY(enqueue_ring_gu(&s, experts + s.gate_off, experts + s.up_off, x));
+        HH_TRY(enqueue_ring_dn(&s, experts + s.down_off, y, y));
+        ffn_calls += 3;
+        return HH_OK;
+    }
+    HH_TRY(grow(&ws_f, &ws_f_cap, T * dm * sizeof(float)));
+    for (size_t b0 = 0; b0 < T; b0 += kMmrMaxTokens) {
+        const size_t nb = std::min(kMmrMaxTokens, T - b0);
+        HH_TRY(enqueue_ffn_batched(&s, experts, x + b0 * dm, nb, (float*)ws_f + b0 * dm));
+    }
+    hipFunction_t fn;
+    HH_TRY(kernel("hh_add_kernel", &fn));
+    hh_add_args aa{y, (const float*)ws_f, y, (uint32_t)(T * dm), 0u};
+    return launch(fn, (uint32_t)((T * dm + 255) / 256), 256, aa);
+}
+
 // ---------------------------------------------------------------- bring-up -----------
 
 static std::vector<std::string> required_kernels() {

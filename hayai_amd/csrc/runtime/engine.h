@@ -267,6 +267,9 @@ struct hh_engine {
     hh_status enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* experts, const float* x, size_t T,
                               int32_t* ids, float* wts, float* y, const float* logits = nullptr,
                               const float* bias = nullptr);
+    // The shared expert of an MoE layer (moe_infer.rs:456-493), after the routed experts:
+    // y[t] += FFN_shared(x[t]).  Nothing when the descriptor has none.
+    hh_status enqueue_moe_shared(const hh_moe_desc* d, const uint8_t* experts, const float* x, size_t T, float* y);
     // Q4 LUT GEMV (hayai's 4-bit dictionary format): W m rows of n/2 bytes, lut 16 f32.
     hh_status enqueue_lut(size_t m, size_t n, const uint8_t* w, const float* lut, const float* x, float* y);
     // Reports (and clears) a grid-barrier timeout recorded by a fused kernel.  Syncs.

@@ -499,11 +499,14 @@ class HipEngine:
     def moe_desc(d_model: int, d_ff: int, n_experts: int, top_k: int, expert_stride: int, offs,
                  ggml_type: int = Q4_K, act: int = ACT_SILU, n_group: int = 0, topk_group: int = 0,
                  gating: int = 0, norm_topk_prob: bool = False,
-                 routed_scaling_factor: float = 1.0) -> _abi.MoeDesc:
-        """MoeMeta (exec_plan.rs:244-271) + the resident expert layout (moe_infer.rs:330-339)."""
+                 routed_scaling_factor: float = 1.0, shared=None) -> _abi.MoeDesc:
+        """MoeMeta (exec_plan.rs:244-271) + the resident expert layout (moe_infer.rs:330-339).
+        shared: (shared_d_ff, (gate_off, up_off, down_off)) of the always-active shared expert
+        (moe_infer.rs:456-493), offsets in the experts buffer; None: no shared expert."""
         g, u, dn = offs
+        sd, (sg, su, sdn) = shared if shared is not None else (0, (0, 0, 0))
         return _abi.MoeDesc(ggml_type, act, d_model, d_ff, n_experts, top_k, expert_stride, g, u, dn, n_group,
-                            topk_group, gating, int(norm_topk_prob), routed_scaling_factor)
+                            topk_group, gating, int(norm_topk_prob), routed_scaling_factor, sd, sg, su, sdn)
 
     def route_experts(self, desc: _abi.MoeDesc, logits: np.ndarray, bias=None):
         """route_experts (moe_infer.rs:865-934) for logits of shape (T, n_experts): returns

@@ -334,6 +334,12 @@ typedef struct hh_moe_desc {
     int gating;           /* 0 softmax over all experts, 1 sigmoid */
     int norm_topk_prob;   /* renormalise the top_k weights */
     float routed_scaling_factor;
+    /* Shared expert (DeepSeek-style, moe_infer.rs:456-493): always active with weight 1 and
+     * added after the routed experts, y[t] += down_s(act(gate_s . x[t]) * (up_s . x[t])),
+     * its tensors (of `type`, shared_d_ff wide) at these byte offsets from experts_off.
+     * shared_d_ff 0: no shared expert (shared_*_off unused). */
+    size_t shared_d_ff;
+    size_t shared_gate_off, shared_up_off, shared_down_off;
 } hh_moe_desc;
 
 /* route_experts + top_k_indices (crates/hayai-core/src/moe_infer.rs:852-934) for T tokens:
@@ -350,8 +356,9 @@ hh_status hh_route_experts(hh_engine* e, const hh_moe_desc* d, const float* logi
 
 /* The routed-expert FFN and combine of moe_infer.rs:342-455 for T tokens:
  * y[t] = sum_s weights[t][s] * down_e(act(gate_e x[t]) * up_e x[t]), e = ids[t][s], in slot
- * order.  Ids outside [0, n_experts) (the -1 of an empty slot) contribute nothing.  Experts
- * live in one device buffer at experts_off.  Enqueue only. */
+ * order, then the shared expert's output (when the descriptor has one, :456-493).  Ids
+ * outside [0, n_experts) (the -1 of an empty slot) contribute nothing.  Experts live in one
+ * device buffer at experts_off.  Enqueue only. */
 hh_status hh_moe_ffn_dev(hh_engine* e, const hh_moe_desc* d, const hh_buf* experts, size_t experts_off,
                          const hh_buf* x, size_t x_off, size_t T, const hh_buf* ids, size_t ids_off,
                          const hh_buf* weights, size_t weights_off, hh_buf* y, size_t y_off);

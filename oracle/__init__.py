@@ -63,6 +63,7 @@ def lib():
         L.or_route_experts.argtypes = [P, C.c_int, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                        C.c_float, P, P]
         L.or_moe_token.argtypes = [C.c_int, sz, sz, P, sz, sz, sz, sz, C.c_int, P, P, P, P]
+        L.or_moe_shared.argtypes = [C.c_int, sz, sz, P, P, P, P, P]
         L.or_quantize_q4_k.argtypes = [P, sz, P]
         L.or_quantize_act_q8.argtypes = [P, sz, P, P]
         L.or_ffn_q8.argtypes = [C.c_int, C.c_int, C.c_int, sz, sz, P, sz, P, sz, P, sz, C.c_int, P, P]
@@ -250,7 +251,9 @@ def route_experts(scores, top_k: int, bias=None, n_group: int = 0, topk_group: i
     return ids[:k].tolist(), w[:k]
 
 
-def moe_token(t: int, d_model: int, d_ff: int, w, expert_stride: int, offs, ids, wts, x, acc=None):
+def moe_token(t: int, d_model: int, d_ff: int, w, expert_stride: int, offs, ids, wts, x, acc=None, shared=None):
+    """The routed experts of one token (moe_infer.rs:342-455) accumulated into acc, then the
+    shared expert (:456-493) when shared = (shared_d_ff, wg, wu, wd) is given."""
     w = np.ascontiguousarray(w, dtype=np.uint8)
     ids = np.ascontiguousarray(ids, dtype=np.int32)
     wts = np.ascontiguousarray(wts, dtype=np.float32)
@@ -259,6 +262,10 @@ def moe_token(t: int, d_model: int, d_ff: int, w, expert_stride: int, offs, ids,
     g_off, u_off, d_off = offs
     _check(lib().or_moe_token(t, d_model, d_ff, _p(w), expert_stride, g_off, u_off, d_off, ids.size,
                               _p(ids), _p(wts), _p(x), _p(acc)), "moe_token")
+    if shared is not None:
+        sdf, sg, su, sd = shared
+        sg, su, sd = (np.ascontiguousarray(a, dtype=np.uint8) for a in (sg, su, sd))
+        _check(lib().or_moe_shared(t, d_model, sdf, _p(sg), _p(su), _p(sd), _p(x), _p(acc)), "moe_shared")
     return acc
 
 

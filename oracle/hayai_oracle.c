@@ -61,7 +61,7 @@ int or_max_threads(void) {
 
 /* Planted mistakes for the tests that pin this oracle: a pin check must fail when one of
  * these is switched on (0 = none, 1 = or_ffn swaps gate and up, 2 = or_moe_token reads
- * expert ids[t] + 1 instead of ids[t]). */
+ * expert ids[t] + 1 instead of ids[t], 3 = or_moe_shared swaps its gate and up). */
 static int g_mutation = 0;
 
 void or_set_mutation(int m) { g_mutation = m; }
@@ -782,6 +782,35 @@ int or_moe_token(int type, size_t d_model, size_t d_ff, const uint8_t* w, size_t
         if (rc == OR_OK)
             for (size_t j = 0; j < d_model; j++) acc[j] += wts[t] * d[j];
     }
+    free(g);
+    free(u);
+    free(d);
+    return rc;
+}
+
+/* The shared expert of an MoE layer; crates/hayai-core/src/moe_infer.rs:456-493: always
+ * active with weight 1, after the routed experts: g = gate_s . x, u = up_s . x,
+ * g[j] = (g[j] / (1 + exp(-g[j]))) * u[j], d = down_s . g, acc[j] += d[j]. */
+int or_moe_shared(int type, size_t d_model, size_t d_ff, const uint8_t* wg, const uint8_t* wu, const uint8_t* wd,
+                  const float* x, float* acc) {
+    size_t rg = row_bytes_or0(type, d_model), rd = row_bytes_or0(type, d_ff);
+    float* g = (float*)malloc(d_ff * sizeof(float));
+    float* u = (float*)malloc(d_ff * sizeof(float));
+    float* d = (float*)malloc(d_model * sizeof(float));
+    int rc = (g && u && d) ? OR_OK : OR_EINVAL;
+    if (g_mutation == 3) { /* planted: the shared expert reads its up tensor as gate */
+        const uint8_t* t = wg;
+        wg = wu;
+        wu = t;
+    }
+    if (rc == OR_OK) rc = or_gemv(type, d_ff, d_model, wg, d_ff * rg, x, g);
+    if (rc == OR_OK) rc = or_gemv(type, d_ff, d_model, wu, d_ff * rg, x, u);
+    if (rc == OR_OK) {
+        for (size_t j = 0; j < d_ff; j++) g[j] = (g[j] / (1.0f + expf(-g[j]))) * u[j];
+        rc = or_gemv(type, d_model, d_ff, wd, d_model * rd, g, d);
+    }
+    if (rc == OR_OK)
+        for (size_t j = 0; j < d_model; j++) acc[j] += d[j];
     free(g);
     free(u);
     free(d);

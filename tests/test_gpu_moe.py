@@ -95,6 +95,7 @@ def make_experts(engine, E, d_model, d_ff, seed):
 
 
 @pytest.mark.parametrize("E,k,d_model,d_ff,T", [
+    (128, 8, 2048, 768, 1),    # config 4 at one token: 128 experts, routing inside the ring kernels
     (32, 8, 2048, 768, 1),     # Qwen3-30B-A3B expert shape (one token: the ring kernels)
     (32, 8, 2048, 768, 5),
     (8, 2, 4096, 1024, 1),     # one token, 64 lanes per gate/up row
@@ -131,6 +132,54 @@ def test_moe_ffn_matches_oracle(engine, E, k, d_model, d_ff, T):
         assert err <= REL_TOL
 
 
+@pytest.mark.parametrize("T", [1, 5, 20])
+def test_moe_shared_expert_matches_oracle(engine, T):
+    # The always-active shared expert (moe_infer.rs:456-493) after the routed experts, weight
+    # 1: one token on the ring kernels (down adds into y), several in passes of <= 16 tokens on
+    # the f16 MFMA kernels then an add; against the oracle's routed loop + or_moe_shared, in
+    # both calls (routing on the device, and ids/weights given)
+    E, k, d_model, d_ff, sdf = 16, 4, 2048, 768, 1536
+    oracle.set_threads(min(16, oracle.max_threads()))
+    print(f"[case] moe + shared expert E={E} k={k} {d_model}x{d_ff} shared {sdf} T={T}", flush=True)
+    rin, rsf = hayai_amd.row_bytes(Q4_K, d_model), hayai_amd.row_bytes(Q4_K, sdf)
+    buf0, host, stride, offs = make_experts(engine, E, d_model, d_ff, 90)
+    base = E * stride
+    s_offs = (base, base + sdf * rin, base + 2 * sdf * rin)
+    buf = engine.alloc(base + 2 * sdf * rin + d_model * rsf)
+    buf.copy_from(buf0, base)
+    lo, hi = synth.SCALE_RANGE[Q4_K]
+    for mat, off, rows, cols in ((synth.GATE, s_offs[0], sdf, d_model), (synth.UP, s_offs[1], sdf, d_model),
+                                 (synth.DOWN, s_offs[2], d_model, sdf)):
+        engine.synth_weights_dev(Q4_K, buf, off, rows * cols // 256, synth.seed_for(91, 0, mat), lo, hi)
+    sg = buf.read(np.uint8, sdf * rin, s_offs[0])
+    su = buf.read(np.uint8, sdf * rin, s_offs[1])
+    sd = buf.read(np.uint8, d_model * rsf, s_offs[2])
+    d = engine.moe_desc(d_model, d_ff, E, k, stride, offs, norm_topk_prob=True, shared=(sdf, s_offs))
+    rng = np.random.default_rng(T)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    x = synth.normal(synth.seed_for(9, T, synth.ACT), T * d_model).reshape(T, d_model)
+    lb, xb = engine.upload(logits), engine.upload(x)
+    ids_b, w_b = engine.alloc(4 * T * k), engine.alloc(4 * T * k)
+    y1, y2 = engine.alloc(4 * T * d_model), engine.alloc(4 * T * d_model)
+    engine.moe_dev(d, buf, 0, lb, 0, None, 0, xb, 0, T, y1, 0)
+    engine.route_experts_dev(d, lb, 0, None, 0, T, ids_b, 0, w_b, 0)
+    engine.moe_ffn_dev(d, buf, 0, xb, 0, T, ids_b, 0, w_b, 0, y2, 0)
+    Y1 = y1.read(np.float32, T * d_model).reshape(T, d_model)
+    Y2 = y2.read(np.float32, T * d_model).reshape(T, d_model)
+    np.testing.assert_array_equal(Y1, Y2)
+    ids = ids_b.read(np.int32, T * k).reshape(T, k)
+    w = w_b.read(np.float32, T * k).reshape(T, k)
+    for t in range(T):
+        ref = oracle.moe_token(Q4_K, d_model, d_ff, host, stride, offs, ids[t], w[t], x[t], shared=(sdf, sg, su, sd))
+        routed = oracle.moe_token(Q4_K, d_model, d_ff, host, stride, offs, ids[t], w[t], x[t])
+        err = float(np.max(np.abs(Y1[t] - ref)) / np.max(np.abs(ref)))
+        # the shared expert moves the output (a path that skipped it would fail here)
+        assert float(np.max(np.abs(ref - routed)) / np.max(np.abs(ref))) > 50 * REL_TOL
+        if t in (0, T - 1):
+            print(f"  token {t}: rel err {err:.3e}", flush=True)
+        assert err <= REL_TOL
+
+
 def test_moe_empty_slots_contribute_nothing(engine):
     E, k, d_model, d_ff = 8, 3, 1024, 512
     buf, host, stride, offs = make_experts(engine, E, d_model, d_ff, 77)
@@ -157,6 +206,8 @@ def test_moe_rejects_bad_descriptors(engine):
         engine.moe_desc(d_model, d_ff, E + 1, k, stride, offs),             # experts past the buffer
         engine.moe_desc(d_model, d_ff, E, k, stride + 8, offs),             # misaligned stride
         engine.moe_desc(d_model, 300, E, k, stride, offs),                  # d_ff not a block multiple
+        engine.moe_desc(d_model, d_ff, E, k, stride, offs, shared=(512, (E * stride, 0, 0))),  # shared past the end
+        engine.moe_desc(d_model, d_ff, E, k, stride, offs, shared=(300, (0, 0, 0))),  # shared d_ff not a block multiple
     ]
     for d in bad:
         with pytest.raises(hayai_amd.HipError):

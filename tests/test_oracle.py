@@ -671,6 +671,43 @@ def test_moe_pin_catches_expert_index_slip():
     assert not np.all(np.abs(bad - ref) <= bound)
 
 
+def _shared_setup(t, d_model, d_ff, seed):
+    import hayai_amd.synth as synth
+
+    return (synth.matrix(t, d_ff, d_model, seed), synth.matrix(t, d_ff, d_model, seed + 1),
+            synth.matrix(t, d_model, d_ff, seed + 2))
+
+
+@pytest.mark.parametrize("t,d_model,d_ff,sdf", [(oracle.Q4_K, 256, 256, 512), (oracle.Q4_0, 128, 96, 64)])
+def test_moe_shared_expert_pinned(t, d_model, d_ff, sdf):
+    # or_moe_shared (moe_infer.rs:456-493): the shared expert's SiLU FFN, weight 1, added to
+    # the accumulator.  Pinned on its own by the float64 FFN composition under the propagated
+    # bound (one more rounding for acc += d), and in the layer: after the routed experts, once,
+    # bit for bit fl(routed + shared)
+    sg, su, sd = _shared_setup(t, d_model, sdf, 1500 + t)
+    rng = np.random.default_rng(41)
+    x = rng.normal(size=d_model).astype(np.float32)
+    acc0 = rng.normal(size=d_model).astype(np.float32)
+    buf, stride, offs = _moe_setup(t, 5, d_model, d_ff, 1400 + t)
+    only = oracle.moe_token(t, d_model, d_ff, buf, stride, offs, [], [], x, acc=acc0, shared=(sdf, sg, su, sd))
+    y64, by, _, _ = _ffn64_with_bound((t, t, t), d_model, sdf, sg, su, sd, x, 0)
+    ref = acc0.astype(np.float64) + y64
+    bound = by + U32 * (np.abs(acc0) + np.abs(y64) + by)
+    assert np.all(np.abs(only - ref) <= bound)
+    assert np.max(np.abs(only - ref)) <= 1e-5 * np.max(np.abs(y64))
+    d = oracle.moe_token(t, d_model, d_ff, buf, stride, offs, [], [], x, shared=(sdf, sg, su, sd))
+    ids, wts = [2, 0, 4], np.array([0.5, 0.3, 0.2], np.float32)
+    routed = oracle.moe_token(t, d_model, d_ff, buf, stride, offs, ids, wts, x)
+    both = oracle.moe_token(t, d_model, d_ff, buf, stride, offs, ids, wts, x, shared=(sdf, sg, su, sd))
+    np.testing.assert_array_equal(both, routed + d)
+    oracle.set_mutation(3)
+    try:
+        bad = oracle.moe_token(t, d_model, d_ff, buf, stride, offs, [], [], x, acc=acc0, shared=(sdf, sg, su, sd))
+    finally:
+        oracle.set_mutation(0)
+    assert not np.all(np.abs(bad - ref) <= bound)
+
+
 def test_ffn_q8_composes_the_pinned_pieces():
     # or_ffn_q8 (the batched int8 path's FFN) = or_ffn on x -> q*s, then the down GEMV of
     # h -> q*s, with or_quantize_act_q8, or_ffn and or_gemv each pinned above: bit-exact

@@ -69,14 +69,24 @@ def test_noalloc_equals_ffn_dev_twice(engine, types, big, small):
             assert np.max(np.abs(got - r)) / np.max(np.abs(r)) <= 1e-3
 
 
-def test_noalloc_under_capture_on_fresh_engine():
+# every form the entry point takes: the ring kernels (Q4_K), the fused two-step form
+# (IQ2_XXS, Q4_0) and the unfused form with a Q6_K down GEMV
+CAPTURE_CASES = [
+    ((Q4_K, Q4_K, Q4_K), 2048, 5632),
+    ((IQ2, IQ2, IQ2), 2048, 5632),
+    ((Q4_0, Q4_0, Q4_0), 576, 1536),
+    ((IQ3, Q8_0, Q6_K), 1024, 2048),
+]
+
+
+@pytest.mark.parametrize("types,d_model,d_ff", CAPTURE_CASES)
+def test_noalloc_under_capture_on_fresh_engine(types, d_model, d_ff):
     # A fresh engine owns no workspaces, and any allocation inside a capture is refused: the
     # entry point captures and replays anyway, equal to its eager result on every replay.
-    print("[case] noalloc graph capture", flush=True)
+    print(f"[case] noalloc graph capture types={types} {d_model}x{d_ff}", flush=True)
     eng = hayai_amd.HipEngine(0)
     try:
-        d_model, d_ff = 2048, 5632
-        desc, pack, mats = make_layer(eng, (Q4_K, Q4_K, Q4_K), d_model, d_ff, 301)
+        desc, pack, mats = make_layer(eng, types, d_model, d_ff, 301)
         x = synth.normal(302, d_model)
         xbuf = eng.upload(x)
         y = eng.alloc(4 * d_model)
@@ -85,7 +95,7 @@ def test_noalloc_under_capture_on_fresh_engine():
         eng.ffn_dev_noalloc(desc, pack, 0, xbuf, 0, y_eager, 0)
         eng.sync()
         ref = y_eager.read(np.float32, d_model)
-        r = oracle.ffn((Q4_K,) * 3, d_model, d_ff, *mats, x)
+        r = oracle.ffn(types, d_model, d_ff, *mats, x)
         assert np.max(np.abs(ref - r)) / np.max(np.abs(r)) <= 1e-3
         for rep in range(3):
             y.fill(0)
