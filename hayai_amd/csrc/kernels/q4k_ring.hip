@@ -32,10 +32,10 @@
 
 #define HH_RING_BLOCK (HH_RING_CW * HH_WAVE)
 
-// Phase timeline of the ring kernels, compiled in only for the timeline tool
-// (csrc/trace/ring_timeline.cpp builds a separate code object with HH_RING_TRACE): one
-// timestamp of the 100 MHz realtime counter per workgroup and phase, indexed by the layer
-// that the weight pointer falls in ((w - base) / stride, set by the tool).
+// Phase timeline of the ring kernels, compiled in only when a separate code object is built
+// with -DHH_RING_TRACE for a timeline probe (never in the library): one timestamp of the
+// 100 MHz realtime counter per workgroup and phase, indexed by the layer that the weight
+// pointer falls in ((w - base) / stride, both set by the probe's host side).
 #ifdef HH_RING_TRACE
 __device__ unsigned long long hh_ring_trace[2][64][512][8];  // [gate/up, down][layer][workgroup][phase]
 __constant__ const uint8_t* hh_ring_trace_base;  // constant: scalar loads, no vector-memory wait
@@ -418,9 +418,11 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
             __builtin_amdgcn_sched_barrier(0);
             F::make_h(hraw, u2, hr);
 #ifdef HH_RING_TRACE
-            const float hchk = __builtin_bit_cast(float, hraw.a[0].x ^ hraw.b[3].w) + hraw.s1.w;
-            HH_RING_MARK(1, a.wd, 4, tid == 0 && hchk != -1.f);                     // h arrived (wave 0)
-            HH_RING_MARK(1, a.wd, 5, tid == HH_RING_BLOCK - HH_WAVE && hchk != -1.f);  // h arrived (last wave)
+            if constexpr (__is_same(typename F::hraw_t, hh_hd_raw)) {  // Q4_K's digit form
+                const float hchk = __builtin_bit_cast(float, hraw.a[0].x ^ hraw.b[3].w) + hraw.s1.w;
+                HH_RING_MARK(1, a.wd, 4, tid == 0 && hchk != -1.f);                     // h arrived (wave 0)
+                HH_RING_MARK(1, a.wd, 5, tid == HH_RING_BLOCK - HH_WAVE && hchk != -1.f);  // h arrived (last wave)
+            }
 #endif
         } else {
 #pragma unroll

@@ -6,7 +6,7 @@
  * in crates/hayai-core that calls it; the comment on each declaration names the reference
  * interface (file:line, paths relative to the reference repository root).  Plain C types
  * only: pointers, sizes, integers.  A Rust `hayai-hip` crate binds this header with an
- * `extern "C"` block; INTEGRATION.md shows that binding.
+ * `extern "C"` block that declares these functions and mirrors the structs field by field.
  *
  * Conventions
  *   - Every function returns hh_status (0 = HH_OK).  On failure a message is stored in a
@@ -171,8 +171,17 @@ void hh_pending_destroy(hh_pending* p);
 /* ggml_gemv_batched_q4_k (crates/hayai-opencl/src/compute.rs:179-257) generalised to every
  * type, as execute_quant_gemv_batched does (crates/hayai-core/src/orchestrator.rs:240-269):
  * outputs[b*m + r] = W[r] . inputs[b*n .. b*n+n) for b < batch.  Host weights and
- * activations, blocking.  Q4_K with batch >= 2 runs on the matrix cores (f16 operands, f32
- * accumulation) in chunks of up to 64 tokens; other types loop over tokens. */
+ * activations, blocking.  Q4_K with batch >= 2 runs on the matrix cores in passes of up to
+ * 64 tokens; other types loop over tokens.  Precision of the Q4_K passes:
+ *   - passes of 2..16 tokens: f32 activations (as f16 hi + lo pairs), f32 accumulation:
+ *     within ~1e-6 of the f32 product;
+ *   - passes of 17..64 tokens: each token's activations are first quantized to int8 per
+ *     32-element block (s = max|x| / 127, q = round-half-away(x / s), clamped to +-127)
+ *     and multiplied exactly on the int8 matrix cores; the
+ *     result differs from the f32 product by that quantization: measured 0.7-1.9% of
+ *     max|y| per token on N(0,1) activations (the tests bound it at 4%).
+ * Set HAYAI_HIP_MMQ=0 in the environment before creating the engine to keep f32
+ * activations for every batch size (17..64 tokens then run one token at a time). */
 hh_status hh_gemv_batched(hh_engine* e, int ggml_type, size_t m, size_t n, const uint8_t* weights,
                           size_t weights_len, const float* inputs, float* outputs, size_t batch);
 /* Same with device buffers (weights at w_off; x: batch*n floats, y: batch*m floats);
@@ -265,9 +274,7 @@ hh_status hh_ffn_block_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pac
  * callers that run FFN blocks with no other op between them (FFN-only layer stacks, the
  * chained-layer benchmark): small all-Q4_0 / all-Q8_0 layers (d_model, d_ff <= 2048) run
  * every layer in one persistent launch that requests each layer's weights ahead of the
- * activation exchanges; all-Q4_K layers (d_model <= 4096, d_ff <= 16384) do so when the
- * engine was created with HAYAI_HIP_Q4K_STACK=1; other layouts run hh_ffn_block_dev per
- * layer.  Results match
+ * activation exchanges; other layouts run hh_ffn_block_dev per layer.  Results match
  * hh_ffn_block_dev applied layer by layer to f32 rounding (sums in another order).
  * HH_ERR_INVALID for n_layers 0 or ranges outside the buffers.  Enqueue only. */
 hh_status hh_ffn_block_stack_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
@@ -277,9 +284,12 @@ hh_status hh_ffn_block_stack_dev(hh_engine* e, const hh_ffn_desc* d, const hh_bu
 
 /* The FFN op for `batch` tokens (x, y: batch rows of d_model floats): the batched-prefill
  * form of the op (prefill_wave.rs:577-584 drives execute_quant_gemv_batched for FFN
- * matrices).  All-Q4_K FFNs run gate/up(+act) and down on the matrix cores; other formats
- * run the single-token op per token.  _dev: device buffers, enqueue only; without: host
- * x / y, blocking. */
+ * matrices).  All-Q4_K FFNs run gate/up(+act) and down on the matrix cores with the
+ * precision hh_gemv_batched states: passes of 17..64 tokens quantize x, and then h, to
+ * int8 per 32-element block, which moves the FFN output by 3-13% of max|y| per token on
+ * N(0,1) inputs (h is heavy-tailed; the tests bound it at 25%); passes of 2..16 tokens stay
+ * within 1e-3 of the f32 FFN (h enters down as f16).  Other formats run the single-token op
+ * per token.  _dev: device buffers, enqueue only; without: host x / y, blocking. */
 hh_status hh_ffn_batched_dev(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
                              const hh_buf* x, size_t x_off, size_t batch, hh_buf* y, size_t y_off);
 hh_status hh_ffn_batched(hh_engine* e, const hh_ffn_desc* d, const hh_buf* pack, size_t pack_off,
