@@ -1016,106 +1016,101 @@ hh_status hh_engine::enqueue_q4k_mmr(int kind, size_t m, size_t n, const uint8_t
     return HH_OK;
 }
 
-// ---- int8 MFMA batched Q4_K (q4k_mmq.hip) ----
+// ---- batched Q4_K with int8 activations (q4k_mmi.hip) ----
 
-// Must match struct hh_mmq_prep_args / hh_mmq_args in kernels/q4k_mmq.hip.
-struct MmqPrepArgs {
+// Batched Q4_K with int8 activations (q4k_mmi.hip) from 17 tokens on: at 16 the f16
+// weight-stream kernels (q4k_mmr.hip) are faster on the MI355X (8B FFN, 32 layers: 1.32 ms
+// f16 vs 1.54-1.58 ms int8).
+constexpr size_t kMmqMinTokens = 17, kMmqMaxTokens = 64;
+
+bool hh_engine::mmq_ok(size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const {
+    return mmq && !q4k_generic && b >= std::min(mmi_min, kMmqMinTokens) && b >= 2 && b <= kMmqMaxTokens && m >= 1 &&
+           m <= 0xFFFFFFFFu && n >= 256 && n % 256 == 0 && n <= 0xFFFFFFFFu &&
+           ((((uintptr_t)w0 | (uintptr_t)w1 | (uintptr_t)x) & 15u) == 0);
+}
+
+// Must match struct hh_mmi_prep_args / hh_mmi_args in kernels/q4k_mmi.hip.
+struct MmiPrepArgs {
     const float* x;
     uint8_t* xs;
-    uint32_t n, b, tp, pad;
+    uint32_t n, b, tt, pad;
 };
-struct MmqArgs {
+struct MmiArgs {
     const uint8_t* w0;
     const uint8_t* w1;
     const uint8_t* xs;
     float* y;
+    uint8_t* hs;
     float* part;
     unsigned* cnt;
     uint64_t row_bytes;
-    uint32_t m, n, b, nw, kc;
+    uint32_t m, n, b, kc, sbc;
     int32_t act;
 };
-// From 17 tokens the int8 kernels beat the f16 ones on the MI355X (8B FFN, 32 layers: 16
-// tokens 1.61 ms int8 vs 1.32 ms f16; 24 tokens 2.39 vs 2.88; 64 tokens 3.23 vs 4.59).
-constexpr size_t kMmqMinTokens = 17, kMmqMaxTokens = 64;
-static size_t mmq_stage_bytes(size_t tp) { return 320 * tp; }
-
-bool hh_engine::mmq_ok(size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const {
-    return mmq && !q4k_generic && b >= kMmqMinTokens && b <= kMmqMaxTokens && m >= 1 && m <= 0xFFFFFFFFu &&
-           n >= 256 && n % 256 == 0 && n <= 0xFFFFFFFFu &&
-           ((((uintptr_t)w0 | (uintptr_t)w1 | (uintptr_t)x) & 15u) == 0);
+constexpr size_t kMmiStage = 9216, kMmiWaves = 4, kMmiLds = 147456;
+// 16-token tiles of a pass: an FFN's three token tiles run as four (its gate/up kernel is
+// instantiated for 1, 2 and 4), and its prep, gate/up and down agree on the count
+static size_t mmi_tiles(bool ffn, size_t b) {
+    const size_t tt = (b + 15) / 16;
+    return ffn && tt == 3 ? 4 : tt;
 }
 
-hh_status hh_engine::enqueue_mmq_prep(const float* x, size_t b, size_t n, size_t tp, void* xs) {
+hh_status hh_engine::enqueue_mmi_prep(const float* x, size_t b, size_t n, size_t tt, void* xs) {
     hipFunction_t fn;
-    HH_TRY(kernel("hh_mmq_prep", &fn));
-    MmqPrepArgs a{x, (uint8_t*)xs, (uint32_t)n, (uint32_t)b, (uint32_t)tp, 0u};
-    const size_t blocks = tp * (n / 32);  // one 32-lane team per (token, block), 8 per workgroup
-    return launch(fn, (uint32_t)((blocks + 7) / 8), 256, a);
+    HH_TRY(kernel("hh_mmi_prep", &fn));
+    MmiPrepArgs a{x, (uint8_t*)xs, (uint32_t)n, (uint32_t)b, (uint32_t)tt, 0u};
+    const size_t teams = 16 * tt * (n / 32);  // one 32-lane team per (token, block), 8 per workgroup
+    return launch(fn, (uint32_t)((teams + 7) / 8), 256, a);
 }
 
-hh_status hh_engine::enqueue_q4k_mmq(bool ffn, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1,
-                                     const void* xs, size_t b, float* y, int act) {
-    const size_t tt = (b + 15) / 16, tp = 16 * tt, nsb = n / 256, nu = (m + 15) / 16;
-    // Superblocks per chunk and units per workgroup, as measured on the MI355X (8B shapes, 16
-    // and 64 tokens): up to 32 tokens, long chunks (whole rows where they fit: no split-K
-    // partials) on 4-wave workgroups; 48..64 tokens, whose stages leave room for few
-    // superblocks, 8-wave workgroups over chunks of 7 (or 4) superblocks.
-    static const int kS[5][6] = {{0}, {2, 4, 7, 8, 14, 16}, {2, 4, 7, 8, 14, 0}, {2, 4, 7, 8, 0, 0}, {2, 4, 6, 7, 0, 0}};
-    const size_t lds = (size_t)props.sharedMemPerBlock;
-    auto fits = [&](int cand) { return cand > 0 && (size_t)cand * mmq_stage_bytes(tp) + 64 <= lds; };
-    int S = 0;
-    for (int i = 0; i < 6; i++) {
-        const int cand = kS[tt][i];
-        if (!fits(cand)) continue;
-        if (mmq_s > 0) {  // HAYAI_HIP_MMQ_S: a fixed chunk size where instantiated
-            if (cand == mmq_s) S = cand;
-            continue;
-        }
-        if (tt <= 2) {
-            // the longest chunk that divides the row (else the longest it holds)
-            if ((size_t)cand <= nsb && (nsb % (size_t)cand == 0 || S == 0 || nsb % (size_t)S != 0)) S = cand;
-        } else if (nsb % 7 == 0 ? cand == 7 : cand == 4) {
-            S = cand;
-        }
+// Workgroups of 4 units (64 rows) + a copy wave.  FFN gate/up: whole rows (one chunk), so the
+// workgroup quantizes its own rows of h; GEMM / down: the superblocks split into chunks so that
+// the grid fills the CUs once, the chunks' partial sums added by the last workgroup of a group.
+hh_status hh_engine::enqueue_q4k_mmi(bool ffn, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1,
+                                     const void* xs, size_t b, float* y, void* hs, int act, size_t tiles) {
+    const size_t tt = tiles ? tiles : mmi_tiles(ffn, b), nsb = n / 256, nu = (m + 15) / 16;
+    const size_t groups = (nu + kMmiWaves - 1) / kMmiWaves;
+    size_t kc = 1, sbc = nsb;
+    if (!ffn) {
+        const size_t cus = (size_t)props.multiProcessorCount;
+        kc = std::max<size_t>(1, std::min(nsb, (cus + groups / 2) / groups));
+        sbc = (nsb + kc - 1) / kc;
+        kc = (nsb + sbc - 1) / sbc;
     }
-    if (S == 0)
-        for (int i = 0; i < 6 && S == 0; i++)
-            if (fits(kS[tt][i])) S = kS[tt][i];
-    if (S == 0) return HH_ERR_UNSUPPORTED_DEVICE;
-    const uint32_t kc = (uint32_t)((nsb + S - 1) / S);
-    const size_t nw_want = mmq_nw > 0 ? (size_t)mmq_nw : (tt <= 2 ? 4 : 8);
-    const uint32_t nw = (uint32_t)std::min<size_t>(nw_want, nu);
-    const uint32_t groups = (uint32_t)((nu + nw - 1) / nw);
-    const size_t nt = ffn ? 2 : 1;
+    const size_t slot = kMmiStage * tt, ring = std::min<size_t>(16, kMmiLds / slot);
+    const bool refill = sbc > ring;  // the chunk's stages stream through the LDS ring
+    const int D = ffn ? 2 : mmi_d == 2 || mmi_d == 4 ? mmi_d : (sbc % 4 == 0 ? 4 : 2);
     if (kc > 1) {
-        HH_TRY(grow(&ws_part, &ws_part_cap, (size_t)groups * kc * nw * nt * tt * 4 * 64 * sizeof(float)));
+        HH_TRY(grow(&ws_part, &ws_part_cap, groups * kc * kMmiWaves * tt * 4 * 64 * sizeof(float)));
         if (ws_cnt_cap < groups * sizeof(unsigned)) {
             HH_TRY(grow(&ws_cnt, &ws_cnt_cap, groups * sizeof(unsigned)));
             HH_TRY_HIP(hipMemsetAsync(ws_cnt, 0, ws_cnt_cap, stream), "hipMemsetAsync(counters)");
         }
     }
     hipFunction_t fn;
-    HH_TRY(kernel(std::string(ffn ? "hh_q4k_mmq_gu_s" : "hh_q4k_mmq_s") + std::to_string(S) + "_t" + std::to_string(tt),
+    HH_TRY(kernel(std::string(ffn ? "hh_q4k_mmi_gu_t" : "hh_q4k_mmi_t") + std::to_string(tt) + "_d" + std::to_string(D) +
+                      (refill ? "_r" : "_w"),
                   &fn));
-    MmqArgs a{};
+    MmiArgs a{};
     a.w0 = w0;
     a.w1 = ffn ? w1 : w0;
     a.xs = (const uint8_t*)xs;
     a.y = y;
+    a.hs = (uint8_t*)hs;
     a.part = (float*)ws_part;
     a.cnt = (unsigned*)ws_cnt;
     a.row_bytes = (uint64_t)(nsb * 144);
     a.m = (uint32_t)m;
     a.n = (uint32_t)n;
     a.b = (uint32_t)b;
-    a.nw = nw;
-    a.kc = kc;
+    a.kc = (uint32_t)kc;
+    a.sbc = (uint32_t)sbc;
     a.act = act;
+    const size_t smem = (refill ? ring : sbc) * slot;
     void* params[] = {&a};
-    const size_t smem = (size_t)S * mmq_stage_bytes(tp);
-    hipError_t err = hipModuleLaunchKernel(fn, groups * kc, 1, 1, nw * 64, 1, 1, (unsigned)smem, stream, params, nullptr);
-    if (err != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel(q4k_mmq)");
+    hipError_t err = hipModuleLaunchKernel(fn, (unsigned)(groups * kc), 1, 1, (unsigned)((kMmiWaves + 1) * 64), 1, 1,
+                                           (unsigned)smem, stream, params, nullptr);
+    if (err != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel(q4k_mmi)");
     return HH_OK;
 }
 
@@ -1134,11 +1129,12 @@ hh_status hh_engine::enqueue_gemv_batched(int type, size_t m, size_t n, const ui
             HH_TRY(enqueue_gemv(type, m, n, w, x + b0 * n, y + b0 * m));
             continue;
         }
-        if (mmq_ok(m, n, nb, w, w, x + b0 * n)) {  // 17..64 tokens: int8 MFMA
-            const size_t tp = 16 * ((nb + 15) / 16);
-            HH_TRY(grow(&ws_xop, &ws_xop_cap, (n / 256) * mmq_stage_bytes(tp)));
-            HH_TRY(enqueue_mmq_prep(x + b0 * n, nb, n, tp, ws_xop));
-            HH_TRY(enqueue_q4k_mmq(false, m, n, w, nullptr, ws_xop, nb, y + b0 * m, 0));
+        if (nb >= mmi_min && mmq_ok(m, n, nb, w, w, x + b0 * n)) {
+            // int8 activations on the f16 matrix cores
+            const size_t tt = (nb + 15) / 16;
+            HH_TRY(grow(&ws_xop, &ws_xop_cap, (n / 256) * tt * kMmiStage));
+            HH_TRY(enqueue_mmi_prep(x + b0 * n, nb, n, tt, ws_xop));
+            HH_TRY(enqueue_q4k_mmi(false, m, n, w, nullptr, ws_xop, nb, y + b0 * m, nullptr, 0));
             continue;
         }
         if (nb <= kMmrMaxTokens && mmr_ok(m, n, nb, w, w, x + b0 * n)) {
@@ -1196,17 +1192,16 @@ hh_status hh_engine::enqueue_ffn_batched(const hh_ffn_desc* d, const uint8_t* pa
             HH_TRY(enqueue_ffn(d, pack, x + b0 * dm, y + b0 * dm));
             continue;
         }
-        if (df % 256 == 0 && mmq_ok(df, dm, nb, wg, wu, x + b0 * dm) && mmq_ok(dm, df, nb, wd, wd, wd)) {
-            // 17..64 tokens on the int8 matrix cores: x -> int8 stages, gate/up + act -> h (f32),
-            // h -> int8 stages, down
-            const size_t tp = 16 * ((nb + 15) / 16);
-            HH_TRY(grow(&ws_xop, &ws_xop_cap, (dm / 256) * mmq_stage_bytes(tp)));
-            HH_TRY(grow(&ws_hop, &ws_hop_cap, (df / 256) * mmq_stage_bytes(tp)));
-            HH_TRY(grow(&ws_h, &ws_h_cap, nb * df * sizeof(float)));
-            HH_TRY(enqueue_mmq_prep(x + b0 * dm, nb, dm, tp, ws_xop));
-            HH_TRY(enqueue_q4k_mmq(true, df, dm, wg, wu, ws_xop, nb, (float*)ws_h, d->act));
-            HH_TRY(enqueue_mmq_prep((const float*)ws_h, nb, df, tp, ws_hop));
-            HH_TRY(enqueue_q4k_mmq(false, dm, df, wd, nullptr, ws_hop, nb, y + b0 * dm, 0));
+        if (nb >= mmi_min && df % 256 == 0 && mmq_ok(df, dm, nb, wg, wu, x + b0 * dm) &&
+            mmq_ok(dm, df, nb, wd, wd, wd)) {
+            // int8 activations on the f16 matrix cores: x -> stages, gate/up + act -> h stages
+            // (quantized in the gate/up kernel), down
+            const size_t tt = mmi_tiles(true, nb);
+            HH_TRY(grow(&ws_xop, &ws_xop_cap, (dm / 256) * tt * kMmiStage));
+            HH_TRY(grow(&ws_hop, &ws_hop_cap, (df / 256) * tt * kMmiStage));
+            HH_TRY(enqueue_mmi_prep(x + b0 * dm, nb, dm, tt, ws_xop));
+            HH_TRY(enqueue_q4k_mmi(true, df, dm, wg, wu, ws_xop, nb, nullptr, ws_hop, d->act));
+            HH_TRY(enqueue_q4k_mmi(false, dm, df, wd, nullptr, ws_hop, nb, y + b0 * dm, nullptr, 0, tt));
             ffn_stage_valid = false;
             ffn_calls += 3 * nb;
             continue;
@@ -1490,10 +1485,11 @@ static std::vector<std::string> required_kernels() {
     for (int S : {2, 4, 7, 8})
         for (const char* kind : {"hh_q4k_mmr_s", "hh_q4k_mmr_gu_s"}) k.push_back(std::string(kind) + std::to_string(S));
     for (int S : {2, 4, 7, 8, 14, 16}) k.push_back("hh_q4k_mmr_dn_s" + std::to_string(S));
-    k.push_back("hh_mmq_prep");
-    for (const char* st : {"s2_t1", "s4_t1", "s7_t1", "s8_t1", "s14_t1", "s16_t1", "s2_t2", "s4_t2", "s7_t2", "s8_t2",
-                           "s14_t2", "s2_t3", "s4_t3", "s7_t3", "s8_t3", "s2_t4", "s4_t4", "s6_t4", "s7_t4"})
-        for (const char* kind : {"hh_q4k_mmq_", "hh_q4k_mmq_gu_"}) k.push_back(std::string(kind) + st);
+    k.push_back("hh_mmi_prep");
+    for (int t = 1; t <= 4; t++)
+        for (const char* f : {"_d2_w", "_d4_w", "_d2_r", "_d4_r"}) k.push_back("hh_q4k_mmi_t" + std::to_string(t) + f);
+    for (const char* f : {"t1_d2_w", "t1_d2_r", "t2_d2_w", "t2_d2_r", "t4_d2_w", "t4_d2_r"})
+        k.push_back(std::string("hh_q4k_mmi_gu_") + f);
     k.push_back("hh_lut_gemv");
     for (const char* f : {"gu_ring_g1", "gu_ring_g2", "gu_ring_g1_n", "gu_ring_g2_n", "dn_ring_d1", "dn_ring_d2", "dn_ring_d4", "dn_ring_d8"})
         k.push_back(std::string("hh_q4k_") + f);
@@ -1579,12 +1575,12 @@ hh_status engine_create(int device, hh_engine** out) {
     if (const char* f = getenv("HAYAI_HIP_SMALL_STACK")) e->small_stack = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_STACK_GRID")) e->stack_grid = atoi(f);
     if (const char* f = getenv("HAYAI_HIP_MMQ")) e->mmq = atoi(f) != 0;
-    if (const char* f = getenv("HAYAI_HIP_MMQ_S")) e->mmq_s = atoi(f);
-    if (const char* f = getenv("HAYAI_HIP_MMQ_NW")) e->mmq_nw = std::min(8, std::max(0, atoi(f)));
     if (const char* f = getenv("HAYAI_HIP_DMA_SPLIT")) e->dma_split = atoi(f) != 0;
     if (const char* f = getenv("HAYAI_HIP_RING_GU_PER_CU")) e->ring_gu_per_cu = std::max(1, atoi(f));
     if (const char* f = getenv("HAYAI_HIP_RING_DN_PER_CU")) e->ring_dn_per_cu = std::max(1, atoi(f));
     if (const char* f = getenv("HAYAI_HIP_MMR")) e->mmr = atoi(f) != 0;
+    if (const char* f = getenv("HAYAI_HIP_MMI_MIN")) e->mmi_min = (size_t)std::max(2, atoi(f));
+    if (const char* f = getenv("HAYAI_HIP_MMI_D")) e->mmi_d = atoi(f);
     err = hipMalloc(&e->grid_sync, kBarBytes);
     if (err == hipSuccess) err = hipMemset(e->grid_sync, 0, kBarBytes);
     if (err != hipSuccess) return bail(hip_fail(err, "hipMalloc(grid_sync)"));

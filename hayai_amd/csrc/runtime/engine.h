@@ -157,9 +157,9 @@ struct hh_engine {
     int ring_gu_per_cu = 1;     // HAYAI_HIP_RING_GU_PER_CU: ring gate/up workgroups per CU
     int ring_dn_per_cu = 1;     // HAYAI_HIP_RING_DN_PER_CU: ring down workgroups per CU
     bool mmr = true;            // HAYAI_HIP_MMR=0: batched Q4_K (<= 16 tokens) one token at a time
-    bool mmq = true;            // HAYAI_HIP_MMQ=0: batched Q4_K (>= 17 tokens) one token at a time, not int8
-    int mmq_s = 0;              // HAYAI_HIP_MMQ_S: superblocks per chunk of an int8 batched launch (0: chosen)
-    int mmq_nw = 0;             // HAYAI_HIP_MMQ_NW: units (waves) per workgroup (0: 8)
+    bool mmq = true;            // HAYAI_HIP_MMQ=0: batched Q4_K (>= 17 tokens) one token at a time, no int8
+    size_t mmi_min = 17;        // HAYAI_HIP_MMI_MIN: fewest tokens per pass on the int8 kernels (>= 2)
+    int mmi_d = 0;              // HAYAI_HIP_MMI_D: ring depth of the int8 f16-MFMA kernels (0: chosen)
     int blocks_per_cu_override = 0;  // HAYAI_HIP_BLOCKS_PER_CU
     bool q4k_generic = false;        // HAYAI_HIP_Q4K_GENERIC=1: skip the int8-digit Q4_K kernels
 
@@ -251,13 +251,15 @@ struct hh_engine {
     // token stages, y).  HH_ERR_UNSUPPORTED_DEVICE when shape or alignment does not fit.
     enum { MMR_GEMM = 0, MMR_GU = 1, MMR_DN = 2 };
     bool mmr_ok(size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const;
-    // int8 MFMA batched Q4_K (q4k_mmq.hip) for 17..64 tokens: tokens [b][n] f32 -> int8
-    // stages (per 32-element block: s = amax / 127, q = round_half_away(x / s)) in `xs`,
-    // then Y[b][m] = W . X (ffn == false) or H[b][m] = act(W_gate . X) * (W_up . X).
+    // batched Q4_K with int8 activations (q4k_mmi.hip) applies: 17..64 tokens (HAYAI_HIP_MMI_MIN
+    // lowers the bound), shapes of whole superblocks, 16-byte aligned pointers
     bool mmq_ok(size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const;
-    hh_status enqueue_mmq_prep(const float* x, size_t b, size_t n, size_t tp, void* xs);
-    hh_status enqueue_q4k_mmq(bool ffn, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* xs,
-                              size_t b, float* y, int act);
+    // int8 activations on the f16 matrix cores (q4k_mmi.hip): tokens [b][n] f32 -> stages
+    // (9216 bytes per superblock and 16-token tile), then GEMM (y) or FFN gate/up (h stages)
+    hh_status enqueue_mmi_prep(const float* x, size_t b, size_t n, size_t tt, void* xs);
+    // tiles: 16-token tiles of the stages (0: from b)
+    hh_status enqueue_q4k_mmi(bool ffn, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* xs,
+                              size_t b, float* y, void* hs, int act, size_t tiles = 0);
     hh_status enqueue_q4k_mmr(int kind, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1, const void* x,
                               size_t b, float* y, int act);
     // MoE routing of T tokens (device pointers) and the grouped expert FFN.

@@ -177,11 +177,13 @@ void hh_pending_destroy(hh_pending* p);
  *     within ~1e-6 of the f32 product;
  *   - passes of 17..64 tokens: each token's activations are first quantized to int8 per
  *     32-element block (s = max|x| / 127, q = round-half-away(x / s), clamped to +-127)
- *     and multiplied exactly on the int8 matrix cores; the
+ *     and multiplied exactly (integer products with the weights' sc * q on the matrix
+ *     cores); the
  *     result differs from the f32 product by that quantization: measured 0.7-1.9% of
  *     max|y| per token on N(0,1) activations (the tests bound it at 4%).
  * Set HAYAI_HIP_MMQ=0 in the environment before creating the engine to keep f32
- * activations for every batch size (17..64 tokens then run one token at a time). */
+ * activations for every batch size (17..64 tokens then run one token at a time);
+ * HAYAI_HIP_MMI_MIN=16 moves passes of 16 tokens onto the int8 form. */
 hh_status hh_gemv_batched(hh_engine* e, int ggml_type, size_t m, size_t n, const uint8_t* weights,
                           size_t weights_len, const float* inputs, float* outputs, size_t batch);
 /* Same with device buffers (weights at w_off; x: batch*n floats, y: batch*m floats);

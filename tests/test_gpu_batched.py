@@ -3,8 +3,9 @@
 ggml_gemv_batched_q4_k (crates/hayai-opencl/src/compute.rs:179-257) computes B GEMVs that
 share W; execute_quant_gemv_batched (crates/hayai-core/src/orchestrator.rs:240-269) runs
 other types token by token.  Two matrix-core paths:
-- 17..64 tokens per pass (at 16 tokens the f16 kernels are faster):
-  activations quantized to int8 per 32-element block, int8 MFMA (q4k_mmq.hip); parity against
+- 17..64 tokens per pass (at 16 tokens the f16 kernels are faster,
+  HAYAI_HIP_MMI_MIN=16 moves 16 onto this path): activations quantized to int8 per 32-element
+  block, their exact products with sc * q on the matrix cores (q4k_mmi.hip); parity against
   the oracle fed the same quantized activations (oracle.dequant_act_q8 / oracle.ffn_q8), the
   quantization's own error printed beside it;
 - 2..16 tokens: f16 operands with f32-level accuracy, against the oracle's f32 restatement.
@@ -147,6 +148,7 @@ def make_pack(engine, types, d_model, d_ff, cfg):
 @pytest.mark.parametrize("types,d_model,d_ff,batch,act", [
     ((12, 12, 12), 4096, 14336, 4, 0), ((12, 12, 12), 4096, 14336, 16, 0), ((12, 12, 12), 4096, 14336, 64, 0),
     ((12, 12, 12), 2048, 768, 32, 0), ((12, 12, 12), 1024, 2048, 9, 1), ((2, 2, 2), 576, 1536, 3, 0),
+    ((12, 12, 12), 8192, 1024, 40, 1),  # three token tiles (run as four), d_model past the LDS stage ring
 ])
 def test_ffn_batched_matches_oracle(engine, types, d_model, d_ff, batch, act):
     print(f"[case] ffn batched types={types} {d_model}x{d_ff} batch={batch} act={act}", flush=True)
@@ -182,5 +184,32 @@ def test_int8_path_off_keeps_f32_activations(monkeypatch, batch):
         X = synth.normal(72 + batch, batch * n).reshape(batch, n)
         Y = eng.ggml_gemv_batched_q4_k(m, n, w, X, batch).reshape(batch, m)
         assert per_token_err(Y, oracle.gemv_batched(Q4_K, m, n, w, X)) <= REL_TOL
+    finally:
+        eng.close()
+
+
+@pytest.mark.parametrize("m,n", [(14336, 4096), (4096, 14336), (300, 768)])
+def test_int8_path_at_16_tokens(monkeypatch, m, n):
+    # HAYAI_HIP_MMI_MIN=16: one 16-token tile on the int8-activation kernels (whole stages in
+    # LDS for the 8B shapes, ragged rows for 300), held to the quantized-activation oracle
+    print(f"[case] int8 batched at 16 tokens m={m} n={n}", flush=True)
+    monkeypatch.setenv("HAYAI_HIP_MMI_MIN", "16")
+    eng = hayai_amd.HipEngine(0)
+    try:
+        w = synth.matrix(Q4_K, m, n, 81)
+        X = synth.normal(82, 16 * n).reshape(16, n)
+        Y = eng.ggml_gemv_batched_q4_k(m, n, w, X, 16).reshape(16, m)
+        Xq = np.stack([oracle.dequant_act_q8(X[b]) for b in range(16)])
+        err = per_token_err(Y, oracle.gemv_batched(Q4_K, m, n, w, Xq))
+        print(f"  per-token max rel err {err:.3e}", flush=True)
+        assert err <= REL_TOL
+        # the FFN at 16 tokens: gate/up with whole rows of x in LDS, h quantized in-kernel
+        if m == 14336:
+            lay, (wg, wu, wd), pack = make_pack(eng, (Q4_K,) * 3, n, m, 77)
+            desc = eng.ffn_desc((Q4_K,) * 3, n, m, lay, 0)
+            Xf = synth.normal(83, 16 * n).reshape(16, n)
+            Yf = eng.ffn_batched(desc, pack, 0, Xf)
+            R = np.stack([oracle.ffn_q8((Q4_K,) * 3, n, m, wg, wu, wd, Xf[b]) for b in range(16)])
+            assert per_token_err(Yf, R) <= REL_TOL
     finally:
         eng.close()
