@@ -526,7 +526,7 @@ HH_DEV void hh_dn_ring_body(const hh_dnr_args& a) {
 #define HH_Q4K_DN_RING_D 2
 #endif
 #ifndef HH_Q4K_GU_RING_P
-#define HH_Q4K_GU_RING_P 1  // gate/up ring items issued before x is quantized
+#define HH_Q4K_GU_RING_P 2  // gate/up ring items issued before x is quantized (1: 689 us per 8B step, 2: 687)
 #endif
 
 // The ring kernels (Q4_K here, Q6_K and IQ in their files) take hh_gur_args' / hh_dnr_args'
