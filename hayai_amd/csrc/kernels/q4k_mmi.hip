@@ -34,22 +34,23 @@
 //                  of token l % 16 at superblock elements 32 j + 8 (l / 16) + e, e = 0..7
 //   [8192, 8704)   s_tj f32 at (8 t + j) * 4
 //   [8704, 9216)   u_tj f32 at (16 j + t) * 4
-// Weights: lane (quarter c, row r) holds, for each 32-byte qs group g, bytes 8c .. 8c + 7:
-// the low nibbles are elements 8c .. 8c + 7 of sub-block 2g, the high nibbles those of
-// sub-block 2g + 1 (q4k.rs:178-203): the A fragment of either sub-block in the stage's order.
+// The A fragment of sub-blocks 2g (low nibbles) and 2g + 1 (high nibbles) in the stage's order
+// is, for lane (quarter c, row r), bytes 8c .. 8c + 7 of the row's 32-byte qs group g
+// (q4k.rs:178-203).
 //
-// Work split: a workgroup is 4 compute waves owning 4 consecutive 16-row units (64 rows)
-// over a chunk of superblocks, plus one copy wave.  Each compute wave streams its unit's
-// superblocks through a register ring of D items (per tile: the 16-byte block header and four
-// 8-byte qs pieces at fixed lane offsets, so wait counts are static).  The copy wave brings the
-// chunk's token stages into an LDS ring of R superblock slots by global->LDS DMA; when the
-// chunk is longer than R, every superblock ends at a workgroup barrier after which the copy
-// wave refills the slot just consumed (only the copy wave issues DMA, so the compute waves'
-// wait counts never include it).  Gate/up takes whole rows (one chunk): its 4 units are 64
-// rows, two 32-row blocks of h, so the workgroup quantizes its h itself (the pair of units of
-// a block exchange their maxima and sums through LDS).  Chunks of one row group (GEMM and
-// down) meet in a workspace; the last workgroup to arrive adds them in chunk order
-// (deterministic).
+// Work split: a workgroup is 8 compute waves, two per 16-row unit (4 consecutive units, 64
+// rows), over a chunk of superblocks, plus a wave that copies the token stages; the wave of half h takes sub-blocks 4h .. 4h + 3 of every
+// superblock (the split below).  Each wave streams its unit's superblocks through a register
+// ring of D items (per item and matrix the 16-byte block header and 16 bytes of qs at fixed
+// lane offsets, so wait counts are static).  The chunk's token stages sit in an LDS ring of R
+// superblock slots, copied there by global->LDS DMA; when the chunk is longer than R they
+// stream through in rounds of R / 2 superblocks, one barrier per round (below).  Gate/up takes whole rows (one
+// chunk): its 4 units are 64 rows, two 32-row blocks of h, so the workgroup quantizes its h
+// itself (the pair of units of a block exchange their maxima and sums through LDS).  Chunks of
+// one row group (GEMM and down) meet in a workspace; the last workgroup to arrive adds them in
+// chunk order (deterministic).  Against one compute wave per unit (8-byte qs loads, a barrier
+// per superblock): 64 tokens 3.16 -> 2.52 ms per 32 8B layers, 17 tokens 1.98 -> 1.90; the
+// compute waves copying the stages themselves instead of the ninth wave: 2-3% slower.
 
 #define HH_MMI_STAGE 9216u
 #define HH_MMI_WAVES 4  // units (16 rows each) per workgroup
@@ -143,27 +144,49 @@ HH_DEV void hh_mmi_lds_barrier() {
 // s_waitcnt immediate for vmcnt <= n (expcnt and lgkmcnt not waited for)
 constexpr int hh_mmi_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// Two waves per 16-row unit (two per SIMD), wave half h taking sub-blocks 4h .. 4h + 3 of every
+// superblock: per item and matrix one 16-byte header load and one 16-byte qs load per lane (the
+// lane's row r16 = l % 16, bytes 64h + 16c .. + 15 of its qs, c = l / 16: 16-byte loads stream
+// such 16-row tiles at ~4.6-5 TB/s where 8-byte pieces reach ~3.3-3.6), which two lane swaps
+// turn into the A fragments of the four sub-blocks (below).  The halves' sums meet in LDS at
+// the end, half 0 adding half 1's (a fixed order), and half 0 runs the epilogue.
+//
+// The swaps: lane group c holds X_c = qs bytes 64h + 16c .. + 7 and Y_c = the next 8; the
+// fragment of sub-blocks 4h, 4h + 1 (qs group 2h) wants bytes 64h + 8c .. + 7 in group c,
+// i.e. (X_0, Y_0, X_1, Y_1) over the four groups, and that of sub-blocks 4h + 2, 4h + 3 (qs
+// group 2h + 1) wants (X_2, Y_2, X_3, Y_3).  v_permlane16_swap(X, Y) exchanges X's odd
+// 16-lane rows with Y's even rows: X = (X_0, Y_0, X_2, Y_2), Y = (X_1, Y_1, X_3, Y_3); then
+// v_permlane32_swap(X, Y) exchanges X's upper half with Y's lower half: X = (X_0, Y_0, X_1,
+// Y_1), Y = (X_2, Y_2, X_3, Y_3).  Two swaps per dword pair, four per 16 bytes.
 template <int NT, int TT, int D, bool REFILL>
 HH_DEV void hh_mmi_body(const hh_mmi_args& a) {
-    constexpr uint32_t NCW = HH_MMI_WAVES;  // compute waves; wave NCW copies
+    constexpr uint32_t NU = HH_MMI_WAVES;  // units per workgroup
+    constexpr uint32_t NCW = 2 * NU;       // compute waves, two per unit; wave NCW copies the stages
     extern __shared__ __attribute__((aligned(16))) char hh_smem[];  // the stage ring
-    __shared__ float xch[2][HH_MMI_WAVES][TT * 16];                  // gate/up: h block exchange
+    __shared__ float xch[2][NU][TT * 16];                            // gate/up: h block exchange
     __shared__ int last_flag;
-    constexpr uint32_t SBT = HH_MMI_STAGE * TT;  // one superblock's stages: a ring slot
+    constexpr uint32_t SBT = HH_MMI_STAGE * TT;
     constexpr uint32_t R = HH_MMI_LDS / SBT < 16 ? HH_MMI_LDS / SBT : 16;
-    constexpr uint32_t CHUNKS = SBT / 1024u;     // 1 KB DMA instructions per slot
+    constexpr uint32_t CHUNKS = SBT / 1024u;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid % HH_WAVE;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / HH_WAVE);
     const uint32_t nsb = a.n / 256;
     const uint32_t grp = blockIdx.x / a.kc, kci = blockIdx.x % a.kc;
     const uint32_t sb0 = kci * a.sbc;
-    const uint32_t ns = min(a.sbc, nsb - sb0);  // superblocks of this chunk (>= 1)
-    const uint32_t nsp = (ns + D - 1) / D * D;  // padded to whole ring rounds: items past ns add nothing
+    const uint32_t ns = min(a.sbc, nsb - sb0);
+    // Stages stream through the ring in rounds of P items (half the ring): at the end of round r
+    // the waves meet, after which the copy wave puts items rP + R .. rP + P - 1 + R into the
+    // slots the round used; those land while round r + 1 runs on the other half.  Compute waves
+    // cover DP items per loop body (a multiple of D and P), so the barriers sit at fixed places.
+    constexpr uint32_t P = REFILL ? (R / 2 < 1 ? 1 : R / 2) : D;
+    constexpr uint32_t DP = (D % P == 0) ? D : (P % D == 0 ? P : D * P);
+    const uint32_t nsp = (ns + DP - 1) / DP * DP;
     char* const slots = hh_smem;
 
     if (wave == NCW) {
-        // copy wave: superblock k of the chunk (clamped to the last) -> its slot
+        // superblock k (clamped to the chunk's last) -> a slot; only this wave issues DMA, so
+        // the compute waves' wait counts never include it
         auto copy = [&](uint32_t k, uint32_t slot) {
             const uint8_t* src = a.xs + (size_t)(sb0 + min(k, ns - 1u)) * SBT + lane * 16u;
             char* dst = slots + (size_t)slot * SBT;
@@ -173,35 +196,33 @@ HH_DEV void hh_mmi_body(const hh_mmi_args& a) {
                                                  (__attribute__((address_space(3))) void*)(dst + i * 1024u), 16, 0, 0);
         };
         if constexpr (REFILL) {
-            // Slots 0 .. R-1 first; then after each item k every compute wave is done with
-            // slot k % R, which takes superblock k + R (past the chunk: a copy of its last
-            // superblock into a slot nobody reads again, so every step issues the same
-            // copies).  Before that barrier the slot of item k + 1 has landed: every copy but
-            // the last R - 2 slots' is complete.
-            for (uint32_t k = 0; k < R; k++) copy(k, k);
-            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-            hh_mmi_lds_barrier();                // the first slots are in LDS
-            for (uint32_t k = 0; k < nsp; k++) {
-                constexpr int later = (int)((R - 2) * CHUNKS) < 63 ? (int)((R - 2) * CHUNKS) : 63;
-                __builtin_amdgcn_s_waitcnt(hh_mmi_vmcnt(later));
+            // the first round's slots, then the rest of the ring (landing during the first
+            // round); before each round's barrier every copy issued so far has landed (they
+            // are for the round after the next, or the next)
+            for (uint32_t k = 0; k < P; k++) copy(k, k);
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            hh_mmi_lds_barrier();
+            for (uint32_t k = P; k < R; k++) copy(k, k);
+            for (uint32_t k0 = 0; k0 < nsp; k0 += P) {
+                __builtin_amdgcn_s_waitcnt(0x0F70);
                 hh_mmi_lds_barrier();
-                copy(k + R, k % R);
+                for (uint32_t k = k0; k < k0 + P; k++) copy(k + R, k % R);
             }
         } else {
-            // the whole chunk fits the ring
             for (uint32_t k = 0; k < ns; k++) copy(k, k);
             __builtin_amdgcn_s_waitcnt(0x0F70);
             hh_mmi_lds_barrier();
         }
-        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // every copy has landed before the ring is reused
     }
 
-    // compute waves: unit us of the group
     const uint32_t c = lane >> 4, r16 = lane & 15u;
     const uint32_t nu = (a.m + 15) / 16;
-    const uint32_t us = min(wave, NCW - 1u);
-    const uint32_t u0 = grp * HH_MMI_WAVES + us;
-    const bool live = wave < NCW && u0 < nu;  // waves past the last unit repeat it, store nothing
+    const uint32_t us = wave % NU;           // the copy wave: unit 0, half 0, owns nothing
+    const uint32_t half = (wave / NU) & 1u;
+    const bool own = wave < NU;  // half 0: owns the unit's outputs
+    const uint32_t u0 = grp * NU + us;
+    const bool live = own && u0 < nu;
     const uint32_t unit = min(u0, nu - 1);
     const uint32_t row = min(unit * 16 + r16, a.m - 1);
     const size_t lofs = (size_t)row * a.row_bytes + (size_t)sb0 * 144;
@@ -209,7 +230,7 @@ HH_DEV void hh_mmi_body(const hh_mmi_args& a) {
     const uint8_t* const p1 = (NT == 2 ? a.w1 : a.w0) + lofs;
     struct Item {
         uint4 h;
-        uint2 q[4];
+        uint4 q;
     };
     hh_f4 acc[NT][TT];
 #pragma unroll
@@ -219,84 +240,87 @@ HH_DEV void hh_mmi_body(const hh_mmi_args& a) {
 
     if (wave < NCW) {
         Item ring[D][NT];
-        auto issue = [&](uint32_t k, Item* it) {  // items past the chunk re-read its last superblock
+        const uint32_t qofs = 16u + 64u * half + 16u * c;
+        auto issue = [&](uint32_t k, Item* it) {
             const uint32_t off = min(k, ns - 1u) * 144u;
 #pragma unroll
             for (int q = 0; q < NT; q++) {
                 const uint8_t* p = (q ? p1 : p0) + off;
                 it[q].h = hh_ld16(p);
-#pragma unroll
-                for (int g = 0; g < 4; g++) it[q].q[g] = *reinterpret_cast<const uint2*>(p + 16u + 32u * g + 8u * c);
+                it[q].q = hh_ld16(p + qofs);
             }
         };
 #pragma unroll
         for (int s = 0; s < D; s++) issue((uint32_t)s, ring[s]);
-        hh_mmi_lds_barrier();  // the first slots are in LDS
+        hh_mmi_lds_barrier();  // the first round's stages are in LDS
 
 #pragma unroll 1
-        for (uint32_t k0 = 0; k0 < nsp; k0 += D) {
+        for (uint32_t k0 = 0; k0 < nsp; k0 += DP) {
 #pragma unroll
-            for (int s = 0; s < D; s++) {
+            for (int s = 0; s < (int)DP; s++) {
                 const uint32_t k = k0 + (uint32_t)s;
                 const bool valid = k < ns;
-                const char* st = slots + (size_t)(min(k, ns - 1u) % R) * SBT;  // padded items: any valid slot
-                // the item's A operands (sc_j q for the 8 sub-blocks), d and dmin of the lane's
-                // four output rows, -dmin m_j of sub-blocks c and c + 4; then the ring slot is
-                // refilled at once
-                hh_h8 wa[NT][8];
+                Item* const cur = ring[s % D];
+                const char* st = slots + (size_t)(min(k, ns - 1u) % R) * SBT;
+                hh_h8 wa[NT][4];
                 float d4[NT][4];
-                hh_mmi_head hd[NT];
+                float nm[NT];
 #pragma unroll
                 for (int q = 0; q < NT; q++) {
-                    uint4 h = ring[s][q].h;
-                    if (!valid) h.x = 0u;  // d = dmin = 0
-                    const uint32_t sc03 = h.y & 0x3F3F3F3Fu;
-                    const uint32_t sc47 = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+                    uint4 h = cur[q].h;
+                    if (!valid) h.x = 0u;
+                    const uint4 w = cur[q].q;
+                    const auto s0 = __builtin_amdgcn_permlane16_swap(w.x, w.z, false, false);
+                    const auto s1 = __builtin_amdgcn_permlane16_swap(w.y, w.w, false, false);
+                    const auto t0 = __builtin_amdgcn_permlane32_swap(s0[0], s0[1], false, false);
+                    const auto t1 = __builtin_amdgcn_permlane32_swap(s1[0], s1[1], false, false);
+                    const uint2 g[2] = {make_uint2(t0[0], t1[0]), make_uint2(t0[1], t1[1])};
+                    const uint32_t sch = half ? (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u) : h.y & 0x3F3F3F3Fu;
 #pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const uint32_t b = (uint32_t)(j & 3);
+                    for (int jj = 0; jj < 4; jj++) {
+                        const uint32_t b = (uint32_t)jj;
                         const uint32_t sel = b | (4u << 8) | (b << 16) | (4u << 24);
-                        const hh_h2 s1024 = hh_h2_bits(__builtin_amdgcn_perm(0x64646464u, j < 4 ? sc03 : sc47, sel));
+                        const hh_h2 s1024 = hh_h2_bits(__builtin_amdgcn_perm(0x64646464u, sch, sel));
                         const hh_h2 sc2 = s1024 - hh_h2{(_Float16)1024.0f, (_Float16)1024.0f};
                         const hh_h2 nb2 = sc2 * hh_h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
-                        const uint2 p = ring[s][q].q[j >> 1];
-                        const uint32_t lo = (j & 1) ? (p.x >> 4) & 0x0F0F0F0Fu : p.x & 0x0F0F0F0Fu;
-                        const uint32_t hi = (j & 1) ? (p.y >> 4) & 0x0F0F0F0Fu : p.y & 0x0F0F0F0Fu;
+                        const uint2 pq = g[jj >> 1];
+                        const uint32_t lo = (jj & 1) ? (pq.x >> 4) & 0x0F0F0F0Fu : pq.x & 0x0F0F0F0Fu;
+                        const uint32_t hi = (jj & 1) ? (pq.y >> 4) & 0x0F0F0F0Fu : pq.y & 0x0F0F0F0Fu;
                         hh_h2 r[4];
                         hh_mm_scq(lo, sc2, nb2, r);
                         hh_mm_scq(hi, sc2, nb2, r + 2);
-                        wa[q][j] = hh_h8{r[0].x, r[0].y, r[1].x, r[1].y, r[2].x, r[2].y, r[3].x, r[3].y};
+                        wa[q][jj] = hh_h8{r[0].x, r[0].y, r[1].x, r[1].y, r[2].x, r[2].y, r[3].x, r[3].y};
                     }
                     const float d = hh_f16(h.x & 0xFFFFu);
 #pragma unroll
                     for (int i = 0; i < 4; i++)
                         d4[q][i] = __builtin_bit_cast(
                             float, __builtin_amdgcn_ds_bpermute((int)((c * 4u + (uint32_t)i) * 4u), __builtin_bit_cast(int, d)));
-                    hh_mmi_mins(h, c, hd[q]);
+                    hh_mmi_head hd;
+                    hh_mmi_mins(h, c, hd);
+                    nm[q] = half ? hd.nm1 : hd.nm0;  // -dmin m_j of sub-block 4 half + c
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                issue(k + D, ring[s]);
+                issue(k + D, cur);
 #pragma unroll
                 for (int tt = 0; tt < TT; tt++) {
                     const char* sg = st + tt * HH_MMI_STAGE;
-                    const float4 sa = *reinterpret_cast<const float4*>(sg + 8192u + r16 * 32u);
-                    const float4 sb = *reinterpret_cast<const float4*>(sg + 8192u + r16 * 32u + 16u);
-                    const float sj[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
-                    const float u0v = *reinterpret_cast<const float*>(sg + 8704u + (c * 16u + r16) * 4u);
-                    const float u1v = *reinterpret_cast<const float*>(sg + 8704u + ((c + 4u) * 16u + r16) * 4u);
+                    const float4 sa = *reinterpret_cast<const float4*>(sg + 8192u + r16 * 32u + 16u * half);
+                    const float sj[4] = {sa.x, sa.y, sa.z, sa.w};
+                    const float uv = *reinterpret_cast<const float*>(sg + 8704u + ((4u * half + c) * 16u + r16) * 4u);
                     hh_f4 ps[NT];
 #pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const hh_h8 xb = *reinterpret_cast<const hh_h8*>(sg + ((uint32_t)j * 64u + lane) * 16u);
+                    for (int jj = 0; jj < 4; jj++) {
+                        const hh_h8 xb = *reinterpret_cast<const hh_h8*>(sg + ((4u * half + (uint32_t)jj) * 64u + lane) * 16u);
 #pragma unroll
                         for (int q = 0; q < NT; q++) {
-                            const hh_f4 pj = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[q][j], xb, hh_f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                            if (j == 0) {
+                            const hh_f4 pj = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[q][jj], xb, hh_f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                            if (jj == 0) {
 #pragma unroll
                                 for (int i = 0; i < 4; i++) ps[q][i] = pj[i] * sj[0];
                             } else {
 #pragma unroll
-                                for (int i = 0; i < 4; i++) ps[q][i] = fmaf(pj[i], sj[j], ps[q][i]);
+                                for (int i = 0; i < 4; i++) ps[q][i] = fmaf(pj[i], sj[jj], ps[q][i]);
                             }
                         }
                     }
@@ -304,21 +328,40 @@ HH_DEV void hh_mmi_body(const hh_mmi_args& a) {
                     for (int q = 0; q < NT; q++) {
 #pragma unroll
                         for (int i = 0; i < 4; i++) acc[q][tt][i] = fmaf(d4[q][i], ps[q][i], acc[q][tt][i]);
-                        acc[q][tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(hd[q].nm0, u0v, acc[q][tt], 0, 0, 0);
-                        acc[q][tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(hd[q].nm1, u1v, acc[q][tt], 0, 0, 0);
+                        acc[q][tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(nm[q], uv, acc[q][tt], 0, 0, 0);
                     }
                 }
-                if constexpr (REFILL) hh_mmi_lds_barrier();  // done with this item's slot
+                if constexpr (REFILL) {
+                    if (((uint32_t)s + 1) % P == 0) hh_mmi_lds_barrier();  // the round's slots are free
+                }
             }
         }
     }
 
-    // C lane (quarter c, token r16): acc[q][tt][i] is row R0 + 4c + i of token 16 tt + r16
+    // the halves meet: the ring is free once every wave (the copy wave after its last copy
+    // landed) has passed this barrier
+    __syncthreads();
+    float* const xs2 = reinterpret_cast<float*>(slots) + (size_t)us * (NT * TT * 4u * HH_WAVE) + lane;
+    if (wave < NCW && half == 1u) {
+#pragma unroll
+        for (int q = 0; q < NT; q++)
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) xs2[((q * TT + tt) * 4 + i) * HH_WAVE] = acc[q][tt][i];
+    }
+    __syncthreads();
+    if (own) {
+#pragma unroll
+        for (int q = 0; q < NT; q++)
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[q][tt][i] += xs2[((q * TT + tt) * 4 + i) * HH_WAVE];
+    }
+
     const uint32_t R0 = unit * 16;
     if constexpr (NT == 2) {
-        // h of the unit's rows; per token the max |h| and the sum of the quantized values over
-        // each 32-row block, the pair of units of a block meeting through LDS (every wave,
-        // the copy wave included, passes both barriers)
         float hv[TT][4];
         int qi[TT][4];
         float am[TT];
@@ -333,16 +376,15 @@ HH_DEV void hh_mmi_body(const hh_mmi_args& a) {
             am[tt] = fmaxf(am[tt], __shfl_xor(am[tt], 16, HH_WAVE));
             am[tt] = fmaxf(am[tt], __shfl_xor(am[tt], 32, HH_WAVE));
         }
-        const uint32_t wv = us;
-        if (wave < NCW && c == 0)
+        if (own && c == 0)
 #pragma unroll
-            for (int tt = 0; tt < TT; tt++) xch[0][wv][tt * 16 + r16] = am[tt];
+            for (int tt = 0; tt < TT; tt++) xch[0][us][tt * 16 + r16] = am[tt];
         __syncthreads();
         float sc[TT];
         int xsum[TT];
 #pragma unroll
         for (int tt = 0; tt < TT; tt++) {
-            sc[tt] = fmaxf(am[tt], xch[0][wv ^ 1u][tt * 16 + r16]) / 127.0f;
+            sc[tt] = fmaxf(am[tt], xch[0][us ^ 1u][tt * 16 + r16]) / 127.0f;
             xsum[tt] = 0;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -354,15 +396,12 @@ HH_DEV void hh_mmi_body(const hh_mmi_args& a) {
             xsum[tt] += __shfl_xor(xsum[tt], 16, HH_WAVE);
             xsum[tt] += __shfl_xor(xsum[tt], 32, HH_WAVE);
         }
-        if (wave < NCW && c == 0)
+        if (own && c == 0)
 #pragma unroll
-            for (int tt = 0; tt < TT; tt++) xch[1][wv][tt * 16 + r16] = (float)xsum[tt];
+            for (int tt = 0; tt < TT; tt++) xch[1][us][tt * 16 + r16] = (float)xsum[tt];
         __syncthreads();
         if (!live) return;
-        // stage (sbd, tt) of the down projection: this unit is half `half` of sub-block jd;
-        // lanes of even quarters gather the next quarter's four rows and store 8 consecutive
-        // rows of one token (one 16-byte fragment piece)
-        const uint32_t sbd = R0 / 256, jd = (R0 % 256) / 32, half = (R0 / 16) & 1u;
+        const uint32_t sbd = R0 / 256, jd = (R0 % 256) / 32, hf = (R0 / 16) & 1u;
 #pragma unroll
         for (int tt = 0; tt < TT; tt++) {
             uint8_t* st = a.hs + ((size_t)sbd * TT + tt) * HH_MMI_STAGE;
@@ -371,27 +410,24 @@ HH_DEV void hh_mmi_body(const hh_mmi_args& a) {
             const uint32_t w1 = f16b(qi[tt][2]) | (f16b(qi[tt][3]) << 16);
             const uint32_t x0 = __shfl_xor(w0, 16, HH_WAVE), x1 = __shfl_xor(w1, 16, HH_WAVE);
             if ((c & 1u) == 0)
-                *reinterpret_cast<uint4*>(st + (size_t)(jd * 64u + (2u * half + c / 2u) * 16u + r16) * 16u) =
+                *reinterpret_cast<uint4*>(st + (size_t)(jd * 64u + (2u * hf + c / 2u) * 16u + r16) * 16u) =
                     make_uint4(w0, w1, x0, x1);
-            if (half == 0 && c == 0) {
-                const float xs = (float)(xsum[tt] + (int)xch[1][wv ^ 1u][tt * 16 + r16]);
+            if (hf == 0 && c == 0) {
+                const float xsv = (float)(xsum[tt] + (int)xch[1][us ^ 1u][tt * 16 + r16]);
                 *reinterpret_cast<float*>(st + 8192u + (r16 * 8u + jd) * 4u) = sc[tt];
-                *reinterpret_cast<float*>(st + 8704u + (jd * 16u + r16) * 4u) = sc[tt] * xs;
+                *reinterpret_cast<float*>(st + 8704u + (jd * 16u + r16) * 4u) = sc[tt] * xsv;
             }
         }
     } else {
-        // partials [wave][tile][i][lane]: every store and load instruction covers 256
-        // contiguous bytes
         if (a.kc > 1) {
             constexpr uint32_t PT = TT * 4u * HH_WAVE;
-            const uint32_t wv = us;
-            float* my = a.part + (((size_t)grp * a.kc + kci) * HH_MMI_WAVES + wv) * PT + lane;
-            if (wave < NCW)
+            float* my = a.part + (((size_t)grp * a.kc + kci) * NU + us) * PT + lane;
+            if (own)
 #pragma unroll
                 for (int tt = 0; tt < TT; tt++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) hh_store_coherent_f(my + (tt * 4 + i) * HH_WAVE, acc[0][tt][i]);
-            __builtin_amdgcn_s_waitcnt(0);  // partial stores complete before the arrival
+            __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
             if (tid == 0) {
                 const unsigned old = __hip_atomic_fetch_add(a.cnt + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -400,12 +436,11 @@ HH_DEV void hh_mmi_body(const hh_mmi_args& a) {
                 last_flag = last;
             }
             __syncthreads();
-            if (!last_flag || wave >= NCW) return;
-            // the last to arrive adds all chunks' partials in chunk order
+            if (!last_flag || !own) return;
 #pragma unroll
             for (int tt = 0; tt < TT; tt++) acc[0][tt] = hh_f4{0.f, 0.f, 0.f, 0.f};
             for (uint32_t k = 0; k < a.kc; k++) {
-                const float* p = a.part + (((size_t)grp * a.kc + k) * HH_MMI_WAVES + wv) * PT + lane;
+                const float* p = a.part + (((size_t)grp * a.kc + k) * NU + us) * PT + lane;
 #pragma unroll
                 for (int tt = 0; tt < TT; tt++)
 #pragma unroll
@@ -419,22 +454,21 @@ HH_DEV void hh_mmi_body(const hh_mmi_args& a) {
             if (tok >= a.b) continue;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const uint32_t R = R0 + 4u * c + (uint32_t)i;
-                if (R < a.m) a.y[(size_t)tok * a.m + R] = acc[0][tt][i];
+                const uint32_t Rr = R0 + 4u * c + (uint32_t)i;
+                if (Rr < a.m) a.y[(size_t)tok * a.m + Rr] = acc[0][tt][i];
             }
         }
     }
 }
 
-#define HH_MMI_BLOCK ((HH_MMI_WAVES + 1) * HH_WAVE)
+// GEMM / down: tiles 1..4, ring depth 2 or 4, stages whole (_w) or streamed in rounds (_r).
+// Gate/up (two matrices per item) keeps ring depth 2 (depth 4 measured slower at 64 tokens:
+// 2.73 vs 2.55 ms per 32 layers); three token tiles run as four.
+#define HH_MMI_BLOCK ((2 * HH_MMI_WAVES + 1) * HH_WAVE)
 #define HH_MMI_K(NAME, NT, TT, D, RF)                                                          \
     extern "C" __global__ void __launch_bounds__(HH_MMI_BLOCK) NAME(const hh_mmi_args a) { \
         hh_mmi_body<NT, TT, D, RF>(a);                                                      \
     }
-// GEMM / down: tiles 1..4, ring depth 2 or 4, stages whole (_w) or refilled (_r).  Gate/up
-// (two tiles per item) keeps ring depth 2: at depth 4 the compiler no longer keeps the ring
-// in place and waits for every load at the head of each round; three token tiles run as four
-// (their register allocation spills).
 #define HH_MMI_GEMM(TT)                                  \
     HH_MMI_K(hh_q4k_mmi_t##TT##_d2_w, 1, TT, 2, false) \
     HH_MMI_K(hh_q4k_mmi_t##TT##_d4_w, 1, TT, 4, false) \

@@ -1020,7 +1020,7 @@ hh_status hh_engine::enqueue_q4k_mmr(int kind, size_t m, size_t n, const uint8_t
 
 // Batched Q4_K with int8 activations (q4k_mmi.hip) from 17 tokens on: at 16 the f16
 // weight-stream kernels (q4k_mmr.hip) are faster on the MI355X (8B FFN, 32 layers: 1.32 ms
-// f16 vs 1.54-1.58 ms int8).
+// f16 vs 1.50 ms int8).
 constexpr size_t kMmqMinTokens = 17, kMmqMaxTokens = 64;
 
 bool hh_engine::mmq_ok(size_t m, size_t n, size_t b, const void* w0, const void* w1, const void* x) const {
@@ -1063,9 +1063,10 @@ hh_status hh_engine::enqueue_mmi_prep(const float* x, size_t b, size_t n, size_t
     return launch(fn, (uint32_t)((teams + 7) / 8), 256, a);
 }
 
-// Workgroups of 4 units (64 rows) + a copy wave.  FFN gate/up: whole rows (one chunk), so the
-// workgroup quantizes its own rows of h; GEMM / down: the superblocks split into chunks so that
-// the grid fills the CUs once, the chunks' partial sums added by the last workgroup of a group.
+// Workgroups of 4 units (64 rows), two waves per unit, + a copy wave.  FFN gate/up: whole rows
+// (one chunk), so the workgroup quantizes its own rows of h; GEMM / down: the superblocks split
+// into chunks so that the grid fills the CUs once, the chunks' partial sums added by the last
+// workgroup of a group.
 hh_status hh_engine::enqueue_q4k_mmi(bool ffn, size_t m, size_t n, const uint8_t* w0, const uint8_t* w1,
                                      const void* xs, size_t b, float* y, void* hs, int act, size_t tiles) {
     const size_t tt = tiles ? tiles : mmi_tiles(ffn, b), nsb = n / 256, nu = (m + 15) / 16;
@@ -1108,7 +1109,7 @@ hh_status hh_engine::enqueue_q4k_mmi(bool ffn, size_t m, size_t n, const uint8_t
     a.act = act;
     const size_t smem = (refill ? ring : sbc) * slot;
     void* params[] = {&a};
-    hipError_t err = hipModuleLaunchKernel(fn, (unsigned)(groups * kc), 1, 1, (unsigned)((kMmiWaves + 1) * 64), 1, 1,
+    hipError_t err = hipModuleLaunchKernel(fn, (unsigned)(groups * kc), 1, 1, (unsigned)((2 * kMmiWaves + 1) * 64), 1, 1,
                                            (unsigned)smem, stream, params, nullptr);
     if (err != hipSuccess) return hip_fail(err, "hipModuleLaunchKernel(q4k_mmi)");
     return HH_OK;
