@@ -11,7 +11,7 @@
 //                            SiLU * up, crates/hayai-core/src/prefill_wave.rs:569-584, fused),
 //                            quantized the same way and written as the token stages of the
 //                            down projection
-// (Compiled after mm_common.hip: its vector types, the f16 weight decode hh_mm_scq and the
+// (Compiled after mm_common.hip: its vector types and the
 // coherent partial-sum helpers.)
 //
 // Arithmetic.  A Q4_K weight is d sc_j q - dmin m_j for sub-block j (32 columns) and a token
@@ -31,12 +31,13 @@
 // Token stage of one (superblock, 16-token tile), 9216 bytes; stage (sb, tt) at
 // (sb * TT + tt) * 9216:
 //   [0, 8192)      B fragments: sub-block j, lane l: 8 f16 at (64 j + l) * 16, the values xq
-//                  of token l % 16 at superblock elements 32 j + 8 (l / 16) + e, e = 0..7
+//                  of token l % 16 at superblock elements 32 j + 8 (l / 16) + e, e in the
+//                  order 0 2 1 3 4 6 5 7 (the order the weight decode produces)
 //   [8192, 8704)   s_tj f32 at (8 t + j) * 4
 //   [8704, 9216)   u_tj f32 at (16 j + t) * 4
-// The A fragment of sub-blocks 2g (low nibbles) and 2g + 1 (high nibbles) in the stage's order
-// is, for lane (quarter c, row r), bytes 8c .. 8c + 7 of the row's 32-byte qs group g
-// (q4k.rs:178-203).
+// The A fragment of sub-blocks 2g (low nibbles) and 2g + 1 (high nibbles) is, for lane
+// (quarter c, row r), bytes 8c .. 8c + 7 of the row's 32-byte qs group g (q4k.rs:178-203), in
+// the stage's element order.
 //
 // Work split: a workgroup is 8 compute waves, two per 16-row unit (4 consecutive units, 64
 // rows), over a chunk of superblocks, plus a wave that copies the token stages; the wave of half h takes sub-blocks 4h .. 4h + 3 of every
@@ -86,11 +87,12 @@ extern "C" __global__ void __launch_bounds__(256) hh_mmi_prep(const hh_mmi_prep_
     int sum = (int)q;
 #pragma unroll
     for (int m = 1; m < 32; m <<= 1) sum += __shfl_xor(sum, m, 32);
-    // f16 of q; lanes 2i hold elements 2i | 2i + 1 << 16, lanes 8c gather their quarter
+    // f16 of q; lanes e with bit 1 clear hold elements e | e + 2 << 16, lanes 8c gather their
+    // quarter as the pairs (0, 2) (1, 3) (4, 6) (5, 7): the weight fragments' element order
     const uint32_t hb = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q);
-    uint32_t w = (e & 1u) ? hb << 16 : hb;
-    w |= __shfl_xor(w, 1, 32);
-    const uint32_t w1 = __shfl_down(w, 2, 32), w2 = __shfl_down(w, 4, 32), w3 = __shfl_down(w, 6, 32);
+    uint32_t w = (e & 2u) ? hb << 16 : hb;
+    w |= __shfl_xor(w, 2, 32);
+    const uint32_t w1 = __shfl_down(w, 1, 32), w2 = __shfl_down(w, 4, 32), w3 = __shfl_down(w, 5, 32);
     if ((e & 7u) == 0)
         *reinterpret_cast<uint4*>(st + (size_t)(j * 64u + (e / 8u) * 16u + t16) * 16u) = make_uint4(w, w1, w2, w3);
     if (e == 0) {
@@ -239,6 +241,13 @@ HH_DEV void hh_mmi_body(const hh_mmi_args& a) {
         for (int tt = 0; tt < TT; tt++) acc[q][tt] = hh_f4{0.f, 0.f, 0.f, 0.f};
 
     if (wave < NCW) {
+        // the decode's constants in registers: a gfx9 VOP3 instruction takes no literal, so
+        // held this way (two masks in SGPRs, the f16 exponent bits in a VGPR: one scalar operand
+        // per instruction) each (v & mask) | magic is one v_and_or_b32
+        uint32_t mlo, mhi, magic;
+        asm volatile("s_mov_b32 %0, 0x000F000F" : "=s"(mlo));
+        asm volatile("s_mov_b32 %0, 0x00F000F0" : "=s"(mhi));
+        asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
         Item ring[D][NT];
         const uint32_t qofs = 16u + 64u * half + 16u * c;
         auto issue = [&](uint32_t k, Item* it) {
@@ -276,20 +285,31 @@ HH_DEV void hh_mmi_body(const hh_mmi_args& a) {
                     const auto t1 = __builtin_amdgcn_permlane32_swap(s1[0], s1[1], false, false);
                     const uint2 g[2] = {make_uint2(t0[0], t1[0]), make_uint2(t0[1], t1[1])};
                     const uint32_t sch = half ? (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u) : h.y & 0x3F3F3F3Fu;
+                    // sub-blocks 2pr (low nibbles) and 2pr + 1 (high nibbles) of the half from
+                    // qs dwords g[pr]: (v & 0x000F000F) | 0x64006400 is the f16 pair (1024 + n)
+                    // of bytes 0 and 2, with mask 0x00F000F0 (1024 + 16 n); the pair's scales
+                    // (sc_a, sc_b / 16) and offsets (-1024 sc_a, -64 sc_b) make one FMA per two
+                    // weights give n sc exactly.  Elements come in the order 0 2 1 3 4 6 5 7 of
+                    // the lane's eight (the stage stores B in the same order).
 #pragma unroll
-                    for (int jj = 0; jj < 4; jj++) {
-                        const uint32_t b = (uint32_t)jj;
-                        const uint32_t sel = b | (4u << 8) | (b << 16) | (4u << 24);
+                    for (int pr = 0; pr < 2; pr++) {
+                        const uint32_t sel = (2u * pr) | (4u << 8) | ((2u * pr + 1u) << 16) | (4u << 24);
                         const hh_h2 s1024 = hh_h2_bits(__builtin_amdgcn_perm(0x64646464u, sch, sel));
-                        const hh_h2 sc2 = s1024 - hh_h2{(_Float16)1024.0f, (_Float16)1024.0f};
-                        const hh_h2 nb2 = sc2 * hh_h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
-                        const uint2 pq = g[jj >> 1];
-                        const uint32_t lo = (jj & 1) ? (pq.x >> 4) & 0x0F0F0F0Fu : pq.x & 0x0F0F0F0Fu;
-                        const uint32_t hi = (jj & 1) ? (pq.y >> 4) & 0x0F0F0F0Fu : pq.y & 0x0F0F0F0Fu;
-                        hh_h2 r[4];
-                        hh_mm_scq(lo, sc2, nb2, r);
-                        hh_mm_scq(hi, sc2, nb2, r + 2);
-                        wa[q][jj] = hh_h8{r[0].x, r[0].y, r[1].x, r[1].y, r[2].x, r[2].y, r[3].x, r[3].y};
+                        const hh_h2 scab = s1024 - hh_h2{(_Float16)1024.0f, (_Float16)1024.0f};
+                        const hh_h2 mult = scab * hh_h2{(_Float16)1.0f, (_Float16)0.0625f};
+                        const hh_h2 off = mult * hh_h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+                        const hh_h2 ma = hh_h2{mult.x, mult.x}, oa = hh_h2{off.x, off.x};
+                        const hh_h2 mb = hh_h2{mult.y, mult.y}, ob = hh_h2{off.y, off.y};
+                        const uint2 pq = g[pr];
+                        const uint32_t v[4] = {pq.x, pq.x >> 8, pq.y, pq.y >> 8};
+                        hh_h2 ra[4], rb[4];
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            ra[i] = __builtin_elementwise_fma(hh_h2_bits((v[i] & mlo) | magic), ma, oa);
+                            rb[i] = __builtin_elementwise_fma(hh_h2_bits((v[i] & mhi) | magic), mb, ob);
+                        }
+                        wa[q][2 * pr] = hh_h8{ra[0].x, ra[0].y, ra[1].x, ra[1].y, ra[2].x, ra[2].y, ra[3].x, ra[3].y};
+                        wa[q][2 * pr + 1] = hh_h8{rb[0].x, rb[0].y, rb[1].x, rb[1].y, rb[2].x, rb[2].y, rb[3].x, rb[3].y};
                     }
                     const float d = hh_f16(h.x & 0xFFFFu);
 #pragma unroll
@@ -406,8 +426,8 @@ HH_DEV void hh_mmi_body(const hh_mmi_args& a) {
         for (int tt = 0; tt < TT; tt++) {
             uint8_t* st = a.hs + ((size_t)sbd * TT + tt) * HH_MMI_STAGE;
             auto f16b = [](int v) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)v); };
-            const uint32_t w0 = f16b(qi[tt][0]) | (f16b(qi[tt][1]) << 16);
-            const uint32_t w1 = f16b(qi[tt][2]) | (f16b(qi[tt][3]) << 16);
+            const uint32_t w0 = f16b(qi[tt][0]) | (f16b(qi[tt][2]) << 16);  // rows in the order 0 2 1 3
+            const uint32_t w1 = f16b(qi[tt][1]) | (f16b(qi[tt][3]) << 16);
             const uint32_t x0 = __shfl_xor(w0, 16, HH_WAVE), x1 = __shfl_xor(w1, 16, HH_WAVE);
             if ((c & 1u) == 0)
                 *reinterpret_cast<uint4*>(st + (size_t)(jd * 64u + (2u * hf + c / 2u) * 16u + r16) * 16u) =
