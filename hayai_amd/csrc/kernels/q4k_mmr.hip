@@ -53,8 +53,8 @@ struct hh_mmr_args {
 #define HH_MMR_STAGE_HI 9216u  // single-f16 stage: operands, sums hi, sums lo
 
 // Superblock header of this lane's row, decoded for its group c: the sub-block scales as
-// (sc, -1024 sc) f16 pairs (for hh_mm_scq), the mins as the B operand of the min MFMA, d
-// and dmin (q4k.rs:34-43).
+// (sc, -1024 sc) f16 pairs for the low nibbles and (sc / 16, -64 sc) for the high ones (see
+// hh_mmr_wstep), the mins as the B operand of the min MFMA, d and dmin (q4k.rs:34-43).
 struct hh_mmr_head {
     hh_h2 sl, sh, nl, nh;
     hh_h4 amin;
@@ -76,27 +76,32 @@ HH_DEV void hh_mmr_head_decode(const uint4& h, uint32_t c, hh_mmr_head& t) {
     const _Float16 mhi = (_Float16)(-hh_ub3(s));
     t.amin = hh_h4{mlo, mlo, mhi, mhi};
     t.sl = hh_h2{(_Float16)sc_lo, (_Float16)sc_lo};
-    t.sh = hh_h2{(_Float16)sc_hi, (_Float16)sc_hi};
+    t.sh = hh_h2{(_Float16)(0.0625f * sc_hi), (_Float16)(0.0625f * sc_hi)};
     t.nl = hh_h2{(_Float16)(-1024.0f * sc_lo), (_Float16)(-1024.0f * sc_lo)};
-    t.nh = hh_h2{(_Float16)(-1024.0f * sc_hi), (_Float16)(-1024.0f * sc_hi)};
+    t.nh = hh_h2{(_Float16)(-64.0f * sc_hi), (_Float16)(-64.0f * sc_hi)};
 }
 
-// Weight operand of MFMA step s (the k order of hh_mm_decode): s < 4 takes the low nibbles
-// of qs dwords 2s, 2s+1 of this lane's group, s >= 4 the high nibbles of dwords 2(s-4),
-// 2(s-4)+1; each weight becomes sc * q, exact in f16.
+// Weight operand of MFMA step s: s < 4 takes the low nibbles of qs dwords 2s, 2s+1 of this
+// lane's group, s >= 4 the high nibbles of dwords 2(s-4), 2(s-4)+1; each weight becomes sc * q,
+// exact in f16.  (v & 0x000F000F) | 0x64006400 is the f16 pair (1024 + q) of bytes 0 and 2 of
+// v, with mask 0x00F000F0 (1024 + 16 q): one v_and_or_b32 (masks and exponent bits held in
+// registers: a gfx9 VOP3 instruction takes no literal) and one packed FMA per two weights;
+// the elements come in the order 0 2 1 3 4 6 5 7 of the lane's eight (the token stages hold B
+// in that order).
+struct hh_mmr_consts {
+    uint32_t mlo, mhi, magic;
+};
 template <int S_>
-HH_DEV hh_h8 hh_mmr_wstep(const uint4& q0, const uint4& q1, const hh_mmr_head& t) {
+HH_DEV hh_h8 hh_mmr_wstep(const uint4& q0, const uint4& q1, const hh_mmr_head& t, const hh_mmr_consts& k) {
     constexpr int s4 = S_ & 3;
     const uint32_t w0 = s4 == 0 ? q0.x : s4 == 1 ? q0.z : s4 == 2 ? q1.x : q1.z;
     const uint32_t w1 = s4 == 0 ? q0.y : s4 == 1 ? q0.w : s4 == 2 ? q1.y : q1.w;
+    const uint32_t v[4] = {w0, w0 >> 8, w1, w1 >> 8};
+    const uint32_t mask = S_ < 4 ? k.mlo : k.mhi;
+    const hh_h2 m = S_ < 4 ? t.sl : t.sh, o = S_ < 4 ? t.nl : t.nh;
     hh_h2 r[4];
-    if constexpr (S_ < 4) {
-        hh_mm_scq(w0 & 0x0F0F0F0Fu, t.sl, t.nl, r);
-        hh_mm_scq(w1 & 0x0F0F0F0Fu, t.sl, t.nl, r + 2);
-    } else {
-        hh_mm_scq((w0 >> 4) & 0x0F0F0F0Fu, t.sh, t.nh, r);
-        hh_mm_scq((w1 >> 4) & 0x0F0F0F0Fu, t.sh, t.nh, r + 2);
-    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) r[i] = __builtin_elementwise_fma(hh_h2_bits((v[i] & mask) | k.magic), m, o);
     return hh_h8{r[0].x, r[0].y, r[1].x, r[1].y, r[2].x, r[2].y, r[3].x, r[3].y};
 }
 
@@ -145,6 +150,10 @@ HH_DEV void hh_mmr_body(const hh_mmr_args& a) {
         }
     };
     constexpr int D0 = D < S ? D : S;
+    hh_mmr_consts kc;
+    asm volatile("s_mov_b32 %0, 0x000F000F" : "=s"(kc.mlo));
+    asm volatile("s_mov_b32 %0, 0x00F000F0" : "=s"(kc.mhi));
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(kc.magic));
 
     // the chunk's stages -> LDS (SB / 16 = 17 * 64 or 9 * 64 chunks of 16 bytes per stage),
     // complete before the first weight request; then the ring
@@ -209,7 +218,7 @@ HH_DEV void hh_mmr_body(const hh_mmr_args& a) {
         }
 #define HH_MMR_STEP(SS)                                                                     \
     _Pragma("unroll") for (int q = 0; q < NT; q++) {                                         \
-        const hh_h8 w = hh_mmr_wstep<SS>(qa[q], qb[q], hd[q]);                               \
+        const hh_h8 w = hh_mmr_wstep<SS>(qa[q], qb[q], hd[q], kc);                           \
         ah[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[SS], w, ah[q], 0, 0, 0);           \
         if constexpr (LO) al[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[8 + ((SS) & 7)], w, al[q], 0, 0, 0); \
     }
@@ -298,7 +307,8 @@ HH_DEV void hh_mmr_body(const hh_mmr_args& a) {
         __builtin_amdgcn_wave_barrier();
         if (lane < 32) {
             const uint32_t run = lane >> 4, tok = lane & 15u;
-            const hh_h8 chunk = *reinterpret_cast<const hh_h8*>(tp + tok * 16 + 8 * run);
+            const hh_h8 c8 = *reinterpret_cast<const hh_h8*>(tp + tok * 16 + 8 * run);
+            const hh_h8 chunk = __builtin_shufflevector(c8, c8, 0, 2, 1, 3, 4, 6, 5, 7);  // the stage order
             uint8_t* st = a.hop + (size_t)(R0 / 256) * HH_MMR_STAGE_HI;
             *reinterpret_cast<hh_h8*>(st + hh_mm_elem_off(tok, (R0 & 255u) + 8 * run)) = chunk;
         }

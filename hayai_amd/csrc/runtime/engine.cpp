@@ -1019,7 +1019,7 @@ hh_status hh_engine::enqueue_q4k_mmr(int kind, size_t m, size_t n, const uint8_t
 // ---- batched Q4_K with int8 activations (q4k_mmi.hip) ----
 
 // Batched Q4_K with int8 activations (q4k_mmi.hip) from 17 tokens on: at 16 the f16
-// weight-stream kernels (q4k_mmr.hip) are faster on the MI355X (8B FFN, 32 layers: 1.32 ms
+// weight-stream kernels (q4k_mmr.hip) are faster on the MI355X (8B FFN, 32 layers: 1.26 ms
 // f16 vs 1.50 ms int8).
 constexpr size_t kMmqMinTokens = 17, kMmqMaxTokens = 64;
 
