@@ -238,6 +238,36 @@ HH_DEV void hh_moeg_stage(uint8_t* lds, const uint8_t* src, const int32_t* order
     __syncthreads();
 }
 
+// The first batch's token forms requested ahead of a workgroup's weight loads, by global->LDS
+// DMA (no registers held): 64 consecutive 16-byte chunks of the stage per instruction, wave w
+// taking chunk runs w, w + 4, ...  Vector loads complete in order, so once at most the weight
+// loads issued after them are outstanding the forms are in LDS (hh_moeg_stage_wait); a form
+// loaded after the weights, as hh_moeg_stage does, waits for all of them.
+HH_DEV void hh_moeg_stage_dma(uint8_t* lds, const uint8_t* src, const int32_t* order, int p0, int n, uint32_t k_div,
+                              size_t bytes) {
+    const uint32_t per = (uint32_t)(bytes / 16), tot = (uint32_t)n * per;
+    const uint32_t wave = threadIdx.x / HH_WAVE, lane = threadIdx.x % HH_WAVE;
+    for (uint32_t c0 = wave * HH_WAVE; c0 < tot; c0 += 4u * HH_WAVE) {  // 4 waves per workgroup
+        const uint32_t c = c0 + lane;
+        if (c < tot) {
+            const uint32_t i = c / per, o = c % per;
+            const uint32_t p = (uint32_t)order[p0 + (int)i], id = k_div ? p / k_div : p;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + id * bytes + o * 16u),
+                                             (__attribute__((address_space(3))) void*)(lds + (size_t)c0 * 16u), 16, 0, 0);
+        }
+    }
+    // the weight loads that follow stay after these copies in the instruction stream
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+// after the weight loads: the DMA of hh_moeg_stage_dma has landed (at most NW loads newer than
+// it outstanding), then every wave's part is visible
+template <int NW>
+HH_DEV void hh_moeg_stage_wait() {
+    __builtin_amdgcn_s_waitcnt((NW & 15) | ((NW >> 4) << 14) | (7 << 4) | (15 << 8));
+    __syncthreads();
+}
+
 // Gate/up: a team of TEAM lanes per row (lane = 64-column unit, d_model <= 64 * TEAM); each
 // team takes HH_MOEG_GU_RPT rows with all their loads in flight, then dots them with every token
 // of the expert (the lane's slice of the token's digits, staged in LDS HH_MOEG_NS tokens at a
@@ -258,6 +288,7 @@ HH_DEV void hh_moe_gu_grp_body(const hh_moeg_args& a) {
     const uint8_t* pack = a.experts + (size_t)e * a.expert_stride;
     const bool act = l < P;
     const uint32_t u = act ? l : 0u;
+    hh_moeg_stage_dma(stage, a.xq, a.order, p0, min(HH_MOEG_NS, np), a.k, xbytes);
     hh_q4k_data g[HH_MOEG_GU_RPT], up[HH_MOEG_GU_RPT];
 #pragma unroll
     for (int r = 0; r < HH_MOEG_GU_RPT; r++) {
@@ -267,8 +298,12 @@ HH_DEV void hh_moe_gu_grp_body(const hh_moeg_args& a) {
     }
     for (int i0 = 0; i0 < np; i0 += HH_MOEG_NS) {
         const int n = min(HH_MOEG_NS, np - i0);
-        if (i0 > 0) __syncthreads();  // the previous tokens' digits are consumed
-        hh_moeg_stage(stage, a.xq, a.order, p0, i0, n, a.k, xbytes);
+        if (i0 == 0) {
+            hh_moeg_stage_wait<3 * 2 * HH_MOEG_GU_RPT>();  // three loads per (row, matrix)
+        } else {
+            __syncthreads();  // the previous tokens' digits are consumed
+            hh_moeg_stage(stage, a.xq, a.order, p0, i0, n, a.k, xbytes);
+        }
         for (int i = 0; i < n; i++) {
             const uint32_t p = (uint32_t)a.order[p0 + i0 + i];
             hh_q4k_x xr;
@@ -311,13 +346,18 @@ HH_DEV void hh_moe_dn_grp_body(const hh_moeg_args& a) {
     const uint8_t* pack = a.experts + (size_t)e * a.expert_stride;
     const bool act = l < P;
     const uint32_t u = act ? l : 0u;
+    hh_moeg_stage_dma(stage, a.hq, a.order, p0, min(HH_MOEG_NS, np), 0u, hbytes);
     hh_q4k_data w[HH_MOEG_DN_RPT];
 #pragma unroll
     for (int r = 0; r < HH_MOEG_DN_RPT; r++) hh_q4k_load(pack + a.down_off + (size_t)min(j0 + r, dm - 1) * a.rb_ff, u, w[r]);
     for (int i0 = 0; i0 < np; i0 += HH_MOEG_NS) {
         const int n = min(HH_MOEG_NS, np - i0);
-        if (i0 > 0) __syncthreads();
-        hh_moeg_stage(stage, a.hq, a.order, p0, i0, n, 0u, hbytes);
+        if (i0 == 0) {
+            hh_moeg_stage_wait<3 * HH_MOEG_DN_RPT>();
+        } else {
+            __syncthreads();
+            hh_moeg_stage(stage, a.hq, a.order, p0, i0, n, 0u, hbytes);
+        }
         for (int i = 0; i < n; i++) {
             const uint32_t p = (uint32_t)a.order[p0 + i0 + i];
             hh_q4k_x hr;
