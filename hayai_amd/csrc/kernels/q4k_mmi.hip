@@ -143,9 +143,6 @@ HH_DEV void hh_mmi_lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// s_waitcnt immediate for vmcnt <= n (expcnt and lgkmcnt not waited for)
-constexpr int hh_mmi_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-
 // Two waves per 16-row unit (two per SIMD), wave half h taking sub-blocks 4h .. 4h + 3 of every
 // superblock: per item and matrix one 16-byte header load and one 16-byte qs load per lane (the
 // lane's row r16 = l % 16, bytes 64h + 16c .. + 15 of its qs, c = l / 16: 16-byte loads stream
@@ -199,8 +196,8 @@ HH_DEV void hh_mmi_body(const hh_mmi_args& a) {
         };
         if constexpr (REFILL) {
             // the first round's slots, then the rest of the ring (landing during the first
-            // round); before each round's barrier every copy issued so far has landed (they
-            // are for the round after the next, or the next)
+            // round); at the barrier closing each round every copy issued so far has landed,
+            // so the next round's slots are in LDS when it starts
             for (uint32_t k = 0; k < P; k++) copy(k, k);
             __builtin_amdgcn_s_waitcnt(0x0F70);
             hh_mmi_lds_barrier();
