@@ -4,8 +4,9 @@
 // crates/hayai-core/src/moe_infer.rs:342-455 (y[t] = sum over slots s of
 // w[t][s] * down_e(act(gate_e x_t) * up_e x_t), e = ids[t][s]):
 //   hh_moe_prep:         (token, slot) pairs p = t * k + s grouped by expert, in p order
-//                        within an expert, the active experts in ascending order; and every
-//                        token's x as int8 digits (hh_moe_route_prep: the routing too)
+//                        within an expert, the active experts in ascending order, with one
+//                        record per active expert (hh_moeg_args::rec); and every token's x as
+//                        int8 digits (hh_moe_route_prep: the routing too)
 //   hh_moe_gu_grp_t<TM>: grid.y = active expert; every row of gate and up is read once and
 //                        dotted with each of the expert's tokens: h[p][row] = act(g) * u
 //   hh_moe_hdigits:      h as digits, by pair
@@ -26,8 +27,9 @@ struct hh_moeg_args {
     float* yp;               // [T * k][d_model], by pair
     float* y;                // [T][d_model]
     int32_t* order;          // [T * k] pairs grouped by expert
-    int32_t* estart;         // [E + 1] first position of each expert in order
-    int32_t* elist;          // [E + 1] active experts ascending; elist[E] = their count
+    int32_t* rec;            // [min(E, T * k)][8]: per active expert y (ascending): the expert,
+                             // its first position in order, its pair count, its first
+                             // HH_MOEG_NS pairs; expert -1 past the active ones
     uint8_t* xq;             // [T] digit forms of x (hh_moe_digits layout, d_model elements)
     uint8_t* hq;             // [T * k] digit forms of h (d_ff elements)
     uint32_t T, k, d_model, d_ff, n_experts;
@@ -39,6 +41,7 @@ struct hh_moeg_args {
 #define HH_MOEG_GU_RPT 2      // rows per team, loads issued together (gate/up: 2 matrices)
 #define HH_MOEG_DN_RPT 4
 #define HH_MOEG_NS 4          // tokens whose digits a workgroup stages in LDS at a time
+#define HH_MOEG_REC 8         // ints per expert record (3 + HH_MOEG_NS, padded to 32 bytes)
 #define HH_MOEG_STAGE (HH_MOEG_NS * (2 * 4096 + (4096 / 32) * 8))  // d_model, d_ff <= 4096
 
 // bytes of the digit form of n elements (q1, q2, scale and sum per 32), as hh_moe_digits lays
@@ -103,10 +106,13 @@ HH_DEV int2 hh_moeg_scan256(int a, int b, int* ta, int* tb) {
     return make_int2(oa + ia - a, ob + ib - b);
 }
 
-// The grouping, by one workgroup of 256 threads.
+// The grouping, by one workgroup of 256 threads.  Each active expert's record carries what
+// its gate/up and down workgroups need before their first loads (one scalar load of 32 bytes
+// instead of a chain of dependent reads).
 HH_DEV void hh_moeg_group(const hh_moeg_args& a) {
     __shared__ int cnt[HH_MOEG_MAX_E];
     __shared__ int first[HH_MOEG_MAX_E];
+    __shared__ int apos[HH_MOEG_MAX_E];  // an active expert's position in ascending order
     __shared__ int pid[HH_MOEG_MAX_P];
     __shared__ uint32_t mask[HH_MOEG_MASK_WORDS];
     const uint32_t tid = threadIdx.x;
@@ -134,18 +140,27 @@ HH_DEV void hh_moeg_group(const hh_moeg_args& a) {
         const int2 ex = hh_moeg_scan256(c0 + c1, (c0 > 0) + (c1 > 0), &tot, &tot_a);
         if (e0 < E) {
             first[e0] = ex.x;
-            a.estart[e0] = ex.x;
-            if (c0) a.elist[ex.y] = (int)e0;
+            if (c0) {
+                int* r = a.rec + (size_t)ex.y * HH_MOEG_REC;
+                r[0] = (int)e0;
+                r[1] = ex.x;
+                r[2] = c0;
+                apos[e0] = ex.y;
+            }
         }
         if (e1 < E) {
             first[e1] = ex.x + c0;
-            a.estart[e1] = ex.x + c0;
-            if (c1) a.elist[ex.y + (c0 > 0)] = (int)e1;
+            if (c1) {
+                const int y = ex.y + (c0 > 0);
+                int* r = a.rec + (size_t)y * HH_MOEG_REC;
+                r[0] = (int)e1;
+                r[1] = ex.x + c0;
+                r[2] = c1;
+                apos[e1] = y;
+            }
         }
-        if (tid == 0) {
-            a.estart[E] = tot;
-            a.elist[E] = tot_a;
-        }
+        // the records past the active experts, up to the grid's min(E, P) rows
+        for (uint32_t y = (uint32_t)tot_a + tid; y < min(E, P); y += 256) a.rec[(size_t)y * HH_MOEG_REC] = -1;
     }
     __syncthreads();
     for (uint32_t p = tid; p < P; p += 256) {
@@ -160,6 +175,7 @@ HH_DEV void hh_moeg_group(const hh_moeg_args& a) {
             for (uint32_t q = 0; q < p; q++) r += pid[q] == e;
         }
         a.order[first[e] + r] = (int)p;
+        if (r < HH_MOEG_NS) a.rec[(size_t)apos[e] * HH_MOEG_REC + 3 + r] = (int)p;
     }
 }
 
@@ -238,20 +254,22 @@ HH_DEV void hh_moeg_stage(uint8_t* lds, const uint8_t* src, const int32_t* order
     __syncthreads();
 }
 
-// The first batch's token forms requested ahead of a workgroup's weight loads, by global->LDS
-// DMA (no registers held): 64 consecutive 16-byte chunks of the stage per instruction, wave w
+// The first batch's token forms (pairs from the expert's record) requested ahead of a
+// workgroup's weight loads, by global->LDS DMA (no registers held): 64 consecutive 16-byte chunks of the stage per instruction, wave w
 // taking chunk runs w, w + 4, ...  Vector loads complete in order, so once at most the weight
 // loads issued after them are outstanding the forms are in LDS (hh_moeg_stage_wait); a form
 // loaded after the weights, as hh_moeg_stage does, waits for all of them.
-HH_DEV void hh_moeg_stage_dma(uint8_t* lds, const uint8_t* src, const int32_t* order, int p0, int n, uint32_t k_div,
+HH_DEV void hh_moeg_stage_dma(uint8_t* lds, const uint8_t* src, const int (&first)[HH_MOEG_NS], int n, uint32_t k_div,
                               size_t bytes) {
+    static_assert(HH_MOEG_NS == 4, "the pair select below");
     const uint32_t per = (uint32_t)(bytes / 16), tot = (uint32_t)n * per;
     const uint32_t wave = threadIdx.x / HH_WAVE, lane = threadIdx.x % HH_WAVE;
     for (uint32_t c0 = wave * HH_WAVE; c0 < tot; c0 += 4u * HH_WAVE) {  // 4 waves per workgroup
         const uint32_t c = c0 + lane;
         if (c < tot) {
             const uint32_t i = c / per, o = c % per;
-            const uint32_t p = (uint32_t)order[p0 + (int)i], id = k_div ? p / k_div : p;
+            const int f = i == 0 ? first[0] : i == 1 ? first[1] : i == 2 ? first[2] : first[3];
+            const uint32_t p = (uint32_t)f, id = k_div ? p / k_div : p;
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + id * bytes + o * 16u),
                                              (__attribute__((address_space(3))) void*)(lds + (size_t)c0 * 16u), 16, 0, 0);
         }
@@ -275,10 +293,11 @@ HH_DEV void hh_moeg_stage_wait() {
 template <int TEAM>
 HH_DEV void hh_moe_gu_grp_body(const hh_moeg_args& a) {
     __shared__ __attribute__((aligned(16))) uint8_t stage[HH_MOEG_STAGE];
-    const int na = a.elist[a.n_experts];
-    if ((int)blockIdx.y >= na) return;  // grid.y covers the most experts a call can select
-    const int e = a.elist[blockIdx.y];
-    const int p0 = a.estart[e], np = a.estart[e + 1] - p0;
+    const int* const rc = a.rec + (size_t)blockIdx.y * HH_MOEG_REC;
+    const int e = rc[0];
+    if (e < 0) return;  // grid.y covers the most experts a call can select
+    const int p0 = rc[1], np = rc[2];
+    const int first[HH_MOEG_NS] = {rc[3], rc[4], rc[5], rc[6]};
     const uint32_t dm = a.d_model, df = a.d_ff, P = dm / 64;
     const size_t xbytes = hh_digits_bytes_dev(dm);
     constexpr uint32_t TPB = 256 / TEAM;
@@ -288,7 +307,7 @@ HH_DEV void hh_moe_gu_grp_body(const hh_moeg_args& a) {
     const uint8_t* pack = a.experts + (size_t)e * a.expert_stride;
     const bool act = l < P;
     const uint32_t u = act ? l : 0u;
-    hh_moeg_stage_dma(stage, a.xq, a.order, p0, min(HH_MOEG_NS, np), a.k, xbytes);
+    hh_moeg_stage_dma(stage, a.xq, first, min(HH_MOEG_NS, np), a.k, xbytes);
     hh_q4k_data g[HH_MOEG_GU_RPT], up[HH_MOEG_GU_RPT];
 #pragma unroll
     for (int r = 0; r < HH_MOEG_GU_RPT; r++) {
@@ -333,10 +352,11 @@ HH_DEV void hh_moe_gu_grp_body(const hh_moeg_args& a) {
 template <int TEAM>
 HH_DEV void hh_moe_dn_grp_body(const hh_moeg_args& a) {
     __shared__ __attribute__((aligned(16))) uint8_t stage[HH_MOEG_STAGE];
-    const int na = a.elist[a.n_experts];
-    if ((int)blockIdx.y >= na) return;
-    const int e = a.elist[blockIdx.y];
-    const int p0 = a.estart[e], np = a.estart[e + 1] - p0;
+    const int* const rc = a.rec + (size_t)blockIdx.y * HH_MOEG_REC;
+    const int e = rc[0];
+    if (e < 0) return;
+    const int p0 = rc[1], np = rc[2];
+    const int first[HH_MOEG_NS] = {rc[3], rc[4], rc[5], rc[6]};
     const uint32_t dm = a.d_model, df = a.d_ff, P = df / 64;
     const size_t hbytes = hh_digits_bytes_dev(df);
     constexpr uint32_t TPB = 256 / TEAM;
@@ -346,7 +366,7 @@ HH_DEV void hh_moe_dn_grp_body(const hh_moeg_args& a) {
     const uint8_t* pack = a.experts + (size_t)e * a.expert_stride;
     const bool act = l < P;
     const uint32_t u = act ? l : 0u;
-    hh_moeg_stage_dma(stage, a.hq, a.order, p0, min(HH_MOEG_NS, np), 0u, hbytes);
+    hh_moeg_stage_dma(stage, a.hq, first, min(HH_MOEG_NS, np), 0u, hbytes);
     hh_q4k_data w[HH_MOEG_DN_RPT];
 #pragma unroll
     for (int r = 0; r < HH_MOEG_DN_RPT; r++) hh_q4k_load(pack + a.down_off + (size_t)min(j0 + r, dm - 1) * a.rb_ff, u, w[r]);

@@ -1252,6 +1252,7 @@ constexpr int kMoeBlock = 256;
 constexpr size_t kLdsBytes = 160 * 1024;  // LDS per workgroup on gfx950
 constexpr size_t kMoeDownRows = 4;  // output rows per down workgroup (moe.hip)
 constexpr size_t kMoegGuRows = 2, kMoegDnRows = 4;  // grouped MoE rows per team (HH_MOEG_*_RPT, moe_group.hip)
+constexpr size_t kMoegRecInts = 8;                   // ints per grouped-MoE expert record (HH_MOEG_REC)
 
 static int moe_team(size_t units) { return units <= 16 ? 16 : (units <= 32 ? 32 : 64); }
 
@@ -1338,7 +1339,8 @@ hh_status hh_engine::enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* expert
     if (moe_grouped && P <= 4096 && E <= 512 && dm / 64 <= 64 && df / 64 <= 64 &&
         ((d->expert_stride | d->gate_off | d->up_off | d->down_off | (uintptr_t)experts | (uintptr_t)x) & 15u) == 0) {
         HH_TRY(grow(&ws_moe_yp, &ws_moe_yp_cap, P * dm * sizeof(float)));
-        HH_TRY(grow(&ws_moe_grp, &ws_moe_grp_cap, (P + 2 * (E + 1)) * sizeof(int32_t)));
+        const size_t gy = std::min(E, P);  // grid rows of the grouped kernels: the most active experts
+        HH_TRY(grow(&ws_moe_grp, &ws_moe_grp_cap, (P + gy * kMoegRecInts) * sizeof(int32_t)));
         const size_t xqb = hh_digits_bytes(dm), hqb = hh_digits_bytes(df);
         HH_TRY(grow(&ws_moe_q, &ws_moe_q_cap, T * xqb + P * hqb));
         struct {
@@ -1348,13 +1350,13 @@ hh_status hh_engine::enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* expert
             const float* wts;
             const float* x;
             float *h, *yp, *y;
-            int32_t *order, *estart, *elist;
+            int32_t *order, *rec;
             uint8_t *xq, *hq;
             uint32_t T, k, d_model, d_ff, n_experts;
             int32_t act;
         } g{experts, d->expert_stride, d->gate_off, d->up_off, d->down_off, a.rb_in, a.rb_ff, ids, wts, x,
-            (float*)ws_moe_h, (float*)ws_moe_yp, y, (int32_t*)ws_moe_grp, (int32_t*)ws_moe_grp + P,
-            (int32_t*)ws_moe_grp + P + E + 1, (uint8_t*)ws_moe_q, (uint8_t*)ws_moe_q + T * xqb, (uint32_t)T,
+            (float*)ws_moe_h, (float*)ws_moe_yp, y, (int32_t*)ws_moe_grp + gy * kMoegRecInts,
+            (int32_t*)ws_moe_grp, (uint8_t*)ws_moe_q, (uint8_t*)ws_moe_q + T * xqb, (uint32_t)T,
             (uint32_t)k, (uint32_t)dm, (uint32_t)df, (uint32_t)E, d->act};
         hipFunction_t fn;
         if (logits) {
@@ -1375,13 +1377,12 @@ hh_status hh_engine::enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* expert
             HH_TRY(kernel("hh_moe_prep", &fn));
             HH_TRY(launch(fn, (uint32_t)(1 + T), 256, g));
         }
-        const uint32_t gy = (uint32_t)std::min(E, P);
         {
             const int team = moe_team(dm / 64);
             const size_t rows = (size_t)(kMoeBlock / team) * kMoegGuRows;
             HH_TRY(kernel("hh_moe_gu_grp_t" + std::to_string(team), &fn));
             void* gp[] = {&g};
-            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)((df + rows - 1) / rows), gy, 1, kMoeBlock, 1, 1, 0, stream,
+            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)((df + rows - 1) / rows), (uint32_t)gy, 1, kMoeBlock, 1, 1, 0, stream,
                                              gp, nullptr),
                        "launch(moe grouped gate/up)");
         }
@@ -1392,7 +1393,7 @@ hh_status hh_engine::enqueue_moe_ffn(const hh_moe_desc* d, const uint8_t* expert
             const size_t rows = (size_t)(kMoeBlock / team) * kMoegDnRows;
             HH_TRY(kernel("hh_moe_dn_grp_t" + std::to_string(team), &fn));
             void* gp[] = {&g};
-            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)((dm + rows - 1) / rows), gy, 1, kMoeBlock, 1, 1, 0, stream,
+            HH_TRY_HIP(hipModuleLaunchKernel(fn, (uint32_t)((dm + rows - 1) / rows), (uint32_t)gy, 1, kMoeBlock, 1, 1, 0, stream,
                                              gp, nullptr),
                        "launch(moe grouped down)");
         }

@@ -140,7 +140,7 @@ struct hh_engine {
     size_t ws_moe_w_cap = 0;
     void* ws_moe_yp = nullptr;   // grouped MoE: per-pair down outputs [T*k][d_model]
     size_t ws_moe_yp_cap = 0;
-    void* ws_moe_grp = nullptr;  // grouped MoE: pair order, expert starts, active experts
+    void* ws_moe_grp = nullptr;  // grouped MoE: the active experts' records, the pairs grouped by expert
     size_t ws_moe_grp_cap = 0;
     void* ws_moe_q = nullptr;    // grouped MoE: x digits per token, h digits per pair
     size_t ws_moe_q_cap = 0;
