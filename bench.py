@@ -1480,7 +1480,9 @@ def main() -> int:
         "data": "synthetic (seeded Q4_K blocks, N(0,1) f32 activations, norm weights 1 + 0.1 N(0,1))",
         "config": {"workload": "llama3-8b-ffn-q4_k-bs1-32layers-resident", "d_model": D_MODEL, "d_ff": D_FF,
                    "layers": LAYERS, "batch": 1, "weights": "Q4_K", "act": "silu",
-                   "step": "32 layers chained on one residual stream (RMSNorm + FFN + residual, ffn_apply)",
+                   "step": "32 layers chained on one residual stream (RMSNorm + FFN + residual, ffn_apply); "
+                           "a bandwidth harness: random weights, the stream carried from step to step "
+                           "(its values grow; the kernels' time does not depend on them)",
                    "launch": "eager, 2 kernels per layer"},
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "ffn_tok_s": round(1e3 / ms, 2),
