@@ -271,3 +271,37 @@ def _engine_with_env(**env):
                 del os.environ[k]
             else:
                 os.environ[k] = v
+
+
+@pytest.mark.parametrize("T", [512, 513])
+def test_moe_grouped_at_the_pair_limit(engine, T):
+    # 512 tokens x top-8 = 4096 (token, slot) pairs, the most the grouped kernels take in one
+    # call (every expert active, ~32 pairs each: several LDS passes per expert, records and
+    # rank masks at full size); 513 tokens go to the per-(token, expert) kernels instead.
+    # Routed on the GPU (hh_moe_dev) and from given ids (hh_moe_ffn_dev): bit-identical, and
+    # each token against the oracle.
+    E, k, d_model, d_ff = 128, 8, 256, 256
+    oracle.set_threads(min(16, oracle.max_threads()))
+    print(f"[case] moe pair limit E={E} k={k} {d_model}x{d_ff} T={T}", flush=True)
+    buf, host, stride, offs = make_experts(engine, E, d_model, d_ff, 333)
+    d = engine.moe_desc(d_model, d_ff, E, k, stride, offs, norm_topk_prob=True)
+    rng = np.random.default_rng(T)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    x = synth.normal(synth.seed_for(6, T, synth.ACT), T * d_model).reshape(T, d_model)
+    lb, xb = engine.upload(logits), engine.upload(x)
+    ids_b, w_b = engine.alloc(4 * T * k), engine.alloc(4 * T * k)
+    y1, y2 = engine.alloc(4 * T * d_model), engine.alloc(4 * T * d_model)
+    engine.route_experts_dev(d, lb, 0, None, 0, T, ids_b, 0, w_b, 0)
+    engine.moe_ffn_dev(d, buf, 0, xb, 0, T, ids_b, 0, w_b, 0, y1, 0)
+    engine.moe_dev(d, buf, 0, lb, 0, None, 0, xb, 0, T, y2, 0)
+    ids = ids_b.read(np.int32, T * k).reshape(T, k)
+    w = w_b.read(np.float32, T * k).reshape(T, k)
+    Y = y1.read(np.float32, T * d_model).reshape(T, d_model)
+    np.testing.assert_array_equal(Y, y2.read(np.float32, T * d_model).reshape(T, d_model))
+    assert len(np.unique(ids)) == E  # every expert has pairs
+    worst = 0.0
+    for t in range(T):
+        ref = oracle.moe_token(Q4_K, d_model, d_ff, host, stride, offs, ids[t], w[t], x[t])
+        worst = max(worst, float(np.max(np.abs(Y[t] - ref)) / np.max(np.abs(ref))))
+    print(f"  worst token rel err {worst:.3e}", flush=True)
+    assert worst <= REL_TOL
